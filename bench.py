@@ -1,0 +1,338 @@
+"""Benchmark of the fused Qwen3 layer operators on one MI355X.
+
+Headline workload: prefill n = 2811 at Qwen3-1.7B shape
+(H = 2048, 16 q heads, 8 kv heads, head_dim 128, I = 6144), all 28 layers, each
+layer with its own seeded buffers and weights. One step = for every layer:
+  residual add + RMSNorm      [n, H]              (rpg_op_add_rms_norm)
+  q/k norm + RoPE + fp16 KV   [n, 16|8, 128]      (rpg_op_qk_norm_rope_kv)
+  SwiGLU                      [n, I]              (rpg_op_silu_mul_inplace)
+`value` = algorithmic bytes of the step / step time (GB/s); per-kernel averages
+come from HIP events around every launch of the timed steps. The 28 layers'
+buffers total ~9 GB, far above the 256 MB Infinity Cache, so every launch reads
+from HBM. Also reported: decode n = 1 (us per layer, eager and HIP graph), the
+Q4_K / Q6_K embedding gather at n = 2811, a streaming-copy ceiling, and the CPU
+oracle on the host cores as a baseline.
+
+python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, REPO)
+
+METRIC = "fused layer-op HBM GB/s (% of MI355X peak) at n=1 decode and n=2811 prefill"
+PEAK_GBPS = 8000.0
+
+H, HQ, HKV, D, INTER, LAYERS = 2048, 16, 8, 128, 6144, 28
+MAX_SEQ, EPS, THETA = 4096, 1e-6, 1e6
+N_PREFILL = 2811
+VOCAB = 151936
+
+
+def bytes_add_rms(n, h=H):
+    return 16 * n * h + 4 * h
+
+
+def bytes_qk(n, hq=HQ, hkv=HKV, d=D):
+    return n * (8 * hq * d + 12 * hkv * d + 4 * d) + 8 * d
+
+
+def bytes_swiglu(n, inter=INTER):
+    return 12 * n * inter
+
+
+def bytes_gather(n, bb, h=H):
+    return n * (4 + (h // 256) * bb + 4 * h)
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Layer:
+    """One layer's device buffers (all distinct per layer)."""
+
+    def __init__(self, torch, n, gen):
+        f32 = dict(dtype=torch.float32, device="cuda")
+        self.x = torch.randn((n, H), generator=gen, **f32)
+        self.d = torch.randn((n, H), generator=gen, **f32)
+        self.h = torch.empty((n, H), **f32)
+        self.w = 1.0 + 0.1 * torch.randn(H, generator=gen, **f32)
+        self.q = torch.randn((n, HQ, D), generator=gen, **f32)
+        self.k = torch.randn((n, HKV, D), generator=gen, **f32)
+        self.v = torch.randn((n, HKV, D), generator=gen, **f32)
+        self.qn = 1.0 + 0.1 * torch.randn(D, generator=gen, **f32)
+        self.kn = 1.0 + 0.1 * torch.randn(D, generator=gen, **f32)
+        self.kc = torch.zeros(HKV * MAX_SEQ * D, dtype=torch.int16, device="cuda")
+        self.vc = torch.zeros_like(self.kc)
+        self.gate = torch.randn((n, INTER), generator=gen, **f32)
+        self.up = torch.randn((n, INTER), generator=gen, **f32)
+
+
+def run_layer(ops, L, n, tab, pos0):
+    ops.GpuAddRmsNorm(L.x, L.d, L.w, n, H, EPS, L.h)
+    ops.GpuQkNormRopeKv(L.q, L.k, L.v, L.qn, L.kn, HQ, HKV, D, tab, MAX_SEQ, pos0, n, EPS, L.kc, L.vc, MAX_SEQ)
+    ops.GpuSiluMulInPlace(L.gate, L.up, n * INTER)
+
+
+OP_NAMES = ("add_rms_norm", "qk_norm_rope_kv", "swiglu")
+KERNEL_NAMES = {"add_rms_norm": "AddRmsNormWaveKernel<8>", "qk_norm_rope_kv": "QkNormRopeKvKernel<false>",
+                "swiglu": "BinaryVecKernel<SiluMulOp>"}
+
+
+def timed_prefill(torch, ops, layers, tab, n, steps, warmup):
+    """Returns (ms_per_step, {op: [per-launch ms]})."""
+    for _ in range(warmup):
+        for L in layers:
+            run_layer(ops, L, n, tab, 0)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = []
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for _ in range(steps):
+        for L in layers:
+            marks = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+            marks[0].record(stream)
+            ops.GpuAddRmsNorm(L.x, L.d, L.w, n, H, EPS, L.h)
+            marks[1].record(stream)
+            ops.GpuQkNormRopeKv(L.q, L.k, L.v, L.qn, L.kn, HQ, HKV, D, tab, MAX_SEQ, 0, n, EPS, L.kc, L.vc, MAX_SEQ)
+            marks[2].record(stream)
+            ops.GpuSiluMulInPlace(L.gate, L.up, n * INTER)
+            marks[3].record(stream)
+            ev.append(marks)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    total_ms = t0.elapsed_time(t1)
+    per = {name: [] for name in OP_NAMES}
+    for marks in ev:
+        for i, name in enumerate(OP_NAMES):
+            per[name].append(marks[i].elapsed_time(marks[i + 1]))
+    return total_ms / steps, per
+
+
+def measure_decode(torch, ops, tab, steps):
+    """n = 1 decode at a random position: us per layer for the 3 fused ops, eager and as a HIP graph."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(3)
+    layers = [Layer(torch, 1, gen) for _ in range(LAYERS)]
+    pos = 2731
+    for _ in range(5):
+        for L in layers:
+            run_layer(ops, L, 1, tab, pos)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        for L in layers:
+            run_layer(ops, L, 1, tab, pos)
+    torch.cuda.synchronize()
+    eager_us = (time.perf_counter() - t0) * 1e6 / (steps * LAYERS)
+
+    graph_us = None
+    try:
+        g = torch.cuda.CUDAGraph()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            with ops.ScopedEngineStream(s):
+                g.capture_begin()
+                for L in layers:
+                    run_layer(ops, L, 1, tab, pos)
+                g.capture_end()
+        torch.cuda.synchronize()
+        ops.stage_pos0(pos)
+        torch.cuda.synchronize()
+        for _ in range(5):
+            g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        graph_us = e0.elapsed_time(e1) * 1e3 / (steps * LAYERS)
+    except Exception as exc:  # graph capture unavailable: report eager only
+        log(f"decode graph capture failed: {exc}")
+    b = bytes_add_rms(1) + bytes_qk(1) + bytes_swiglu(1)
+    return {"us_per_layer_eager": round(eager_us, 3),
+            "us_per_layer_graph": None if graph_us is None else round(graph_us, 3),
+            "bytes_per_layer": b, "position": pos, "launches_per_layer": 3}
+
+
+def measure_gather(torch, ops, ggml_type, bb, copies=4, reps=20):
+    """n = 2811 ids gathered from a [151936, 2048] table, rotating over `copies` table copies."""
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(10 + ggml_type)
+    row_bytes = (H // 256) * bb
+    tables = [torch.randint(0, 256, (VOCAB * row_bytes,), dtype=torch.uint8, device="cuda", generator=gen)
+              for _ in range(copies)]
+    toks = torch.randint(0, VOCAB, (N_PREFILL,), dtype=torch.int32, device="cuda", generator=gen)
+    outs = [torch.empty((N_PREFILL, H), dtype=torch.float32, device="cuda") for _ in range(copies)]
+    embs = [ops.GpuTensor(t, ggml_type, VOCAB, H) for t in tables]
+    for i in range(copies):
+        ops.GpuEmbeddingLookup(embs[i], toks, N_PREFILL, outs[i])
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    times = []
+    for r in range(reps):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record(stream)
+        ops.GpuEmbeddingLookup(embs[r % copies], toks, N_PREFILL, outs[r % copies])
+        b.record(stream)
+        times.append((a, b))
+    torch.cuda.synchronize()
+    ms = sorted(a.elapsed_time(b) for a, b in times)
+    med = ms[len(ms) // 2]
+    nbytes = bytes_gather(N_PREFILL, bb)
+    del tables, outs
+    return {"us": round(med * 1e3, 2), "GBps": round(nbytes / (med * 1e-3) / 1e9, 1), "bytes": nbytes}
+
+
+def measure_copy(torch, ops, nbytes=1 << 30, reps=10):
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    ops.GpuStreamCopy(src, dst, nbytes)
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        ops.GpuStreamCopy(src, dst, nbytes)
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / reps
+    del src, dst
+    return round(2 * nbytes / (ms * 1e-3) / 1e9, 1)
+
+
+def profile_traffic(kernel_tag):
+    """HBM bytes per launch of `kernel_tag` from the committed rocprofv3 counter summary, if any."""
+    path = os.path.join(REPO, "profiles", "pmc_traffic_prefill_n2811.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        m = re.match(r"\s*traffic_bytes_per_launch\[(.+?)\]\s*=\s*([0-9.eE+]+)", line)
+        if m and m.group(1) == kernel_tag:
+            return float(m.group(2))
+    return None
+
+
+def cpu_baseline():
+    """The oracle's C restatement of one layer of the chain (n = 2811, 1.7B shape)
+    on the host cores, median of 5; a reported baseline only."""
+    from oracle import pyoracle
+
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    sec = pyoracle.bench_layer_chain(threads, N_PREFILL, H, HQ, HKV, INTER, 5)
+    if sec <= 0:
+        return None
+    b = bytes_add_rms(N_PREFILL) + bytes_qk(N_PREFILL) + bytes_swiglu(N_PREFILL)
+    return {"value": round(b / sec / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"one layer of the n={N_PREFILL} chain (add+RMSNorm, qk-norm+RoPE+fp16 KV, SwiGLU; "
+                      f"{b} B) by the C oracle, rows split over {threads} threads, median of 5 runs "
+                      f"({sec * 1e3:.1f} ms each)"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-extras", action="store_true", help="only the headline prefill workload")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from rpgbarenginecuda_amd import ops
+
+    ops.load_library()
+    ops.init()
+    ops.set_stream(torch.cuda.current_stream())
+    ok, desc = ops.device_info()
+    log(desc)
+    from oracle import pyoracle  # noqa: F401  (rope table comes from the library, not the oracle)
+
+    tab = torch.from_numpy(ops.build_rope_table(D, THETA, MAX_SEQ)).cuda()
+
+    log(f"allocating {LAYERS} layers of prefill buffers (n={N_PREFILL})")
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(2026)
+    layers = [Layer(torch, N_PREFILL, gen) for _ in range(LAYERS)]
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps after {args.warmup} warmup")
+    ms_step, per = timed_prefill(torch, ops, layers, tab, N_PREFILL, args.steps, args.warmup)
+    step_bytes = LAYERS * (bytes_add_rms(N_PREFILL) + bytes_qk(N_PREFILL) + bytes_swiglu(N_PREFILL))
+    value = step_bytes / (ms_step * 1e-3) / 1e9
+    op_bytes = {"add_rms_norm": bytes_add_rms(N_PREFILL), "qk_norm_rope_kv": bytes_qk(N_PREFILL),
+                "swiglu": bytes_swiglu(N_PREFILL)}
+    op_stats = {}
+    for name in OP_NAMES:
+        avg = sum(per[name]) / len(per[name])
+        op_stats[name] = {"us": round(avg * 1e3, 2), "GBps": round(op_bytes[name] / (avg * 1e-3) / 1e9, 1),
+                          "pct_peak": round(op_bytes[name] / (avg * 1e-3) / 1e9 / PEAK_GBPS * 100, 1),
+                          "bytes": op_bytes[name], "kernel": KERNEL_NAMES[name]}
+    dominant = max(OP_NAMES, key=lambda k: op_stats[k]["us"])
+    d_avg_s = op_stats[dominant]["us"] * 1e-6
+    achieved = op_bytes[dominant] / d_avg_s / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_GBPS, 4), "traffic": profile_traffic(KERNEL_NAMES[dominant]),
+                "kernel": KERNEL_NAMES[dominant], "algorithmic_bytes_per_launch": op_bytes[dominant]}
+    del layers
+    torch.cuda.empty_cache()
+
+    extras = {}
+    if not args.no_extras:
+        log("decode n=1")
+        extras["decode_n1"] = measure_decode(torch, ops, tab, max(20, args.steps))
+        log("gather Q4_K / Q6_K")
+        extras["gather_q4k_n2811"] = measure_gather(torch, ops, ops.GGML_Q4_K, 144)
+        extras["gather_q6k_n2811"] = measure_gather(torch, ops, ops.GGML_Q6_K, 210)
+        log("stream copy ceiling")
+        extras["stream_copy_GBps"] = measure_copy(torch, ops)
+    cpu = None if args.no_cpu else cpu_baseline()
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded torch.randn activations and N(1,0.1) norm weights per layer)",
+        "config": {"workload": "configs[3]: prefill n=2811, Qwen3-1.7B shape, 28 layers with independent buffers; "
+                               "per layer residual+RMSNorm, q/k-norm+RoPE+fp16 KV write, SwiGLU",
+                   "n_tokens": N_PREFILL, "layers": LAYERS, "hidden": H, "n_heads": HQ, "n_kv_heads": HKV,
+                   "head_dim": D, "intermediate": INTER, "max_seq": MAX_SEQ, "bytes_per_step": step_bytes},
+        "pct_of_peak": round(value / PEAK_GBPS * 100, 2),
+        "ops": op_stats,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        **extras,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,151 @@
+/* rpg_ops.h -- C ABI of the MI355X hot-path operators of the Qwen3 layer.
+ *
+ * librpg_ops.so exports exactly the functions declared here. Every argument is a
+ * plain pointer or integer; every pointer named *_dev / x / q / k / v / w / out is
+ * a device pointer owned by the caller. Launches are asynchronous on the engine
+ * stream (rpg_ops_set_stream; NULL = the null stream) and nothing synchronises.
+ *
+ * Status convention (the reference ABI's, include/rpg_engine.h:46-55): 0 on
+ * success, a negative value on failure with the reason available from
+ * rpg_ops_last_error() (thread-local). Argument errors are detected on the host
+ * before anything is launched, and no C++ exception crosses this boundary.
+ *
+ * Each operator cites the reference interface it replaces. The C++ operator
+ * layer with the reference's own signatures (namespace rpg, src/kernels_gpu.h)
+ * lives in rpgbarenginecuda_amd/csrc/kernels_gpu.h; these entry points forward
+ * to it one to one.
+ */
+#ifndef RPG_OPS_H
+#define RPG_OPS_H
+
+#include <stdint.h>
+
+#if defined(__GNUC__)
+#define RPG_OPS_API __attribute__((visibility("default")))
+#else
+#define RPG_OPS_API
+#endif
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RPG_OPS_OK 0
+
+/* ggml type ids accepted by the device path (src/quant.h:22-38). */
+#define RPG_GGML_F32 0u
+#define RPG_GGML_Q4_K 12u
+#define RPG_GGML_Q6_K 14u
+
+/* ---------------------------------------------------------------- library */
+
+/* Version string of this library, e.g. "0.1.0". */
+RPG_OPS_API const char* rpg_ops_version(void);
+
+/* Text of the last failure on the calling thread (do not free).
+ * Replaces: rpg_engine_last_error, include/rpg_engine.h:55. */
+RPG_OPS_API const char* rpg_ops_last_error(void);
+
+/* Allocates the fixed-address pos0 scalar on the current device. Must be
+ * called once before any operator is captured into a HIP graph (allocation is
+ * illegal during capture). Replaces: PosStagingPtr, src/cuda_common.h:153. */
+RPG_OPS_API int32_t rpg_ops_init(void);
+
+/* Routes every following launch to `stream` (a hipStream_t; NULL = null stream).
+ * Replaces: ScopedEngineStream / EngineStream, src/cuda_common.h:116-137. */
+RPG_OPS_API int32_t rpg_ops_set_stream(void* stream);
+RPG_OPS_API void* rpg_ops_get_stream(void);
+
+/* Writes pos into the pos0 scalar read by captured (graph) launches; a graph
+ * replay loop calls it before each replay. Replaces: StagePos0,
+ * src/cuda_common.h:154. */
+RPG_OPS_API int32_t rpg_ops_stage_pos0(int64_t pos);
+
+/* One-line description of device 0 written into buf (NUL-terminated).
+ * Returns 1 if a device is available, 0 if not (buf says why), <0 on error.
+ * Replaces: QueryDevice / DescribeDevice, src/cuda_common.h:52-56. */
+RPG_OPS_API int32_t rpg_ops_device_info(char* buf, int32_t cap);
+
+/* Bytes of n_elems elements of a device type (n_elems a block multiple);
+ * negative on error. Replaces: TypeRowBytes, src/quant.h:57. */
+RPG_OPS_API int64_t rpg_ops_type_row_bytes(uint32_t type, int64_t n_elems);
+
+/* Host RoPE table [n_pos][head_dim] fp32 (cos half | sin half), angles in
+ * double, into caller-provided host memory of n_pos*head_dim floats.
+ * Replaces: GpuModel::BuildRopeTable, src/gpu_model.cu:90-120. */
+RPG_OPS_API int32_t rpg_ops_build_rope_table(int32_t head_dim, double theta, int64_t n_pos, float* out_host);
+
+/* ---------------------------------------------------------------- reference operators */
+
+/* One row of n_elems elements of `type` -> fp32, bit-exact with the CPU dequant.
+ * Replaces: GpuDequantRow, src/kernels_gpu.h:39-40. */
+RPG_OPS_API int32_t rpg_op_dequant_row(uint32_t type, const uint8_t* src_dev, int64_t n_elems, float* dst_dev);
+
+/* out[r] = x[r] * float(1/sqrt(sum(x[r]^2)/n + eps)) * w over n_rows rows of n
+ * elements spaced `stride` apart; out may equal x.
+ * Replaces: GpuRmsNorm, src/kernels_gpu.h:65-66. */
+RPG_OPS_API int32_t rpg_op_rms_norm(const float* x, const float* w, int64_t n_rows, int64_t n, int64_t stride,
+                                    float eps, float* out);
+
+/* NeoX RoPE in place on x[n_rows][n_heads][head_dim] at positions pos0 + row;
+ * rope_tab is [positions][head_dim] (cos | sin).
+ * Replaces: GpuRope, src/kernels_gpu.h:71-72. */
+RPG_OPS_API int32_t rpg_op_rope(float* x, int32_t n_heads, int32_t head_dim, const float* rope_tab, int64_t pos0,
+                                int64_t n_rows);
+
+/* k, v [seq][n_kv_heads][head_dim] fp32 -> k_layer, v_layer [n_kv_heads][max_seq][head_dim]
+ * fp16 bits (IEEE round-to-nearest-even) at positions pos0..pos0+seq-1.
+ * Replaces: GpuKvWrite, src/kernels_gpu.h:97-99. */
+RPG_OPS_API int32_t rpg_op_kv_write(const float* k, const float* v, int32_t n_kv_heads, int32_t head_dim,
+                                    int64_t pos0, int64_t seq, uint16_t* k_layer, uint16_t* v_layer,
+                                    int64_t max_seq);
+
+/* gate[i] = silu(gate[i]) * up[i]; n <= 0 is a no-op.
+ * Replaces: GpuSiluMulInPlace, src/kernels_gpu.h:147. */
+RPG_OPS_API int32_t rpg_op_silu_mul_inplace(float* gate, const float* up, int64_t n);
+
+/* a[i] += b[i]; n <= 0 is a no-op. Replaces: GpuVecAddInPlace, src/kernels_gpu.h:150. */
+RPG_OPS_API int32_t rpg_op_vec_add_inplace(float* a, const float* b, int64_t n);
+
+/* x[t] = dequantised row toks[t] of the [rows][cols] table of `type` (raw GGUF
+ * bytes); ids outside [0, rows) give a zero row.
+ * Replaces: GpuEmbeddingLookup, src/kernels_gpu.h:153-154 (its GpuTensor
+ * argument flattened to type / data / rows / cols). */
+RPG_OPS_API int32_t rpg_op_embedding_lookup(uint32_t type, const uint8_t* emb, int64_t rows, int64_t cols,
+                                            const int32_t* toks, int64_t seq, float* x);
+
+/* ---------------------------------------------------------------- fused operators */
+
+/* x[r] += d[r] (bit-exact fp32 add, written back), then out[r] = RMSNorm(x[r]) * w,
+ * rows contiguous (stride n); out must not alias x or d.
+ * Replaces: GpuVecAddInPlace + GpuRmsNorm, src/qwen3_gpu.cu:100->103 and :108->69. */
+RPG_OPS_API int32_t rpg_op_add_rms_norm(float* x, const float* d, const float* w, int64_t n_rows, int64_t n,
+                                        float eps, float* out);
+
+/* Per token t (position pos0 + t): q <- RoPE(RMSNorm(q) * q_norm) in place;
+ * k' = RoPE(RMSNorm(k) * k_norm); k_layer/v_layer[h][pos0+t] <- fp16_rne(k'), fp16_rne(v);
+ * k <- k' only if write_k_f32 != 0 (head_dim != 128 always writes it).
+ * rope_rows = rows of rope_tab. q [seq][n_heads][head_dim], k/v [seq][n_kv_heads][head_dim].
+ * Replaces: GpuRmsNorm(q), GpuRmsNorm(k), GpuRope(q), GpuRope(k), GpuKvWrite,
+ * src/qwen3_gpu.cu:77-91. */
+RPG_OPS_API int32_t rpg_op_qk_norm_rope_kv(float* q, float* k, const float* v, const float* q_norm,
+                                           const float* k_norm, int32_t n_heads, int32_t n_kv_heads,
+                                           int32_t head_dim, const float* rope_tab, int64_t rope_rows,
+                                           int64_t pos0, int64_t seq, float eps, uint16_t* k_layer,
+                                           uint16_t* v_layer, int64_t max_seq, int32_t write_k_f32);
+
+/* ---------------------------------------------------------------- measurement / verification */
+
+/* dst <- src, `bytes` a positive multiple of 16, both 16-byte aligned: the
+ * streaming-bandwidth probe. Replaces: BwCopyKernel, tools/matmul_bench.cu:230-289. */
+RPG_OPS_API int32_t rpg_op_stream_copy(const void* src, void* dst, int64_t bytes);
+
+/* out_dev[i] = fp32 value of the binary16 bit pattern i, i in [0, 65536).
+ * Replaces: F16SweepKernel, tools/dequant_check.cu:44-48. */
+RPG_OPS_API int32_t rpg_op_f16_sweep(float* out_dev);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* RPG_OPS_H */

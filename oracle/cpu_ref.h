@@ -1,0 +1,95 @@
+/* cpu_ref.h -- CPU oracle for the hot-path operators.
+ *
+ * TEST INFRASTRUCTURE ONLY. This is a plain-C restatement of the reference's
+ * algorithms, used as the checker by tests/, by __graft_entry__.smoke() and by
+ * the cpu_baseline leg of bench.py. The product (librpg_ops.so) never links,
+ * loads or calls it.
+ *
+ * Built with gcc -O2 -ffp-contract=off (oracle/Makefile) so every fp32 op is
+ * rounded separately, as in the reference CPU build (CMakeLists.txt:120-127).
+ *
+ * Pinning (how each function is checked independently of its own formula; the
+ * tests named here live in tests/test_oracle.py):
+ *   ora_f16_to_f32       exhaustive 65536 values vs numpy float16->float32, and
+ *                        vs the reference's own F16ToF32 (oracle/_ref) when built
+ *   ora_f32_to_f16_rne   numpy astype(float16) (an independent IEEE RNE routine)
+ *                        on random values, every tie class, subnormals, overflow
+ *   ora_dequantize_row   golden vectors written by the reference quant.cc
+ *                        (tests/golden/), oracle/_ref directly when built, a
+ *                        per-element pure-Python restatement on tiny inputs,
+ *                        and closed-form special blocks
+ *   ora_embedding_lookup row-by-row equality with ora_dequantize_row
+ *   ora_rms_norm         float64 closed forms (constant rows), scale invariance,
+ *                        unit-RMS output with w = 1, numpy float64 restatement
+ *   ora_build_rope_table numpy float64 cos/sin cast to float32
+ *   ora_rope             pos 0 is the identity, pair norms preserved, complex
+ *                        multiplication form (x_i + j x_{i+64}) * e^{j*angle}
+ *   ora_kv_write         the reference's integer-coded KAT
+ *                        (tools/kv_map_check.cu:51-186) plus "untouched stays 0"
+ *   ora_silu_mul         silu(0)=0, v->-inf gives -0, v>>0 gives v*up, numpy f64
+ *   ora_vec_add          numpy float32 addition, bitwise
+ */
+#ifndef RPG_ORACLE_CPU_REF_H
+#define RPG_ORACLE_CPU_REF_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ORA_GGML_F32 0u
+#define ORA_GGML_Q4_K 12u
+#define ORA_GGML_Q6_K 14u
+
+/* ---- fp16 ---------------------------------------------------------------- */
+float ora_f16_to_f32(uint16_t h);
+uint16_t ora_f32_to_f16_rne(float f);
+void ora_f16_to_f32_array(const uint16_t* src, int64_t n, float* dst);
+void ora_f32_to_f16_rne_array(const float* src, int64_t n, uint16_t* dst);
+
+/* ---- dequant / gather ----------------------------------------------------- */
+int64_t ora_type_row_bytes(uint32_t type, int64_t n_elems); /* <0 if unsupported */
+int ora_dequantize_row(uint32_t type, const uint8_t* src, int64_t n_elems, float* dst);
+int ora_embedding_lookup(uint32_t type, const uint8_t* emb, int64_t rows, int64_t cols, const int32_t* toks,
+                         int64_t seq, float* x);
+
+/* ---- layer ops, fp32 in the reference's op order -------------------------- */
+void ora_rms_norm(const float* x, const float* w, int64_t n_rows, int64_t n, int64_t stride, float eps, float* out);
+void ora_build_rope_table(int32_t head_dim, double theta, int64_t n_pos, float* out);
+void ora_rope(float* x, int32_t n_heads, int32_t head_dim, const float* tab, int64_t pos0, int64_t n_rows);
+int ora_kv_write(const float* k, const float* v, int32_t n_kv_heads, int32_t head_dim, int64_t pos0, int64_t seq,
+                 uint16_t* k_layer, uint16_t* v_layer, int64_t max_seq);
+void ora_silu_mul(float* gate, const float* up, int64_t n);
+void ora_vec_add(float* a, const float* b, int64_t n);
+
+/* Compositions the fused operators must equal (src/qwen3_gpu.cu:77-91, :100-103). */
+void ora_add_rms_norm(float* x, const float* d, const float* w, int64_t n_rows, int64_t n, float eps, float* out);
+int ora_qk_norm_rope_kv(float* q, float* k, const float* v, const float* q_norm, const float* k_norm,
+                        int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, const float* tab, int64_t pos0,
+                        int64_t seq, float eps, uint16_t* k_layer, uint16_t* v_layer, int64_t max_seq);
+
+/* ---- float64 restatements (the tolerance gate's reference values) ---------- */
+void ora_rms_norm_f64(const float* x, const float* w, int64_t n_rows, int64_t n, int64_t stride, double eps,
+                      double* out);
+void ora_rope_f64(const float* x, int32_t n_heads, int32_t head_dim, const float* tab, int64_t pos0, int64_t n_rows,
+                  double* out);
+void ora_silu_mul_f64(const float* gate, const float* up, int64_t n, double* out);
+void ora_norm_rope_f64(const float* x, const float* w, int32_t n_heads, int32_t head_dim, const float* tab,
+                       int64_t pos0, int64_t n_rows, double eps, double* out);
+
+/* ---- CPU baseline timing (bench.py cpu_baseline leg) ----------------------- */
+/* Runs the one-layer chain (residual add + RMSNorm over [n,H], q/k norm + RoPE +
+ * fp16 KV write over [n,Hq|Hkv,128], SwiGLU over [n,I]) `reps` times on
+ * `threads` threads (rows partitioned), on synthetic inputs it allocates
+ * itself. Returns the median seconds per chain, or a negative value on error. */
+double ora_bench_layer_chain(int threads, int64_t n, int64_t hidden, int32_t n_heads, int32_t n_kv_heads,
+                             int64_t inter, int reps);
+/* Same for the embedding gather of `seq` ids from a rows x cols table of `type`. */
+double ora_bench_gather(int threads, uint32_t type, int64_t rows, int64_t cols, int64_t seq, int reps);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RPG_ORACLE_CPU_REF_H */

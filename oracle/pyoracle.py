@@ -1,0 +1,253 @@
+"""numpy/ctypes binding of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and the
+cpu_baseline leg of bench.py, always as the checker, never as the measured or
+shipped path. Also binds oracle/_ref/libref_quant.so (the reference's own
+quant.cc, built by `make -C oracle ref`) when that library exists.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "liboracle.so")
+REF_LIB_PATH = os.path.join(HERE, "_ref", "libref_quant.so")
+
+F32, Q4_K, Q6_K = 0, 12, 14
+
+_vp, _i32, _i64, _u32, _f32, _f64 = (ctypes.c_void_p, ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32,
+                                     ctypes.c_float, ctypes.c_double)
+_SIGS = {
+    "ora_f16_to_f32": (_f32, [ctypes.c_uint16]),
+    "ora_f32_to_f16_rne": (ctypes.c_uint16, [_f32]),
+    "ora_f32_to_f16_rne_array": (None, [_vp, _i64, _vp]),
+    "ora_f16_to_f32_array": (None, [_vp, _i64, _vp]),
+    "ora_type_row_bytes": (_i64, [_u32, _i64]),
+    "ora_dequantize_row": (ctypes.c_int, [_u32, _vp, _i64, _vp]),
+    "ora_embedding_lookup": (ctypes.c_int, [_u32, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "ora_rms_norm": (None, [_vp, _vp, _i64, _i64, _i64, _f32, _vp]),
+    "ora_build_rope_table": (None, [_i32, _f64, _i64, _vp]),
+    "ora_rope": (None, [_vp, _i32, _i32, _vp, _i64, _i64]),
+    "ora_kv_write": (ctypes.c_int, [_vp, _vp, _i32, _i32, _i64, _i64, _vp, _vp, _i64]),
+    "ora_silu_mul": (None, [_vp, _vp, _i64]),
+    "ora_vec_add": (None, [_vp, _vp, _i64]),
+    "ora_add_rms_norm": (None, [_vp, _vp, _vp, _i64, _i64, _f32, _vp]),
+    "ora_qk_norm_rope_kv": (ctypes.c_int, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _f32, _vp,
+                                           _vp, _i64]),
+    "ora_rms_norm_f64": (None, [_vp, _vp, _i64, _i64, _i64, _f64, _vp]),
+    "ora_rope_f64": (None, [_vp, _i32, _i32, _vp, _i64, _i64, _vp]),
+    "ora_silu_mul_f64": (None, [_vp, _vp, _i64, _vp]),
+    "ora_norm_rope_f64": (None, [_vp, _vp, _i32, _i32, _vp, _i64, _i64, _f64, _vp]),
+    "ora_bench_layer_chain": (_f64, [ctypes.c_int, _i64, _i64, _i32, _i32, _i64, ctypes.c_int]),
+    "ora_bench_gather": (_f64, [ctypes.c_int, _u32, _i64, _i64, _i64, ctypes.c_int]),
+}
+
+_lib = None
+_ref = None
+
+
+def build() -> None:
+    """Compiles liboracle.so (gcc) in place."""
+    subprocess.run(["make", "-s", "-C", HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def ref_lib():
+    """The reference's own quant.cc compiled into oracle/_ref, or None if absent."""
+    global _ref
+    if _ref is None and os.path.exists(REF_LIB_PATH):
+        R = ctypes.CDLL(REF_LIB_PATH)
+        R.ref_dequantize_row.restype = ctypes.c_int
+        R.ref_dequantize_row.argtypes = [_u32, _vp, _i64, _vp]
+        R.ref_type_row_bytes.restype = _i64
+        R.ref_type_row_bytes.argtypes = [_u32, _i64]
+        R.ref_f16_to_f32_array.restype = None
+        R.ref_f16_to_f32_array.argtypes = [_vp, _i64, _vp]
+        R.ref_f32_to_f16_dtypes.restype = ctypes.c_uint16
+        R.ref_f32_to_f16_dtypes.argtypes = [_f32]
+        _ref = R
+    return _ref
+
+
+def _p(a: np.ndarray):
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be C-contiguous"
+    return a.ctypes.data_as(ctypes.c_void_p)
+
+
+def _f(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+# ------------------------------------------------------------------------- fp16
+
+
+def f16_to_f32(bits: np.ndarray) -> np.ndarray:
+    bits = np.ascontiguousarray(bits, dtype=np.uint16).ravel()
+    out = np.empty(bits.size, dtype=np.float32)
+    lib().ora_f16_to_f32_array(_p(bits), bits.size, _p(out))
+    return out
+
+
+def ref_f16_to_f32(bits: np.ndarray):
+    R = ref_lib()
+    if R is None:
+        return None
+    bits = np.ascontiguousarray(bits, dtype=np.uint16).ravel()
+    out = np.empty(bits.size, dtype=np.float32)
+    R.ref_f16_to_f32_array(_p(bits), bits.size, _p(out))
+    return out
+
+
+def f32_to_f16_rne(x: np.ndarray) -> np.ndarray:
+    x = _f(x)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().ora_f32_to_f16_rne_array(_p(x), x.size, _p(out))
+    return out
+
+
+# ------------------------------------------------------------------------- dequant
+
+
+def row_bytes(ggml_type: int, n: int) -> int:
+    return int(lib().ora_type_row_bytes(ggml_type, n))
+
+
+def dequantize_row(ggml_type: int, raw: np.ndarray, n: int) -> np.ndarray:
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    assert raw.size >= row_bytes(ggml_type, n)
+    out = np.empty(n, dtype=np.float32)
+    assert lib().ora_dequantize_row(ggml_type, _p(raw), n, _p(out)) == 0
+    return out
+
+
+def embedding_lookup(ggml_type: int, table: np.ndarray, rows: int, cols: int, toks: np.ndarray) -> np.ndarray:
+    table = np.ascontiguousarray(table, dtype=np.uint8)
+    toks = np.ascontiguousarray(toks, dtype=np.int32)
+    out = np.empty((toks.size, cols), dtype=np.float32)
+    assert lib().ora_embedding_lookup(ggml_type, _p(table), rows, cols, _p(toks), toks.size, _p(out)) == 0
+    return out
+
+
+def ref_dequantize_row(ggml_type: int, raw: np.ndarray, n: int):
+    R = ref_lib()
+    if R is None:
+        return None
+    raw = np.ascontiguousarray(raw, dtype=np.uint8)
+    out = np.empty(n, dtype=np.float32)
+    assert R.ref_dequantize_row(ggml_type, _p(raw), n, _p(out)) == 0
+    return out
+
+
+# ------------------------------------------------------------------------- layer ops (fp32)
+
+
+def rms_norm(x: np.ndarray, w: np.ndarray, n_rows: int, n: int, stride: int, eps: float) -> np.ndarray:
+    x = _f(x)
+    out = x.copy()
+    lib().ora_rms_norm(_p(x), _p(_f(w)), n_rows, n, stride, eps, _p(out))
+    return out
+
+
+def build_rope_table(head_dim: int, theta: float, n_pos: int) -> np.ndarray:
+    out = np.empty((n_pos, head_dim), dtype=np.float32)
+    lib().ora_build_rope_table(head_dim, theta, n_pos, _p(out))
+    return out
+
+
+def rope(x: np.ndarray, n_heads: int, head_dim: int, tab: np.ndarray, pos0: int, n_rows: int) -> np.ndarray:
+    out = _f(x).copy()
+    lib().ora_rope(_p(out), n_heads, head_dim, _p(_f(tab)), pos0, n_rows)
+    return out
+
+
+def kv_write(k, v, n_kv_heads, head_dim, pos0, seq, k_layer: np.ndarray, v_layer: np.ndarray, max_seq) -> int:
+    assert k_layer.dtype == np.uint16 and v_layer.dtype == np.uint16
+    return lib().ora_kv_write(_p(_f(k)), _p(_f(v)), n_kv_heads, head_dim, pos0, seq, _p(k_layer), _p(v_layer),
+                              max_seq)
+
+
+def silu_mul(gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+    out = _f(gate).copy()
+    lib().ora_silu_mul(_p(out), _p(_f(up)), out.size)
+    return out
+
+
+def vec_add(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    out = _f(a).copy()
+    lib().ora_vec_add(_p(out), _p(_f(b)), out.size)
+    return out
+
+
+def add_rms_norm(x, d, w, n_rows, n, eps):
+    """Returns (x + d, RMSNorm(x + d) * w)."""
+    xs = _f(x).copy()
+    out = np.empty_like(xs)
+    lib().ora_add_rms_norm(_p(xs), _p(_f(d)), _p(_f(w)), n_rows, n, eps, _p(out))
+    return xs, out
+
+
+def qk_norm_rope_kv(q, k, v, q_norm, k_norm, n_heads, n_kv_heads, head_dim, tab, pos0, seq, eps,
+                    k_layer: np.ndarray, v_layer: np.ndarray, max_seq):
+    """Returns (q', k') after the composition; writes the caches in place."""
+    qo = _f(q).copy()
+    ko = _f(k).copy()
+    rc = lib().ora_qk_norm_rope_kv(_p(qo), _p(ko), _p(_f(v)), _p(_f(q_norm)), _p(_f(k_norm)), n_heads, n_kv_heads,
+                                   head_dim, _p(_f(tab)), pos0, seq, eps, _p(k_layer), _p(v_layer), max_seq)
+    assert rc == 0
+    return qo, ko
+
+
+# ------------------------------------------------------------------------- float64 restatements
+
+
+def rms_norm_f64(x, w, n_rows, n, stride, eps) -> np.ndarray:
+    out = np.empty((n_rows, n), dtype=np.float64)
+    lib().ora_rms_norm_f64(_p(_f(x)), _p(_f(w)), n_rows, n, stride, eps, _p(out))
+    return out
+
+
+def rope_f64(x, n_heads, head_dim, tab, pos0, n_rows) -> np.ndarray:
+    out = np.empty(n_rows * n_heads * head_dim, dtype=np.float64)
+    lib().ora_rope_f64(_p(_f(x)), n_heads, head_dim, _p(_f(tab)), pos0, n_rows, _p(out))
+    return out
+
+
+def silu_mul_f64(gate, up) -> np.ndarray:
+    g = _f(gate)
+    out = np.empty(g.size, dtype=np.float64)
+    lib().ora_silu_mul_f64(_p(g), _p(_f(up)), g.size, _p(out))
+    return out
+
+
+def norm_rope_f64(x, w, n_heads, head_dim, tab, pos0, n_rows, eps) -> np.ndarray:
+    out = np.empty(n_rows * n_heads * head_dim, dtype=np.float64)
+    lib().ora_norm_rope_f64(_p(_f(x)), _p(_f(w)), n_heads, head_dim, _p(_f(tab)), pos0, n_rows, eps, _p(out))
+    return out
+
+
+# ------------------------------------------------------------------------- CPU baseline timing
+
+
+def bench_layer_chain(threads, n, hidden, n_heads, n_kv_heads, inter, reps) -> float:
+    return float(lib().ora_bench_layer_chain(threads, n, hidden, n_heads, n_kv_heads, inter, reps))
+
+
+def bench_gather(threads, ggml_type, rows, cols, seq, reps) -> float:
+    return float(lib().ora_bench_gather(threads, ggml_type, rows, cols, seq, reps))

@@ -1,0 +1,102 @@
+// Device helpers shared by the hot-path kernels (included only by .hip files).
+//
+// Everything here is written for CDNA4 wave64: reductions run over the 64 lanes
+// of a wavefront (or over an aligned 16-lane group of it) with cross-lane
+// shuffles, never through LDS, and all activation traffic moves as 128-bit
+// float4 loads/stores.
+#ifndef RPG_AMD_DEV_UTIL_H_
+#define RPG_AMD_DEV_UTIL_H_
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace rpg {
+namespace dev {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- reductions
+
+// Sum over all 64 lanes of the wave; every lane receives the total.
+__device__ __forceinline__ double WaveSum(double v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// Sum over the aligned group of W lanes (W a power of two <= 64) that contains
+// the calling lane; every lane of the group receives the group total.
+template <int W>
+__device__ __forceinline__ double GroupSum(double v) {
+#pragma unroll
+  for (int off = W / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, W);
+  return v;
+}
+
+// Sum of squares of a float4, accumulated into a double. Each product of two
+// fp32 values is exact in double, so the fma only rounds the running sum.
+__device__ __forceinline__ double AddSquares(double acc, float4 v) {
+  acc = fma(static_cast<double>(v.x), static_cast<double>(v.x), acc);
+  acc = fma(static_cast<double>(v.y), static_cast<double>(v.y), acc);
+  acc = fma(static_cast<double>(v.z), static_cast<double>(v.z), acc);
+  acc = fma(static_cast<double>(v.w), static_cast<double>(v.w), acc);
+  return acc;
+}
+
+// RMSNorm scale from the double sum of squares: float(1 / sqrt(ss/n + eps)),
+// every step in double as in the reference (src/kernels_gpu.cu:584-585).
+__device__ __forceinline__ float RmsScale(double ss, int64_t n, float eps) {
+  const double mean = ss / static_cast<double>(n);
+  return static_cast<float>(1.0 / sqrt(mean + static_cast<double>(eps)));
+}
+
+// (v * scale) * w per component, left to right as the reference writes
+// `xr[i] * scale * w[i]` (src/kernels_gpu.cu:589).
+__device__ __forceinline__ float4 ScaleMul(float4 v, float scale, float4 w) {
+  return make_float4((v.x * scale) * w.x, (v.y * scale) * w.y, (v.z * scale) * w.z, (v.w * scale) * w.w);
+}
+
+// ---------------------------------------------------------------- fp16
+
+// Exact binary16 -> binary32 from the bit pattern, independent of the f16
+// denormal mode: Inf/NaN keep their payload shifted into the fp32 mantissa,
+// normals are re-biased (+112 in the exponent), and subnormals/zero are
+// mag * 2^-24, which is exact in fp32.
+__device__ __forceinline__ float HalfBitsToFloat(uint32_t h) {
+  const uint32_t sign = (h & 0x8000u) << 16;
+  const uint32_t mag = h & 0x7FFFu;
+  uint32_t bits;
+  if (mag >= 0x7C00u) {
+    bits = 0x7F800000u | ((mag & 0x3FFu) << 13);
+  } else if (mag >= 0x0400u) {
+    bits = (mag << 13) + 0x38000000u;
+  } else {
+    bits = __float_as_uint(static_cast<float>(mag) * 0x1p-24f);
+  }
+  return __uint_as_float(sign | bits);
+}
+
+// fp32 -> binary16 bits with IEEE round-to-nearest-even (the hardware convert
+// under the default round mode; f16 denormals are preserved by the default
+// kernel mode, and |x| >= 65520 becomes Inf).
+__device__ __forceinline__ uint32_t FloatToHalfBits(float f) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, static_cast<_Float16>(f)));
+}
+
+__device__ __forceinline__ uint2 PackHalf4(float4 v) {
+  uint2 r;
+  r.x = FloatToHalfBits(v.x) | (FloatToHalfBits(v.y) << 16);
+  r.y = FloatToHalfBits(v.z) | (FloatToHalfBits(v.w) << 16);
+  return r;
+}
+
+// ---------------------------------------------------------------- memory
+
+__device__ __forceinline__ float4 Load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+__device__ __forceinline__ void Store4(float* p, float4 v) { *reinterpret_cast<float4*>(p) = v; }
+
+}  // namespace dev
+}  // namespace rpg
+
+#endif  // RPG_AMD_DEV_UTIL_H_

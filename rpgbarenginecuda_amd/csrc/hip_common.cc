@@ -1,0 +1,212 @@
+// Host-side implementation of the device runtime glue (see hip_common.h).
+#include "hip_common.h"
+
+#include <hip/hip_runtime_api.h>
+
+#include <climits>
+#include <cstdio>
+#include <string>
+
+namespace rpg {
+
+void ThrowHipError(hipError_t err, const char* expr, const char* file, int line) {
+  Throw("HIP call failed: %s (%d)\n  expression: %s\n  at: %s:%d", hipGetErrorString(err),
+        static_cast<int>(err), expr, file, line);
+}
+
+void CheckLaunch(const char* what) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) Throw("kernel launch failed (%s): %s", what, hipGetErrorString(e));
+}
+
+unsigned GridFor(int64_t n, int threads) {
+  const int64_t g = (n + threads - 1) / threads;
+  RPG_CHECK(g > 0 && g <= 0x7FFFFFFF, "grid dimension out of range: %lld", static_cast<long long>(g));
+  return static_cast<unsigned>(g);
+}
+
+// ---------------------------------------------------------------- device query
+
+DeviceInfo QueryDevice(int index) {
+  DeviceInfo d;
+  int count = 0;
+  const hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess) {
+    d.reason = std::string("hipGetDeviceCount failed: ") + hipGetErrorString(e);
+    return d;
+  }
+  if (count <= 0) {
+    d.reason = "no HIP device found";
+    return d;
+  }
+  if (index < 0 || index >= count) {
+    d.reason = "device index out of range (there are " + std::to_string(count) + " devices)";
+    return d;
+  }
+  hipDeviceProp_t p{};
+  const hipError_t pe = hipGetDeviceProperties(&p, index);
+  if (pe != hipSuccess) {
+    d.reason = std::string("hipGetDeviceProperties failed: ") + hipGetErrorString(pe);
+    return d;
+  }
+  d.available = true;
+  d.name = p.name;
+  d.arch = p.gcnArchName;
+  d.cu_count = p.multiProcessorCount;
+  d.clock_khz = p.clockRate;
+  d.total_mem = p.totalGlobalMem;
+  size_t free_b = 0, total_b = 0;
+  if (hipMemGetInfo(&free_b, &total_b) == hipSuccess) {
+    d.free_mem = free_b;
+    if (total_b > 0) d.total_mem = total_b;
+  }
+  int rt = 0;
+  if (hipRuntimeGetVersion(&rt) == hipSuccess) d.runtime_version = rt;
+  return d;
+}
+
+std::string DescribeDevice(const DeviceInfo& d) {
+  if (!d.available) return "no device: " + d.reason;
+  char buf[384];
+  std::snprintf(buf, sizeof(buf), "%s [%s], %d CUs @ %d MHz, %.1f GiB (%.1f GiB free), HIP runtime %d",
+                d.name.c_str(), d.arch.c_str(), d.cu_count, d.clock_khz / 1000,
+                static_cast<double>(d.total_mem) / 1073741824.0,
+                static_cast<double>(d.free_mem) / 1073741824.0, d.runtime_version);
+  return std::string(buf);
+}
+
+// ---------------------------------------------------------------- DeviceBuffer
+
+DeviceBuffer::DeviceBuffer(DeviceBuffer&& o) noexcept : ptr_(o.ptr_), bytes_(o.bytes_) {
+  o.ptr_ = nullptr;
+  o.bytes_ = 0;
+}
+
+DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& o) noexcept {
+  if (this != &o) {
+    Free();
+    ptr_ = o.ptr_;
+    bytes_ = o.bytes_;
+    o.ptr_ = nullptr;
+    o.bytes_ = 0;
+  }
+  return *this;
+}
+
+void DeviceBuffer::Alloc(size_t bytes) {
+  RPG_CHECK(bytes > 0, "DeviceBuffer::Alloc got 0 bytes");
+  Free();
+  RPG_HIP_CHECK(hipMalloc(&ptr_, bytes));
+  bytes_ = bytes;
+}
+
+void DeviceBuffer::Free() {
+  if (ptr_ == nullptr) return;
+  // Destructors must not throw; a failing free only happens once the runtime
+  // is already tearing down.
+  const hipError_t e = hipFree(ptr_);
+  if (e != hipSuccess) RPG_LOG_WARN("hipFree failed: %s", hipGetErrorString(e));
+  ptr_ = nullptr;
+  bytes_ = 0;
+}
+
+void DeviceBuffer::Upload(const void* src, size_t bytes) {
+  RPG_CHECK(ptr_ != nullptr, "DeviceBuffer::Upload on an unallocated buffer");
+  RPG_CHECK(bytes <= bytes_, "DeviceBuffer::Upload overflow: %llu bytes into %llu",
+            static_cast<unsigned long long>(bytes), static_cast<unsigned long long>(bytes_));
+  RPG_HIP_CHECK(hipMemcpy(ptr_, src, bytes, hipMemcpyHostToDevice));
+}
+
+void DeviceBuffer::Download(void* dst, size_t bytes) const {
+  RPG_CHECK(ptr_ != nullptr, "DeviceBuffer::Download on an unallocated buffer");
+  RPG_CHECK(bytes <= bytes_, "DeviceBuffer::Download overflow: %llu bytes from %llu",
+            static_cast<unsigned long long>(bytes), static_cast<unsigned long long>(bytes_));
+  RPG_HIP_CHECK(hipMemcpy(dst, ptr_, bytes, hipMemcpyDeviceToHost));
+}
+
+// ---------------------------------------------------------------- engine stream
+//
+// Process-lifetime objects, intentionally never released: their release would
+// run from static destructors after the runtime may already be gone.
+namespace {
+
+int64_t* g_pos_staging = nullptr;
+hipStream_t g_engine_stream = nullptr;
+hipStream_t g_capture_stream = nullptr;
+bool g_capture_tried = false;
+// Value currently held by g_pos_staging, maintained only by StagePos0.
+int64_t g_pos_last = INT64_MIN;
+
+}  // namespace
+
+hipStream_t EngineStream() { return g_engine_stream; }
+
+void SetEngineStream(hipStream_t s) { g_engine_stream = s; }
+
+bool EnsureCaptureStream() {
+  if (g_capture_tried) return g_capture_stream != nullptr;
+  g_capture_tried = true;
+  // Blocking stream at the default priority: it stays ordered with the
+  // synchronous copies that go through the null stream.
+  if (hipStreamCreate(&g_capture_stream) != hipSuccess) {
+    g_capture_stream = nullptr;
+    return false;
+  }
+  return true;
+}
+
+hipStream_t CaptureStream() { return EnsureCaptureStream() ? g_capture_stream : nullptr; }
+
+ScopedEngineStream::ScopedEngineStream(hipStream_t s) : prev_(g_engine_stream) { g_engine_stream = s; }
+
+ScopedEngineStream::~ScopedEngineStream() { g_engine_stream = prev_; }
+
+// ---------------------------------------------------------------- pos0 staging
+
+int64_t* PosStagingPtr() {
+  if (g_pos_staging == nullptr) {
+    int64_t* p = nullptr;
+    RPG_HIP_CHECK(hipMalloc(&p, sizeof(int64_t)));
+    g_pos_staging = p;
+  }
+  return g_pos_staging;
+}
+
+bool StreamIsCapturing() {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  const hipError_t e = hipStreamIsCapturing(EngineStream(), &st);
+  if (e != hipSuccess) {
+    (void)hipGetLastError();  // the query failing means "not capturing"; do not leak the error
+    return false;
+  }
+  return st != hipStreamCaptureStatusNone;
+}
+
+void StagePos0(int64_t pos) {
+  int64_t* dev = PosStagingPtr();
+  if (StreamIsCapturing()) return;
+  // Pageable source: the runtime copies it out before this call returns, so the
+  // stack slot may die right after.
+  RPG_HIP_CHECK(hipMemcpyAsync(dev, &pos, sizeof(int64_t), hipMemcpyHostToDevice, EngineStream()));
+  g_pos_last = pos;
+}
+
+int64_t* StagePos0Cached(int64_t pos) {
+  int64_t* dev = PosStagingPtr();
+  if (StreamIsCapturing()) return dev;
+  if (g_pos_last != pos) StagePos0(pos);
+  return dev;
+}
+
+Pos0Arg Pos0ForLaunch(int64_t pos0) {
+  if (StreamIsCapturing()) {
+    // The staging scalar must already exist: allocating inside a capture is illegal.
+    RPG_CHECK(g_pos_staging != nullptr,
+              "pos0 staging scalar not allocated before graph capture; call PosStagingPtr() "
+              "(rpg_ops_init) before beginning the capture");
+    return Pos0Arg{pos0, g_pos_staging};
+  }
+  return Pos0Arg{pos0, nullptr};
+}
+
+}  // namespace rpg

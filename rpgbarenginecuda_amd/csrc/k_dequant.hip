@@ -1,0 +1,308 @@
+// Q4_K / Q6_K row dequantisation and the token_embd row-dequant gather.
+//
+// Values are bit-identical to the reference CPU dequant (src/quant.cc:252-279
+// DeqQ4_K, :321-354 DeqQ6_K, :159-167 GetScaleMinK4; f16 from src/dtypes.h:21-47):
+//   Q4_K: y = (d*sc)*q - (dmin*m)     (three separately rounded fp32 ops)
+//   Q6_K: y = (d*sc)*q                (two separately rounded fp32 ops)
+// The library is compiled with -ffp-contract=off, so no multiply-subtract is
+// fused; signed zeros follow from the same op order (e.g. sc < 0, q = 0 -> -0).
+//
+// MI355X mapping: the unit of work is one 256-element super-block.
+//   Q4_K: 32 lanes per block. Lane j (g = j/8, kq = j%8) loads the 16-byte block
+//     header (d, dmin, 12 scale bytes; one 128-bit load, broadcast in cache) and
+//     one 32-bit word of qs (the 32 lanes cover all 128 qs bytes coalesced); the
+//     low nibbles give elements 64g+4kq..+3, the high nibbles 64g+32+4kq..+3.
+//     The two (scale, min) pairs are unpacked once per lane, in registers.
+//   Q6_K: 16 lanes per block. Lane j (half = j/8, kq = j%8) loads 4 bytes of each
+//     of ql[half*64 + 4kq], ql[half*64 + 32 + 4kq], qh[half*32 + 4kq], the 8 scales
+//     of its half and d, and produces 16 elements: four float4 at
+//     half*128 + 32*quarter + 4kq. Q6_K blocks are 210 bytes, so a block start is
+//     only 2-byte aligned; loads are 16-bit.
+// Every lane ends with float4 stores, so a wave writes 2 KiB (Q4_K) or 4 KiB (Q6_K)
+// of fp32 as full 128-byte lines.
+#include <hip/hip_runtime.h>
+
+#include "dev_util.h"
+#include "kernels_gpu.h"
+
+namespace rpg {
+namespace {
+
+using dev::HalfBitsToFloat;
+using dev::Store4;
+
+constexpr int kBlock = 256;
+
+bool Aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+__device__ __forceinline__ uint32_t ByteOf(uint32_t word, int i) { return (word >> (8 * i)) & 0xFFu; }
+
+// Byte i (0..11) of the Q4_K packed scales held in three little-endian words.
+__device__ __forceinline__ uint32_t ScaleByte(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
+  const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
+  return ByteOf(w, i & 3);
+}
+
+// 6-bit (scale, min) of sub-block j (0..7) from the 12 packed bytes.
+__device__ __forceinline__ void ScaleMinK4(int j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t* sc, uint32_t* m) {
+  if (j < 4) {
+    *sc = ScaleByte(s0, s1, s2, j) & 63u;
+    *m = ScaleByte(s0, s1, s2, j + 4) & 63u;
+  } else {
+    *sc = (ScaleByte(s0, s1, s2, j + 4) & 0x0Fu) | ((ScaleByte(s0, s1, s2, j - 4) >> 6) << 4);
+    *m = (ScaleByte(s0, s1, s2, j + 4) >> 4) | ((ScaleByte(s0, s1, s2, j) >> 6) << 4);
+  }
+}
+
+// One lane's share (8 elements) of a Q4_K block; blk must be 16-byte aligned.
+__device__ __forceinline__ void DecodeQ4KLane(const uint8_t* blk, int j, float* out_blk) {
+  const int g = j >> 3;
+  const int kq = j & 7;
+  const uint4 hdr = *reinterpret_cast<const uint4*>(blk);
+  const uint32_t qw = *reinterpret_cast<const uint32_t*>(blk + 16 + 32 * g + 4 * kq);
+  const float d = HalfBitsToFloat(hdr.x & 0xFFFFu);
+  const float dmin = HalfBitsToFloat(hdr.x >> 16);
+  uint32_t sc0, m0, sc1, m1;
+  ScaleMinK4(2 * g, hdr.y, hdr.z, hdr.w, &sc0, &m0);
+  ScaleMinK4(2 * g + 1, hdr.y, hdr.z, hdr.w, &sc1, &m1);
+  const float d1 = d * static_cast<float>(sc0);
+  const float n1 = dmin * static_cast<float>(m0);
+  const float d2 = d * static_cast<float>(sc1);
+  const float n2 = dmin * static_cast<float>(m1);
+  float lo[4], hi[4];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    lo[b] = d1 * static_cast<float>((qw >> (8 * b)) & 0xFu) - n1;
+    hi[b] = d2 * static_cast<float>((qw >> (8 * b + 4)) & 0xFu) - n2;
+  }
+  Store4(out_blk + 64 * g + 4 * kq, make_float4(lo[0], lo[1], lo[2], lo[3]));
+  Store4(out_blk + 64 * g + 32 + 4 * kq, make_float4(hi[0], hi[1], hi[2], hi[3]));
+}
+
+__device__ __forceinline__ uint32_t Load4Bytes2Aligned(const uint8_t* p) {
+  const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+  return static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16);
+}
+
+// One lane's share (16 elements) of a Q6_K block; blk must be 2-byte aligned.
+__device__ __forceinline__ void DecodeQ6KLane(const uint8_t* blk, int j, float* out_blk) {
+  const int half = j >> 3;
+  const int kq = j & 7;
+  const uint32_t ql0 = Load4Bytes2Aligned(blk + 64 * half + 4 * kq);
+  const uint32_t ql1 = Load4Bytes2Aligned(blk + 64 * half + 32 + 4 * kq);
+  const uint32_t qh = Load4Bytes2Aligned(blk + 128 + 32 * half + 4 * kq);
+  const uint32_t sc_lo = Load4Bytes2Aligned(blk + 192 + 8 * half);      // scales 0..3 of this half
+  const uint32_t sc_hi = Load4Bytes2Aligned(blk + 192 + 8 * half + 4);  // scales 4..7 of this half
+  const float d = HalfBitsToFloat(*reinterpret_cast<const uint16_t*>(blk + 208));
+  const int is = kq >> 2;  // (l >> 4) for l = 4kq..4kq+3
+#pragma unroll
+  for (int quarter = 0; quarter < 4; ++quarter) {
+    const int si = is + 2 * quarter;  // 0..7 within the half
+    const int8_t sc = static_cast<int8_t>(ByteOf(si < 4 ? sc_lo : sc_hi, si & 3));
+    const float ds = d * static_cast<float>(sc);
+    const uint32_t qlw = (quarter & 1) ? ql1 : ql0;
+    const int nib_shift = quarter < 2 ? 0 : 4;
+    float y[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t nib = (qlw >> (8 * b + nib_shift)) & 0xFu;
+      const uint32_t hi2 = (ByteOf(qh, b) >> (2 * quarter)) & 3u;
+      const int q = static_cast<int>(nib | (hi2 << 4)) - 32;
+      y[b] = ds * static_cast<float>(q);
+    }
+    Store4(out_blk + 128 * half + 32 * quarter + 4 * kq, make_float4(y[0], y[1], y[2], y[3]));
+  }
+}
+
+template <uint32_t kType>
+struct QuantTraits;
+template <>
+struct QuantTraits<kGgmlQ4_K> {
+  static constexpr int kLanes = 32;
+  static constexpr int64_t kBytes = kQ4KBlockBytes;
+  __device__ static void Decode(const uint8_t* blk, int j, float* out) { DecodeQ4KLane(blk, j, out); }
+};
+template <>
+struct QuantTraits<kGgmlQ6_K> {
+  static constexpr int kLanes = 16;
+  static constexpr int64_t kBytes = kQ6KBlockBytes;
+  __device__ static void Decode(const uint8_t* blk, int j, float* out) { DecodeQ6KLane(blk, j, out); }
+};
+
+// Gather: unit = (token t, block b). toks == nullptr means "dequantise row 0 of
+// the table", which is how GpuDequantRow reuses the kernel.
+template <uint32_t kType>
+__global__ __launch_bounds__(kBlock) void GatherBlocksKernel(const uint8_t* __restrict__ emb, int64_t rows,
+                                                             int64_t row_bytes, int32_t nb,
+                                                             const int32_t* __restrict__ toks, int64_t n_units,
+                                                             float* __restrict__ x) {
+  using T = QuantTraits<kType>;
+  constexpr int kUnits = kBlock / T::kLanes;
+  const int64_t unit = static_cast<int64_t>(blockIdx.x) * kUnits + threadIdx.x / T::kLanes;
+  const int j = threadIdx.x % T::kLanes;
+  if (unit >= n_units) return;
+  const int64_t t = unit / nb;
+  const int32_t b = static_cast<int32_t>(unit - t * nb);
+  float* out = x + (t * nb + b) * kQK_K;
+  const int64_t tok = toks != nullptr ? static_cast<int64_t>(toks[t]) : 0;
+  if (tok < 0 || tok >= rows) {
+    constexpr int kPerLane = static_cast<int>(kQK_K) / T::kLanes;
+#pragma unroll
+    for (int e = 0; e < kPerLane; e += 4) Store4(out + j * kPerLane + e, make_float4(0.f, 0.f, 0.f, 0.f));
+    return;
+  }
+  T::Decode(emb + tok * row_bytes + b * T::kBytes, j, out);
+}
+
+// F32 tables: rows are plain floats; one float4 per thread.
+__global__ __launch_bounds__(kBlock) void GatherF32Kernel(const float* __restrict__ emb, int64_t rows, int64_t cols,
+                                                          const int32_t* __restrict__ toks, int64_t total4,
+                                                          float* __restrict__ x) {
+  const int64_t i4 = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (i4 >= total4) return;
+  const int64_t i = 4 * i4;
+  const int64_t t = i / cols;
+  const int64_t e = i - t * cols;
+  const int64_t tok = toks != nullptr ? static_cast<int64_t>(toks[t]) : 0;
+  float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (tok >= 0 && tok < rows) v = dev::Load4(emb + tok * cols + e);
+  Store4(x + i, v);
+}
+
+// Per-element fallback for any alignment: element i of the gathered output.
+__device__ float DeqElemAny(uint32_t type, const uint8_t* blk, int e) {
+  if (type == kGgmlF32) {
+    const uint32_t u = static_cast<uint32_t>(blk[4 * e]) | (static_cast<uint32_t>(blk[4 * e + 1]) << 8) |
+                       (static_cast<uint32_t>(blk[4 * e + 2]) << 16) | (static_cast<uint32_t>(blk[4 * e + 3]) << 24);
+    return __uint_as_float(u);
+  }
+  if (type == kGgmlQ4_K) {
+    const int sub = e >> 5;
+    const int l = e & 31;
+    const int g = sub >> 1;
+    const uint8_t qb = blk[16 + 32 * g + l];
+    const uint32_t raw = (sub & 1) ? (qb >> 4) : (qb & 0x0Fu);
+    const uint8_t* s = blk + 4;
+    uint32_t sc, m;
+    if (sub < 4) {
+      sc = s[sub] & 63u;
+      m = s[sub + 4] & 63u;
+    } else {
+      sc = (s[sub + 4] & 0x0Fu) | ((s[sub - 4] >> 6) << 4);
+      m = (s[sub + 4] >> 4) | ((s[sub] >> 6) << 4);
+    }
+    const float d = HalfBitsToFloat(static_cast<uint32_t>(blk[0]) | (static_cast<uint32_t>(blk[1]) << 8));
+    const float dmin = HalfBitsToFloat(static_cast<uint32_t>(blk[2]) | (static_cast<uint32_t>(blk[3]) << 8));
+    const float d1 = d * static_cast<float>(sc);
+    const float m1 = dmin * static_cast<float>(m);
+    return d1 * static_cast<float>(raw) - m1;
+  }
+  // Q6_K
+  const int half = e >> 7;
+  const int r = e & 127;
+  const int quarter = r >> 5;
+  const int l = r & 31;
+  const uint8_t qlb = blk[64 * half + l + ((quarter & 1) ? 32 : 0)];
+  const uint32_t nib = quarter < 2 ? (qlb & 0x0Fu) : (qlb >> 4);
+  const uint32_t hi2 = (blk[128 + 32 * half + l] >> (2 * quarter)) & 3u;
+  const int q = static_cast<int>(nib | (hi2 << 4)) - 32;
+  const int8_t sc = static_cast<int8_t>(blk[192 + 8 * half + (l >> 4) + 2 * quarter]);
+  const float d = HalfBitsToFloat(static_cast<uint32_t>(blk[208]) | (static_cast<uint32_t>(blk[209]) << 8));
+  return (d * static_cast<float>(sc)) * static_cast<float>(q);
+}
+
+__global__ __launch_bounds__(kBlock) void GatherElemKernel(uint32_t type, const uint8_t* __restrict__ emb,
+                                                           int64_t rows, int64_t cols, int64_t row_bytes,
+                                                           int32_t block_elems, int32_t block_bytes,
+                                                           const int32_t* __restrict__ toks, int64_t total,
+                                                           float* __restrict__ x) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= total) return;
+  const int64_t t = i / cols;
+  const int64_t e = i - t * cols;
+  const int64_t tok = toks != nullptr ? static_cast<int64_t>(toks[t]) : 0;
+  if (tok < 0 || tok >= rows) {
+    x[i] = 0.0f;
+    return;
+  }
+  const int64_t bi = e / block_elems;
+  x[i] = DeqElemAny(type, emb + tok * row_bytes + bi * block_bytes, static_cast<int>(e - bi * block_elems));
+}
+
+__global__ __launch_bounds__(kBlock) void F16SweepKernel(float* out) {
+  const int i = blockIdx.x * kBlock + threadIdx.x;
+  if (i < 65536) out[i] = HalfBitsToFloat(static_cast<uint32_t>(i));
+}
+
+// Shared launcher for the gather and the single-row dequant (toks == nullptr,
+// rows == 1, seq == 1, cols == n_elems).
+void LaunchGather(uint32_t type, const uint8_t* emb, int64_t rows, int64_t cols, const int32_t* toks, int64_t seq,
+                  float* x) {
+  const BlockShape bs = DeviceBlockShape(type);
+  RPG_CHECK(cols > 0 && cols % bs.elems == 0, "row width %lld is not a multiple of the %s block size %d",
+            static_cast<long long>(cols), TypeName(type), bs.elems);
+  const int64_t row_bytes = TypeRowBytes(type, cols);
+  if (seq <= 0) return;
+  const int64_t total = seq * cols;
+  if (type == kGgmlQ4_K && Aligned(emb, 16) && Aligned(x, 16)) {
+    const int32_t nb = static_cast<int32_t>(cols / kQK_K);
+    const int64_t units = seq * nb;
+    GatherBlocksKernel<kGgmlQ4_K><<<GridFor(units, kBlock / 32), kBlock, 0, EngineStream()>>>(
+        emb, rows, row_bytes, nb, toks, units, x);
+    CheckLaunch("GatherBlocksKernel<Q4_K>");
+    return;
+  }
+  if (type == kGgmlQ6_K && Aligned(emb, 2) && Aligned(x, 16)) {
+    const int32_t nb = static_cast<int32_t>(cols / kQK_K);
+    const int64_t units = seq * nb;
+    GatherBlocksKernel<kGgmlQ6_K><<<GridFor(units, kBlock / 16), kBlock, 0, EngineStream()>>>(
+        emb, rows, row_bytes, nb, toks, units, x);
+    CheckLaunch("GatherBlocksKernel<Q6_K>");
+    return;
+  }
+  if (type == kGgmlF32 && cols % 4 == 0 && Aligned(emb, 16) && Aligned(x, 16)) {
+    const int64_t total4 = total / 4;
+    GatherF32Kernel<<<GridFor(total4, kBlock), kBlock, 0, EngineStream()>>>(
+        reinterpret_cast<const float*>(emb), rows, cols, toks, total4, x);
+    CheckLaunch("GatherF32Kernel");
+    return;
+  }
+  GatherElemKernel<<<GridFor(total, kBlock), kBlock, 0, EngineStream()>>>(type, emb, rows, cols, row_bytes, bs.elems,
+                                                                          bs.bytes, toks, total, x);
+  CheckLaunch("GatherElemKernel");
+}
+
+}  // namespace
+
+void GpuDequantRow(uint32_t type, const uint8_t* src_dev, int64_t n_elems, float* dst_dev) {
+  const BlockShape bs = DeviceBlockShape(type);
+  RPG_CHECK(n_elems > 0 && n_elems % bs.elems == 0, "dequant length %lld is not a multiple of the block size %d",
+            static_cast<long long>(n_elems), bs.elems);
+  RPG_CHECK(src_dev != nullptr && dst_dev != nullptr, "DequantRow got a null pointer");
+  LaunchGather(type, src_dev, 1, n_elems, nullptr, 1, dst_dev);
+}
+
+void GpuEmbeddingLookupRaw(uint32_t type, const uint8_t* emb_dev, int64_t rows, int64_t cols, const int32_t* toks_dev,
+                           int64_t seq, float* x_dev) {
+  RPG_CHECK(rows > 0 && cols > 0 && seq >= 0, "invalid EmbeddingLookup arguments");
+  if (seq == 0) return;
+  RPG_CHECK(emb_dev != nullptr && toks_dev != nullptr && x_dev != nullptr, "EmbeddingLookup got a null pointer");
+  LaunchGather(type, emb_dev, rows, cols, toks_dev, seq, x_dev);
+}
+
+void GpuEmbeddingLookup(const GpuTensor& emb, const int32_t* toks_dev, int64_t seq, float* x_dev) {
+  RPG_CHECK(emb.valid(), "EmbeddingLookup got an empty tensor");
+  RPG_CHECK(emb.buf.size() >= static_cast<size_t>(emb.rows * emb.row_bytes()),
+            "embedding buffer is smaller than its [%lld, %lld] shape", static_cast<long long>(emb.rows),
+            static_cast<long long>(emb.cols));
+  GpuEmbeddingLookupRaw(emb.type, static_cast<const uint8_t*>(emb.buf.data()), emb.rows, emb.cols, toks_dev, seq,
+                        x_dev);
+}
+
+void GpuF16Sweep(float* out_dev) {
+  RPG_CHECK(out_dev != nullptr, "F16Sweep got a null pointer");
+  F16SweepKernel<<<65536 / kBlock, kBlock, 0, EngineStream()>>>(out_dev);
+  CheckLaunch("F16SweepKernel");
+}
+
+}  // namespace rpg

@@ -1,0 +1,284 @@
+// NeoX RoPE, the fp32 -> fp16 KV-cache write, and their fusion with the
+// per-head q/k RMSNorm.
+//
+// Reference semantics:
+//   RoPE (src/kernels_gpu.cu:598-621): x is [rows][heads][head_dim]; the pair is
+//     (i, i + head_dim/2); with c = tab[(pos0+row)*head_dim + i] and
+//     s = tab[(pos0+row)*head_dim + head_dim/2 + i]:
+//       x_i <- a*c - b*s,   x_{i+half} <- b*c + a*s.
+//   KV write (src/kernels_gpu.cu:708-727): source [t][h][d] fp32, destination
+//     [h][pos0+t][d] fp16 with IEEE round-to-nearest-even; host checks
+//     pos0 >= 0 and pos0 + seq <= max_seq (src/kernels_gpu.cu:1024-1028).
+//   Layer order (src/qwen3_gpu.cu:77-91): q/k RMSNorm, then RoPE on q and k,
+//     then the K/V cache write; V is never normalised or rotated.
+//
+// MI355X mapping for head_dim = 128: 16 lanes own one head row; lane L holds
+// elements 4L..4L+3 and 64+4L..64+4L+3 as two float4, so both members of every
+// RoPE pair sit in the same lane and the norm reduction is a 4-step butterfly
+// inside the 16-lane group. The fused kernel reads q, k, v once, writes q back
+// (fp32) and k, v as fp16 straight into the cache (each head row of the cache is
+// 256 contiguous bytes, written as two 128-byte runs of 8-byte stores).
+//
+// pos0 arrives by value on eager launches; a launch being captured into a graph
+// receives the staging address instead (Pos0ForLaunch) and reads it on device.
+#include <hip/hip_runtime.h>
+
+#include "dev_util.h"
+#include "kernels_gpu.h"
+
+namespace rpg {
+namespace {
+
+using dev::AddSquares;
+using dev::Load4;
+using dev::PackHalf4;
+using dev::RmsScale;
+using dev::ScaleMul;
+using dev::Store4;
+
+constexpr int kBlock = 256;
+constexpr int kHeadDim = 128;
+
+bool Aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+__device__ __forceinline__ int64_t ReadPos0(int64_t value, const int64_t* dev) {
+  return dev != nullptr ? *dev : value;
+}
+
+// a, b are the two halves owned by a lane; c, s the matching cos / sin.
+__device__ __forceinline__ void Rotate(float4& a, float4& b, float4 c, float4 s) {
+  const float4 ra = make_float4(a.x * c.x - b.x * s.x, a.y * c.y - b.y * s.y, a.z * c.z - b.z * s.z,
+                                a.w * c.w - b.w * s.w);
+  const float4 rb = make_float4(b.x * c.x + a.x * s.x, b.y * c.y + a.y * s.y, b.z * c.z + a.z * s.z,
+                                b.w * c.w + a.w * s.w);
+  a = ra;
+  b = rb;
+}
+
+// ---------------------------------------------------------------- RoPE
+
+__global__ __launch_bounds__(kBlock) void RopeHead128Kernel(float* x, int32_t n_heads, const float* __restrict__ tab,
+                                                            int64_t pos0_val, const int64_t* __restrict__ pos0_dev,
+                                                            int64_t n_units) {
+  const int l = threadIdx.x & 15;
+  const int64_t unit = static_cast<int64_t>(blockIdx.x) * (kBlock / 16) + (threadIdx.x >> 4);
+  if (unit >= n_units) return;
+  const int64_t row = unit / n_heads;
+  const float* cs = tab + (ReadPos0(pos0_val, pos0_dev) + row) * kHeadDim;
+  float* p = x + unit * kHeadDim;
+  float4 a = Load4(p + 4 * l);
+  float4 b = Load4(p + 64 + 4 * l);
+  Rotate(a, b, Load4(cs + 4 * l), Load4(cs + 64 + 4 * l));
+  Store4(p + 4 * l, a);
+  Store4(p + 64 + 4 * l, b);
+}
+
+// Any even head_dim: one thread per rotation pair.
+__global__ __launch_bounds__(kBlock) void RopePairKernel(float* x, int32_t n_heads, int32_t head_dim,
+                                                         const float* __restrict__ tab, int64_t pos0_val,
+                                                         const int64_t* __restrict__ pos0_dev, int64_t total) {
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (idx >= total) return;
+  const int32_t half = head_dim / 2;
+  const int64_t per_row = static_cast<int64_t>(n_heads) * half;
+  const int64_t row = idx / per_row;
+  const int64_t rem = idx - row * per_row;
+  const int32_t h = static_cast<int32_t>(rem / half);
+  const int32_t i = static_cast<int32_t>(rem - static_cast<int64_t>(h) * half);
+  const float* c_t = tab + (ReadPos0(pos0_val, pos0_dev) + row) * head_dim;
+  float* xh = x + (row * n_heads + h) * head_dim;
+  const float a = xh[i];
+  const float b = xh[i + half];
+  const float c = c_t[i];
+  const float s = c_t[half + i];
+  xh[i] = a * c - b * s;
+  xh[i + half] = b * c + a * s;
+}
+
+// ---------------------------------------------------------------- KV write
+
+// Four consecutive elements per thread (head_dim % 4 == 0): one float4 load per
+// tensor, one 8-byte store of four halves per tensor.
+__global__ __launch_bounds__(kBlock) void KvWriteVec4Kernel(const float* __restrict__ k, const float* __restrict__ v,
+                                                            int32_t n_kv_heads, int32_t head_dim, int64_t pos0_val,
+                                                            const int64_t* __restrict__ pos0_dev, int64_t max_seq,
+                                                            int64_t total4, uint16_t* __restrict__ kc,
+                                                            uint16_t* __restrict__ vc) {
+  const int64_t i4 = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (i4 >= total4) return;
+  const int64_t i = 4 * i4;
+  const int64_t dd = i % head_dim;
+  const int64_t r = i / head_dim;  // t * n_kv_heads + h
+  const int64_t h = r % n_kv_heads;
+  const int64_t t = r / n_kv_heads;
+  const int64_t pos = ReadPos0(pos0_val, pos0_dev) + t;
+  if (pos < 0 || pos >= max_seq) return;  // only reachable through a replayed graph with a bad staged pos0
+  const int64_t dst = (h * max_seq + pos) * head_dim + dd;
+  *reinterpret_cast<uint2*>(kc + dst) = PackHalf4(Load4(k + i));
+  *reinterpret_cast<uint2*>(vc + dst) = PackHalf4(Load4(v + i));
+}
+
+__global__ __launch_bounds__(kBlock) void KvWriteScalarKernel(const float* __restrict__ k, const float* __restrict__ v,
+                                                              int32_t n_kv_heads, int32_t head_dim, int64_t pos0_val,
+                                                              const int64_t* __restrict__ pos0_dev, int64_t max_seq,
+                                                              int64_t total, uint16_t* __restrict__ kc,
+                                                              uint16_t* __restrict__ vc) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  if (i >= total) return;
+  const int64_t dd = i % head_dim;
+  const int64_t r = i / head_dim;
+  const int64_t h = r % n_kv_heads;
+  const int64_t t = r / n_kv_heads;
+  const int64_t pos = ReadPos0(pos0_val, pos0_dev) + t;
+  if (pos < 0 || pos >= max_seq) return;
+  const int64_t dst = (h * max_seq + pos) * head_dim + dd;
+  kc[dst] = static_cast<uint16_t>(dev::FloatToHalfBits(k[i]));
+  vc[dst] = static_cast<uint16_t>(dev::FloatToHalfBits(v[i]));
+}
+
+// ---------------------------------------------------------------- fused q/k norm + RoPE + KV
+
+// Work units per token: n_heads q rows, then n_kv k rows, then n_kv v rows;
+// 16 lanes per unit, 16 units per 256-thread block. With n_heads and n_kv
+// multiples of 4 every wave handles units of a single kind.
+template <bool kWriteK>
+__global__ __launch_bounds__(kBlock) void QkNormRopeKvKernel(
+    float* q, float* k, const float* __restrict__ v, const float* __restrict__ qw, const float* __restrict__ kw,
+    int32_t n_heads, int32_t n_kv, const float* __restrict__ tab, int64_t rope_rows, int64_t pos0_val,
+    const int64_t* __restrict__ pos0_dev, uint32_t n_units, float eps, uint16_t* __restrict__ kc,
+    uint16_t* __restrict__ vc, int64_t max_seq) {
+  const int l = threadIdx.x & 15;
+  const uint32_t unit = blockIdx.x * (kBlock / 16) + (threadIdx.x >> 4);
+  if (unit >= n_units) return;
+  const uint32_t per_tok = static_cast<uint32_t>(n_heads + 2 * n_kv);
+  const uint32_t t = unit / per_tok;
+  const int32_t j = static_cast<int32_t>(unit - t * per_tok);
+  const int64_t pos = ReadPos0(pos0_val, pos0_dev) + t;
+  const bool kv_slot_ok = pos >= 0 && pos < max_seq;
+
+  if (j < n_heads + n_kv) {
+    const bool is_q = j < n_heads;
+    const int32_t h = is_q ? j : j - n_heads;
+    float* p = is_q ? q + (static_cast<int64_t>(t) * n_heads + h) * kHeadDim
+                    : k + (static_cast<int64_t>(t) * n_kv + h) * kHeadDim;
+    const float* w = is_q ? qw : kw;
+    float4 a = Load4(p + 4 * l);
+    float4 b = Load4(p + 64 + 4 * l);
+    double ss = AddSquares(AddSquares(0.0, a), b);
+    ss = dev::GroupSum<16>(ss);
+    const float scale = RmsScale(ss, kHeadDim, eps);
+    a = ScaleMul(a, scale, Load4(w + 4 * l));
+    b = ScaleMul(b, scale, Load4(w + 64 + 4 * l));
+    if (pos >= 0 && pos < rope_rows) {
+      const float* cs = tab + pos * kHeadDim;
+      Rotate(a, b, Load4(cs + 4 * l), Load4(cs + 64 + 4 * l));
+    }
+    if (is_q || kWriteK) {
+      Store4(p + 4 * l, a);
+      Store4(p + 64 + 4 * l, b);
+    }
+    if (!is_q && kv_slot_ok) {
+      uint16_t* dst = kc + (static_cast<int64_t>(h) * max_seq + pos) * kHeadDim;
+      *reinterpret_cast<uint2*>(dst + 4 * l) = PackHalf4(a);
+      *reinterpret_cast<uint2*>(dst + 64 + 4 * l) = PackHalf4(b);
+    }
+  } else {
+    const int32_t h = j - n_heads - n_kv;
+    const float* p = v + (static_cast<int64_t>(t) * n_kv + h) * kHeadDim;
+    const float4 a = Load4(p + 4 * l);
+    const float4 b = Load4(p + 64 + 4 * l);
+    if (kv_slot_ok) {
+      uint16_t* dst = vc + (static_cast<int64_t>(h) * max_seq + pos) * kHeadDim;
+      *reinterpret_cast<uint2*>(dst + 4 * l) = PackHalf4(a);
+      *reinterpret_cast<uint2*>(dst + 64 + 4 * l) = PackHalf4(b);
+    }
+  }
+}
+
+}  // namespace
+
+void GpuRope(float* x, int32_t n_heads, int32_t head_dim, const float* rope_tab, int64_t pos0, int64_t n_rows) {
+  RPG_CHECK(head_dim > 0 && head_dim % 2 == 0, "head_dim %d must be even (RoPE pairs half-dimensions)", head_dim);
+  RPG_CHECK(n_heads > 0 && n_rows >= 0, "invalid Rope arguments");
+  RPG_CHECK(pos0 >= 0, "RoPE position %lld must not be negative", static_cast<long long>(pos0));
+  if (n_rows == 0) return;
+  RPG_CHECK(x != nullptr && rope_tab != nullptr, "Rope got a null pointer");
+  const Pos0Arg p0 = Pos0ForLaunch(pos0);
+  if (head_dim == kHeadDim && Aligned(x, 16) && Aligned(rope_tab, 16)) {
+    const int64_t units = n_rows * n_heads;
+    RopeHead128Kernel<<<GridFor(units, kBlock / 16), kBlock, 0, EngineStream()>>>(x, n_heads, rope_tab, p0.value,
+                                                                                  p0.dev, units);
+    CheckLaunch("RopeHead128Kernel");
+    return;
+  }
+  const int64_t total = n_rows * n_heads * (head_dim / 2);
+  RopePairKernel<<<GridFor(total, kBlock), kBlock, 0, EngineStream()>>>(x, n_heads, head_dim, rope_tab, p0.value,
+                                                                        p0.dev, total);
+  CheckLaunch("RopePairKernel");
+}
+
+void GpuKvWrite(const float* k_dev, const float* v_dev, int32_t n_kv_heads, int32_t head_dim, int64_t pos0,
+                int64_t seq, uint16_t* k_cache_layer, uint16_t* v_cache_layer, int64_t max_seq) {
+  RPG_CHECK(seq > 0 && n_kv_heads > 0 && head_dim > 0, "invalid KvWrite arguments");
+  RPG_CHECK(pos0 >= 0, "write position %lld must not be negative", static_cast<long long>(pos0));
+  RPG_CHECK(pos0 + seq <= max_seq, "write range [%lld, %lld) exceeds the cache capacity %lld",
+            static_cast<long long>(pos0), static_cast<long long>(pos0 + seq), static_cast<long long>(max_seq));
+  RPG_CHECK(k_dev != nullptr && v_dev != nullptr && k_cache_layer != nullptr && v_cache_layer != nullptr,
+            "KvWrite got a null pointer");
+  const int64_t total = seq * n_kv_heads * head_dim;
+  const Pos0Arg p0 = Pos0ForLaunch(pos0);
+  if (head_dim % 4 == 0 && Aligned(k_dev, 16) && Aligned(v_dev, 16) && Aligned(k_cache_layer, 8) &&
+      Aligned(v_cache_layer, 8)) {
+    const int64_t total4 = total / 4;
+    KvWriteVec4Kernel<<<GridFor(total4, kBlock), kBlock, 0, EngineStream()>>>(
+        k_dev, v_dev, n_kv_heads, head_dim, p0.value, p0.dev, max_seq, total4, k_cache_layer, v_cache_layer);
+    CheckLaunch("KvWriteVec4Kernel");
+    return;
+  }
+  KvWriteScalarKernel<<<GridFor(total, kBlock), kBlock, 0, EngineStream()>>>(
+      k_dev, v_dev, n_kv_heads, head_dim, p0.value, p0.dev, max_seq, total, k_cache_layer, v_cache_layer);
+  CheckLaunch("KvWriteScalarKernel");
+}
+
+void GpuQkNormRopeKv(float* q, float* k, const float* v, const float* q_norm, const float* k_norm, int32_t n_heads,
+                     int32_t n_kv_heads, int32_t head_dim, const float* rope_tab, int64_t rope_rows, int64_t pos0,
+                     int64_t seq, float eps, uint16_t* k_cache_layer, uint16_t* v_cache_layer, int64_t max_seq,
+                     bool write_k_f32) {
+  RPG_CHECK(seq > 0 && n_heads > 0 && n_kv_heads > 0 && head_dim > 0, "invalid QkNormRopeKv arguments");
+  RPG_CHECK(head_dim % 2 == 0, "head_dim %d must be even", head_dim);
+  RPG_CHECK(pos0 >= 0, "write position %lld must not be negative", static_cast<long long>(pos0));
+  RPG_CHECK(pos0 + seq <= max_seq, "write range [%lld, %lld) exceeds the cache capacity %lld",
+            static_cast<long long>(pos0), static_cast<long long>(pos0 + seq), static_cast<long long>(max_seq));
+  RPG_CHECK(pos0 + seq <= rope_rows, "positions [%lld, %lld) exceed the RoPE table (%lld rows)",
+            static_cast<long long>(pos0), static_cast<long long>(pos0 + seq), static_cast<long long>(rope_rows));
+  RPG_CHECK(q && k && v && q_norm && k_norm && rope_tab && k_cache_layer && v_cache_layer,
+            "QkNormRopeKv got a null pointer");
+  const int64_t units = seq * (n_heads + 2 * static_cast<int64_t>(n_kv_heads));
+  const bool fast = head_dim == kHeadDim && units <= 0x7FFFFFFF && Aligned(q, 16) && Aligned(k, 16) &&
+                    Aligned(v, 16) && Aligned(q_norm, 16) && Aligned(k_norm, 16) && Aligned(rope_tab, 16) &&
+                    Aligned(k_cache_layer, 8) && Aligned(v_cache_layer, 8);
+  if (!fast) {
+    // Other head sizes / layouts: the unfused reference sequence (k then holds
+    // the rotated values, as it does in the reference layer).
+    GpuRmsNorm(q, q_norm, seq * n_heads, head_dim, head_dim, eps, q);
+    GpuRmsNorm(k, k_norm, seq * n_kv_heads, head_dim, head_dim, eps, k);
+    GpuRope(q, n_heads, head_dim, rope_tab, pos0, seq);
+    GpuRope(k, n_kv_heads, head_dim, rope_tab, pos0, seq);
+    GpuKvWrite(k, v, n_kv_heads, head_dim, pos0, seq, k_cache_layer, v_cache_layer, max_seq);
+    return;
+  }
+  const Pos0Arg p0 = Pos0ForLaunch(pos0);
+  const unsigned grid = GridFor(units, kBlock / 16);
+  if (write_k_f32) {
+    QkNormRopeKvKernel<true><<<grid, kBlock, 0, EngineStream()>>>(
+        q, k, v, q_norm, k_norm, n_heads, n_kv_heads, rope_tab, rope_rows, p0.value, p0.dev,
+        static_cast<uint32_t>(units), eps, k_cache_layer, v_cache_layer, max_seq);
+  } else {
+    QkNormRopeKvKernel<false><<<grid, kBlock, 0, EngineStream()>>>(
+        q, k, v, q_norm, k_norm, n_heads, n_kv_heads, rope_tab, rope_rows, p0.value, p0.dev,
+        static_cast<uint32_t>(units), eps, k_cache_layer, v_cache_layer, max_seq);
+  }
+  CheckLaunch("QkNormRopeKvKernel");
+}
+
+}  // namespace rpg

@@ -1,0 +1,175 @@
+// Hot-path operators of the Qwen3 layer, MI355X (gfx950) implementation.
+//
+// The seven reference operators keep their exact C++ signatures
+// (reference src/kernels_gpu.h), so the engine code that sequences them
+// (src/qwen3_gpu.cu:47-109, 139-140, 168) links against this library unchanged:
+//   GpuDequantRow        src/kernels_gpu.h:39-40
+//   GpuRmsNorm           src/kernels_gpu.h:65-66
+//   GpuRope              src/kernels_gpu.h:71-72
+//   GpuKvWrite           src/kernels_gpu.h:97-99
+//   GpuSiluMulInPlace    src/kernels_gpu.h:147
+//   GpuVecAddInPlace     src/kernels_gpu.h:150
+//   GpuEmbeddingLookup   src/kernels_gpu.h:153-154
+// and three fused operators replace the unfused sequences of GpuForwardLayer:
+//   GpuAddRmsNorm        GpuVecAddInPlace(x += d) ; GpuRmsNorm(x -> out)
+//                        (src/qwen3_gpu.cu:100 -> 103, and :108 -> next layer's :69)
+//   GpuQkNormRopeKv      GpuRmsNorm(q), GpuRmsNorm(k), GpuRope(q), GpuRope(k),
+//                        GpuKvWrite(k, v)   (src/qwen3_gpu.cu:77-91)
+//   GpuSiluMulInPlace    already one kernel in the reference (src/qwen3_gpu.cu:106)
+//
+// Conventions (same as the reference operator layer):
+//   * every pointer is a device pointer; the caller owns all buffers;
+//   * launches are asynchronous on EngineStream(); nothing synchronises;
+//   * argument errors throw rpg::Error before anything is launched;
+//   * out may alias x for RMSNorm / RoPE / SiLU-mul / add.
+//
+// Numerics (what the parity tests hold each operator to):
+//   * dequant / gather: bit-exact with the reference CPU dequant (quant.cc):
+//     Q4_K y = (d*sc)*q - (dmin*m), Q6_K y = (d*sc)*q, each op rounded
+//     separately (the library is built with -ffp-contract=off);
+//   * residual add: one IEEE fp32 add, bit-exact;
+//   * fp16 KV store: IEEE round-to-nearest-even, bit-exact;
+//   * RMSNorm: sum of squares accumulated in double, scale = float(1/sqrt(ss/n + eps)),
+//     out = (x*scale)*w in fp32;  RoPE: a*c - b*s, b*c + a*s;  SiLU-mul: v/(1+exp(-v))*up.
+#ifndef RPG_AMD_KERNELS_GPU_H_
+#define RPG_AMD_KERNELS_GPU_H_
+
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "hip_common.h"
+#include "quant_types.h"
+
+namespace rpg {
+
+// ---------------------------------------------------------------- shapes
+
+// The subset of the reference's model metadata (src/model_meta.h:27-65) that
+// the hot path reads.
+struct ModelMeta {
+  int32_t n_layers = 0;
+  int64_t hidden = 0;
+  int32_t n_heads = 0;
+  int32_t n_kv_heads = 0;
+  int32_t head_dim = 0;
+  int64_t intermediate = 0;
+  int64_t vocab = 0;
+  int64_t context_length = 0;
+  float rms_eps = 1e-6f;
+  double rope_theta = 1e6;
+};
+
+// A weight tensor resident in device memory as its raw GGUF bytes
+// (reference src/gpu_model.h:42-55).
+struct GpuTensor {
+  DeviceBuffer buf;
+  uint32_t type = kGgmlF32;
+  bool matrix = false;
+  int64_t rows = 0;  // dims[1]
+  int64_t cols = 0;  // dims[0]
+  int64_t n_elements = 0;
+
+  bool valid() const { return !buf.empty(); }
+  const char* type_name() const { return TypeName(type); }
+  int64_t bytes() const { return static_cast<int64_t>(buf.size()); }
+  int64_t row_bytes() const { return TypeRowBytes(type, cols); }
+};
+
+// Device-resident fp16 KV cache with the reference layout
+// [n_layers][n_kv_heads][max_seq][head_dim] (src/kv_cache_gpu.h:1-30, :50-100).
+class GpuKvCache {
+ public:
+  GpuKvCache() = default;
+  GpuKvCache(const ModelMeta& c, int64_t max_seq);
+
+  int64_t len() const { return len_; }
+  int64_t max_seq() const { return max_seq_; }
+  int32_t n_layers() const { return n_layers_; }
+  int32_t n_kv_heads() const { return n_kv_heads_; }
+  int32_t head_dim() const { return head_dim_; }
+  bool valid() const { return max_seq_ > 0; }
+
+  // Base of layer `layer`: [n_kv_heads][max_seq][head_dim] fp16 bits.
+  uint16_t* k_layer(int32_t layer);
+  uint16_t* v_layer(int32_t layer);
+  const uint16_t* k_layer(int32_t layer) const;
+
+  void Reset() { len_ = 0; }
+  void SetLen(int64_t n);
+  void AddLen(int64_t n) { SetLen(len_ + n); }
+  int64_t bytes() const { return static_cast<int64_t>(k_.size() + v_.size()); }
+  std::string Describe() const;
+
+ private:
+  int64_t LayerElems() const { return static_cast<int64_t>(n_kv_heads_) * max_seq_ * head_dim_; }
+
+  int32_t n_layers_ = 0;
+  int32_t n_kv_heads_ = 0;
+  int32_t head_dim_ = 0;
+  int64_t max_seq_ = 0;
+  int64_t len_ = 0;
+  DeviceBuffer k_;
+  DeviceBuffer v_;
+};
+
+// Host-built RoPE table, [n_pos][head_dim] fp32, cos in the first half of a row and
+// sin in the second; angles computed in double (reference src/gpu_model.cu:90-120).
+// n_pos = min(max_pos, context_length), at least 1.
+std::vector<float> BuildRopeTable(int32_t head_dim, double theta, int64_t n_pos);
+
+// ---------------------------------------------------------------- reference operators
+
+void GpuDequantRow(uint32_t type, const uint8_t* src_dev, int64_t n_elems, float* dst_dev);
+
+void GpuRmsNorm(const float* x, const float* w, int64_t n_rows, int64_t n, int64_t stride, float eps,
+                float* out);
+
+void GpuRope(float* x, int32_t n_heads, int32_t head_dim, const float* rope_tab, int64_t pos0,
+             int64_t n_rows);
+
+void GpuKvWrite(const float* k_dev, const float* v_dev, int32_t n_kv_heads, int32_t head_dim, int64_t pos0,
+                int64_t seq, uint16_t* k_cache_layer, uint16_t* v_cache_layer, int64_t max_seq);
+
+void GpuSiluMulInPlace(float* gate_dev, const float* up_dev, int64_t n);
+
+void GpuVecAddInPlace(float* a_dev, const float* b_dev, int64_t n);
+
+void GpuEmbeddingLookup(const GpuTensor& emb, const int32_t* toks_dev, int64_t seq, float* x_dev);
+
+// ---------------------------------------------------------------- fused operators
+
+// x[r] += d[r] (one IEEE add, written back to x), then out[r] = RMSNorm(x[r]) * w.
+// Rows are contiguous with stride n. out must not alias x or d.
+void GpuAddRmsNorm(float* x, const float* d, const float* w, int64_t n_rows, int64_t n, float eps, float* out);
+
+// Per token t (position pos0 + t):
+//   q[t,h,:]  <- RoPE(RMSNorm(q[t,h,:]) * q_norm)          in place, h < n_heads
+//   k'        <- RoPE(RMSNorm(k[t,h,:]) * k_norm)          h < n_kv_heads
+//   k_layer[h][pos0+t][:] <- fp16_rne(k');  v_layer[h][pos0+t][:] <- fp16_rne(v[t,h,:])
+//   if write_k_f32: k[t,h,:] <- k' (needed only by the no-cache attention path)
+// rope_rows is the number of rows in rope_tab (bounds check on pos0 + seq).
+void GpuQkNormRopeKv(float* q, float* k, const float* v, const float* q_norm, const float* k_norm,
+                     int32_t n_heads, int32_t n_kv_heads, int32_t head_dim, const float* rope_tab,
+                     int64_t rope_rows, int64_t pos0, int64_t seq, float eps, uint16_t* k_cache_layer,
+                     uint16_t* v_cache_layer, int64_t max_seq, bool write_k_f32);
+
+// Embedding gather from a raw (non-owning) device table; GpuEmbeddingLookup
+// forwards here. Token ids outside [0, rows) produce a zero row instead of an
+// out-of-bounds read.
+void GpuEmbeddingLookupRaw(uint32_t type, const uint8_t* emb_dev, int64_t rows, int64_t cols,
+                           const int32_t* toks_dev, int64_t seq, float* x_dev);
+
+// ---------------------------------------------------------------- measurement / verification
+
+// Streaming copy of `bytes` (multiple of 16) used to calibrate bandwidth and
+// HBM counters (the reference's streaming-bandwidth probe, tools/matmul_bench.cu:230-289).
+void GpuStreamCopy(const void* src, void* dst, int64_t bytes);
+
+// out[i] = binary16 bits i converted to fp32, i in [0, 65536): exhaustive check
+// of the device f16 -> f32 conversion (tools/dequant_check.cu:44-48).
+void GpuF16Sweep(float* out_dev);
+
+}  // namespace rpg
+
+#endif  // RPG_AMD_KERNELS_GPU_H_

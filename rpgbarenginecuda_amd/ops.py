@@ -1,0 +1,288 @@
+"""Host-side mirror of the reference operator layer, over librpg_ops.so (ctypes).
+
+Names, argument order and meaning follow the reference's operators
+(src/kernels_gpu.h:39-154) so callers and tests read like the reference's own
+tools (tools/kv_map_check.cu, tools/dequant_check.cu). Arguments that are
+device buffers may be torch tensors on the GPU (their size and dtype are checked
+against what the operator will touch before anything is launched) or raw
+integer device addresses (then the caller vouches for the sizes).
+
+Failures raise RpgError carrying rpg_ops_last_error(); nothing falls back to a
+CPU path: if the library is missing, loading it raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from typing import Optional
+
+PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG_DIR, "librpg_ops.so")
+
+GGML_F32 = 0
+GGML_Q4_K = 12
+GGML_Q6_K = 14
+QK_K = 256
+BLOCK_BYTES = {GGML_F32: 4, GGML_Q4_K: 144, GGML_Q6_K: 210}
+BLOCK_ELEMS = {GGML_F32: 1, GGML_Q4_K: 256, GGML_Q6_K: 256}
+
+# Every symbol include/rpg_ops.h declares, with its ctypes signature.
+_i32, _i64, _u32, _f32, _f64, _vp = (ctypes.c_int32, ctypes.c_int64, ctypes.c_uint32, ctypes.c_float,
+                                     ctypes.c_double, ctypes.c_void_p)
+SIGNATURES = {
+    "rpg_ops_version": (ctypes.c_char_p, []),
+    "rpg_ops_last_error": (ctypes.c_char_p, []),
+    "rpg_ops_init": (_i32, []),
+    "rpg_ops_set_stream": (_i32, [_vp]),
+    "rpg_ops_get_stream": (_vp, []),
+    "rpg_ops_stage_pos0": (_i32, [_i64]),
+    "rpg_ops_device_info": (_i32, [ctypes.c_char_p, _i32]),
+    "rpg_ops_type_row_bytes": (_i64, [_u32, _i64]),
+    "rpg_ops_build_rope_table": (_i32, [_i32, _f64, _i64, _vp]),
+    "rpg_op_dequant_row": (_i32, [_u32, _vp, _i64, _vp]),
+    "rpg_op_rms_norm": (_i32, [_vp, _vp, _i64, _i64, _i64, _f32, _vp]),
+    "rpg_op_rope": (_i32, [_vp, _i32, _i32, _vp, _i64, _i64]),
+    "rpg_op_kv_write": (_i32, [_vp, _vp, _i32, _i32, _i64, _i64, _vp, _vp, _i64]),
+    "rpg_op_silu_mul_inplace": (_i32, [_vp, _vp, _i64]),
+    "rpg_op_vec_add_inplace": (_i32, [_vp, _vp, _i64]),
+    "rpg_op_embedding_lookup": (_i32, [_u32, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "rpg_op_add_rms_norm": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _vp]),
+    "rpg_op_qk_norm_rope_kv": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _i64, _f32,
+                                      _vp, _vp, _i64, _i32]),
+    "rpg_op_stream_copy": (_i32, [_vp, _vp, _i64]),
+    "rpg_op_f16_sweep": (_i32, [_vp]),
+}
+
+
+class RpgError(RuntimeError):
+    """An operator rejected its arguments or a HIP call failed."""
+
+
+_lib: Optional[ctypes.CDLL] = None
+
+
+def load_library() -> ctypes.CDLL:
+    """Loads librpg_ops.so once. torch is imported first so the library binds to
+    the HIP runtime torch already loaded (both carry SONAME libamdhip64.so.7)
+    and device pointers from torch allocations are valid in it."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    import torch  # noqa: F401  (load order matters, see above)
+
+    if not os.path.exists(LIB_PATH):
+        raise RpgError(f"{LIB_PATH} is not built; run __graft_entry__.build() "
+                       "(python -m rpgbarenginecuda_amd.build)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def _check(rc: int) -> int:
+    if rc < 0:
+        msg = load_library().rpg_ops_last_error()
+        raise RpgError(msg.decode("utf-8", "replace") if msg else f"error {rc}")
+    return rc
+
+
+def _addr(buf, nbytes: int = 0, dtype=None, name: str = "buffer"):
+    """Device address of `buf` (torch tensor or int), checking that a tensor is
+    on the GPU, contiguous, of `dtype` and at least `nbytes` long."""
+    if buf is None:
+        return None
+    if isinstance(buf, int):
+        return buf
+    import torch
+
+    if not isinstance(buf, torch.Tensor):
+        raise TypeError(f"{name}: expected a torch tensor or a device address, got {type(buf)}")
+    if not buf.is_cuda:
+        raise RpgError(f"{name}: tensor is not on the GPU")
+    if not buf.is_contiguous():
+        raise RpgError(f"{name}: tensor must be contiguous")
+    if dtype is not None and buf.dtype != dtype:
+        raise RpgError(f"{name}: expected dtype {dtype}, got {buf.dtype}")
+    have = buf.numel() * buf.element_size()
+    if have < nbytes:
+        raise RpgError(f"{name}: operator touches {nbytes} bytes but the tensor holds {have}")
+    return buf.data_ptr()
+
+
+def _t():
+    import torch
+
+    return torch
+
+
+# ----------------------------------------------------------------------------- runtime
+
+
+def version() -> str:
+    return load_library().rpg_ops_version().decode()
+
+
+def init() -> None:
+    """Allocates the pos0 staging scalar (required before any graph capture)."""
+    _check(load_library().rpg_ops_init())
+
+
+def set_stream(stream) -> None:
+    """Routes launches to `stream` (torch.cuda.Stream, raw hipStream_t int, or None)."""
+    handle = getattr(stream, "cuda_stream", stream)
+    _check(load_library().rpg_ops_set_stream(handle or None))
+
+
+def get_stream() -> int:
+    return load_library().rpg_ops_get_stream() or 0
+
+
+class ScopedEngineStream:
+    """Context manager mirroring ScopedEngineStream (src/cuda_common.h:128-137)."""
+
+    def __init__(self, stream):
+        self._stream = stream
+        self._prev = None
+
+    def __enter__(self):
+        self._prev = get_stream()
+        set_stream(self._stream)
+        return self
+
+    def __exit__(self, *exc):
+        set_stream(self._prev)
+        return False
+
+
+def stage_pos0(pos: int) -> None:
+    _check(load_library().rpg_ops_stage_pos0(int(pos)))
+
+
+def device_info() -> tuple[bool, str]:
+    buf = ctypes.create_string_buffer(512)
+    rc = _check(load_library().rpg_ops_device_info(buf, 512))
+    return rc == 1, buf.value.decode()
+
+
+def type_row_bytes(ggml_type: int, n_elems: int) -> int:
+    return _check(load_library().rpg_ops_type_row_bytes(ggml_type, n_elems))
+
+
+def build_rope_table(head_dim: int, theta: float, n_pos: int):
+    """Host RoPE table as a numpy float32 array [n_pos, head_dim]."""
+    import numpy as np
+
+    out = np.empty((n_pos, head_dim), dtype=np.float32)
+    _check(load_library().rpg_ops_build_rope_table(head_dim, float(theta), n_pos,
+                                                   out.ctypes.data_as(ctypes.c_void_p)))
+    return out
+
+
+class GpuTensor:
+    """Raw GGUF bytes of a weight tensor resident on the GPU (src/gpu_model.h:42-55)."""
+
+    def __init__(self, data, ggml_type: int, rows: int, cols: int):
+        self.buf = data
+        self.type = int(ggml_type)
+        self.rows = int(rows)
+        self.cols = int(cols)
+        self.matrix = True
+        self.n_elements = self.rows * self.cols
+
+    def row_bytes(self) -> int:
+        return (self.cols // BLOCK_ELEMS[self.type]) * BLOCK_BYTES[self.type]
+
+
+# ----------------------------------------------------------------------------- reference operators
+
+
+def GpuDequantRow(ggml_type: int, src, n_elems: int, dst) -> None:
+    torch = _t()
+    nbytes = type_row_bytes(ggml_type, n_elems) if ggml_type in BLOCK_BYTES else 0
+    _check(load_library().rpg_op_dequant_row(ggml_type, _addr(src, nbytes, name="src"), n_elems,
+                                             _addr(dst, 4 * n_elems, torch.float32, "dst")))
+
+
+def GpuRmsNorm(x, w, n_rows: int, n: int, stride: int, eps: float, out) -> None:
+    torch = _t()
+    span = 4 * ((n_rows - 1) * stride + n) if n_rows > 0 else 0
+    _check(load_library().rpg_op_rms_norm(_addr(x, span, torch.float32, "x"), _addr(w, 4 * n, torch.float32, "w"),
+                                          n_rows, n, stride, eps, _addr(out, span, torch.float32, "out")))
+
+
+def GpuRope(x, n_heads: int, head_dim: int, rope_tab, pos0: int, n_rows: int) -> None:
+    torch = _t()
+    _check(load_library().rpg_op_rope(
+        _addr(x, 4 * n_rows * n_heads * head_dim, torch.float32, "x"), n_heads, head_dim,
+        _addr(rope_tab, 4 * (pos0 + n_rows) * head_dim, torch.float32, "rope_tab"), pos0, n_rows))
+
+
+def GpuKvWrite(k, v, n_kv_heads: int, head_dim: int, pos0: int, seq: int, k_layer, v_layer, max_seq: int) -> None:
+    torch = _t()
+    src = 4 * seq * n_kv_heads * head_dim
+    dst = 2 * n_kv_heads * max_seq * head_dim
+    _check(load_library().rpg_op_kv_write(
+        _addr(k, src, torch.float32, "k"), _addr(v, src, torch.float32, "v"), n_kv_heads, head_dim, pos0, seq,
+        _addr(k_layer, dst, None, "k_layer"), _addr(v_layer, dst, None, "v_layer"), max_seq))
+
+
+def GpuSiluMulInPlace(gate, up, n: int) -> None:
+    torch = _t()
+    nb = 4 * max(n, 0)
+    _check(load_library().rpg_op_silu_mul_inplace(_addr(gate, nb, torch.float32, "gate"),
+                                                  _addr(up, nb, torch.float32, "up"), n))
+
+
+def GpuVecAddInPlace(a, b, n: int) -> None:
+    torch = _t()
+    nb = 4 * max(n, 0)
+    _check(load_library().rpg_op_vec_add_inplace(_addr(a, nb, torch.float32, "a"), _addr(b, nb, torch.float32, "b"),
+                                                 n))
+
+
+def GpuEmbeddingLookup(emb: GpuTensor, toks, seq: int, x) -> None:
+    torch = _t()
+    _check(load_library().rpg_op_embedding_lookup(
+        emb.type, _addr(emb.buf, emb.rows * emb.row_bytes(), name="emb"), emb.rows, emb.cols,
+        _addr(toks, 4 * seq, torch.int32, "toks"), seq, _addr(x, 4 * seq * emb.cols, torch.float32, "x")))
+
+
+# ----------------------------------------------------------------------------- fused operators
+
+
+def GpuAddRmsNorm(x, d, w, n_rows: int, n: int, eps: float, out) -> None:
+    torch = _t()
+    span = 4 * n_rows * n
+    _check(load_library().rpg_op_add_rms_norm(
+        _addr(x, span, torch.float32, "x"), _addr(d, span, torch.float32, "d"), _addr(w, 4 * n, torch.float32, "w"),
+        n_rows, n, eps, _addr(out, span, torch.float32, "out")))
+
+
+def GpuQkNormRopeKv(q, k, v, q_norm, k_norm, n_heads: int, n_kv_heads: int, head_dim: int, rope_tab,
+                    rope_rows: int, pos0: int, seq: int, eps: float, k_layer, v_layer, max_seq: int,
+                    write_k_f32: bool = False) -> None:
+    torch = _t()
+    kvb = 4 * seq * n_kv_heads * head_dim
+    cache = 2 * n_kv_heads * max_seq * head_dim
+    _check(load_library().rpg_op_qk_norm_rope_kv(
+        _addr(q, 4 * seq * n_heads * head_dim, torch.float32, "q"), _addr(k, kvb, torch.float32, "k"),
+        _addr(v, kvb, torch.float32, "v"), _addr(q_norm, 4 * head_dim, torch.float32, "q_norm"),
+        _addr(k_norm, 4 * head_dim, torch.float32, "k_norm"), n_heads, n_kv_heads, head_dim,
+        _addr(rope_tab, 4 * rope_rows * head_dim, torch.float32, "rope_tab"), rope_rows, pos0, seq, eps,
+        _addr(k_layer, cache, None, "k_layer"), _addr(v_layer, cache, None, "v_layer"), max_seq,
+        1 if write_k_f32 else 0))
+
+
+# ----------------------------------------------------------------------------- measurement
+
+
+def GpuStreamCopy(src, dst, nbytes: int) -> None:
+    _check(load_library().rpg_op_stream_copy(_addr(src, nbytes, name="src"), _addr(dst, nbytes, name="dst"), nbytes))
+
+
+def GpuF16Sweep(out) -> None:
+    torch = _t()
+    _check(load_library().rpg_op_f16_sweep(_addr(out, 4 * 65536, torch.float32, "out")))

@@ -1,0 +1,110 @@
+"""Seeded synthetic inputs shaped like the BASELINE configs (test infrastructure).
+
+All generators take a numpy Generator so a test's seed fixes its inputs.
+Q4_K / Q6_K tables follow the BASELINE's description of the synthetic token_embd:
+  Q4_K: d, dmin = fp16_rne(|N(0, 0.01)|); the 12 packed scale bytes uniform
+        (every unpacked 6-bit scale/min uniform over 0..63); qs uniform bytes.
+  Q6_K: d = fp16_rne(|N(0, 0.01)|); scales int8 uniform over -32..31; ql / qh
+        uniform bytes (6-bit quants uniform).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+Q4K_BYTES = 144
+Q6K_BYTES = 210
+
+QWEN3_1_7B = dict(hidden=2048, n_heads=16, n_kv_heads=8, head_dim=128, inter=6144, n_layers=28)
+QWEN3_4B = dict(hidden=2560, n_heads=32, n_kv_heads=8, head_dim=128, inter=9728, n_layers=36)
+EPS = 1e-6
+THETA = 1e6
+
+
+def f16_bits(x: np.ndarray) -> np.ndarray:
+    return np.asarray(x, dtype=np.float32).astype(np.float16).view(np.uint16)
+
+
+def q4k_blocks(rng: np.random.Generator, n_blocks: int) -> np.ndarray:
+    """n_blocks raw Q4_K super-blocks, shape [n_blocks, 144] uint8."""
+    b = rng.integers(0, 256, size=(n_blocks, Q4K_BYTES), dtype=np.uint8)
+    d = f16_bits(np.abs(rng.normal(0.0, 0.01, n_blocks)))
+    dmin = f16_bits(np.abs(rng.normal(0.0, 0.01, n_blocks)))
+    b[:, 0:2] = d.view(np.uint8).reshape(n_blocks, 2)
+    b[:, 2:4] = dmin.view(np.uint8).reshape(n_blocks, 2)
+    return b
+
+
+def q6k_blocks(rng: np.random.Generator, n_blocks: int) -> np.ndarray:
+    """n_blocks raw Q6_K super-blocks, shape [n_blocks, 210] uint8."""
+    b = rng.integers(0, 256, size=(n_blocks, Q6K_BYTES), dtype=np.uint8)
+    b[:, 192:208] = rng.integers(-32, 32, size=(n_blocks, 16)).astype(np.int8).view(np.uint8)
+    d = f16_bits(np.abs(rng.normal(0.0, 0.01, n_blocks)))
+    b[:, 208:210] = d.view(np.uint8).reshape(n_blocks, 2)
+    return b
+
+
+def quant_table(rng: np.random.Generator, ggml_type: int, rows: int, cols: int) -> np.ndarray:
+    """A [rows, cols] table as raw bytes, shape [rows * row_bytes] uint8."""
+    nb = cols // 256
+    if ggml_type == 12:
+        return q4k_blocks(rng, rows * nb).reshape(-1)
+    if ggml_type == 14:
+        return q6k_blocks(rng, rows * nb).reshape(-1)
+    if ggml_type == 0:
+        return rng.normal(0.0, 1.0, rows * cols).astype(np.float32).view(np.uint8)
+    raise ValueError(ggml_type)
+
+
+def special_q4k_blocks() -> np.ndarray:
+    """Hand-made Q4_K blocks that reach the edge cases of the formula."""
+    out = []
+    z = np.zeros(Q4K_BYTES, np.uint8)
+    out.append(z.copy())                                   # all zero
+    b = np.full(Q4K_BYTES, 0xFF, np.uint8)                 # d = dmin = NaN pattern 0xFFFF avoided below
+    b[0:4] = np.array([0x00, 0x3C, 0x00, 0x3C], np.uint8)  # d = dmin = 1.0, every scale/min 63, q = 15
+    out.append(b)
+    b = z.copy()
+    b[0:2] = [0x01, 0x00]                                  # d = smallest f16 subnormal 2^-24
+    b[2:4] = [0xFF, 0x03]                                  # dmin = largest subnormal
+    b[4:16] = np.arange(12, dtype=np.uint8) * 21           # mixed 6-bit scales / high bits
+    b[16:] = np.arange(128, dtype=np.uint8)
+    out.append(b)
+    b = z.copy()
+    b[0:2] = [0x00, 0x3C]                                  # d = 1, dmin = 0 -> y = sc*q exactly
+    b[4:16] = 0x3F
+    b[16:] = 0xA5
+    out.append(b)
+    b = z.copy()
+    b[0:2] = [0x00, 0x00]                                  # d = 0 -> y = -(dmin*m) (negative or -0)
+    b[2:4] = [0x00, 0x40]                                  # dmin = 2
+    b[4:16] = np.array([0, 1, 2, 63, 0, 5, 6, 63, 0xC1, 0x72, 0x0F, 0xF0], np.uint8)
+    b[16:] = 0x3C
+    out.append(b)
+    return np.stack(out)
+
+
+def special_q6k_blocks() -> np.ndarray:
+    """Hand-made Q6_K blocks: zero, q = 32 with negative scales (-0.0), extremes, subnormal d."""
+    out = []
+    z = np.zeros(Q6K_BYTES, np.uint8)
+    out.append(z.copy())                                   # all zero: q = -32, sc = 0
+    b = z.copy()
+    b[0:128] = 0x00                                        # low nibbles 0
+    b[128:192] = 0xAA                                      # every 2-bit high part = 2 -> q = 32 - 32 = 0
+    b[192:208] = np.array([-1, -32, 5, -7] * 4, np.int8).view(np.uint8)
+    b[208:210] = [0x00, 0x3C]                              # d = 1: y = (1*sc)*0 = -0.0 for sc < 0
+    out.append(b)
+    b = np.full(Q6K_BYTES, 0xFF, np.uint8)                 # q = 31 everywhere
+    b[192:208] = np.array([-32, 31] * 8, np.int8).view(np.uint8)
+    b[208:210] = [0xFF, 0x7B]                              # d = 65504 (largest finite half)
+    out.append(b)
+    b = z.copy()
+    b[0:192] = np.arange(192, dtype=np.uint8)
+    b[192:208] = np.arange(-8, 8, dtype=np.int8).view(np.uint8)
+    b[208:210] = [0x01, 0x00]                              # d = 2^-24 (subnormal)
+    out.append(b)
+    return np.stack(out)
+
+
+def normal(rng: np.random.Generator, shape, mean=0.0, std=1.0) -> np.ndarray:
+    return rng.normal(mean, std, size=shape).astype(np.float32)
