@@ -7,7 +7,8 @@ layer with its own seeded buffers and weights. One step = for every layer:
   q/k norm + RoPE + fp16 KV   [n, 16|8, 128]      (rpg_op_qk_norm_rope_kv)
   SwiGLU                      [n, I]              (rpg_op_silu_mul_inplace)
 `value` = algorithmic bytes of the step / step time (GB/s); per-kernel averages
-come from HIP events around every launch of the timed steps. The 28 layers'
+come from HIP events attached to every kernel dispatch of the timed steps
+(librpg_ops launch profiling, hipExtLaunchKernel). The 28 layers'
 buffers total ~9 GB, far above the 256 MB Infinity Cache, so every launch reads
 from HBM. Also reported: decode n = 1 (us per layer, eager and HIP graph), the
 Q4_K / Q6_K embedding gather at n = 2811, a streaming-copy ceiling, and the CPU
@@ -34,6 +35,7 @@ H, HQ, HKV, D, INTER, LAYERS = 2048, 16, 8, 128, 6144, 28
 MAX_SEQ, EPS, THETA = 4096, 1e-6, 1e6
 N_PREFILL = 2811
 VOCAB = 151936
+CALIB_BYTES = 256 << 20
 
 
 def bytes_add_rms(n, h=H):
@@ -83,41 +85,43 @@ def run_layer(ops, L, n, tab, pos0):
 
 
 OP_NAMES = ("add_rms_norm", "qk_norm_rope_kv", "swiglu")
-KERNEL_NAMES = {"add_rms_norm": "AddRmsNormWaveKernel<8>", "qk_norm_rope_kv": "QkNormRopeKvKernel<false>",
-                "swiglu": "BinaryVecKernel<SiluMulOp>"}
+KERNEL_NAMES = {"add_rms_norm": "AddRmsNormRowBlockKernel", "qk_norm_rope_kv": "QkNormRopeKvKernel",
+                "swiglu": "SiluMulKernel"}
 
 
 def timed_prefill(torch, ops, layers, tab, n, steps, warmup):
-    """Returns (ms_per_step, {op: [per-launch ms]})."""
+    """K steps over all layers, bracketed by stream events, twice: once as the
+    product runs (this pass gives ms_per_step and `value`), then again with
+    dispatch-attached HIP events on every launch (ops.profile_*), which give each
+    kernel's execution time but add host-side launch cost to the step.
+    Returns (ms_per_step, ms_per_step_profiled, per-kernel report)."""
     for _ in range(warmup):
         for L in layers:
             run_layer(ops, L, n, tab, 0)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
-    ev = []
-    t0 = torch.cuda.Event(enable_timing=True)
-    t1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t0.record(stream)
-    for _ in range(steps):
-        for L in layers:
-            marks = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
-            marks[0].record(stream)
-            ops.GpuAddRmsNorm(L.x, L.d, L.w, n, H, EPS, L.h)
-            marks[1].record(stream)
-            ops.GpuQkNormRopeKv(L.q, L.k, L.v, L.qn, L.kn, HQ, HKV, D, tab, MAX_SEQ, 0, n, EPS, L.kc, L.vc, MAX_SEQ)
-            marks[2].record(stream)
-            ops.GpuSiluMulInPlace(L.gate, L.up, n * INTER)
-            marks[3].record(stream)
-            ev.append(marks)
-    t1.record(stream)
-    torch.cuda.synchronize()
-    total_ms = t0.elapsed_time(t1)
-    per = {name: [] for name in OP_NAMES}
-    for marks in ev:
-        for i, name in enumerate(OP_NAMES):
-            per[name].append(marks[i].elapsed_time(marks[i + 1]))
-    return total_ms / steps, per
+
+    def timed(profile):
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        if profile:
+            ops.profile_start(steps * len(layers) * 3)
+        torch.cuda.synchronize()
+        t0.record(stream)
+        for _ in range(steps):
+            for L in layers:
+                run_layer(ops, L, n, tab, 0)
+        t1.record(stream)
+        torch.cuda.synchronize()
+        report = None
+        if profile:
+            ops.profile_stop()
+            report = ops.profile_report()
+        return t0.elapsed_time(t1) / steps, report
+
+    ms_plain, _ = timed(False)
+    ms_prof, report = timed(True)
+    return ms_plain, ms_prof, report
 
 
 def measure_decode(torch, ops, tab, steps):
@@ -183,21 +187,17 @@ def measure_gather(torch, ops, ggml_type, bb, copies=4, reps=20):
     for i in range(copies):
         ops.GpuEmbeddingLookup(embs[i], toks, N_PREFILL, outs[i])
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    times = []
+    name = "GatherQ4KKernel" if ggml_type == ops.GGML_Q4_K else "GatherQ6KKernel"
+    ops.profile_start(reps)
     for r in range(reps):
-        a = torch.cuda.Event(enable_timing=True)
-        b = torch.cuda.Event(enable_timing=True)
-        a.record(stream)
         ops.GpuEmbeddingLookup(embs[r % copies], toks, N_PREFILL, outs[r % copies])
-        b.record(stream)
-        times.append((a, b))
-    torch.cuda.synchronize()
-    ms = sorted(a.elapsed_time(b) for a, b in times)
-    med = ms[len(ms) // 2]
+    ops.profile_stop()
+    rep = ops.profile_report()[name]
+    avg_ms = rep["avg_us"] * 1e-3
     nbytes = bytes_gather(N_PREFILL, bb)
     del tables, outs
-    return {"us": round(med * 1e3, 2), "GBps": round(nbytes / (med * 1e-3) / 1e9, 1), "bytes": nbytes}
+    return {"us": round(avg_ms * 1e3, 2), "GBps": round(nbytes / (avg_ms * 1e-3) / 1e9, 1), "bytes": nbytes,
+            "kernel": name, "launches": rep["count"]}
 
 
 def measure_copy(torch, ops, nbytes=1 << 30, reps=10):
@@ -218,7 +218,8 @@ def measure_copy(torch, ops, nbytes=1 << 30, reps=10):
 
 
 def profile_traffic(kernel_tag):
-    """HBM bytes per launch of `kernel_tag` from the committed rocprofv3 counter summary, if any."""
+    """HBM bytes per launch of `kernel_tag` from the committed rocprofv3 counter summary
+    (FETCH_SIZE + WRITE_SIZE, each scaled by the calibration copy), if present."""
     path = os.path.join(REPO, "profiles", "pmc_traffic_prefill_n2811.md")
     if not os.path.exists(path):
         return None
@@ -277,17 +278,20 @@ def main():
     layers = [Layer(torch, N_PREFILL, gen) for _ in range(LAYERS)]
     torch.cuda.synchronize()
     log(f"timing {args.steps} steps after {args.warmup} warmup")
-    ms_step, per = timed_prefill(torch, ops, layers, tab, N_PREFILL, args.steps, args.warmup)
+    ms_step, ms_prof, report = timed_prefill(torch, ops, layers, tab, N_PREFILL, args.steps, args.warmup)
+    log(f"ms/step {ms_step:.4f} ({ms_prof:.4f} with launch profiling); kernels: {json.dumps(report)}")
     step_bytes = LAYERS * (bytes_add_rms(N_PREFILL) + bytes_qk(N_PREFILL) + bytes_swiglu(N_PREFILL))
     value = step_bytes / (ms_step * 1e-3) / 1e9
     op_bytes = {"add_rms_norm": bytes_add_rms(N_PREFILL), "qk_norm_rope_kv": bytes_qk(N_PREFILL),
                 "swiglu": bytes_swiglu(N_PREFILL)}
     op_stats = {}
     for name in OP_NAMES:
-        avg = sum(per[name]) / len(per[name])
-        op_stats[name] = {"us": round(avg * 1e3, 2), "GBps": round(op_bytes[name] / (avg * 1e-3) / 1e9, 1),
-                          "pct_peak": round(op_bytes[name] / (avg * 1e-3) / 1e9 / PEAK_GBPS * 100, 1),
-                          "bytes": op_bytes[name], "kernel": KERNEL_NAMES[name]}
+        k = report[KERNEL_NAMES[name]]
+        assert k["count"] == args.steps * LAYERS, (name, k)
+        avg_s = k["avg_us"] * 1e-6
+        op_stats[name] = {"us": round(k["avg_us"], 2), "GBps": round(op_bytes[name] / avg_s / 1e9, 1),
+                          "pct_peak": round(op_bytes[name] / avg_s / 1e9 / PEAK_GBPS * 100, 1),
+                          "bytes": op_bytes[name], "kernel": KERNEL_NAMES[name], "launches": k["count"]}
     dominant = max(OP_NAMES, key=lambda k: op_stats[k]["us"])
     d_avg_s = op_stats[dominant]["us"] * 1e-6
     achieved = op_bytes[dominant] / d_avg_s / 1e9
@@ -296,6 +300,16 @@ def main():
                 "kernel": KERNEL_NAMES[dominant], "algorithmic_bytes_per_launch": op_bytes[dominant]}
     del layers
     torch.cuda.empty_cache()
+
+    # Calibration dispatch for the rocprofv3 counter runs: one StreamCopyKernel of
+    # exactly CALIB_BYTES read + CALIB_BYTES written, whose FETCH_SIZE / WRITE_SIZE
+    # give the counters' scale against known traffic.
+    calib_src = torch.empty(CALIB_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    calib_dst = torch.empty_like(calib_src)
+    torch.cuda.synchronize()
+    ops.GpuStreamCopy(calib_src, calib_dst, CALIB_BYTES)
+    torch.cuda.synchronize()
+    del calib_src, calib_dst
 
     extras = {}
     if not args.no_extras:
@@ -316,6 +330,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
+        "ms_per_step_profiled_pass": round(ms_prof, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,

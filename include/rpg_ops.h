@@ -144,6 +144,17 @@ RPG_OPS_API int32_t rpg_op_stream_copy(const void* src, void* dst, int64_t bytes
  * Replaces: F16SweepKernel, tools/dequant_check.cu:44-48. */
 RPG_OPS_API int32_t rpg_op_f16_sweep(float* out_dev);
 
+/* Kernel-execution timing: after rpg_ops_profile_start(n), each of the next n
+ * launches (outside graph capture) carries a HIP start/stop event pair attached
+ * to its dispatch. rpg_ops_profile_report synchronises on the last launch and
+ * writes per-kernel JSON {"<kernel>": {"count", "avg_us", "min_us", "max_us",
+ * "total_us"}} into buf; it returns the length of the JSON (which may exceed
+ * cap-1, then the text is truncated) or a negative status. Takes the place of
+ * the reference's host-clock timing in tools/matmul_bench.cu:45-49,114-133. */
+RPG_OPS_API int32_t rpg_ops_profile_start(int32_t max_launches);
+RPG_OPS_API int32_t rpg_ops_profile_stop(void);
+RPG_OPS_API int32_t rpg_ops_profile_report(char* buf, int32_t cap);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

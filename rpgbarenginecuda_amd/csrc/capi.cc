@@ -137,4 +137,24 @@ int32_t rpg_op_f16_sweep(float* out_dev) {
   return Guard([&] { rpg::GpuF16Sweep(out_dev); });
 }
 
+int32_t rpg_ops_profile_start(int32_t max_launches) {
+  return Guard([&] { rpg::ProfileStart(max_launches); });
+}
+
+int32_t rpg_ops_profile_stop(void) {
+  return Guard([] { rpg::ProfileStop(); });
+}
+
+int32_t rpg_ops_profile_report(char* buf, int32_t cap) {
+  int32_t len = 0;
+  const int32_t rc = Guard([&] {
+    RPG_CHECK(buf != nullptr && cap > 0, "profile_report needs a buffer");
+    const std::string s = rpg::ProfileReport();
+    std::strncpy(buf, s.c_str(), static_cast<size_t>(cap) - 1);
+    buf[cap - 1] = '\0';
+    len = static_cast<int32_t>(s.size());
+  });
+  return rc < 0 ? rc : len;
+}
+
 }  // extern "C"

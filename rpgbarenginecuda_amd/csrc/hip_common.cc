@@ -3,9 +3,12 @@
 
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstdio>
 #include <string>
+#include <utility>
+#include <vector>
 
 namespace rpg {
 
@@ -196,6 +199,83 @@ int64_t* StagePos0Cached(int64_t pos) {
   if (StreamIsCapturing()) return dev;
   if (g_pos_last != pos) StagePos0(pos);
   return dev;
+}
+
+// ---------------------------------------------------------------- launch profiling
+
+namespace {
+
+struct ProfileState {
+  std::vector<LaunchTiming> pairs;
+  std::vector<const char*> names;  // kernel names are string literals
+  size_t used = 0;
+  bool active = false;
+};
+
+ProfileState& Prof() {
+  static ProfileState s;  // never destroyed before the runtime: events are leaked at exit on purpose
+  return s;
+}
+
+}  // namespace
+
+void ProfileStart(int max_launches) {
+  RPG_CHECK(max_launches > 0 && max_launches <= (1 << 20), "profile capacity %d out of range", max_launches);
+  ProfileState& s = Prof();
+  while (s.pairs.size() < static_cast<size_t>(max_launches)) {
+    LaunchTiming t{};
+    RPG_HIP_CHECK(hipEventCreate(&t.start));
+    RPG_HIP_CHECK(hipEventCreate(&t.stop));
+    s.pairs.push_back(t);
+  }
+  s.names.assign(static_cast<size_t>(max_launches), nullptr);
+  s.used = 0;
+  s.active = true;
+}
+
+void ProfileStop() { Prof().active = false; }
+
+const LaunchTiming* NextLaunchTiming(const char* kernel_name) {
+  ProfileState& s = Prof();
+  if (!s.active || s.used >= s.names.size()) return nullptr;
+  if (StreamIsCapturing()) return nullptr;
+  s.names[s.used] = kernel_name;
+  return &s.pairs[s.used++];
+}
+
+std::string ProfileReport() {
+  ProfileState& s = Prof();
+  struct Agg {
+    int count = 0;
+    double total = 0, mn = 1e30, mx = 0;
+  };
+  std::vector<std::pair<std::string, Agg>> aggs;
+  if (s.used > 0) RPG_HIP_CHECK(hipEventSynchronize(s.pairs[s.used - 1].stop));
+  for (size_t i = 0; i < s.used; ++i) {
+    float ms = 0.f;
+    RPG_HIP_CHECK(hipEventElapsedTime(&ms, s.pairs[i].start, s.pairs[i].stop));
+    const double us = 1e3 * static_cast<double>(ms);
+    auto it = std::find_if(aggs.begin(), aggs.end(), [&](const auto& a) { return a.first == s.names[i]; });
+    if (it == aggs.end()) {
+      aggs.emplace_back(s.names[i], Agg{});
+      it = aggs.end() - 1;
+    }
+    Agg& a = it->second;
+    ++a.count;
+    a.total += us;
+    a.mn = std::min(a.mn, us);
+    a.mx = std::max(a.mx, us);
+  }
+  std::string out = "{";
+  char buf[320];
+  for (size_t i = 0; i < aggs.size(); ++i) {
+    const Agg& a = aggs[i].second;
+    std::snprintf(buf, sizeof(buf),
+                  "%s\"%s\": {\"count\": %d, \"avg_us\": %.4f, \"min_us\": %.4f, \"max_us\": %.4f, \"total_us\": %.4f}",
+                  i ? ", " : "", aggs[i].first.c_str(), a.count, a.total / a.count, a.mn, a.mx, a.total);
+    out += buf;
+  }
+  return out + "}";
 }
 
 Pos0Arg Pos0ForLaunch(int64_t pos0) {

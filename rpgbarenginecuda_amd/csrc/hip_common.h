@@ -144,6 +144,25 @@ struct Pos0Arg {
 };
 Pos0Arg Pos0ForLaunch(int64_t pos0);
 
+// ---------------------------------------------------------------- launch profiling
+//
+// Kernel-execution timing with HIP events attached to the dispatches
+// (hipExtLaunchKernel). ProfileStart(n) creates n event pairs (allocation
+// happens here, never during the timed launches); each launch while active
+// takes the next pair, until n are used. ProfileReport synchronises on the last
+// event and returns per-kernel counts and durations as JSON:
+//   {"<kernel>": {"count": c, "avg_us": a, "min_us": m, "max_us": M, "total_us": t}, ...}
+struct LaunchTiming {
+  hipEvent_t start;
+  hipEvent_t stop;
+};
+void ProfileStart(int max_launches);
+void ProfileStop();
+std::string ProfileReport();
+// Event pair for the next launch of `kernel_name`, or nullptr when profiling
+// is off, exhausted, or the engine stream is being captured.
+const LaunchTiming* NextLaunchTiming(const char* kernel_name);
+
 }  // namespace rpg
 
 #endif  // RPG_AMD_HIP_COMMON_H_

@@ -24,12 +24,13 @@
 
 #include "dev_util.h"
 #include "kernels_gpu.h"
+#include "launch.h"
 
 namespace rpg {
 namespace {
 
 using dev::HalfBitsToFloat;
-using dev::Store4;
+using dev::StoreStream4;
 
 constexpr int kBlock = 256;
 
@@ -75,8 +76,8 @@ __device__ __forceinline__ void DecodeQ4KLane(const uint8_t* blk, int j, float* 
     lo[b] = d1 * static_cast<float>((qw >> (8 * b)) & 0xFu) - n1;
     hi[b] = d2 * static_cast<float>((qw >> (8 * b + 4)) & 0xFu) - n2;
   }
-  Store4(out_blk + 64 * g + 4 * kq, make_float4(lo[0], lo[1], lo[2], lo[3]));
-  Store4(out_blk + 64 * g + 32 + 4 * kq, make_float4(hi[0], hi[1], hi[2], hi[3]));
+  StoreStream4(out_blk + 64 * g + 4 * kq, make_float4(lo[0], lo[1], lo[2], lo[3]));
+  StoreStream4(out_blk + 64 * g + 32 + 4 * kq, make_float4(hi[0], hi[1], hi[2], hi[3]));
 }
 
 __device__ __forceinline__ uint32_t Load4Bytes2Aligned(const uint8_t* p) {
@@ -110,7 +111,7 @@ __device__ __forceinline__ void DecodeQ6KLane(const uint8_t* blk, int j, float* 
       const int q = static_cast<int>(nib | (hi2 << 4)) - 32;
       y[b] = ds * static_cast<float>(q);
     }
-    Store4(out_blk + 128 * half + 32 * quarter + 4 * kq, make_float4(y[0], y[1], y[2], y[3]));
+    StoreStream4(out_blk + 128 * half + 32 * quarter + 4 * kq, make_float4(y[0], y[1], y[2], y[3]));
   }
 }
 
@@ -148,7 +149,7 @@ __global__ __launch_bounds__(kBlock) void GatherBlocksKernel(const uint8_t* __re
   if (tok < 0 || tok >= rows) {
     constexpr int kPerLane = static_cast<int>(kQK_K) / T::kLanes;
 #pragma unroll
-    for (int e = 0; e < kPerLane; e += 4) Store4(out + j * kPerLane + e, make_float4(0.f, 0.f, 0.f, 0.f));
+    for (int e = 0; e < kPerLane; e += 4) StoreStream4(out + j * kPerLane + e, make_float4(0.f, 0.f, 0.f, 0.f));
     return;
   }
   T::Decode(emb + tok * row_bytes + b * T::kBytes, j, out);
@@ -166,7 +167,7 @@ __global__ __launch_bounds__(kBlock) void GatherF32Kernel(const float* __restric
   const int64_t tok = toks != nullptr ? static_cast<int64_t>(toks[t]) : 0;
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
   if (tok >= 0 && tok < rows) v = dev::Load4(emb + tok * cols + e);
-  Store4(x + i, v);
+  StoreStream4(x + i, v);
 }
 
 // Per-element fallback for any alignment: element i of the gathered output.
@@ -247,29 +248,25 @@ void LaunchGather(uint32_t type, const uint8_t* emb, int64_t rows, int64_t cols,
   if (type == kGgmlQ4_K && Aligned(emb, 16) && Aligned(x, 16)) {
     const int32_t nb = static_cast<int32_t>(cols / kQK_K);
     const int64_t units = seq * nb;
-    GatherBlocksKernel<kGgmlQ4_K><<<GridFor(units, kBlock / 32), kBlock, 0, EngineStream()>>>(
-        emb, rows, row_bytes, nb, toks, units, x);
-    CheckLaunch("GatherBlocksKernel<Q4_K>");
+    Launch("GatherQ4KKernel", GatherBlocksKernel<kGgmlQ4_K>, dim3(GridFor(units, kBlock / 32)), dim3(kBlock), emb,
+           rows, row_bytes, nb, toks, units, x);
     return;
   }
   if (type == kGgmlQ6_K && Aligned(emb, 2) && Aligned(x, 16)) {
     const int32_t nb = static_cast<int32_t>(cols / kQK_K);
     const int64_t units = seq * nb;
-    GatherBlocksKernel<kGgmlQ6_K><<<GridFor(units, kBlock / 16), kBlock, 0, EngineStream()>>>(
-        emb, rows, row_bytes, nb, toks, units, x);
-    CheckLaunch("GatherBlocksKernel<Q6_K>");
+    Launch("GatherQ6KKernel", GatherBlocksKernel<kGgmlQ6_K>, dim3(GridFor(units, kBlock / 16)), dim3(kBlock), emb,
+           rows, row_bytes, nb, toks, units, x);
     return;
   }
   if (type == kGgmlF32 && cols % 4 == 0 && Aligned(emb, 16) && Aligned(x, 16)) {
     const int64_t total4 = total / 4;
-    GatherF32Kernel<<<GridFor(total4, kBlock), kBlock, 0, EngineStream()>>>(
-        reinterpret_cast<const float*>(emb), rows, cols, toks, total4, x);
-    CheckLaunch("GatherF32Kernel");
+    Launch("GatherF32Kernel", GatherF32Kernel, dim3(GridFor(total4, kBlock)), dim3(kBlock),
+           reinterpret_cast<const float*>(emb), rows, cols, toks, total4, x);
     return;
   }
-  GatherElemKernel<<<GridFor(total, kBlock), kBlock, 0, EngineStream()>>>(type, emb, rows, cols, row_bytes, bs.elems,
-                                                                          bs.bytes, toks, total, x);
-  CheckLaunch("GatherElemKernel");
+  Launch("GatherElemKernel", GatherElemKernel, dim3(GridFor(total, kBlock)), dim3(kBlock), type, emb, rows, cols,
+         row_bytes, bs.elems, bs.bytes, toks, total, x);
 }
 
 }  // namespace
@@ -301,8 +298,7 @@ void GpuEmbeddingLookup(const GpuTensor& emb, const int32_t* toks_dev, int64_t s
 
 void GpuF16Sweep(float* out_dev) {
   RPG_CHECK(out_dev != nullptr, "F16Sweep got a null pointer");
-  F16SweepKernel<<<65536 / kBlock, kBlock, 0, EngineStream()>>>(out_dev);
-  CheckLaunch("F16SweepKernel");
+  Launch("F16SweepKernel", F16SweepKernel, dim3(65536 / kBlock), dim3(kBlock), out_dev);
 }
 
 }  // namespace rpg

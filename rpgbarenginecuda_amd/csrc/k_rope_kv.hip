@@ -25,16 +25,19 @@
 
 #include "dev_util.h"
 #include "kernels_gpu.h"
+#include "launch.h"
 
 namespace rpg {
 namespace {
 
 using dev::AddSquares;
 using dev::Load4;
+using dev::LoadStream4;
 using dev::PackHalf4;
 using dev::RmsScale;
 using dev::ScaleMul;
-using dev::Store4;
+using dev::StoreStream4;
+using dev::StoreStreamHalf4;
 
 constexpr int kBlock = 256;
 constexpr int kHeadDim = 128;
@@ -66,11 +69,11 @@ __global__ __launch_bounds__(kBlock) void RopeHead128Kernel(float* x, int32_t n_
   const int64_t row = unit / n_heads;
   const float* cs = tab + (ReadPos0(pos0_val, pos0_dev) + row) * kHeadDim;
   float* p = x + unit * kHeadDim;
-  float4 a = Load4(p + 4 * l);
-  float4 b = Load4(p + 64 + 4 * l);
+  float4 a = LoadStream4(p + 4 * l);
+  float4 b = LoadStream4(p + 64 + 4 * l);
   Rotate(a, b, Load4(cs + 4 * l), Load4(cs + 64 + 4 * l));
-  Store4(p + 4 * l, a);
-  Store4(p + 64 + 4 * l, b);
+  StoreStream4(p + 4 * l, a);
+  StoreStream4(p + 64 + 4 * l, b);
 }
 
 // Any even head_dim: one thread per rotation pair.
@@ -114,8 +117,8 @@ __global__ __launch_bounds__(kBlock) void KvWriteVec4Kernel(const float* __restr
   const int64_t pos = ReadPos0(pos0_val, pos0_dev) + t;
   if (pos < 0 || pos >= max_seq) return;  // only reachable through a replayed graph with a bad staged pos0
   const int64_t dst = (h * max_seq + pos) * head_dim + dd;
-  *reinterpret_cast<uint2*>(kc + dst) = PackHalf4(Load4(k + i));
-  *reinterpret_cast<uint2*>(vc + dst) = PackHalf4(Load4(v + i));
+  StoreStreamHalf4(kc + dst, PackHalf4(LoadStream4(k + i)));
+  StoreStreamHalf4(vc + dst, PackHalf4(LoadStream4(v + i)));
 }
 
 __global__ __launch_bounds__(kBlock) void KvWriteScalarKernel(const float* __restrict__ k, const float* __restrict__ v,
@@ -162,8 +165,8 @@ __global__ __launch_bounds__(kBlock) void QkNormRopeKvKernel(
     float* p = is_q ? q + (static_cast<int64_t>(t) * n_heads + h) * kHeadDim
                     : k + (static_cast<int64_t>(t) * n_kv + h) * kHeadDim;
     const float* w = is_q ? qw : kw;
-    float4 a = Load4(p + 4 * l);
-    float4 b = Load4(p + 64 + 4 * l);
+    float4 a = LoadStream4(p + 4 * l);
+    float4 b = LoadStream4(p + 64 + 4 * l);
     double ss = AddSquares(AddSquares(0.0, a), b);
     ss = dev::GroupSum<16>(ss);
     const float scale = RmsScale(ss, kHeadDim, eps);
@@ -174,23 +177,23 @@ __global__ __launch_bounds__(kBlock) void QkNormRopeKvKernel(
       Rotate(a, b, Load4(cs + 4 * l), Load4(cs + 64 + 4 * l));
     }
     if (is_q || kWriteK) {
-      Store4(p + 4 * l, a);
-      Store4(p + 64 + 4 * l, b);
+      StoreStream4(p + 4 * l, a);
+      StoreStream4(p + 64 + 4 * l, b);
     }
     if (!is_q && kv_slot_ok) {
       uint16_t* dst = kc + (static_cast<int64_t>(h) * max_seq + pos) * kHeadDim;
-      *reinterpret_cast<uint2*>(dst + 4 * l) = PackHalf4(a);
-      *reinterpret_cast<uint2*>(dst + 64 + 4 * l) = PackHalf4(b);
+      StoreStreamHalf4(dst + 4 * l, PackHalf4(a));
+      StoreStreamHalf4(dst + 64 + 4 * l, PackHalf4(b));
     }
   } else {
     const int32_t h = j - n_heads - n_kv;
     const float* p = v + (static_cast<int64_t>(t) * n_kv + h) * kHeadDim;
-    const float4 a = Load4(p + 4 * l);
-    const float4 b = Load4(p + 64 + 4 * l);
+    const float4 a = LoadStream4(p + 4 * l);
+    const float4 b = LoadStream4(p + 64 + 4 * l);
     if (kv_slot_ok) {
       uint16_t* dst = vc + (static_cast<int64_t>(h) * max_seq + pos) * kHeadDim;
-      *reinterpret_cast<uint2*>(dst + 4 * l) = PackHalf4(a);
-      *reinterpret_cast<uint2*>(dst + 64 + 4 * l) = PackHalf4(b);
+      StoreStreamHalf4(dst + 4 * l, PackHalf4(a));
+      StoreStreamHalf4(dst + 64 + 4 * l, PackHalf4(b));
     }
   }
 }
@@ -206,15 +209,13 @@ void GpuRope(float* x, int32_t n_heads, int32_t head_dim, const float* rope_tab,
   const Pos0Arg p0 = Pos0ForLaunch(pos0);
   if (head_dim == kHeadDim && Aligned(x, 16) && Aligned(rope_tab, 16)) {
     const int64_t units = n_rows * n_heads;
-    RopeHead128Kernel<<<GridFor(units, kBlock / 16), kBlock, 0, EngineStream()>>>(x, n_heads, rope_tab, p0.value,
-                                                                                  p0.dev, units);
-    CheckLaunch("RopeHead128Kernel");
+    Launch("RopeHead128Kernel", RopeHead128Kernel, dim3(GridFor(units, kBlock / 16)), dim3(kBlock), x, n_heads,
+           rope_tab, p0.value, p0.dev, units);
     return;
   }
   const int64_t total = n_rows * n_heads * (head_dim / 2);
-  RopePairKernel<<<GridFor(total, kBlock), kBlock, 0, EngineStream()>>>(x, n_heads, head_dim, rope_tab, p0.value,
-                                                                        p0.dev, total);
-  CheckLaunch("RopePairKernel");
+  Launch("RopePairKernel", RopePairKernel, dim3(GridFor(total, kBlock)), dim3(kBlock), x, n_heads, head_dim, rope_tab,
+         p0.value, p0.dev, total);
 }
 
 void GpuKvWrite(const float* k_dev, const float* v_dev, int32_t n_kv_heads, int32_t head_dim, int64_t pos0,
@@ -230,14 +231,12 @@ void GpuKvWrite(const float* k_dev, const float* v_dev, int32_t n_kv_heads, int3
   if (head_dim % 4 == 0 && Aligned(k_dev, 16) && Aligned(v_dev, 16) && Aligned(k_cache_layer, 8) &&
       Aligned(v_cache_layer, 8)) {
     const int64_t total4 = total / 4;
-    KvWriteVec4Kernel<<<GridFor(total4, kBlock), kBlock, 0, EngineStream()>>>(
-        k_dev, v_dev, n_kv_heads, head_dim, p0.value, p0.dev, max_seq, total4, k_cache_layer, v_cache_layer);
-    CheckLaunch("KvWriteVec4Kernel");
+    Launch("KvWriteVec4Kernel", KvWriteVec4Kernel, dim3(GridFor(total4, kBlock)), dim3(kBlock), k_dev, v_dev,
+           n_kv_heads, head_dim, p0.value, p0.dev, max_seq, total4, k_cache_layer, v_cache_layer);
     return;
   }
-  KvWriteScalarKernel<<<GridFor(total, kBlock), kBlock, 0, EngineStream()>>>(
-      k_dev, v_dev, n_kv_heads, head_dim, p0.value, p0.dev, max_seq, total, k_cache_layer, v_cache_layer);
-  CheckLaunch("KvWriteScalarKernel");
+  Launch("KvWriteScalarKernel", KvWriteScalarKernel, dim3(GridFor(total, kBlock)), dim3(kBlock), k_dev, v_dev,
+         n_kv_heads, head_dim, p0.value, p0.dev, max_seq, total, k_cache_layer, v_cache_layer);
 }
 
 void GpuQkNormRopeKv(float* q, float* k, const float* v, const float* q_norm, const float* k_norm, int32_t n_heads,
@@ -269,16 +268,10 @@ void GpuQkNormRopeKv(float* q, float* k, const float* v, const float* q_norm, co
   }
   const Pos0Arg p0 = Pos0ForLaunch(pos0);
   const unsigned grid = GridFor(units, kBlock / 16);
-  if (write_k_f32) {
-    QkNormRopeKvKernel<true><<<grid, kBlock, 0, EngineStream()>>>(
-        q, k, v, q_norm, k_norm, n_heads, n_kv_heads, rope_tab, rope_rows, p0.value, p0.dev,
-        static_cast<uint32_t>(units), eps, k_cache_layer, v_cache_layer, max_seq);
-  } else {
-    QkNormRopeKvKernel<false><<<grid, kBlock, 0, EngineStream()>>>(
-        q, k, v, q_norm, k_norm, n_heads, n_kv_heads, rope_tab, rope_rows, p0.value, p0.dev,
-        static_cast<uint32_t>(units), eps, k_cache_layer, v_cache_layer, max_seq);
-  }
-  CheckLaunch("QkNormRopeKvKernel");
+  Launch(write_k_f32 ? "QkNormRopeKvKernel<write_k>" : "QkNormRopeKvKernel",
+         write_k_f32 ? QkNormRopeKvKernel<true> : QkNormRopeKvKernel<false>, dim3(grid), dim3(kBlock), q, k, v, q_norm,
+         k_norm, n_heads, n_kv_heads, rope_tab, rope_rows, p0.value, p0.dev, static_cast<uint32_t>(units), eps,
+         k_cache_layer, v_cache_layer, max_seq);
 }
 
 }  // namespace rpg

@@ -51,6 +51,9 @@ SIGNATURES = {
                                       _vp, _vp, _i64, _i32]),
     "rpg_op_stream_copy": (_i32, [_vp, _vp, _i64]),
     "rpg_op_f16_sweep": (_i32, [_vp]),
+    "rpg_ops_profile_start": (_i32, [_i32]),
+    "rpg_ops_profile_stop": (_i32, []),
+    "rpg_ops_profile_report": (_i32, [ctypes.c_char_p, _i32]),
 }
 
 
@@ -281,6 +284,28 @@ def GpuQkNormRopeKv(q, k, v, q_norm, k_norm, n_heads: int, n_kv_heads: int, head
 
 def GpuStreamCopy(src, dst, nbytes: int) -> None:
     _check(load_library().rpg_op_stream_copy(_addr(src, nbytes, name="src"), _addr(dst, nbytes, name="dst"), nbytes))
+
+
+def profile_start(max_launches: int) -> None:
+    """Times the next `max_launches` kernel launches with dispatch-attached HIP events."""
+    _check(load_library().rpg_ops_profile_start(int(max_launches)))
+
+
+def profile_stop() -> None:
+    _check(load_library().rpg_ops_profile_stop())
+
+
+def profile_report() -> dict:
+    """Per-kernel {count, avg_us, min_us, max_us, total_us} of the profiled launches."""
+    import json
+
+    cap = 1 << 16
+    while True:
+        buf = ctypes.create_string_buffer(cap)
+        n = _check(load_library().rpg_ops_profile_report(buf, cap))
+        if n < cap:
+            return json.loads(buf.value.decode())
+        cap = n + 1
 
 
 def GpuF16Sweep(out) -> None:
