@@ -1,6 +1,6 @@
 """Benchmark of the fused Qwen3 layer operators on one MI355X.
 
-Headline workload (BASELINE configs[3]): prefill n = 2811 at Qwen3-1.7B shape
+Headline workload: prefill n = 2811 at Qwen3-1.7B shape
 (H = 2048, 16 q heads, 8 kv heads, head_dim 128, I = 6144), all 28 layers, each
 layer with its own seeded buffers and weights. One step = for every layer:
   residual add + RMSNorm      [n, H]              (rpg_op_add_rms_norm)

@@ -1,7 +1,7 @@
-"""Seeded synthetic inputs shaped like the BASELINE configs (test infrastructure).
+"""Seeded synthetic inputs shaped like the benchmark configurations (test infrastructure).
 
 All generators take a numpy Generator so a test's seed fixes its inputs.
-Q4_K / Q6_K tables follow the BASELINE's description of the synthetic token_embd:
+Q4_K / Q6_K tables follow the benchmark's description of the synthetic token_embd:
   Q4_K: d, dmin = fp16_rne(|N(0, 0.01)|); the 12 packed scale bytes uniform
         (every unpacked 6-bit scale/min uniform over 0..63); qs uniform bytes.
   Q6_K: d = fp16_rne(|N(0, 0.01)|); scales int8 uniform over -32..31; ql / qh

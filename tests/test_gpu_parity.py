@@ -5,7 +5,7 @@ Bars (written into each test):
   * RMSNorm, RoPE, SwiGLU: |gpu - ref| <= 1e-6 + 1e-5 * |ref| against the float64
     restatement, and (where the op order is the same) near-identical to the fp32
     oracle.
-Sizes are the BASELINE configs (Qwen3-1.7B / 4B shapes, n = 1, 21, 2811, 4096)
+Sizes are the benchmark's configurations (Qwen3-1.7B / 4B shapes, n = 1, 21, 2811, 4096)
 plus ragged / unaligned / edge cases. Every case prints its name before launching.
 """
 from __future__ import annotations
@@ -95,7 +95,7 @@ def test_dequant_row_random_and_unaligned(gpu, ora, t, offset):
 
 @pytest.mark.parametrize("t", [12, 14])
 def test_embedding_gather_full_table(gpu, ora, t):
-    """token_embd [151936, 2048], 2811 uniform ids, bit-exact."""
+    """The gather configuration: token_embd [151936, 2048], 2811 uniform ids, bit-exact."""
     import torch
 
     rows, cols, seq = 151936, 2048, 2811
@@ -276,7 +276,7 @@ def test_rope(gpu, ora, rows, heads, head_dim, pos0):
 
 
 QK_CASES = [
-    # (name, Hq, Hkv, seq, pos0) -- BASELINE configs 1, 3, 4, 5
+    # (name, Hq, Hkv, seq, pos0): the n = 21, decode, n = 2811 and 4B n = 4096 configurations
     ("1.7B n=21", 16, 8, 21, 0),
     ("1.7B decode n=1", 16, 8, 1, 2731),
     ("1.7B prefill n=2811", 16, 8, 2811, 0),
