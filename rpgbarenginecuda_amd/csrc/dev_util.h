@@ -51,6 +51,21 @@ __device__ __forceinline__ float RmsScale(double ss, int64_t n, float eps) {
   return static_cast<float>(1.0 / sqrt(mean + static_cast<double>(eps)));
 }
 
+// The same scale for 128-element head rows, with 1/sqrt computed as the hardware
+// reciprocal square root (v_rsq_f64) refined by two Newton-Raphson steps in
+// double: accurate to a few double ulps, so the value cast to fp32 equals the
+// correctly rounded one except when the exact result lies within ~2^-50 of an
+// fp32 rounding boundary. It replaces a double sqrt and a double division (about
+// 30 fp64 instructions per row), which at 24 head rows per token is a visible
+// share of the fused q/k kernel's issue slots. ss/128 is exact (power of two).
+__device__ __forceinline__ float HeadRmsScale(double ss, float eps) {
+  const double x = ss * (1.0 / 128.0) + static_cast<double>(eps);
+  double y = __builtin_amdgcn_rsq(x);
+  y = y * (1.5 - 0.5 * x * y * y);
+  y = y * (1.5 - 0.5 * x * y * y);
+  return static_cast<float>(__builtin_isinf(x) ? 0.0 : y);  // 1/sqrt(inf) = 0, as the division would give
+}
+
 // (v * scale) * w per component, left to right as the reference writes
 // `xr[i] * scale * w[i]` (src/kernels_gpu.cu:589).
 __device__ __forceinline__ float4 ScaleMul(float4 v, float scale, float4 w) {

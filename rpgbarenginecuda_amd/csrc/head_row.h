@@ -1,0 +1,92 @@
+// One 128-element attention head row spread over 8 lanes of a wave64.
+//
+// Lane l (0..7) owns the float4 chunks at elements 4l and 32+4l of the first
+// half (a[0], a[1]) and the same offsets + 64 in the second half (b[0], b[1]).
+// Both members of every NeoX RoPE pair (i, i+64) therefore sit in the same lane,
+// and the row's sum of squares is a 3-step butterfly inside the aligned 8-lane
+// group. Measured on MI355X for the fused q/k kernel at n = 2811: 8 lanes with
+// 4 float4 each beat 16 lanes with 2 (more loads in flight per lane, half the
+// waves, half the per-row scalar work) and 4 or 2 lanes (too few waves).
+//
+// The standalone head RMSNorm, the standalone RoPE and the fused q/k kernel all
+// use these routines, so the fused and unfused paths give identical bits.
+#ifndef RPG_AMD_HEAD_ROW_H_
+#define RPG_AMD_HEAD_ROW_H_
+
+#include "dev_util.h"
+
+namespace rpg {
+namespace dev {
+
+constexpr int kHeadLanes = 8;
+
+struct HeadRow {
+  float4 a[2];  // first half: elements 4l.. and 32+4l..
+  float4 b[2];  // second half: the same offsets + 64
+};
+
+__device__ __forceinline__ int HeadOffset(int l, int c) { return 4 * l + 32 * c; }
+
+__device__ __forceinline__ HeadRow LoadHeadRowStream(const float* p, int l) {
+  HeadRow r;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    r.a[c] = LoadStream4(p + HeadOffset(l, c));
+    r.b[c] = LoadStream4(p + 64 + HeadOffset(l, c));
+  }
+  return r;
+}
+
+__device__ __forceinline__ void StoreHeadRowStream(float* p, int l, const HeadRow& r) {
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    StoreStream4(p + HeadOffset(l, c), r.a[c]);
+    StoreStream4(p + 64 + HeadOffset(l, c), r.b[c]);
+  }
+}
+
+// fp16 (IEEE round-to-nearest-even) copy of the row, 8-byte stores. Plain stores
+// measured slightly faster than nontemporal ones for the scattered 256-byte cache rows.
+__device__ __forceinline__ void StoreHeadRowHalf(uint16_t* p, int l, const HeadRow& r) {
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    *reinterpret_cast<uint2*>(p + HeadOffset(l, c)) = PackHalf4(r.a[c]);
+    *reinterpret_cast<uint2*>(p + 64 + HeadOffset(l, c)) = PackHalf4(r.b[c]);
+  }
+}
+
+// RMSNorm of the row with weight w[128]: sum of squares in double (order a0, b0,
+// a1, b1 per lane, then the 8-lane butterfly), HeadRmsScale, then (x*scale)*w.
+__device__ __forceinline__ void NormHeadRow(HeadRow& r, const float* __restrict__ w, int l, float eps) {
+  double ss = 0.0;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) ss = AddSquares(AddSquares(ss, r.a[c]), r.b[c]);
+  ss = GroupSum<kHeadLanes>(ss);
+  const float scale = HeadRmsScale(ss, eps);
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    r.a[c] = ScaleMul(r.a[c], scale, Load4(w + HeadOffset(l, c)));
+    r.b[c] = ScaleMul(r.b[c], scale, Load4(w + 64 + HeadOffset(l, c)));
+  }
+}
+
+// NeoX rotation with the table row cs (cos in 0..63, sin in 64..127):
+// x_i <- a*c - b*s, x_{i+64} <- b*c + a*s, each product rounded separately.
+__device__ __forceinline__ void RotateHeadRow(HeadRow& r, const float* __restrict__ cs, int l) {
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const float4 co = Load4(cs + HeadOffset(l, c));
+    const float4 si = Load4(cs + 64 + HeadOffset(l, c));
+    const float4 a = r.a[c];
+    const float4 b = r.b[c];
+    r.a[c] = make_float4(a.x * co.x - b.x * si.x, a.y * co.y - b.y * si.y, a.z * co.z - b.z * si.z,
+                         a.w * co.w - b.w * si.w);
+    r.b[c] = make_float4(b.x * co.x + a.x * si.x, b.y * co.y + a.y * si.y, b.z * co.z + a.z * si.z,
+                         b.w * co.w + a.w * si.w);
+  }
+}
+
+}  // namespace dev
+}  // namespace rpg
+
+#endif  // RPG_AMD_HEAD_ROW_H_

@@ -15,13 +15,14 @@
 //     Measured at n = 2811 x 2048 over 28 rotated layers: 5.5 TB/s for the fused
 //     add+norm vs 4.1 TB/s for a wave-per-row layout with plain accesses.
 //   * rows with n % 256 == 0 otherwise: one wave64 per row, V = n/256 float4 per lane.
-//   * head rows (n = 128): 16 lanes per row, lane L owning elements 4L..4L+3 and
-//     64+4L..64+4L+3 (the layout the RoPE fusion needs), 4-step butterfly.
+//   * head rows (n = 128): 8 lanes per row with the layout of head_row.h (the
+//     one the RoPE fusion needs), 3-step butterfly, shared with the fused kernel.
 //   * anything else (odd n, unaligned rows): a 256-thread block per row, two
 //     passes, the second re-reading the row from cache.
 #include <hip/hip_runtime.h>
 
 #include "dev_util.h"
+#include "head_row.h"
 #include "kernels_gpu.h"
 #include "launch.h"
 
@@ -146,22 +147,17 @@ __global__ __launch_bounds__(kBlock) void AddRmsNormWaveKernel(float* x, const f
   for (int c = 0; c < V; ++c) StoreStream4(out + base + 256 * c, ScaleMul(v[c], scale, Load4(wr + 256 * c)));
 }
 
-// ---------------------------------------------------------------- 16 lanes per 128-wide row
+// ---------------------------------------------------------------- 8 lanes per 128-wide row
 
+// Per-head q/k norm (n = 128): the same row routine as the fused q/k kernel.
 __global__ __launch_bounds__(kBlock) void RmsNormHeadKernel(const float* x, const float* __restrict__ w,
                                                             int64_t n_rows, int64_t stride, float eps, float* out) {
-  const int l = threadIdx.x & 15;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / 16) + (threadIdx.x >> 4);
+  const int l = threadIdx.x % dev::kHeadLanes;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / dev::kHeadLanes) + threadIdx.x / dev::kHeadLanes;
   if (row >= n_rows) return;
-  const float* xr = x + row * stride;
-  const float4 a = LoadStream4(xr + 4 * l);
-  const float4 b = LoadStream4(xr + 64 + 4 * l);
-  double ss = AddSquares(AddSquares(0.0, a), b);
-  ss = dev::GroupSum<16>(ss);
-  const float scale = RmsScale(ss, 128, eps);
-  float* orow = out + row * stride;
-  StoreStream4(orow + 4 * l, ScaleMul(a, scale, Load4(w + 4 * l)));
-  StoreStream4(orow + 64 + 4 * l, ScaleMul(b, scale, Load4(w + 64 + 4 * l)));
+  dev::HeadRow r = dev::LoadHeadRowStream(x + row * stride, l);
+  dev::NormHeadRow(r, w, l, eps);
+  dev::StoreHeadRowStream(out + row * stride, l, r);
 }
 
 // ---------------------------------------------------------------- generic fallback
@@ -272,7 +268,8 @@ void GpuRmsNorm(const float* x, const float* w, int64_t n_rows, int64_t n, int64
   RPG_CHECK(x != nullptr && w != nullptr && out != nullptr, "RmsNorm got a null pointer");
   const bool vec_ok = Aligned16(x) && Aligned16(w) && Aligned16(out) && stride % 4 == 0;
   if (vec_ok && n == 128) {
-    Launch("RmsNormHeadKernel", RmsNormHeadKernel, dim3(GridFor(n_rows, kBlock / 16)), dim3(kBlock), x, w, n_rows,
+    Launch("RmsNormHeadKernel", RmsNormHeadKernel, dim3(GridFor(n_rows, kBlock / dev::kHeadLanes)), dim3(kBlock), x,
+           w, n_rows,
            stride, eps, out);
     return;
   }

@@ -12,31 +12,28 @@
 //   Layer order (src/qwen3_gpu.cu:77-91): q/k RMSNorm, then RoPE on q and k,
 //     then the K/V cache write; V is never normalised or rotated.
 //
-// MI355X mapping for head_dim = 128: 16 lanes own one head row; lane L holds
-// elements 4L..4L+3 and 64+4L..64+4L+3 as two float4, so both members of every
-// RoPE pair sit in the same lane and the norm reduction is a 4-step butterfly
-// inside the 16-lane group. The fused kernel reads q, k, v once, writes q back
-// (fp32) and k, v as fp16 straight into the cache (each head row of the cache is
-// 256 contiguous bytes, written as two 128-byte runs of 8-byte stores).
+// MI355X mapping for head_dim = 128: 8 lanes own one head row (head_row.h), so
+// both members of every RoPE pair sit in the same lane and the norm reduction is
+// a 3-step butterfly inside the 8-lane group. The fused kernel reads q, k, v once
+// (streaming loads), writes q back (fp32) and k, v as fp16 straight into the
+// cache (each head row of the cache is 256 contiguous bytes).
 //
 // pos0 arrives by value on eager launches; a launch being captured into a graph
 // receives the staging address instead (Pos0ForLaunch) and reads it on device.
 #include <hip/hip_runtime.h>
 
 #include "dev_util.h"
+#include "head_row.h"
 #include "kernels_gpu.h"
 #include "launch.h"
 
 namespace rpg {
 namespace {
 
-using dev::AddSquares;
-using dev::Load4;
+using dev::HeadRow;
+using dev::kHeadLanes;
 using dev::LoadStream4;
 using dev::PackHalf4;
-using dev::RmsScale;
-using dev::ScaleMul;
-using dev::StoreStream4;
 using dev::StoreStreamHalf4;
 
 constexpr int kBlock = 256;
@@ -48,32 +45,19 @@ __device__ __forceinline__ int64_t ReadPos0(int64_t value, const int64_t* dev) {
   return dev != nullptr ? *dev : value;
 }
 
-// a, b are the two halves owned by a lane; c, s the matching cos / sin.
-__device__ __forceinline__ void Rotate(float4& a, float4& b, float4 c, float4 s) {
-  const float4 ra = make_float4(a.x * c.x - b.x * s.x, a.y * c.y - b.y * s.y, a.z * c.z - b.z * s.z,
-                                a.w * c.w - b.w * s.w);
-  const float4 rb = make_float4(b.x * c.x + a.x * s.x, b.y * c.y + a.y * s.y, b.z * c.z + a.z * s.z,
-                                b.w * c.w + a.w * s.w);
-  a = ra;
-  b = rb;
-}
-
 // ---------------------------------------------------------------- RoPE
 
 __global__ __launch_bounds__(kBlock) void RopeHead128Kernel(float* x, int32_t n_heads, const float* __restrict__ tab,
                                                             int64_t pos0_val, const int64_t* __restrict__ pos0_dev,
                                                             int64_t n_units) {
-  const int l = threadIdx.x & 15;
-  const int64_t unit = static_cast<int64_t>(blockIdx.x) * (kBlock / 16) + (threadIdx.x >> 4);
+  const int l = threadIdx.x % kHeadLanes;
+  const int64_t unit = static_cast<int64_t>(blockIdx.x) * (kBlock / kHeadLanes) + threadIdx.x / kHeadLanes;
   if (unit >= n_units) return;
   const int64_t row = unit / n_heads;
-  const float* cs = tab + (ReadPos0(pos0_val, pos0_dev) + row) * kHeadDim;
   float* p = x + unit * kHeadDim;
-  float4 a = LoadStream4(p + 4 * l);
-  float4 b = LoadStream4(p + 64 + 4 * l);
-  Rotate(a, b, Load4(cs + 4 * l), Load4(cs + 64 + 4 * l));
-  StoreStream4(p + 4 * l, a);
-  StoreStream4(p + 64 + 4 * l, b);
+  HeadRow r = dev::LoadHeadRowStream(p, l);
+  dev::RotateHeadRow(r, tab + (ReadPos0(pos0_val, pos0_dev) + row) * kHeadDim, l);
+  dev::StoreHeadRowStream(p, l, r);
 }
 
 // Any even head_dim: one thread per rotation pair.
@@ -142,16 +126,16 @@ __global__ __launch_bounds__(kBlock) void KvWriteScalarKernel(const float* __res
 // ---------------------------------------------------------------- fused q/k norm + RoPE + KV
 
 // Work units per token: n_heads q rows, then n_kv k rows, then n_kv v rows;
-// 16 lanes per unit, 16 units per 256-thread block. With n_heads and n_kv
-// multiples of 4 every wave handles units of a single kind.
+// 8 lanes per unit, 32 units per 256-thread block. With n_heads and n_kv
+// multiples of 8 every wave handles units of a single kind.
 template <bool kWriteK>
 __global__ __launch_bounds__(kBlock) void QkNormRopeKvKernel(
     float* q, float* k, const float* __restrict__ v, const float* __restrict__ qw, const float* __restrict__ kw,
     int32_t n_heads, int32_t n_kv, const float* __restrict__ tab, int64_t rope_rows, int64_t pos0_val,
     const int64_t* __restrict__ pos0_dev, uint32_t n_units, float eps, uint16_t* __restrict__ kc,
     uint16_t* __restrict__ vc, int64_t max_seq) {
-  const int l = threadIdx.x & 15;
-  const uint32_t unit = blockIdx.x * (kBlock / 16) + (threadIdx.x >> 4);
+  const int l = threadIdx.x % kHeadLanes;
+  const uint32_t unit = blockIdx.x * (kBlock / kHeadLanes) + threadIdx.x / kHeadLanes;
   if (unit >= n_units) return;
   const uint32_t per_tok = static_cast<uint32_t>(n_heads + 2 * n_kv);
   const uint32_t t = unit / per_tok;
@@ -164,37 +148,15 @@ __global__ __launch_bounds__(kBlock) void QkNormRopeKvKernel(
     const int32_t h = is_q ? j : j - n_heads;
     float* p = is_q ? q + (static_cast<int64_t>(t) * n_heads + h) * kHeadDim
                     : k + (static_cast<int64_t>(t) * n_kv + h) * kHeadDim;
-    const float* w = is_q ? qw : kw;
-    float4 a = LoadStream4(p + 4 * l);
-    float4 b = LoadStream4(p + 64 + 4 * l);
-    double ss = AddSquares(AddSquares(0.0, a), b);
-    ss = dev::GroupSum<16>(ss);
-    const float scale = RmsScale(ss, kHeadDim, eps);
-    a = ScaleMul(a, scale, Load4(w + 4 * l));
-    b = ScaleMul(b, scale, Load4(w + 64 + 4 * l));
-    if (pos >= 0 && pos < rope_rows) {
-      const float* cs = tab + pos * kHeadDim;
-      Rotate(a, b, Load4(cs + 4 * l), Load4(cs + 64 + 4 * l));
-    }
-    if (is_q || kWriteK) {
-      StoreStream4(p + 4 * l, a);
-      StoreStream4(p + 64 + 4 * l, b);
-    }
-    if (!is_q && kv_slot_ok) {
-      uint16_t* dst = kc + (static_cast<int64_t>(h) * max_seq + pos) * kHeadDim;
-      StoreStreamHalf4(dst + 4 * l, PackHalf4(a));
-      StoreStreamHalf4(dst + 64 + 4 * l, PackHalf4(b));
-    }
+    HeadRow r = dev::LoadHeadRowStream(p, l);
+    dev::NormHeadRow(r, is_q ? qw : kw, l, eps);
+    if (pos >= 0 && pos < rope_rows) dev::RotateHeadRow(r, tab + pos * kHeadDim, l);
+    if (is_q || kWriteK) dev::StoreHeadRowStream(p, l, r);
+    if (!is_q && kv_slot_ok) dev::StoreHeadRowHalf(kc + (static_cast<int64_t>(h) * max_seq + pos) * kHeadDim, l, r);
   } else {
     const int32_t h = j - n_heads - n_kv;
-    const float* p = v + (static_cast<int64_t>(t) * n_kv + h) * kHeadDim;
-    const float4 a = LoadStream4(p + 4 * l);
-    const float4 b = LoadStream4(p + 64 + 4 * l);
-    if (kv_slot_ok) {
-      uint16_t* dst = vc + (static_cast<int64_t>(h) * max_seq + pos) * kHeadDim;
-      StoreStreamHalf4(dst + 4 * l, PackHalf4(a));
-      StoreStreamHalf4(dst + 64 + 4 * l, PackHalf4(b));
-    }
+    const HeadRow r = dev::LoadHeadRowStream(v + (static_cast<int64_t>(t) * n_kv + h) * kHeadDim, l);
+    if (kv_slot_ok) dev::StoreHeadRowHalf(vc + (static_cast<int64_t>(h) * max_seq + pos) * kHeadDim, l, r);
   }
 }
 
@@ -209,7 +171,7 @@ void GpuRope(float* x, int32_t n_heads, int32_t head_dim, const float* rope_tab,
   const Pos0Arg p0 = Pos0ForLaunch(pos0);
   if (head_dim == kHeadDim && Aligned(x, 16) && Aligned(rope_tab, 16)) {
     const int64_t units = n_rows * n_heads;
-    Launch("RopeHead128Kernel", RopeHead128Kernel, dim3(GridFor(units, kBlock / 16)), dim3(kBlock), x, n_heads,
+    Launch("RopeHead128Kernel", RopeHead128Kernel, dim3(GridFor(units, kBlock / kHeadLanes)), dim3(kBlock), x, n_heads,
            rope_tab, p0.value, p0.dev, units);
     return;
   }
@@ -267,7 +229,7 @@ void GpuQkNormRopeKv(float* q, float* k, const float* v, const float* q_norm, co
     return;
   }
   const Pos0Arg p0 = Pos0ForLaunch(pos0);
-  const unsigned grid = GridFor(units, kBlock / 16);
+  const unsigned grid = GridFor(units, kBlock / kHeadLanes);
   Launch(write_k_f32 ? "QkNormRopeKvKernel<write_k>" : "QkNormRopeKvKernel",
          write_k_f32 ? QkNormRopeKvKernel<true> : QkNormRopeKvKernel<false>, dim3(grid), dim3(kBlock), q, k, v, q_norm,
          k_norm, n_heads, n_kv_heads, rope_tab, rope_rows, p0.value, p0.dev, static_cast<uint32_t>(units), eps,
