@@ -55,9 +55,22 @@ __device__ __forceinline__ void StoreHeadRowHalf(uint16_t* p, int l, const HeadR
   }
 }
 
-// RMSNorm of the row with weight w[128]: sum of squares in double (order a0, b0,
-// a1, b1 per lane, then the 8-lane butterfly), HeadRmsScale, then (x*scale)*w.
-__device__ __forceinline__ void NormHeadRow(HeadRow& r, const float* __restrict__ w, int l, float eps) {
+// Per-lane share of a 128-element vector read from cache (weights, RoPE rows).
+// Issued right after the activation loads so their latency overlaps with HBM's.
+__device__ __forceinline__ HeadRow LoadHeadVec(const float* __restrict__ p, int l) {
+  HeadRow r;
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    r.a[c] = Load4(p + HeadOffset(l, c));
+    r.b[c] = Load4(p + 64 + HeadOffset(l, c));
+  }
+  return r;
+}
+
+// RMSNorm of the row with weight w (the lane's share, from LoadHeadVec): sum of
+// squares in double (order a0, b0, a1, b1 per lane, then the 8-lane butterfly),
+// HeadRmsScale, then (x*scale)*w.
+__device__ __forceinline__ void NormHeadRow(HeadRow& r, const HeadRow& w, float eps) {
   double ss = 0.0;
 #pragma unroll
   for (int c = 0; c < 2; ++c) ss = AddSquares(AddSquares(ss, r.a[c]), r.b[c]);
@@ -65,24 +78,27 @@ __device__ __forceinline__ void NormHeadRow(HeadRow& r, const float* __restrict_
   const float scale = HeadRmsScale(ss, eps);
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
-    r.a[c] = ScaleMul(r.a[c], scale, Load4(w + HeadOffset(l, c)));
-    r.b[c] = ScaleMul(r.b[c], scale, Load4(w + 64 + HeadOffset(l, c)));
+    r.a[c] = ScaleMul(r.a[c], scale, w.a[c]);
+    r.b[c] = ScaleMul(r.b[c], scale, w.b[c]);
   }
 }
 
-// NeoX rotation with the table row cs (cos in 0..63, sin in 64..127):
-// x_i <- a*c - b*s, x_{i+64} <- b*c + a*s, each product rounded separately.
-__device__ __forceinline__ void RotateHeadRow(HeadRow& r, const float* __restrict__ cs, int l) {
+// NeoX rotation with a RoPE table row held as cos = t.a (elements 0..63) and
+// sin = t.b (64..127): x_i <- a*c - b*s, x_{i+64} <- b*c + a*s, each product
+// rounded separately. With apply == false the row is left as it is.
+__device__ __forceinline__ void RotateHeadRow(HeadRow& r, const HeadRow& t, bool apply) {
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
-    const float4 co = Load4(cs + HeadOffset(l, c));
-    const float4 si = Load4(cs + 64 + HeadOffset(l, c));
+    const float4 co = t.a[c];
+    const float4 si = t.b[c];
     const float4 a = r.a[c];
     const float4 b = r.b[c];
-    r.a[c] = make_float4(a.x * co.x - b.x * si.x, a.y * co.y - b.y * si.y, a.z * co.z - b.z * si.z,
-                         a.w * co.w - b.w * si.w);
-    r.b[c] = make_float4(b.x * co.x + a.x * si.x, b.y * co.y + a.y * si.y, b.z * co.z + a.z * si.z,
-                         b.w * co.w + a.w * si.w);
+    const float4 ra = make_float4(a.x * co.x - b.x * si.x, a.y * co.y - b.y * si.y, a.z * co.z - b.z * si.z,
+                                  a.w * co.w - b.w * si.w);
+    const float4 rb = make_float4(b.x * co.x + a.x * si.x, b.y * co.y + a.y * si.y, b.z * co.z + a.z * si.z,
+                                  b.w * co.w + a.w * si.w);
+    r.a[c] = apply ? ra : a;
+    r.b[c] = apply ? rb : b;
   }
 }
 

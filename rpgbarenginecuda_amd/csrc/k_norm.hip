@@ -156,7 +156,7 @@ __global__ __launch_bounds__(kBlock) void RmsNormHeadKernel(const float* x, cons
   const int64_t row = static_cast<int64_t>(blockIdx.x) * (kBlock / dev::kHeadLanes) + threadIdx.x / dev::kHeadLanes;
   if (row >= n_rows) return;
   dev::HeadRow r = dev::LoadHeadRowStream(x + row * stride, l);
-  dev::NormHeadRow(r, w, l, eps);
+  dev::NormHeadRow(r, dev::LoadHeadVec(w, l), eps);
   dev::StoreHeadRowStream(out + row * stride, l, r);
 }
 

@@ -56,7 +56,8 @@ __global__ __launch_bounds__(kBlock) void RopeHead128Kernel(float* x, int32_t n_
   const int64_t row = unit / n_heads;
   float* p = x + unit * kHeadDim;
   HeadRow r = dev::LoadHeadRowStream(p, l);
-  dev::RotateHeadRow(r, tab + (ReadPos0(pos0_val, pos0_dev) + row) * kHeadDim, l);
+  const HeadRow trig = dev::LoadHeadVec(tab + (ReadPos0(pos0_val, pos0_dev) + row) * kHeadDim, l);
+  dev::RotateHeadRow(r, trig, true);
   dev::StoreHeadRowStream(p, l, r);
 }
 
@@ -148,9 +149,18 @@ __global__ __launch_bounds__(kBlock) void QkNormRopeKvKernel(
     const int32_t h = is_q ? j : j - n_heads;
     float* p = is_q ? q + (static_cast<int64_t>(t) * n_heads + h) * kHeadDim
                     : k + (static_cast<int64_t>(t) * n_kv + h) * kHeadDim;
+    // The RoPE row index is clamped so the load is always in bounds; a position
+    // outside the table (reachable only through a replayed graph with a bad
+    // staged pos0) leaves the row unrotated.
+    const bool rope_ok = pos >= 0 && pos < rope_rows;
+    const HeadRow trig = dev::LoadHeadVec(tab + (rope_ok ? pos : 0) * kHeadDim, l);
     HeadRow r = dev::LoadHeadRowStream(p, l);
-    dev::NormHeadRow(r, is_q ? qw : kw, l, eps);
-    if (pos >= 0 && pos < rope_rows) dev::RotateHeadRow(r, tab + pos * kHeadDim, l);
+    // Keep the table and activation loads ahead of the reduction: each RoPE row is
+    // read by a single block per launch, so it usually comes from HBM, not L2.
+    __builtin_amdgcn_sched_barrier(0);
+    const HeadRow w = dev::LoadHeadVec(is_q ? qw : kw, l);
+    dev::NormHeadRow(r, w, eps);
+    dev::RotateHeadRow(r, trig, rope_ok);
     if (is_q || kWriteK) dev::StoreHeadRowStream(p, l, r);
     if (!is_q && kv_slot_ok) dev::StoreHeadRowHalf(kc + (static_cast<int64_t>(h) * max_seq + pos) * kHeadDim, l, r);
   } else {
