@@ -58,30 +58,41 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+QWEN3_1_7B = dict(hidden=H, n_heads=HQ, n_kv_heads=HKV, inter=INTER, layers=LAYERS)
+QWEN3_4B = dict(hidden=2560, n_heads=32, n_kv_heads=8, inter=9728, layers=36)
+
+
 class Layer:
     """One layer's device buffers (all distinct per layer)."""
 
-    def __init__(self, torch, n, gen):
+    def __init__(self, torch, n, gen, shape=QWEN3_1_7B):
         f32 = dict(dtype=torch.float32, device="cuda")
-        self.x = torch.randn((n, H), generator=gen, **f32)
-        self.d = torch.randn((n, H), generator=gen, **f32)
-        self.h = torch.empty((n, H), **f32)
-        self.w = 1.0 + 0.1 * torch.randn(H, generator=gen, **f32)
-        self.q = torch.randn((n, HQ, D), generator=gen, **f32)
-        self.k = torch.randn((n, HKV, D), generator=gen, **f32)
-        self.v = torch.randn((n, HKV, D), generator=gen, **f32)
+        hid, hq, hkv, inter = shape["hidden"], shape["n_heads"], shape["n_kv_heads"], shape["inter"]
+        self.n, self.hid, self.hq, self.hkv, self.inter = n, hid, hq, hkv, inter
+        self.x = torch.randn((n, hid), generator=gen, **f32)
+        self.d = torch.randn((n, hid), generator=gen, **f32)
+        self.h = torch.empty((n, hid), **f32)
+        self.w = 1.0 + 0.1 * torch.randn(hid, generator=gen, **f32)
+        self.q = torch.randn((n, hq, D), generator=gen, **f32)
+        self.k = torch.randn((n, hkv, D), generator=gen, **f32)
+        self.v = torch.randn((n, hkv, D), generator=gen, **f32)
         self.qn = 1.0 + 0.1 * torch.randn(D, generator=gen, **f32)
         self.kn = 1.0 + 0.1 * torch.randn(D, generator=gen, **f32)
-        self.kc = torch.zeros(HKV * MAX_SEQ * D, dtype=torch.int16, device="cuda")
+        self.kc = torch.zeros(hkv * MAX_SEQ * D, dtype=torch.int16, device="cuda")
         self.vc = torch.zeros_like(self.kc)
-        self.gate = torch.randn((n, INTER), generator=gen, **f32)
-        self.up = torch.randn((n, INTER), generator=gen, **f32)
+        self.gate = torch.randn((n, inter), generator=gen, **f32)
+        self.up = torch.randn((n, inter), generator=gen, **f32)
 
 
 def run_layer(ops, L, n, tab, pos0):
-    ops.GpuAddRmsNorm(L.x, L.d, L.w, n, H, EPS, L.h)
-    ops.GpuQkNormRopeKv(L.q, L.k, L.v, L.qn, L.kn, HQ, HKV, D, tab, MAX_SEQ, pos0, n, EPS, L.kc, L.vc, MAX_SEQ)
-    ops.GpuSiluMulInPlace(L.gate, L.up, n * INTER)
+    ops.GpuAddRmsNorm(L.x, L.d, L.w, n, L.hid, EPS, L.h)
+    ops.GpuQkNormRopeKv(L.q, L.k, L.v, L.qn, L.kn, L.hq, L.hkv, D, tab, MAX_SEQ, pos0, n, EPS, L.kc, L.vc, MAX_SEQ)
+    ops.GpuSiluMulInPlace(L.gate, L.up, n * L.inter)
+
+
+def layer_bytes(n, shape):
+    return (bytes_add_rms(n, shape["hidden"]) + bytes_qk(n, shape["n_heads"], shape["n_kv_heads"]) +
+            bytes_swiglu(n, shape["inter"]))
 
 
 OP_NAMES = ("add_rms_norm", "qk_norm_rope_kv", "swiglu")
@@ -168,10 +179,37 @@ def measure_decode(torch, ops, tab, steps):
         graph_us = e0.elapsed_time(e1) * 1e3 / (steps * LAYERS)
     except Exception as exc:  # graph capture unavailable: report eager only
         log(f"decode graph capture failed: {exc}")
-    b = bytes_add_rms(1) + bytes_qk(1) + bytes_swiglu(1)
+    b = layer_bytes(1, QWEN3_1_7B)
     return {"us_per_layer_eager": round(eager_us, 3),
             "us_per_layer_graph": None if graph_us is None else round(graph_us, 3),
             "bytes_per_layer": b, "position": pos, "launches_per_layer": 3}
+
+
+def measure_prefill_4b(torch, ops, tab, steps=5, warmup=2):
+    """Prefill n = 4096 at Qwen3-4B shape, 36 layers (the 4096-slot caches are filled)."""
+    n, shape = 4096, QWEN3_4B
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(4)
+    layers = [Layer(torch, n, gen, shape) for _ in range(shape["layers"])]
+    for _ in range(warmup):
+        for L in layers:
+            run_layer(ops, L, n, tab, 0)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        for L in layers:
+            run_layer(ops, L, n, tab, 0)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    b = shape["layers"] * layer_bytes(n, shape)
+    del layers
+    torch.cuda.empty_cache()
+    return {"ms_per_step": round(ms, 4), "GBps": round(b / (ms * 1e-3) / 1e9, 1),
+            "pct_of_peak": round(b / (ms * 1e-3) / 1e9 / PEAK_GBPS * 100, 2), "bytes_per_step": b,
+            "us_per_layer": round(ms * 1e3 / shape["layers"], 2), "layers": shape["layers"], "n_tokens": n}
 
 
 def measure_gather(torch, ops, ggml_type, bb, copies=4, reps=20):
@@ -232,18 +270,29 @@ def profile_traffic(kernel_tag):
 
 def cpu_baseline():
     """The oracle's C restatement of one layer of the chain (n = 2811, 1.7B shape)
-    on the host cores, median of 5; a reported baseline only."""
+    on the host cores, median of 5; plus per-op and single-thread figures. A
+    reported baseline only."""
     from oracle import pyoracle
 
     threads = max(1, min(os.cpu_count() or 1, 16))
-    sec = pyoracle.bench_layer_chain(threads, N_PREFILL, H, HQ, HKV, INTER, 5)
+    args = (N_PREFILL, H, HQ, HKV, INTER)
+    sec = pyoracle.bench_layer_chain(threads, *args, 5)
     if sec <= 0:
         return None
-    b = bytes_add_rms(N_PREFILL) + bytes_qk(N_PREFILL) + bytes_swiglu(N_PREFILL)
+    b = layer_bytes(N_PREFILL, QWEN3_1_7B)
+    per_op = {}
+    for op, name, nbytes in ((1, "add_rms_norm", bytes_add_rms(N_PREFILL)), (2, "qk_norm_rope_kv", bytes_qk(N_PREFILL)),
+                             (3, "swiglu", bytes_swiglu(N_PREFILL))):
+        t = pyoracle.bench_layer_op(op, threads, *args, 3)
+        per_op[name] = {"ms": round(t * 1e3, 3), "GBps": round(nbytes / t / 1e9, 2)}
+    t1 = pyoracle.bench_layer_chain(1, *args, 1)
+    gq4 = pyoracle.bench_gather(threads, pyoracle.Q4_K, VOCAB, H, N_PREFILL, 3)
     return {"value": round(b / sec / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"one layer of the n={N_PREFILL} chain (add+RMSNorm, qk-norm+RoPE+fp16 KV, SwiGLU; "
                       f"{b} B) by the C oracle, rows split over {threads} threads, median of 5 runs "
-                      f"({sec * 1e3:.1f} ms each)"}
+                      f"({sec * 1e3:.1f} ms each)",
+            "per_op": per_op, "single_thread_GBps": round(b / t1 / 1e9, 2),
+            "gather_q4k_GBps": round(bytes_gather(N_PREFILL, 144) / gq4 / 1e9, 2)}
 
 
 def main():
@@ -280,7 +329,7 @@ def main():
     log(f"timing {args.steps} steps after {args.warmup} warmup")
     ms_step, ms_prof, report = timed_prefill(torch, ops, layers, tab, N_PREFILL, args.steps, args.warmup)
     log(f"ms/step {ms_step:.4f} ({ms_prof:.4f} with launch profiling); kernels: {json.dumps(report)}")
-    step_bytes = LAYERS * (bytes_add_rms(N_PREFILL) + bytes_qk(N_PREFILL) + bytes_swiglu(N_PREFILL))
+    step_bytes = LAYERS * layer_bytes(N_PREFILL, QWEN3_1_7B)
     value = step_bytes / (ms_step * 1e-3) / 1e9
     op_bytes = {"add_rms_norm": bytes_add_rms(N_PREFILL), "qk_norm_rope_kv": bytes_qk(N_PREFILL),
                 "swiglu": bytes_swiglu(N_PREFILL)}
@@ -315,6 +364,8 @@ def main():
     if not args.no_extras:
         log("decode n=1")
         extras["decode_n1"] = measure_decode(torch, ops, tab, max(20, args.steps))
+        log("prefill n=4096 at the 4B shape, 36 layers")
+        extras["prefill_4b_n4096"] = measure_prefill_4b(torch, ops, tab)
         log("gather Q4_K / Q6_K")
         extras["gather_q4k_n2811"] = measure_gather(torch, ops, ops.GGML_Q4_K, 144)
         extras["gather_q6k_n2811"] = measure_gather(torch, ops, ops.GGML_Q6_K, 210)

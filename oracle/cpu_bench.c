@@ -41,6 +41,7 @@ static int cmp_double(const void* a, const void* b) {
 /* ------------------------------------------------------------------ layer chain */
 
 typedef struct {
+  int op; /* 0: the whole chain, 1: residual add + RMSNorm, 2: q/k norm + RoPE + KV, 3: SwiGLU */
   int64_t n, hidden, inter;
   int32_t n_heads, n_kv;
   float *x, *d, *h, *wn, *q, *k, *v, *qn, *kn, *tab, *gate, *up;
@@ -53,20 +54,24 @@ static void* chain_worker(void* p) {
   const ChainArgs* a = (const ChainArgs*)p;
   const int64_t rows = a->t1 - a->t0;
   if (rows <= 0) return NULL;
-  ora_add_rms_norm(a->x + a->t0 * a->hidden, a->d + a->t0 * a->hidden, a->wn, rows, a->hidden, 1e-6f,
-                   a->h + a->t0 * a->hidden);
+  if (a->op == 0 || a->op == 1)
+    ora_add_rms_norm(a->x + a->t0 * a->hidden, a->d + a->t0 * a->hidden, a->wn, rows, a->hidden, 1e-6f,
+                     a->h + a->t0 * a->hidden);
   /* q/k norm + RoPE + KV write for this worker's tokens (positions t0..t1-1). */
-  ora_qk_norm_rope_kv(a->q + a->t0 * a->n_heads * 128, a->k + a->t0 * a->n_kv * 128, a->v + a->t0 * a->n_kv * 128,
-                      a->qn, a->kn, a->n_heads, a->n_kv, 128, a->tab, a->t0, rows, 1e-6f, a->kc, a->vc, a->max_seq);
-  ora_silu_mul(a->gate + a->t0 * a->inter, a->up + a->t0 * a->inter, rows * a->inter);
+  if (a->op == 0 || a->op == 2)
+    ora_qk_norm_rope_kv(a->q + a->t0 * a->n_heads * 128, a->k + a->t0 * a->n_kv * 128,
+                        a->v + a->t0 * a->n_kv * 128, a->qn, a->kn, a->n_heads, a->n_kv, 128, a->tab, a->t0, rows,
+                        1e-6f, a->kc, a->vc, a->max_seq);
+  if (a->op == 0 || a->op == 3) ora_silu_mul(a->gate + a->t0 * a->inter, a->up + a->t0 * a->inter, rows * a->inter);
   return NULL;
 }
 
-double ora_bench_layer_chain(int threads, int64_t n, int64_t hidden, int32_t n_heads, int32_t n_kv_heads,
-                             int64_t inter, int reps) {
-  if (threads < 1 || threads > 256 || n <= 0 || reps < 1 || reps > 64) return -1.0;
+double ora_bench_layer_op(int op, int threads, int64_t n, int64_t hidden, int32_t n_heads, int32_t n_kv_heads,
+                          int64_t inter, int reps) {
+  if (op < 0 || op > 3 || threads < 1 || threads > 256 || n <= 0 || reps < 1 || reps > 64) return -1.0;
   ChainArgs base;
   memset(&base, 0, sizeof(base));
+  base.op = op;
   base.n = n;
   base.hidden = hidden;
   base.inter = inter;
@@ -182,4 +187,9 @@ done:
   free(toks);
   free(x);
   return result;
+}
+
+double ora_bench_layer_chain(int threads, int64_t n, int64_t hidden, int32_t n_heads, int32_t n_kv_heads,
+                             int64_t inter, int reps) {
+  return ora_bench_layer_op(0, threads, n, hidden, n_heads, n_kv_heads, inter, reps);
 }

@@ -85,6 +85,9 @@ void ora_norm_rope_f64(const float* x, const float* w, int32_t n_heads, int32_t 
  * itself. Returns the median seconds per chain, or a negative value on error. */
 double ora_bench_layer_chain(int threads, int64_t n, int64_t hidden, int32_t n_heads, int32_t n_kv_heads,
                              int64_t inter, int reps);
+/* One op of the chain alone: op 1 residual add + RMSNorm, 2 q/k norm + RoPE + KV, 3 SwiGLU (0 = all). */
+double ora_bench_layer_op(int op, int threads, int64_t n, int64_t hidden, int32_t n_heads, int32_t n_kv_heads,
+                          int64_t inter, int reps);
 /* Same for the embedding gather of `seq` ids from a rows x cols table of `type`. */
 double ora_bench_gather(int threads, uint32_t type, int64_t rows, int64_t cols, int64_t seq, int reps);
 

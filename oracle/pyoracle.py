@@ -43,6 +43,7 @@ _SIGS = {
     "ora_silu_mul_f64": (None, [_vp, _vp, _i64, _vp]),
     "ora_norm_rope_f64": (None, [_vp, _vp, _i32, _i32, _vp, _i64, _i64, _f64, _vp]),
     "ora_bench_layer_chain": (_f64, [ctypes.c_int, _i64, _i64, _i32, _i32, _i64, ctypes.c_int]),
+    "ora_bench_layer_op": (_f64, [ctypes.c_int, ctypes.c_int, _i64, _i64, _i32, _i32, _i64, ctypes.c_int]),
     "ora_bench_gather": (_f64, [ctypes.c_int, _u32, _i64, _i64, _i64, ctypes.c_int]),
 }
 
@@ -247,6 +248,10 @@ def norm_rope_f64(x, w, n_heads, head_dim, tab, pos0, n_rows, eps) -> np.ndarray
 
 def bench_layer_chain(threads, n, hidden, n_heads, n_kv_heads, inter, reps) -> float:
     return float(lib().ora_bench_layer_chain(threads, n, hidden, n_heads, n_kv_heads, inter, reps))
+
+
+def bench_layer_op(op, threads, n, hidden, n_heads, n_kv_heads, inter, reps) -> float:
+    return float(lib().ora_bench_layer_op(op, threads, n, hidden, n_heads, n_kv_heads, inter, reps))
 
 
 def bench_gather(threads, ggml_type, rows, cols, seq, reps) -> float:

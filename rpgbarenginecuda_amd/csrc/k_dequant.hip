@@ -155,6 +155,29 @@ __global__ __launch_bounds__(kBlock) void GatherBlocksKernel(const uint8_t* __re
   T::Decode(emb + tok * row_bytes + b * T::kBytes, j, out);
 }
 
+// Gather with one workgroup per token: nb * kLanes threads, the token id is a
+// uniform (scalar) load and the row address is uniform, so each lane's block
+// loads depend on one scalar load instead of a per-lane id load.
+template <uint32_t kType>
+__global__ __launch_bounds__(1024) void GatherRowsKernel(const uint8_t* __restrict__ emb, int64_t rows,
+                                                         int64_t row_bytes, const int32_t* __restrict__ toks,
+                                                         float* __restrict__ x) {
+  using T = QuantTraits<kType>;
+  const int64_t t = blockIdx.x;
+  const int32_t b = static_cast<int32_t>(threadIdx.x / T::kLanes);
+  const int j = threadIdx.x % T::kLanes;
+  const int64_t nb = blockDim.x / T::kLanes;
+  float* out = x + (t * nb + b) * kQK_K;
+  const int64_t tok = static_cast<int64_t>(toks[t]);
+  if (tok < 0 || tok >= rows) {
+    constexpr int kPerLane = static_cast<int>(kQK_K) / T::kLanes;
+#pragma unroll
+    for (int e = 0; e < kPerLane; e += 4) StoreStream4(out + j * kPerLane + e, make_float4(0.f, 0.f, 0.f, 0.f));
+    return;
+  }
+  T::Decode(emb + tok * row_bytes + b * T::kBytes, j, out);
+}
+
 // F32 tables: rows are plain floats; one float4 per thread.
 __global__ __launch_bounds__(kBlock) void GatherF32Kernel(const float* __restrict__ emb, int64_t rows, int64_t cols,
                                                           const int32_t* __restrict__ toks, int64_t total4,
@@ -245,17 +268,30 @@ void LaunchGather(uint32_t type, const uint8_t* emb, int64_t rows, int64_t cols,
   const int64_t row_bytes = TypeRowBytes(type, cols);
   if (seq <= 0) return;
   const int64_t total = seq * cols;
+  const int64_t nb64 = cols / kQK_K;
+  if (toks != nullptr && type == kGgmlQ4_K && nb64 * 32 <= 1024 && Aligned(emb, 16) && Aligned(x, 16)) {
+    RPG_CHECK(seq <= 0x7FFFFFFF, "too many tokens: %lld", static_cast<long long>(seq));
+    Launch("GatherQ4KKernel", GatherRowsKernel<kGgmlQ4_K>, dim3(static_cast<unsigned>(seq)),
+           dim3(static_cast<unsigned>(nb64 * 32)), emb, rows, row_bytes, toks, x);
+    return;
+  }
+  if (toks != nullptr && type == kGgmlQ6_K && nb64 * 16 <= 1024 && Aligned(emb, 2) && Aligned(x, 16)) {
+    RPG_CHECK(seq <= 0x7FFFFFFF, "too many tokens: %lld", static_cast<long long>(seq));
+    Launch("GatherQ6KKernel", GatherRowsKernel<kGgmlQ6_K>, dim3(static_cast<unsigned>(seq)),
+           dim3(static_cast<unsigned>(nb64 * 16)), emb, rows, row_bytes, toks, x);
+    return;
+  }
   if (type == kGgmlQ4_K && Aligned(emb, 16) && Aligned(x, 16)) {
     const int32_t nb = static_cast<int32_t>(cols / kQK_K);
     const int64_t units = seq * nb;
-    Launch("GatherQ4KKernel", GatherBlocksKernel<kGgmlQ4_K>, dim3(GridFor(units, kBlock / 32)), dim3(kBlock), emb,
+    Launch("GatherBlocksQ4KKernel", GatherBlocksKernel<kGgmlQ4_K>, dim3(GridFor(units, kBlock / 32)), dim3(kBlock), emb,
            rows, row_bytes, nb, toks, units, x);
     return;
   }
   if (type == kGgmlQ6_K && Aligned(emb, 2) && Aligned(x, 16)) {
     const int32_t nb = static_cast<int32_t>(cols / kQK_K);
     const int64_t units = seq * nb;
-    Launch("GatherQ6KKernel", GatherBlocksKernel<kGgmlQ6_K>, dim3(GridFor(units, kBlock / 16)), dim3(kBlock), emb,
+    Launch("GatherBlocksQ6KKernel", GatherBlocksKernel<kGgmlQ6_K>, dim3(GridFor(units, kBlock / 16)), dim3(kBlock), emb,
            rows, row_bytes, nb, toks, units, x);
     return;
   }

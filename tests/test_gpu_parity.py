@@ -112,12 +112,14 @@ def test_embedding_gather_full_table(gpu, ora, t):
 
 
 @pytest.mark.parametrize("t", [0, 12, 14])
-def test_embedding_gather_edges(gpu, ora, t):
-    """4B width (2560), duplicates, out-of-range ids -> zero rows, n = 1."""
+@pytest.mark.parametrize("cols", [2560, 8448])
+def test_embedding_gather_edges(gpu, ora, t, cols):
+    """4B width (2560) and a width past one workgroup per token (33 blocks), duplicates,
+    out-of-range ids -> zero rows, n = 1."""
     import torch
 
-    rows, cols = 300, 2560
-    case(f"gather edges type={t}")
+    rows = 300
+    case(f"gather edges type={t} cols={cols}")
     rng = np.random.default_rng(300 + t)
     table = synth.quant_table(rng, t, rows, cols)
     toks = np.array([5, 5, 299, 0, -1, 300, 2 ** 31 - 1, 17], np.int32)
@@ -186,7 +188,7 @@ def test_kv_write_rne_bitexact(gpu, ora, head_dim, pos0, seq):
 # ----------------------------------------------------------------------------- RMSNorm
 
 
-@pytest.mark.parametrize("rows,n", [(21, 2048), (2811, 2048), (1, 2048), (64, 2560), (7, 4096)])
+@pytest.mark.parametrize("rows,n", [(21, 2048), (2811, 2048), (1, 2048), (4096, 2560), (7, 4096)])
 def test_rms_norm_hidden(gpu, ora, rows, n):
     import torch
 
@@ -234,7 +236,7 @@ def test_rms_norm_generic_paths(gpu, ora, rows, n, stride, off):
         assert ok, (r, err)
 
 
-@pytest.mark.parametrize("rows,n", [(21, 2048), (2811, 2048), (1, 2048), (33, 2560), (5, 1000)])
+@pytest.mark.parametrize("rows,n", [(21, 2048), (2811, 2048), (1, 2048), (4096, 2560), (5, 1000), (3, 768)])
 def test_add_rms_norm(gpu, ora, rows, n):
     import torch
 
