@@ -45,13 +45,29 @@ __device__ __forceinline__ void StoreHeadRowStream(float* p, int l, const HeadRo
   }
 }
 
-// fp16 (IEEE round-to-nearest-even) copy of the row, 8-byte stores. Plain stores
-// measured slightly faster than nontemporal ones for the scattered 256-byte cache rows.
+// Swap one dword between the lanes of each even/odd pair (DPP quad_perm [1,0,3,2]).
+__device__ __forceinline__ uint32_t SwapLanePair(uint32_t x) {
+  return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0xB1, 0xF, 0xF, false));
+}
+
+// fp16 (IEEE round-to-nearest-even) copy of the row with 16-byte stores. Lane l
+// holds the packed halves of chunks l and 8+l of each half row; lanes 2m and 2m+1
+// swap one packed chunk so the even lane writes elements 8m..8m+7 (its chunk 2m
+// and the odd lane's 2m+1) and the odd lane 32+8m..32+8m+7. Each store instruction
+// then covers whole 128-byte lines. Both lanes of a pair must be active (the
+// callers' conditions are uniform over the 8 lanes of a row). Plain stores:
+// nontemporal ones measured no faster for these scattered 256-byte cache rows.
 __device__ __forceinline__ void StoreHeadRowHalf(uint16_t* p, int l, const HeadRow& r) {
+  const bool odd = (l & 1) != 0;
+  uint16_t* dst = p + (odd ? 32 + 8 * (l >> 1) : 8 * (l >> 1));
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    *reinterpret_cast<uint2*>(p + HeadOffset(l, c)) = PackHalf4(r.a[c]);
-    *reinterpret_cast<uint2*>(p + 64 + HeadOffset(l, c)) = PackHalf4(r.b[c]);
+  for (int s = 0; s < 2; ++s) {
+    const uint2 c0 = PackHalf4(s == 0 ? r.a[0] : r.b[0]);
+    const uint2 c1 = PackHalf4(s == 0 ? r.a[1] : r.b[1]);
+    const uint2 send = odd ? c0 : c1;
+    const uint2 recv = make_uint2(SwapLanePair(send.x), SwapLanePair(send.y));
+    *reinterpret_cast<uint4*>(dst + 64 * s) =
+        odd ? make_uint4(recv.x, recv.y, c1.x, c1.y) : make_uint4(c0.x, c0.y, recv.x, recv.y);
   }
 }
 

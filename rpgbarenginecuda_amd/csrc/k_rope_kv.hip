@@ -227,7 +227,7 @@ void GpuQkNormRopeKv(float* q, float* k, const float* v, const float* q_norm, co
   const int64_t units = seq * (n_heads + 2 * static_cast<int64_t>(n_kv_heads));
   const bool fast = head_dim == kHeadDim && units <= 0x7FFFFFFF && Aligned(q, 16) && Aligned(k, 16) &&
                     Aligned(v, 16) && Aligned(q_norm, 16) && Aligned(k_norm, 16) && Aligned(rope_tab, 16) &&
-                    Aligned(k_cache_layer, 8) && Aligned(v_cache_layer, 8);
+                    Aligned(k_cache_layer, 16) && Aligned(v_cache_layer, 16);
   if (!fast) {
     // Other head sizes / layouts: the unfused reference sequence (k then holds
     // the rotated values, as it does in the reference layer).

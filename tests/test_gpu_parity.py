@@ -361,6 +361,40 @@ def test_qk_norm_rope_kv_matches_unfused_reference_sequence(gpu, ora):
     assert np.array_equal(host(kc1), host(kc2)) and np.array_equal(host(vc1), host(vc2))
 
 
+@pytest.mark.parametrize("cache_off", [4, 1])
+def test_qk_norm_rope_kv_unaligned_cache_base(gpu, ora, cache_off):
+    """Cache bases that are not 16-byte aligned (offset by `cache_off` halves) take
+    the unfused sequence; the cache and q bits equal those of the fused kernel."""
+    import torch
+
+    case(f"qk cache base offset {cache_off} halves")
+    hq, hkv, d, seq, pos0, max_seq = 16, 8, 128, 40, 5, 128
+    rng = np.random.default_rng(1200 + cache_off)
+    tab = dev(ora.build_rope_table(d, 1e6, max_seq))
+    q = synth.normal(rng, (seq, hq, d))
+    k = synth.normal(rng, (seq, hkv, d))
+    v = synth.normal(rng, (seq, hkv, d))
+    qn = dev(synth.normal(rng, d, 1.0, 0.1))
+    kn = dev(synth.normal(rng, d, 1.0, 0.1))
+    n_cache = hkv * max_seq * d
+    q1, k1 = dev(q), dev(k)
+    kc1 = torch.zeros(n_cache, dtype=torch.int16, device="cuda")
+    vc1 = torch.zeros_like(kc1)
+    gpu.GpuQkNormRopeKv(q1, k1, dev(v), qn, kn, hq, hkv, d, tab, max_seq, pos0, seq, EPS, kc1, vc1, max_seq, True)
+    q2, k2 = dev(q), dev(k)
+    kbuf = torch.zeros(n_cache + 8, dtype=torch.int16, device="cuda")
+    vbuf = torch.zeros_like(kbuf)
+    kc2 = kbuf[cache_off:cache_off + n_cache]
+    vc2 = vbuf[cache_off:cache_off + n_cache]
+    gpu.GpuQkNormRopeKv(q2, k2, dev(v), qn, kn, hq, hkv, d, tab, max_seq, pos0, seq, EPS, kc2, vc2, max_seq, True)
+    assert np.array_equal(bits(host(q1)), bits(host(q2)))
+    assert np.array_equal(bits(host(k1)), bits(host(k2)))
+    assert np.array_equal(host(kc1), host(kc2)) and np.array_equal(host(vc1), host(vc2))
+    kb, vb = host(kbuf), host(vbuf)
+    assert not kb[:cache_off].any() and not kb[cache_off + n_cache:].any()
+    assert not vb[:cache_off].any() and not vb[cache_off + n_cache:].any()
+
+
 # ----------------------------------------------------------------------------- SwiGLU / add
 
 
