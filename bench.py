@@ -11,8 +11,9 @@ come from HIP events attached to every kernel dispatch of the timed steps
 (librpg_ops launch profiling, hipExtLaunchKernel). The 28 layers'
 buffers total ~9 GB, far above the 256 MB Infinity Cache, so every launch reads
 from HBM. Also reported: decode n = 1 (us per layer, eager and HIP graph), the
-Q4_K / Q6_K embedding gather at n = 2811, a streaming-copy ceiling, and the CPU
-oracle on the host cores as a baseline.
+Q4_K / Q6_K embedding gather at n = 2811, a streaming-copy ceiling, same-size
+ceilings (a copy moving each op's bytes, a fill writing its output bytes) timed
+the same way as the ops, and the CPU oracle on the host cores as a baseline.
 
 python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -238,6 +239,51 @@ def measure_gather(torch, ops, ggml_type, bb, copies=4, reps=20):
             "kernel": name, "launches": rep["count"]}
 
 
+def measure_ceilings(torch, ops, sizes, reps=20):
+    """Same-size streaming ceilings, timed like the ops (dispatch-attached events):
+    for each (label, total_bytes, write_bytes), a StreamCopyKernel moving total_bytes
+    (half read, half written) and a StreamFillKernel writing write_bytes. Launches
+    walk through 1 GiB source / destination buffers so no launch reuses a window
+    while it could still sit in the 256 MB Infinity Cache."""
+    span = 1 << 30
+    src = torch.empty(span // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    out = {}
+
+    def timed(kernel, per_launch, launch):
+        windows = max(1, span // per_launch)
+        for r in range(2):
+            launch(r % windows)
+        torch.cuda.synchronize()
+        ops.profile_start(reps)
+        for r in range(reps):
+            launch(r % windows)
+        ops.profile_stop()
+        return ops.profile_report()[kernel]["avg_us"]
+
+    for label, total, written in sizes:
+        half = (total // 2) // 16 * 16
+        w = written // 16 * 16
+
+        def copy(i, half=half):
+            off = i * half // 4
+            ops.GpuStreamCopy(src[off:off + half // 4], dst[off:off + half // 4], half)
+
+        def fill(i, w=w):
+            off = i * w // 4
+            ops.GpuStreamFill(dst[off:off + w // 4], w, 0x3F800000)
+
+        copy_us = timed("StreamCopyKernel", half, copy)
+        fill_us = timed("StreamFillKernel", w, fill)
+        out[label] = {"copy_us": round(copy_us, 2), "fill_us": round(fill_us, 2),
+                      "copy_GBps": round(2 * half / (copy_us * 1e-6) / 1e9, 1),
+                      "fill_GBps": round(w / (fill_us * 1e-6) / 1e9, 1)}
+    del src, dst
+    torch.cuda.empty_cache()
+    return out
+
+
 def measure_copy(torch, ops, nbytes=1 << 30, reps=10):
     src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
     dst = torch.empty_like(src)
@@ -371,6 +417,21 @@ def main():
         extras["gather_q6k_n2811"] = measure_gather(torch, ops, ops.GGML_Q6_K, 210)
         log("stream copy ceiling")
         extras["stream_copy_GBps"] = measure_copy(torch, ops)
+        log("same-size copy / fill ceilings")
+        ceil = measure_ceilings(torch, ops, [
+            ("add_rms_norm", op_bytes["add_rms_norm"], 8 * N_PREFILL * H),
+            ("qk_norm_rope_kv", op_bytes["qk_norm_rope_kv"], N_PREFILL * (4 * HQ * D + 4 * HKV * D)),
+            ("swiglu", op_bytes["swiglu"], 4 * N_PREFILL * INTER),
+            ("gather", bytes_gather(N_PREFILL, 144), 4 * N_PREFILL * H)])
+        for name in OP_NAMES:
+            c = ceil[name]
+            op_stats[name]["copy_ceiling_us"] = c["copy_us"]
+            op_stats[name]["pct_of_copy_ceiling"] = round(c["copy_us"] / op_stats[name]["us"] * 100, 1)
+        for key, bb in (("gather_q4k_n2811", 144), ("gather_q6k_n2811", 210)):
+            g = extras[key]
+            g["write_ceiling_us"] = ceil["gather"]["fill_us"]
+            g["pct_of_write_ceiling"] = round(ceil["gather"]["fill_us"] / g["us"] * 100, 1)
+        extras["ceilings"] = ceil
     cpu = None if args.no_cpu else cpu_baseline()
 
     line = {

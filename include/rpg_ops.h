@@ -140,6 +140,12 @@ RPG_OPS_API int32_t rpg_op_qk_norm_rope_kv(float* q, float* k, const float* v, c
  * streaming-bandwidth probe. Replaces: BwCopyKernel, tools/matmul_bench.cu:230-289. */
 RPG_OPS_API int32_t rpg_op_stream_copy(const void* src, void* dst, int64_t bytes);
 
+/* Every 32-bit word of dst <- pattern, `bytes` a positive multiple of 16, dst
+ * 16-byte aligned: the write-only bandwidth probe (the ceiling of write-dominated
+ * ops such as the embedding gather). No counterpart in the reference, which
+ * probes copies only (tools/matmul_bench.cu:230-289). */
+RPG_OPS_API int32_t rpg_op_stream_fill(void* dst, int64_t bytes, uint32_t pattern);
+
 /* out_dev[i] = fp32 value of the binary16 bit pattern i, i in [0, 65536).
  * Replaces: F16SweepKernel, tools/dequant_check.cu:44-48. */
 RPG_OPS_API int32_t rpg_op_f16_sweep(float* out_dev);

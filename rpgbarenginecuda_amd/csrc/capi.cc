@@ -133,6 +133,10 @@ int32_t rpg_op_stream_copy(const void* src, void* dst, int64_t bytes) {
   return Guard([&] { rpg::GpuStreamCopy(src, dst, bytes); });
 }
 
+int32_t rpg_op_stream_fill(void* dst, int64_t bytes, uint32_t pattern) {
+  return Guard([&] { rpg::GpuStreamFill(dst, bytes, pattern); });
+}
+
 int32_t rpg_op_f16_sweep(float* out_dev) {
   return Guard([&] { rpg::GpuF16Sweep(out_dev); });
 }

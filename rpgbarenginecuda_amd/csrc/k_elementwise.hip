@@ -1,5 +1,5 @@
 // Element-wise operators: SwiGLU gate (silu(gate) * up), the residual add, and
-// the streaming-copy probe used to calibrate bandwidth and HBM counters.
+// the streaming copy / fill probes used to calibrate bandwidth and HBM counters.
 //
 // Reference semantics:
 //   SiluMul (src/kernels_gpu.cu:863-869): gate[i] = (v / (1.0f + expf(-v))) * up[i]
@@ -13,6 +13,8 @@
 // A scalar tail (n % 4) is handled by the first threads of block 0; unaligned
 // pointers take a grid-stride scalar kernel.
 #include <hip/hip_runtime.h>
+
+#include <cstring>
 
 #include "dev_util.h"
 #include "kernels_gpu.h"
@@ -75,6 +77,15 @@ __global__ __launch_bounds__(kBlock) void StreamCopyKernel(const float* __restri
   if (i < n16) StoreStream4(dst + 4 * i, LoadStream4(src + 4 * i));
 }
 
+// Write-only probe: 256-thread blocks measured faster than 512 for pure writes
+// (23 MB: 5.1 vs 5.7 us; 368 MB: 6.9 vs 6.3 TB/s).
+constexpr int kFillBlock = 256;
+
+__global__ __launch_bounds__(kFillBlock) void StreamFillKernel(float* __restrict__ dst, int64_t n16, float value) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kFillBlock + threadIdx.x;
+  if (i < n16) StoreStream4(dst + 4 * i, make_float4(value, value, value, value));
+}
+
 // Blocks for the vector kernels: at least one, so block 0 exists for the tail.
 unsigned VecGrid(int64_t n4) { return n4 > 0 ? GridFor(n4, kBlock) : 1u; }
 
@@ -112,6 +123,17 @@ void GpuStreamCopy(const void* src, void* dst, int64_t bytes) {
   const int64_t n16 = bytes / 16;
   Launch("StreamCopyKernel", StreamCopyKernel, dim3(GridFor(n16, kBlock)), dim3(kBlock),
          static_cast<const float*>(src), static_cast<float*>(dst), n16);
+}
+
+void GpuStreamFill(void* dst, int64_t bytes, uint32_t pattern) {
+  RPG_CHECK(bytes > 0 && bytes % 16 == 0, "stream fill size %lld must be a positive multiple of 16",
+            static_cast<long long>(bytes));
+  RPG_CHECK(Aligned16(dst), "stream fill buffer must be 16-byte aligned");
+  const int64_t n16 = bytes / 16;
+  float value;
+  std::memcpy(&value, &pattern, sizeof(value));
+  Launch("StreamFillKernel", StreamFillKernel, dim3(GridFor(n16, kFillBlock)), dim3(kFillBlock),
+         static_cast<float*>(dst), n16, value);
 }
 
 }  // namespace rpg

@@ -166,6 +166,9 @@ void GpuEmbeddingLookupRaw(uint32_t type, const uint8_t* emb_dev, int64_t rows, 
 // HBM counters (the reference's streaming-bandwidth probe, tools/matmul_bench.cu:230-289).
 void GpuStreamCopy(const void* src, void* dst, int64_t bytes);
 
+// Write-only probe: every 32-bit word of dst <- pattern (`bytes` a multiple of 16).
+void GpuStreamFill(void* dst, int64_t bytes, uint32_t pattern);
+
 // out[i] = binary16 bits i converted to fp32, i in [0, 65536): exhaustive check
 // of the device f16 -> f32 conversion (tools/dequant_check.cu:44-48).
 void GpuF16Sweep(float* out_dev);

@@ -50,6 +50,7 @@ SIGNATURES = {
     "rpg_op_qk_norm_rope_kv": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _i64, _f32,
                                       _vp, _vp, _i64, _i32]),
     "rpg_op_stream_copy": (_i32, [_vp, _vp, _i64]),
+    "rpg_op_stream_fill": (_i32, [_vp, _i64, _u32]),
     "rpg_op_f16_sweep": (_i32, [_vp]),
     "rpg_ops_profile_start": (_i32, [_i32]),
     "rpg_ops_profile_stop": (_i32, []),
@@ -284,6 +285,10 @@ def GpuQkNormRopeKv(q, k, v, q_norm, k_norm, n_heads: int, n_kv_heads: int, head
 
 def GpuStreamCopy(src, dst, nbytes: int) -> None:
     _check(load_library().rpg_op_stream_copy(_addr(src, nbytes, name="src"), _addr(dst, nbytes, name="dst"), nbytes))
+
+
+def GpuStreamFill(dst, nbytes: int, pattern: int) -> None:
+    _check(load_library().rpg_op_stream_fill(_addr(dst, nbytes, name="dst"), nbytes, pattern & 0xFFFFFFFF))
 
 
 def profile_start(max_launches: int) -> None:

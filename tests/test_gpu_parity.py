@@ -439,6 +439,18 @@ def test_stream_copy(gpu):
     assert torch.equal(src, dst)
 
 
+def test_stream_fill(gpu):
+    import torch
+
+    case("stream fill 64 MiB + 16 B inside a larger buffer")
+    buf = torch.zeros((16 << 20) + 12, dtype=torch.int32, device="cuda")
+    n = (16 << 20) + 4
+    gpu.GpuStreamFill(buf[4:4 + n], n * 4, 0x89ABCDEF)
+    got = buf.cpu().numpy().view(np.uint32)
+    assert np.all(got[4:4 + n] == 0x89ABCDEF)
+    assert not got[:4].any() and not got[4 + n:].any()
+
+
 # ----------------------------------------------------------------------------- graph capture
 
 
