@@ -114,6 +114,14 @@ RPG_OPS_API int32_t rpg_op_vec_add_inplace(float* a, const float* b, int64_t n);
 RPG_OPS_API int32_t rpg_op_embedding_lookup(uint32_t type, const uint8_t* emb, int64_t rows, int64_t cols,
                                             const int32_t* toks, int64_t seq, float* x);
 
+/* out[t * rows + r] = dot(row r of the [rows][cols] matrix w of `type`, row t of
+ * x), i.e. OUT[n_tokens, rows] = X[n_tokens, cols] . W^T. Weights are dequantised
+ * bit-exactly and summed in fp32.
+ * Replaces: GpuMatMulQuant, src/kernels_gpu.h:42-49 (its GpuTensor argument
+ * flattened to type / data / rows / cols). */
+RPG_OPS_API int32_t rpg_op_matmul_quant(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols,
+                                        const float* x, int64_t n_tokens, float* out);
+
 /* ---------------------------------------------------------------- fused operators */
 
 /* x[r] += d[r] (bit-exact fp32 add, written back), then out[r] = RMSNorm(x[r]) * w,

@@ -6,6 +6,7 @@
 #include "cpu_ref.h"
 
 #include <math.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* ------------------------------------------------------------------ fp16 */
@@ -180,6 +181,34 @@ int ora_dequantize_row(uint32_t type, const uint8_t* src, int64_t n_elems, float
     default:
       return -1;
   }
+}
+
+/* src/kernels_gpu.cu:166-560 (MatMulQuantKernel and its Q4_K / Q6_K forms):
+ * OUT[t * rows + r] = dot(dequantised row r of W, row t of X). The reference sums
+ * in fp32 in a thread-strided order plus a tree; here every product is exact in
+ * double (fp32 x fp32 fits in 48 bits) and the sum is taken in double. */
+int ora_matmul_quant_f64(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols, const float* x,
+                         int64_t n_tokens, double* out, double* absdot) {
+  const int64_t rb = ora_type_row_bytes(type, cols);
+  if (rb < 0 || rows < 0 || n_tokens < 0) return -1;
+  float* row = (float*)malloc((size_t)(cols > 0 ? cols : 1) * sizeof(float));
+  if (row == NULL) return -1;
+  for (int64_t r = 0; r < rows; ++r) {
+    ora_dequantize_row(type, w + r * rb, cols, row);
+    for (int64_t t = 0; t < n_tokens; ++t) {
+      const float* xt = x + t * cols;
+      double s = 0.0, a = 0.0;
+      for (int64_t e = 0; e < cols; ++e) {
+        const double p = (double)row[e] * (double)xt[e];
+        s += p;
+        a += fabs(p);
+      }
+      out[t * rows + r] = s;
+      if (absdot != NULL) absdot[t * rows + r] = a;
+    }
+  }
+  free(row);
+  return 0;
 }
 
 /* src/kernels_gpu.cu:877-889 (x[t] = dequantised row toks[t]); ids outside

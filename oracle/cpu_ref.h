@@ -28,6 +28,9 @@
  *                        (tools/kv_map_check.cu:51-186) plus "untouched stays 0"
  *   ora_silu_mul         silu(0)=0, v->-inf gives -0, v>>0 gives v*up, numpy f64
  *   ora_vec_add          numpy float32 addition, bitwise
+ *   ora_matmul_quant_f64 numpy float64 dot products (BLAS) of the dequantised
+ *                        matrix, one-hot inputs select exact matrix columns,
+ *                        linearity in X
  */
 #ifndef RPG_ORACLE_CPU_REF_H
 #define RPG_ORACLE_CPU_REF_H
@@ -53,6 +56,16 @@ int64_t ora_type_row_bytes(uint32_t type, int64_t n_elems); /* <0 if unsupported
 int ora_dequantize_row(uint32_t type, const uint8_t* src, int64_t n_elems, float* dst);
 int ora_embedding_lookup(uint32_t type, const uint8_t* emb, int64_t rows, int64_t cols, const int32_t* toks,
                          int64_t seq, float* x);
+
+/* ---- quantized matmul ------------------------------------------------------ */
+/* OUT[t][r] = sum_e W[r][e] * X[t][e] for the raw [rows][row_bytes] matrix W
+ * (src/kernels_gpu.h:42-49 GpuMatMulQuant: OUT = X . W^T, OUT [n_tokens][rows]).
+ * Each row is dequantised exactly (ora_dequantize_row) and the products are
+ * summed in double, so `out` is the dot product to double accuracy; `absdot`
+ * (may be NULL) receives sum_e |W[r][e] * X[t][e]|, the scale of any fp32
+ * summation error. Returns 0, or -1 for an unsupported type / shape. */
+int ora_matmul_quant_f64(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols, const float* x,
+                         int64_t n_tokens, double* out, double* absdot);
 
 /* ---- layer ops, fp32 in the reference's op order -------------------------- */
 void ora_rms_norm(const float* x, const float* w, int64_t n_rows, int64_t n, int64_t stride, float eps, float* out);

@@ -29,6 +29,7 @@ _SIGS = {
     "ora_type_row_bytes": (_i64, [_u32, _i64]),
     "ora_dequantize_row": (ctypes.c_int, [_u32, _vp, _i64, _vp]),
     "ora_embedding_lookup": (ctypes.c_int, [_u32, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "ora_matmul_quant_f64": (ctypes.c_int, [_u32, _vp, _i64, _i64, _vp, _i64, _vp, _vp]),
     "ora_rms_norm": (None, [_vp, _vp, _i64, _i64, _i64, _f32, _vp]),
     "ora_build_rope_table": (None, [_i32, _f64, _i64, _vp]),
     "ora_rope": (None, [_vp, _i32, _i32, _vp, _i64, _i64]),
@@ -144,6 +145,18 @@ def embedding_lookup(ggml_type: int, table: np.ndarray, rows: int, cols: int, to
     out = np.empty((toks.size, cols), dtype=np.float32)
     assert lib().ora_embedding_lookup(ggml_type, _p(table), rows, cols, _p(toks), toks.size, _p(out)) == 0
     return out
+
+
+def matmul_quant_f64(ggml_type: int, w: np.ndarray, rows: int, cols: int, x: np.ndarray):
+    """(out, absdot), both float64 [n_tokens, rows]: OUT = X . W^T to double accuracy and
+    sum |w * x| per output (the scale of fp32 summation error)."""
+    w = np.ascontiguousarray(w, dtype=np.uint8)
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(-1, cols)
+    assert w.size >= rows * row_bytes(ggml_type, cols)
+    out = np.empty((x.shape[0], rows), dtype=np.float64)
+    absdot = np.empty_like(out)
+    assert lib().ora_matmul_quant_f64(ggml_type, _p(w), rows, cols, _p(x), x.shape[0], _p(out), _p(absdot)) == 0
+    return out, absdot
 
 
 def ref_dequantize_row(ggml_type: int, raw: np.ndarray, n: int):

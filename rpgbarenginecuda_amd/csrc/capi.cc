@@ -114,6 +114,11 @@ int32_t rpg_op_embedding_lookup(uint32_t type, const uint8_t* emb, int64_t rows,
   return Guard([&] { rpg::GpuEmbeddingLookupRaw(type, emb, rows, cols, toks, seq, x); });
 }
 
+int32_t rpg_op_matmul_quant(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols, const float* x,
+                            int64_t n_tokens, float* out) {
+  return Guard([&] { rpg::GpuMatMulQuantRaw(type, w, rows, cols, x, n_tokens, out); });
+}
+
 int32_t rpg_op_add_rms_norm(float* x, const float* d, const float* w, int64_t n_rows, int64_t n, float eps,
                             float* out) {
   return Guard([&] { rpg::GpuAddRmsNorm(x, d, w, n_rows, n, eps, out); });

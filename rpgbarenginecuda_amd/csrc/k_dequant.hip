@@ -25,35 +25,20 @@
 #include "dev_util.h"
 #include "kernels_gpu.h"
 #include "launch.h"
+#include "quant_dev.h"
 
 namespace rpg {
 namespace {
 
+using dev::ByteOf;
+using dev::DeqElemAny;
 using dev::HalfBitsToFloat;
+using dev::ScaleMinK4;
 using dev::StoreStream4;
 
 constexpr int kBlock = 256;
 
 bool Aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
-
-__device__ __forceinline__ uint32_t ByteOf(uint32_t word, int i) { return (word >> (8 * i)) & 0xFFu; }
-
-// Byte i (0..11) of the Q4_K packed scales held in three little-endian words.
-__device__ __forceinline__ uint32_t ScaleByte(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
-  const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
-  return ByteOf(w, i & 3);
-}
-
-// 6-bit (scale, min) of sub-block j (0..7) from the 12 packed bytes.
-__device__ __forceinline__ void ScaleMinK4(int j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t* sc, uint32_t* m) {
-  if (j < 4) {
-    *sc = ScaleByte(s0, s1, s2, j) & 63u;
-    *m = ScaleByte(s0, s1, s2, j + 4) & 63u;
-  } else {
-    *sc = (ScaleByte(s0, s1, s2, j + 4) & 0x0Fu) | ((ScaleByte(s0, s1, s2, j - 4) >> 6) << 4);
-    *m = (ScaleByte(s0, s1, s2, j + 4) >> 4) | ((ScaleByte(s0, s1, s2, j) >> 6) << 4);
-  }
-}
 
 // One lane's share (8 elements) of a Q4_K block; blk must be 16-byte aligned.
 __device__ __forceinline__ void DecodeQ4KLane(const uint8_t* blk, int j, float* out_blk) {
@@ -191,48 +176,6 @@ __global__ __launch_bounds__(kBlock) void GatherF32Kernel(const float* __restric
   float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
   if (tok >= 0 && tok < rows) v = dev::Load4(emb + tok * cols + e);
   StoreStream4(x + i, v);
-}
-
-// Per-element fallback for any alignment: element i of the gathered output.
-__device__ float DeqElemAny(uint32_t type, const uint8_t* blk, int e) {
-  if (type == kGgmlF32) {
-    const uint32_t u = static_cast<uint32_t>(blk[4 * e]) | (static_cast<uint32_t>(blk[4 * e + 1]) << 8) |
-                       (static_cast<uint32_t>(blk[4 * e + 2]) << 16) | (static_cast<uint32_t>(blk[4 * e + 3]) << 24);
-    return __uint_as_float(u);
-  }
-  if (type == kGgmlQ4_K) {
-    const int sub = e >> 5;
-    const int l = e & 31;
-    const int g = sub >> 1;
-    const uint8_t qb = blk[16 + 32 * g + l];
-    const uint32_t raw = (sub & 1) ? (qb >> 4) : (qb & 0x0Fu);
-    const uint8_t* s = blk + 4;
-    uint32_t sc, m;
-    if (sub < 4) {
-      sc = s[sub] & 63u;
-      m = s[sub + 4] & 63u;
-    } else {
-      sc = (s[sub + 4] & 0x0Fu) | ((s[sub - 4] >> 6) << 4);
-      m = (s[sub + 4] >> 4) | ((s[sub] >> 6) << 4);
-    }
-    const float d = HalfBitsToFloat(static_cast<uint32_t>(blk[0]) | (static_cast<uint32_t>(blk[1]) << 8));
-    const float dmin = HalfBitsToFloat(static_cast<uint32_t>(blk[2]) | (static_cast<uint32_t>(blk[3]) << 8));
-    const float d1 = d * static_cast<float>(sc);
-    const float m1 = dmin * static_cast<float>(m);
-    return d1 * static_cast<float>(raw) - m1;
-  }
-  // Q6_K
-  const int half = e >> 7;
-  const int r = e & 127;
-  const int quarter = r >> 5;
-  const int l = r & 31;
-  const uint8_t qlb = blk[64 * half + l + ((quarter & 1) ? 32 : 0)];
-  const uint32_t nib = quarter < 2 ? (qlb & 0x0Fu) : (qlb >> 4);
-  const uint32_t hi2 = (blk[128 + 32 * half + l] >> (2 * quarter)) & 3u;
-  const int q = static_cast<int>(nib | (hi2 << 4)) - 32;
-  const int8_t sc = static_cast<int8_t>(blk[192 + 8 * half + (l >> 4) + 2 * quarter]);
-  const float d = HalfBitsToFloat(static_cast<uint32_t>(blk[208]) | (static_cast<uint32_t>(blk[209]) << 8));
-  return (d * static_cast<float>(sc)) * static_cast<float>(q);
 }
 
 __global__ __launch_bounds__(kBlock) void GatherElemKernel(uint32_t type, const uint8_t* __restrict__ emb,

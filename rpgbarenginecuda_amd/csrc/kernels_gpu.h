@@ -160,6 +160,19 @@ void GpuQkNormRopeKv(float* q, float* k, const float* v, const float* q_norm, co
 void GpuEmbeddingLookupRaw(uint32_t type, const uint8_t* emb_dev, int64_t rows, int64_t cols,
                            const int32_t* toks_dev, int64_t seq, float* x_dev);
 
+// ---------------------------------------------------------------- quantised matmul
+
+// OUT[t, r] = dot(row r of W, row t of X), i.e. OUT = X . W^T (src/kernels_gpu.h:42-49):
+//   W   [rows, cols] quantised (raw GGUF bytes on the device, Q4_K / Q6_K / F32)
+//   X   [n_tokens, cols] fp32, row-major
+//   OUT [n_tokens, rows] fp32, row-major
+// Weights are dequantised bit-exactly and accumulated in fp32 (fused multiply-add).
+void GpuMatMulQuant(const GpuTensor& w, const float* X_dev, int64_t n_tokens, float* OUT_dev);
+
+// The same on a raw (non-owning) weight pointer; GpuMatMulQuant forwards here.
+void GpuMatMulQuantRaw(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_t cols, const float* x_dev,
+                       int64_t n_tokens, float* out_dev);
+
 // ---------------------------------------------------------------- measurement / verification
 
 // Streaming copy of `bytes` (multiple of 16) used to calibrate bandwidth and

@@ -46,6 +46,7 @@ SIGNATURES = {
     "rpg_op_silu_mul_inplace": (_i32, [_vp, _vp, _i64]),
     "rpg_op_vec_add_inplace": (_i32, [_vp, _vp, _i64]),
     "rpg_op_embedding_lookup": (_i32, [_u32, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "rpg_op_matmul_quant": (_i32, [_u32, _vp, _i64, _i64, _vp, _i64, _vp]),
     "rpg_op_add_rms_norm": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _vp]),
     "rpg_op_qk_norm_rope_kv": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _i64, _f32,
                                       _vp, _vp, _i64, _i32]),
@@ -252,6 +253,15 @@ def GpuEmbeddingLookup(emb: GpuTensor, toks, seq: int, x) -> None:
     _check(load_library().rpg_op_embedding_lookup(
         emb.type, _addr(emb.buf, emb.rows * emb.row_bytes(), name="emb"), emb.rows, emb.cols,
         _addr(toks, 4 * seq, torch.int32, "toks"), seq, _addr(x, 4 * seq * emb.cols, torch.float32, "x")))
+
+
+def GpuMatMulQuant(w: GpuTensor, x, n_tokens: int, out) -> None:
+    """OUT[n_tokens, rows] = X[n_tokens, cols] . W^T (reference GpuMatMulQuant, src/kernels_gpu.h:42-49)."""
+    torch = _t()
+    _check(load_library().rpg_op_matmul_quant(
+        w.type, _addr(w.buf, w.rows * w.row_bytes(), name="w"), w.rows, w.cols,
+        _addr(x, 4 * n_tokens * w.cols, torch.float32, "x"), n_tokens,
+        _addr(out, 4 * n_tokens * w.rows, torch.float32, "out")))
 
 
 # ----------------------------------------------------------------------------- fused operators

@@ -1,0 +1,173 @@
+"""Quantised matmul (GpuMatMulQuant, src/kernels_gpu.h:42-49) on the GPU against the
+float64 oracle.
+
+Bar: the GPU sums fp32 products of bit-exact dequantised weights, so its error
+against the exact dot product is bounded by fp32 summation error:
+    |gpu - exact| <= D * 2^-24 * sum_e |w_e * x_e|
+with D the longest chain of roundings from one product to the result. Any
+kernel that keeps at least 8 independent partial sums of cols / 8 terms each and
+combines them by a tree of depth <= 7 has D <= cols / 8 + 7; the kernels here
+(at most 32 * ceil(cols / 2048) sequential fused multiply-adds per lane and a
+64-lane butterfly) stay well inside it. A dropped, doubled or misplaced term
+breaks the bound by many orders of magnitude.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import synth
+
+pytestmark = pytest.mark.gpu
+
+U = 2.0 ** -24
+
+
+def case(name: str) -> None:
+    print(f"\n[case] {name}", flush=True)
+
+
+def dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def last_error(gpu) -> str:
+    msg = gpu.load_library().rpg_ops_last_error()
+    return msg.decode("utf-8", "replace") if msg else ""
+
+
+def check(got, exact, absdot, cols):
+    bound = (cols // 8 + 7) * U * absdot + 1e-37
+    err = np.abs(got.astype(np.float64) - exact)
+    worst = float(np.max(err / np.maximum(bound, 1e-300)))
+    assert np.all(err <= bound), f"max error / bound = {worst:.3g}"
+    return worst
+
+
+SHAPES = [
+    # (type, rows, cols, n_tokens): Qwen3-1.7B / 4B decode matrices, small batches, ragged tiles
+    (12, 2048, 2048, 1),     # attn_q / attn_o
+    (12, 1024, 2048, 1),     # attn_k
+    (14, 1024, 2048, 1),     # attn_v (Q6_K in Q4_K_M files)
+    (12, 6144, 2048, 1),     # ffn_gate / ffn_up
+    (14, 2048, 6144, 1),     # ffn_down (Q6_K)
+    (12, 2048, 6144, 1),     # ffn_down (Q4_K)
+    (12, 9728, 2560, 1),     # 4B ffn_gate: 10 blocks per row (not a multiple of 8), 2 rows per wave
+    (14, 2560, 9728, 1),     # 4B ffn_down: 38 blocks per row
+    (12, 40000, 2048, 1),    # 4 rows per wave
+    (14, 40001, 2048, 1),    # 4 rows per wave, ragged last wave
+    (12, 2048, 2048, 2),
+    (14, 2048, 2048, 3),
+    (12, 1000, 2048, 4),
+    (14, 1000, 2560, 5),
+    (12, 777, 2048, 8),
+    (14, 513, 2048, 13),     # two tiles of 8, the second ragged
+    (12, 256, 256, 21),      # the CPU-runnable n = 21
+]
+
+
+@pytest.mark.parametrize("t,rows,cols,n", SHAPES)
+def test_matmul_quant_vs_f64(gpu, ora, t, rows, cols, n):
+    import torch
+
+    case(f"matmul type={t} rows={rows} cols={cols} n={n}")
+    rng = np.random.default_rng(700 + rows + cols + n + t)
+    w = synth.quant_table(rng, t, rows, cols)
+    x = rng.normal(0, 1, (n, cols)).astype(np.float32)
+    out = torch.full((n, rows), np.nan, dtype=torch.float32, device="cuda")
+    gpu.GpuMatMulQuant(gpu.GpuTensor(dev(w), t, rows, cols), dev(x), n, out)
+    exact, absdot = ora.matmul_quant_f64(t, w, rows, cols, x)
+    check(host(out), exact, absdot, cols)
+
+
+def test_matmul_quant_lm_head_shape(gpu, ora):
+    """The 1.7B output projection: [151936, 2048] Q6_K at n = 1."""
+    import torch
+
+    t, rows, cols = 14, 151936, 2048
+    case(f"matmul lm_head rows={rows}")
+    rng = np.random.default_rng(790)
+    w = synth.quant_table(rng, t, rows, cols)
+    x = rng.normal(0, 1, (1, cols)).astype(np.float32)
+    out = torch.empty((1, rows), dtype=torch.float32, device="cuda")
+    wd = dev(w)
+    gpu.GpuMatMulQuant(gpu.GpuTensor(wd, t, rows, cols), dev(x), 1, out)
+    exact, absdot = ora.matmul_quant_f64(t, w, rows, cols, x)
+    got = host(out)
+    check(got, exact, absdot, cols)
+    # deterministic: a second call gives the same bits
+    out2 = torch.empty_like(out)
+    gpu.GpuMatMulQuant(gpu.GpuTensor(wd, t, rows, cols), dev(x), 1, out2)
+    assert np.array_equal(host(out2).view(np.uint32), got.view(np.uint32))
+
+
+@pytest.mark.parametrize("t,w_off,x_off", [(12, 4, 0), (14, 1, 0), (14, 2, 0), (12, 0, 1), (0, 0, 0), (0, 4, 3)])
+def test_matmul_quant_generic_paths(gpu, ora, t, w_off, x_off):
+    """F32 matrices, weights that are not 16- (Q4_K) / 2-byte (Q6_K) aligned and
+    unaligned activations take the per-element kernel; same bar."""
+    import torch
+
+    rows, cols, n = 300, 512, 3
+    case(f"matmul generic type={t} w_off={w_off} x_off={x_off}")
+    rng = np.random.default_rng(800 + t + w_off + x_off)
+    w = synth.quant_table(rng, t, rows, cols)
+    wbuf = np.zeros(w.size + 16, np.uint8)
+    wbuf[w_off:w_off + w.size] = w
+    x = rng.normal(0, 1, (n, cols)).astype(np.float32)
+    xbuf = np.zeros(x.size + 4, np.float32)
+    xbuf[x_off:x_off + x.size] = x.reshape(-1)
+    wd, xd = dev(wbuf), dev(xbuf)
+    out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
+    rc = gpu.load_library().rpg_op_matmul_quant(t, wd.data_ptr() + w_off, rows, cols, xd.data_ptr() + 4 * x_off, n,
+                                                 out.data_ptr())
+    assert rc == 0, last_error(gpu)
+    exact, absdot = ora.matmul_quant_f64(t, w, rows, cols, x)
+    check(host(out), exact, absdot, cols)
+
+
+def test_matmul_quant_one_hot_selects_columns(gpu, ora):
+    """One-hot activations: every output is a single product w * 1.0, so the GPU
+    result equals the dequantised weight bit for bit (no summation error exists)."""
+    import torch
+
+    rows, cols = 1000, 2048
+    for t in (12, 14):
+        case(f"matmul one-hot type={t}")
+        rng = np.random.default_rng(810 + t)
+        w = synth.quant_table(rng, t, rows, cols)
+        picks = [0, 31, 32, 255, 256, 1000, 2047]
+        x = np.zeros((len(picks), cols), np.float32)
+        x[np.arange(len(picks)), picks] = 1.0
+        out = torch.empty((len(picks), rows), dtype=torch.float32, device="cuda")
+        gpu.GpuMatMulQuant(gpu.GpuTensor(dev(w), t, rows, cols), dev(x), len(picks), out)
+        rb = ora.row_bytes(t, cols)
+        wd = np.stack([ora.dequantize_row(t, w[r * rb:(r + 1) * rb], cols) for r in range(rows)])
+        want = wd[:, picks].T
+        got = host(out)
+        # +0 and -0 products sum to +0 in fp32 FMA chains; compare values, not bits, for zeros
+        assert np.array_equal(got == 0, want == 0)
+        nz = want != 0
+        assert np.array_equal(got[nz].view(np.uint32), want[nz].view(np.uint32))
+
+
+def test_matmul_quant_rejects_bad_shapes(gpu):
+    import torch
+
+    case("matmul host errors")
+    w = torch.zeros(144 * 4, dtype=torch.uint8, device="cuda")
+    x = torch.zeros(512, dtype=torch.float32, device="cuda")
+    out = torch.zeros(8, dtype=torch.float32, device="cuda")
+    L = gpu.load_library()
+    assert L.rpg_op_matmul_quant(12, w.data_ptr(), 2, 300, x.data_ptr(), 1, out.data_ptr()) != 0
+    assert "multiple of the block size" in last_error(gpu)
+    assert L.rpg_op_matmul_quant(12, w.data_ptr(), 2, 512, x.data_ptr(), 0, out.data_ptr()) != 0
+    assert L.rpg_op_matmul_quant(99, w.data_ptr(), 2, 512, x.data_ptr(), 1, out.data_ptr()) != 0

@@ -236,6 +236,53 @@ def test_embedding_lookup_is_rowwise_dequant(ora):
                 assert np.all(out[i].view(np.uint32) == 0)
 
 
+# ----------------------------------------------------------------------------- quantized matmul
+
+
+def _dequant_matrix(ora, t, w, rows, cols):
+    rb = ora.row_bytes(t, cols)
+    return np.stack([ora.dequantize_row(t, w[r * rb:(r + 1) * rb], cols) for r in range(rows)])
+
+
+@pytest.mark.parametrize("t", [0, 12, 14])
+def test_matmul_quant_f64_vs_numpy_blas(ora, t):
+    """OUT = X . W^T against numpy's float64 matmul of the dequantised matrix (an
+    independent BLAS summation), and absdot against |W| . |X|^T."""
+    rng = np.random.default_rng(600 + t)
+    rows, cols, n = 23, 768, 3
+    w = synth.quant_table(rng, t, rows, cols)
+    x = rng.normal(0, 1, (n, cols)).astype(np.float32)
+    out, absdot = ora.matmul_quant_f64(t, w, rows, cols, x)
+    wd = _dequant_matrix(ora, t, w, rows, cols).astype(np.float64)
+    want = x.astype(np.float64) @ wd.T
+    assert out.shape == (n, rows)
+    assert np.allclose(out, want, rtol=1e-12, atol=1e-12 * np.max(np.abs(want)))
+    assert np.allclose(absdot, np.abs(x.astype(np.float64)) @ np.abs(wd).T, rtol=1e-12)
+
+
+def test_matmul_quant_f64_one_hot_and_linearity(ora):
+    """One-hot X rows select exact matrix columns (bit-exact, no rounding is
+    possible); OUT is linear in X (a dropped or doubled term breaks both)."""
+    rng = np.random.default_rng(610)
+    rows, cols = 9, 512
+    for t in (12, 14):
+        w = synth.quant_table(rng, t, rows, cols)
+        wd = _dequant_matrix(ora, t, w, rows, cols)
+        picks = [0, 1, 255, 256, 300, 511]
+        x = np.zeros((len(picks), cols), np.float32)
+        x[np.arange(len(picks)), picks] = 1.0
+        out, _ = ora.matmul_quant_f64(t, w, rows, cols, x)
+        assert np.array_equal(out, wd[:, picks].T.astype(np.float64))
+        a = rng.normal(0, 1, (1, cols)).astype(np.float32)
+        b = rng.normal(0, 1, (1, cols)).astype(np.float32)
+        a[:, cols // 2:] = 0.0          # disjoint supports: a + b is exact in fp32
+        b[:, :cols // 2] = 0.0
+        oa, _ = ora.matmul_quant_f64(t, w, rows, cols, a)
+        ob, _ = ora.matmul_quant_f64(t, w, rows, cols, b)
+        oc, _ = ora.matmul_quant_f64(t, w, rows, cols, 2.0 * a + b)   # power-of-two scaling is exact
+        assert np.allclose(oc, 2.0 * oa + ob, rtol=1e-13, atol=1e-13 * np.max(np.abs(oc)))
+
+
 # ----------------------------------------------------------------------------- RMSNorm
 
 
