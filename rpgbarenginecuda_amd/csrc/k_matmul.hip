@@ -53,18 +53,9 @@ __device__ __forceinline__ float WaveSumF(float v) {
   return v;
 }
 
-// 8 bytes at a 2-byte aligned address, from aligned dwords (a Q6_K block starts
-// at a multiple of 210 bytes). The third dword is read only when the address is
-// not 4-byte aligned, so no byte past p + 9 is ever touched.
-__device__ __forceinline__ uint2 Load8Align2(const uint8_t* p) {
-  const uintptr_t a = reinterpret_cast<uintptr_t>(p);
-  const uint32_t* base = reinterpret_cast<const uint32_t*>(a & ~static_cast<uintptr_t>(3));
-  const bool odd = (a & 3) != 0;
-  const uint32_t w0 = base[0];
-  const uint32_t w1 = base[1];
-  const uint32_t w2 = base[odd ? 2 : 1];
-  return odd ? make_uint2(__builtin_amdgcn_alignbyte(w1, w0, 2), __builtin_amdgcn_alignbyte(w2, w1, 2))
-             : make_uint2(w0, w1);
+// 8 bytes starting `sh` (0 or 2) bytes into the 12-byte window w0..w2.
+__device__ __forceinline__ uint2 Window8(uint3 w, uint32_t sh) {
+  return make_uint2(__builtin_amdgcn_alignbyte(w.y, w.x, sh), __builtin_amdgcn_alignbyte(w.z, w.y, sh));
 }
 
 // ---------------------------------------------------------------- per-lane block decode
@@ -105,6 +96,12 @@ struct LaneBytes {
   uint32_t d6;  // Q6_K: d (f16 bits)
 };
 
+// Q6_K blocks start at multiples of 210 bytes, so a block base is only 2-byte
+// aligned. Each 8-byte field is read as the three aligned dwords around it
+// (one dwordx3 load from the 4-aligned base ab = blk - sh) and byte-aligned.
+// Every window lies inside the block except up to 2 bytes before its start,
+// which share an aligned dword (hence a page) with the block's first bytes, so
+// no window can touch memory outside pages the tensor occupies.
 template <uint32_t kType>
 __device__ __forceinline__ LaneBytes LoadLaneBytes(const uint8_t* __restrict__ blk, int s) {
   LaneBytes r;
@@ -117,10 +114,21 @@ __device__ __forceinline__ LaneBytes LoadLaneBytes(const uint8_t* __restrict__ b
   } else {
     const int h = s >> 2;
     const int lq = 8 * (s & 3);
-    const uint2 ql0 = Load8Align2(blk + 64 * h + lq);
-    const uint2 ql1 = Load8Align2(blk + 64 * h + 32 + lq);
-    const uint2 qh = Load8Align2(blk + 128 + 32 * h + lq);
-    const uint2 sc = Load8Align2(blk + 192 + 8 * h);
+    const uint32_t sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(blk) & 3u);
+    const uint8_t* ab = blk - sh;
+    const uint3 f0 = *reinterpret_cast<const uint3*>(ab + 64 * h + lq);
+    const uint3 f1 = *reinterpret_cast<const uint3*>(ab + 64 * h + 32 + lq);
+    const uint3 fh = *reinterpret_cast<const uint3*>(ab + 128 + 32 * h + lq);
+    // scales: dwords at ab + 192 + 8h, + 4, and + 8 (sh == 2) or + 4 again (sh == 0),
+    // so the window never passes byte 209 of the block; the third address is
+    // arithmetic, not a select, so all loads stay unconditional.
+    const uint8_t* sp = ab + 192 + 8 * h;
+    const uint3 fs = make_uint3(*reinterpret_cast<const uint32_t*>(sp), *reinterpret_cast<const uint32_t*>(sp + 4),
+                                *reinterpret_cast<const uint32_t*>(sp + 4 + 2 * sh));
+    const uint2 ql0 = Window8(f0, sh);
+    const uint2 ql1 = Window8(f1, sh);
+    const uint2 qh = Window8(fh, sh);
+    const uint2 sc = Window8(fs, sh);
     r.a = make_uint4(ql0.x, ql0.y, ql1.x, ql1.y);
     r.b = make_uint4(qh.x, qh.y, sc.x, sc.y);
     r.d6 = *reinterpret_cast<const uint16_t*>(blk + 208);
@@ -128,7 +136,29 @@ __device__ __forceinline__ LaneBytes LoadLaneBytes(const uint8_t* __restrict__ b
   return r;
 }
 
+// Byte k of a word as an exact float (v_cvt_f32_ubyte{0..3}).
+__device__ __forceinline__ float UByteF(uint32_t w, int k) { return static_cast<float>((w >> (8 * k)) & 0xFFu); }
+
+// Hides a packed-quant word's known-zero bits from the optimiser, which would
+// otherwise extract each field with a bit-field extract and then convert it (two
+// instructions per weight) instead of converting the byte directly (one). Emits
+// no instruction.
+__device__ __forceinline__ uint32_t Opaque(uint32_t w) {
+  __asm__("" : "+v"(w));
+  return w;
+}
+
 // The lane's 32 weights, in the same order as LoadLaneX's activations.
+//
+// Bit-exact with the reference's separately rounded ops, with one fused
+// multiply-add per weight: d and dmin are fp16 values (11 significant bits), the
+// 6-bit scale / min and the 4- or 6-bit quants are small integers, so
+//   Q4_K: d * sc and dmin * m need <= 17 bits, (d * sc) * q <= 21 bits: all exact
+//         in fp32, and fma(d * sc, q, -(dmin * m)) rounds once, exactly where
+//         fl(fl(d * sc) * q) - fl(dmin * m) does;
+//   Q6_K: d * sc needs <= 18 bits and (d * sc) * (q - 32) <= 24 bits: exact, and
+//         fma(d * sc, q, -32 * (d * sc)) equals it (32 * ds is exact too).
+// Infinities, NaNs and signed zeros come out the same way in both forms.
 template <uint32_t kType>
 __device__ __forceinline__ void DecodeLane(const LaneBytes& r, int s, float (&wv)[32]) {
   if (kType == kGgmlQ4_K) {
@@ -139,15 +169,19 @@ __device__ __forceinline__ void DecodeLane(const LaneBytes& r, int s, float (&wv
     ScaleMinK4(2 * g, r.a.y, r.a.z, r.a.w, &sc0, &m0);
     ScaleMinK4(2 * g + 1, r.a.y, r.a.z, r.a.w, &sc1, &m1);
     const float d1 = d * static_cast<float>(sc0);
-    const float n1 = dmin * static_cast<float>(m0);
+    const float n1 = -(dmin * static_cast<float>(m0));
     const float d2 = d * static_cast<float>(sc1);
-    const float n2 = dmin * static_cast<float>(m1);
+    const float n2 = -(dmin * static_cast<float>(m1));
     const uint32_t qw[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const uint32_t byte = ByteOf(qw[i >> 2], i & 3);
-      wv[i] = d1 * static_cast<float>(byte & 0x0Fu) - n1;
-      wv[16 + i] = d2 * static_cast<float>(byte >> 4) - n2;
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t lo = Opaque(qw[k] & 0x0F0F0F0Fu);
+      const uint32_t hi = Opaque((qw[k] >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        wv[4 * k + j] = __builtin_fmaf(d1, UByteF(lo, j), n1);
+        wv[16 + 4 * k + j] = __builtin_fmaf(d2, UByteF(hi, j), n2);
+      }
     }
   } else {
     const int is = (s & 3) >> 1;  // (l >> 4) for l = 8(s % 4) .. +7
@@ -160,12 +194,15 @@ __device__ __forceinline__ void DecodeLane(const LaneBytes& r, int s, float (&wv
       const int si = is + 2 * q;
       const int8_t sc = static_cast<int8_t>(ByteOf(scw[si >> 2], si & 3));
       const float ds = d * static_cast<float>(sc);
-      const int shift = q < 2 ? 0 : 4;
+      const float off = -32.0f * ds;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t nib = (ByteOf(ql[q & 1][i >> 2], i & 3) >> shift) & 0x0Fu;
-        const uint32_t hi2 = (ByteOf(qh[i >> 2], i & 3) >> (2 * q)) & 3u;
-        wv[8 * q + i] = ds * static_cast<float>(static_cast<int>(nib | (hi2 << 4)) - 32);
+      for (int k = 0; k < 2; ++k) {
+        // the 6-bit quants of 4 consecutive elements, one per byte
+        const uint32_t nib = ((q < 2 ? ql[q & 1][k] : ql[q & 1][k] >> 4)) & 0x0F0F0F0Fu;
+        const uint32_t hi2 = (2 * q >= 4 ? qh[k] >> (2 * q - 4) : qh[k] << (4 - 2 * q)) & 0x30303030u;
+        const uint32_t q6 = Opaque(nib | hi2);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wv[8 * q + 4 * k + j] = __builtin_fmaf(ds, UByteF(q6, j), off);
       }
     }
   }
@@ -253,6 +290,213 @@ __global__ __launch_bounds__(kMmBlock) void MatMulQuantKernel(const uint8_t* __r
   }
 }
 
+// ---------------------------------------------------------------- decode (one token)
+//
+// One token, rows of at most 16 super-blocks (cols <= 4096: every Qwen3-1.7B /
+// 4B matrix except ffn_down): persistent waves. Each lane loads its 32 (or 64)
+// activations once and keeps them in registers, then the wave walks rows
+// wave, wave + W, ... (W = all waves of the grid), RI rows per step, with the
+// next step's weight bytes in flight while the current ones are decoded.
+//
+// Per-weight work is one byte-to-float conversion and one fused multiply-add:
+//   Q6_K: the 6-bit quant q becomes the signed byte 4(q - 32) = ((q << 2) ^ 0x80)
+//         (converted exactly with a sign-extending byte select), and a group of 8
+//         weights sharing a scale contributes (d * sc / 4) * sum_i 4(q_i - 32) x_i.
+//         d * sc / 4 is exact, so this differs from summing the dequantised
+//         weights w_i = d * sc * (q_i - 32) (also exact) only in rounding order.
+//   Q4_K: w_i = d1 q_i - m1 per sub-block, so a lane's 16 weights of one
+//         sub-block contribute d1 * sum_i q_i x_i - m1 * sum_i x_i, with the
+//         activation sums taken once per kernel. The two products can partly
+//         cancel, so the error bound of this form is in terms of
+//         sum_i (|d1 q_i| + |m1|) |x_i| rather than sum_i |w_i x_i|.
+// The RI row sums are then reduced together: two cross-half exchanges leave each
+// 16-lane row of the wave with one of the RI rows, and DPP steps finish the sum.
+
+__device__ __forceinline__ float DppAdd(float v, int ctrl_sel) {
+  int m;
+  switch (ctrl_sel) {
+    case 0: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false); break;   // quad_perm 1,0,3,2
+    case 1: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false); break;   // quad_perm 2,3,0,1
+    case 2: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false); break;  // row_half_mirror
+    default: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false); break; // row_mirror
+  }
+  return v + __int_as_float(m);
+}
+
+// Sum over the 16 lanes of each DPP row; every lane of the row gets the total.
+__device__ __forceinline__ float RowSum16(float v) {
+  v = DppAdd(v, 0);
+  v = DppAdd(v, 1);
+  v = DppAdd(v, 2);
+  return DppAdd(v, 3);
+}
+
+// Reduces RI (1, 2 or 4) per-lane values over the wave. Afterwards lane l holds
+// the total of row (l >> 4) & (RI - 1) (for RI == 1: every lane holds row 0).
+template <int RI>
+__device__ __forceinline__ float ReduceRows(const float (&v)[RI], int lane) {
+  if (RI == 1) {
+    float a = RowSum16(v[0]);
+    a += __shfl_xor(a, 16, 64);
+    return a + __shfl_xor(a, 32, 64);
+  } else if (RI == 2) {
+    const bool hi = (lane & 16) != 0;
+    float a = (hi ? v[1] : v[0]) + __shfl_xor(hi ? v[0] : v[1], 16, 64);
+    a += __shfl_xor(a, 32, 64);
+    return RowSum16(a);
+  } else {
+    const bool b5 = (lane & 32) != 0;
+    const bool b4 = (lane & 16) != 0;
+    // lanes with bit 5 set keep rows 2, 3; the others rows 0, 1
+    const float k0 = b5 ? v[2] : v[0];
+    const float k1 = b5 ? v[3] : v[1];
+    const float s0 = b5 ? v[0] : v[2];
+    const float s1 = b5 ? v[1] : v[3];
+    const float n0 = k0 + __shfl_xor(s0, 32, 64);
+    const float n1 = k1 + __shfl_xor(s1, 32, 64);
+    // bit 4 picks one of the two
+    const float a = (b4 ? n1 : n0) + __shfl_xor(b4 ? n0 : n1, 16, 64);
+    return RowSum16(a);
+  }
+}
+
+// Row index (0..RI-1) whose total lane `lane` holds after ReduceRows.
+template <int RI>
+__device__ __forceinline__ int ReducedRow(int lane) {
+  return RI == 1 ? 0 : (RI == 2 ? (lane >> 4) & 1 : (((lane >> 5) & 1) << 1) | ((lane >> 4) & 1));
+}
+
+// Signed byte k of a word as an exact float (sign-extending byte select).
+__device__ __forceinline__ float SByteF(uint32_t w, int k) {
+  return static_cast<float>(static_cast<int8_t>(static_cast<uint8_t>(w >> (8 * k))));
+}
+
+// Lane contribution of one block for one row, given resident activations.
+// sx: Q4_K only, the lane's activation sums (low-nibble run, high-nibble run).
+template <uint32_t kType>
+__device__ __forceinline__ float BlockDot(const LaneBytes& r, int s, const float (&xv)[32], const float (&sx)[2]) {
+  if (kType == kGgmlQ4_K) {
+    const int g = s >> 1;
+    const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.a.x & 0xFFFFu)));
+    const float dmin = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.a.x >> 16)));
+    uint32_t sc0, m0, sc1, m1;
+    ScaleMinK4(2 * g, r.a.y, r.a.z, r.a.w, &sc0, &m0);
+    ScaleMinK4(2 * g + 1, r.a.y, r.a.z, r.a.w, &sc1, &m1);
+    const uint32_t qw[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
+    float slo = 0.0f, shi = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t lo = Opaque(qw[k] & 0x0F0F0F0Fu);
+      const uint32_t hi = Opaque((qw[k] >> 4) & 0x0F0F0F0Fu);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        slo = __builtin_fmaf(UByteF(lo, j), xv[4 * k + j], slo);
+        shi = __builtin_fmaf(UByteF(hi, j), xv[16 + 4 * k + j], shi);
+      }
+    }
+    float acc = (d * static_cast<float>(sc0)) * slo;
+    acc = __builtin_fmaf(-(dmin * static_cast<float>(m0)), sx[0], acc);
+    acc = __builtin_fmaf(d * static_cast<float>(sc1), shi, acc);
+    return __builtin_fmaf(-(dmin * static_cast<float>(m1)), sx[1], acc);
+  } else {
+    const int is = (s & 3) >> 1;
+    const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.d6)));
+    const uint32_t ql[2][2] = {{r.a.x, r.a.y}, {r.a.z, r.a.w}};
+    const uint32_t qh[2] = {r.b.x, r.b.y};
+    const uint32_t scw[2] = {r.b.z, r.b.w};
+    float acc = 0.0f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int si = is + 2 * q;
+      const int8_t sc = static_cast<int8_t>(ByteOf(scw[si >> 2], si & 3));
+      float part = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const uint32_t nib = (q < 2 ? ql[q & 1][k] : ql[q & 1][k] >> 4) & 0x0F0F0F0Fu;
+        const uint32_t hi2 = (2 * q >= 4 ? qh[k] >> (2 * q - 4) : qh[k] << (4 - 2 * q)) & 0x30303030u;
+        // bytes 4(q6 - 32) as signed int8: (q6 << 2) ^ 0x80 with q6 = nib | hi2 < 64
+        const uint32_t b = Opaque(((nib | hi2) << 2) ^ 0x80808080u);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) part = __builtin_fmaf(SByteF(b, j), xv[8 * q + 4 * k + j], part);
+      }
+      acc = __builtin_fmaf((d * static_cast<float>(sc)) * 0.25f, part, acc);
+    }
+    return acc;
+  }
+}
+
+template <uint32_t kType, int NX, int RI>
+__global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(const uint8_t* __restrict__ w, int64_t rows,
+                                                              int64_t row_bytes, int32_t nb,
+                                                              const float* __restrict__ x, float* __restrict__ out) {
+  constexpr int64_t kBB = BlockBytesOf<kType>::value;
+  const int lane = threadIdx.x & 63;
+  const int c = lane / kGroupLanes;
+  const int s = lane % kGroupLanes;
+  // Row bookkeeping is uniform over the wave: keep it in scalar registers.
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kWavesPerBlock * RI;
+  int64_t r0 = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(
+                   static_cast<int>(blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6)))) * RI;
+  if (r0 >= rows) return;
+
+  float xv[NX][32];
+  float sx[NX][2];
+  int64_t lane_off[NX];  // byte offset of this lane's block inside a row (clamped to the last block)
+#pragma unroll
+  for (int it = 0; it < NX; ++it) {
+    const int b = c + kGroups * it;
+    lane_off[it] = static_cast<int64_t>(b < nb ? b : nb - 1) * kBB;
+    if (b < nb) {
+      LoadLaneX<kType>(x, static_cast<int64_t>(b) * kQK_K, s, xv[it]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) xv[it][i] = 0.0f;
+    }
+    float a = 0.0f, z = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      a += xv[it][i];
+      z += xv[it][16 + i];
+    }
+    sx[it][0] = a;
+    sx[it][1] = z;
+  }
+
+  // Rows past the end are clamped to the last row (loads stay in bounds; results are dropped).
+  auto load = [&](int64_t base_row, LaneBytes (&lb)[RI][NX]) {
+#pragma unroll
+    for (int r = 0; r < RI; ++r) {
+      const int64_t row = base_row + r < rows ? base_row + r : rows - 1;
+      const uint8_t* rp = w + row * row_bytes;
+#pragma unroll
+      for (int it = 0; it < NX; ++it) lb[r][it] = LoadLaneBytes<kType>(rp + lane_off[it], s);
+    }
+  };
+
+  LaneBytes cur[RI][NX];
+  load(r0, cur);
+  for (; r0 < rows; r0 += stride) {
+    LaneBytes nxt[RI][NX];
+    load(r0 + stride < rows ? r0 + stride : r0, nxt);
+    float acc[RI];
+#pragma unroll
+    for (int r = 0; r < RI; ++r) {
+      acc[r] = 0.0f;
+#pragma unroll
+      for (int it = 0; it < NX; ++it) {
+        if (c + kGroups * it < nb) acc[r] += BlockDot<kType>(cur[r][it], s, xv[it], sx[it]);
+      }
+    }
+    const float total = ReduceRows<RI>(acc, lane);
+    const int rr = ReducedRow<RI>(lane);
+    if ((lane & 15) == 0 && lane < 16 * RI && r0 + rr < rows) out[r0 + rr] = total;
+#pragma unroll
+    for (int r = 0; r < RI; ++r)
+#pragma unroll
+      for (int it = 0; it < NX; ++it) cur[r][it] = nxt[r][it];
+  }
+}
+
 // Any type, any alignment: one wave per (row, token), lanes strided over the
 // columns, per-element byte-wise decode; fp32 FMA accumulation and the same
 // butterfly.
@@ -288,11 +532,31 @@ void LaunchQuant(const char* name, const uint8_t* w, int64_t rows, int64_t row_b
          dim3(kMmBlock), w, rows, row_bytes, nb, x, cols, n_tokens, out);
 }
 
+// Decode: persistent waves, 2 rows per step (4 for Q4_K matrices of 32768 rows
+// or more), at most kDecodeGrid workgroups (16 waves per CU).
+constexpr int64_t kDecodeGrid = 1024;
+
+template <uint32_t kType, int NX, int RI>
+void LaunchDecode(const char* name, const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb, const float* x,
+                  float* out) {
+  const int64_t need = (rows + kWavesPerBlock * RI - 1) / (kWavesPerBlock * RI);
+  const unsigned grid = static_cast<unsigned>(need < kDecodeGrid ? need : kDecodeGrid);
+  Launch(name, MatVecQuantKernel<kType, NX, RI>, dim3(grid), dim3(kMmBlock), w, rows, row_bytes, nb, x, out);
+}
+
 // Rows per wave: enough waves to cover the chip first (a wave per row below
 // 8192 rows), then 2 or 4 rows so each lane's activations serve several rows.
 template <uint32_t kType>
 void LaunchByShape(const char* name, const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb, const float* x,
                    int64_t cols, int64_t n_tokens, float* out) {
+  if (n_tokens == 1 && nb <= 2 * kGroups) {
+    const char* dname = kType == kGgmlQ4_K ? "MatVecQ4KKernel" : "MatVecQ6KKernel";
+    if (nb <= kGroups) {
+      if (kType == kGgmlQ4_K && rows >= 32768) return LaunchDecode<kType, 1, 4>(dname, w, rows, row_bytes, nb, x, out);
+      return LaunchDecode<kType, 1, 2>(dname, w, rows, row_bytes, nb, x, out);
+    }
+    return LaunchDecode<kType, 2, 2>(dname, w, rows, row_bytes, nb, x, out);
+  }
   if (n_tokens == 1) {
     if (rows >= 32768) return LaunchQuant<kType, 4, 1>(name, w, rows, row_bytes, nb, x, cols, n_tokens, out);
     if (rows >= 8192) return LaunchQuant<kType, 2, 1>(name, w, rows, row_bytes, nb, x, cols, n_tokens, out);

@@ -25,21 +25,23 @@ namespace dev {
 
 __device__ __forceinline__ uint32_t ByteOf(uint32_t word, int i) { return (word >> (8 * i)) & 0xFFu; }
 
-// Byte i (0..11) of the Q4_K packed scales held in three little-endian words.
-__device__ __forceinline__ uint32_t ScaleByte(uint32_t s0, uint32_t s1, uint32_t s2, int i) {
-  const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
-  return ByteOf(w, i & 3);
-}
-
-// 6-bit (scale, min) of sub-block j (0..7) from the 12 packed bytes.
+// 6-bit (scale, min) of sub-block j (0..7) from the 12 packed bytes
+// (GetScaleMinK4, src/quant.cc:159-167):
+//   j < 4:  sc = q[j] & 63,                          m = q[j + 4] & 63
+//   j >= 4: sc = (q[j + 4] & 15) | ((q[j - 4] >> 6) << 4),
+//           m  = (q[j + 4] >> 4) | ((q[j] >> 6) << 4)
+// With k = j & 3 both forms read byte k of each of the three words, so both are
+// computed and one is selected: no branch on j, which is lane-dependent in the
+// kernels and would otherwise split the wave.
 __device__ __forceinline__ void ScaleMinK4(int j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t* sc, uint32_t* m) {
-  if (j < 4) {
-    *sc = ScaleByte(s0, s1, s2, j) & 63u;
-    *m = ScaleByte(s0, s1, s2, j + 4) & 63u;
-  } else {
-    *sc = (ScaleByte(s0, s1, s2, j + 4) & 0x0Fu) | ((ScaleByte(s0, s1, s2, j - 4) >> 6) << 4);
-    *m = (ScaleByte(s0, s1, s2, j + 4) >> 4) | ((ScaleByte(s0, s1, s2, j) >> 6) << 4);
-  }
+  const int k = j & 3;
+  const uint32_t b0 = ByteOf(s0, k);
+  const uint32_t b1 = ByteOf(s1, k);
+  const uint32_t b2 = ByteOf(s2, k);
+  const uint32_t hi_sc = (b2 & 0x0Fu) | ((b0 >> 6) << 4);
+  const uint32_t hi_m = (b2 >> 4) | ((b1 >> 6) << 4);
+  *sc = j < 4 ? (b0 & 63u) : hi_sc;
+  *m = j < 4 ? (b1 & 63u) : hi_m;
 }
 
 // Element e of one quantised block (or of an F32 row) with byte loads only, so
