@@ -314,6 +314,64 @@ def profile_traffic(kernel_tag):
     return None
 
 
+# Qwen3-1.7B decode matrices as a Q4_K_M file stores them (attn_v / ffn_down in Q6_K
+# on the layers that get more bits; the output projection in Q6_K).
+DECODE_MATRICES = [
+    ("attn_q", 12, 2048, 2048), ("attn_k", 12, 1024, 2048), ("attn_v", 14, 1024, 2048),
+    ("attn_output", 12, 2048, 2048), ("ffn_gate", 12, INTER, 2048), ("ffn_up", 12, INTER, 2048),
+    ("ffn_down", 14, 2048, INTER),
+]
+OUTPUT_MATRIX = ("output", 14, VOCAB, 2048)
+
+
+def measure_matmul_decode(torch, ops, reps=20, span=768 << 20):
+    """GpuMatMulQuant at n = 1 on each decode matrix: weight copies rotated so that a
+    launch never finds its matrix in the 256 MB Infinity Cache; kernel time from
+    dispatch-attached events. Bytes = weights + x + out."""
+    res = {}
+    layer_us = 0.0
+    for name, t, rows, cols in DECODE_MATRICES + [OUTPUT_MATRIX]:
+        rb = (cols // 256) * (144 if t == 12 else 210)
+        wbytes = rows * rb
+        copies = max(2, min(512, span // wbytes + 1))
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(20 + rows + cols + t)
+        blob = torch.randint(0, 256, (copies * wbytes,), dtype=torch.uint8, device="cuda", generator=gen)
+        # keep the fp16 scales finite: clear the exponent's top bit of every d / dmin
+        blocks = blob.view(-1, 144 if t == 12 else 210)
+        if t == 12:
+            blocks[:, 1] &= 0x3B
+            blocks[:, 3] &= 0x3B
+        else:
+            blocks[:, 209] &= 0x3B
+        x = torch.randn((1, cols), dtype=torch.float32, device="cuda", generator=gen)
+        out = torch.empty((1, rows), dtype=torch.float32, device="cuda")
+        mats = [ops.GpuTensor(blob[i * wbytes:(i + 1) * wbytes], t, rows, cols) for i in range(copies)]
+        for i in range(min(copies, 4)):
+            ops.GpuMatMulQuant(mats[i], x, 1, out)
+        torch.cuda.synchronize()
+        ops.profile_start(reps)
+        for r in range(reps):
+            ops.GpuMatMulQuant(mats[r % copies], x, 1, out)
+        ops.profile_stop()
+        rep = ops.profile_report()
+        kname, k = next(iter(rep.items()))
+        nbytes = wbytes + 4 * cols + 4 * rows
+        us = k["avg_us"]
+        res[name] = {"type": "Q4_K" if t == 12 else "Q6_K", "rows": rows, "cols": cols, "us": round(us, 2),
+                     "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "pct_peak": round(nbytes / (us * 1e-6) / 1e9 / PEAK_GBPS * 100, 1), "kernel": kname,
+                     "bytes": nbytes}
+        if name != OUTPUT_MATRIX[0]:
+            layer_us += us
+        del blob, blocks, mats, x, out
+        torch.cuda.empty_cache()
+    token_us = LAYERS * layer_us + res[OUTPUT_MATRIX[0]]["us"]
+    return {"matrices": res, "layer_us": round(layer_us, 2), "token_matmul_us": round(token_us, 1),
+            "note": "n = 1, Qwen3-1.7B Q4_K_M layout; token_matmul_us = 28 layers + output projection, "
+                    "matmuls only"}
+
+
 def cpu_baseline():
     """The oracle's C restatement of one layer of the chain (n = 2811, 1.7B shape)
     on the host cores, median of 5; plus per-op and single-thread figures. A
@@ -333,12 +391,16 @@ def cpu_baseline():
         per_op[name] = {"ms": round(t * 1e3, 3), "GBps": round(nbytes / t / 1e9, 2)}
     t1 = pyoracle.bench_layer_chain(1, *args, 1)
     gq4 = pyoracle.bench_gather(threads, pyoracle.Q4_K, VOCAB, H, N_PREFILL, 3)
+    mm = pyoracle.bench_matmul(pyoracle.Q6_K, 4096, 2048, 3)
     return {"value": round(b / sec / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"one layer of the n={N_PREFILL} chain (add+RMSNorm, qk-norm+RoPE+fp16 KV, SwiGLU; "
                       f"{b} B) by the C oracle, rows split over {threads} threads, median of 5 runs "
                       f"({sec * 1e3:.1f} ms each)",
             "per_op": per_op, "single_thread_GBps": round(b / t1 / 1e9, 2),
-            "gather_q4k_GBps": round(bytes_gather(N_PREFILL, 144) / gq4 / 1e9, 2)}
+            "gather_q4k_GBps": round(bytes_gather(N_PREFILL, 144) / gq4 / 1e9, 2),
+            "matmul_q6k_n1_GBps": round((4096 * 8 * 210 + 4 * 2048 + 4 * 4096) / mm / 1e9, 3),
+            "matmul_sample": "4096 x 2048 Q6_K rows times one fp32 vector by the oracle's float64 "
+                             "restatement, one thread"}
 
 
 def main():
@@ -363,7 +425,6 @@ def main():
     ops.set_stream(torch.cuda.current_stream())
     ok, desc = ops.device_info()
     log(desc)
-    from oracle import pyoracle  # noqa: F401  (rope table comes from the library, not the oracle)
 
     tab = torch.from_numpy(ops.build_rope_table(D, THETA, MAX_SEQ)).cuda()
 
@@ -412,6 +473,8 @@ def main():
         extras["decode_n1"] = measure_decode(torch, ops, tab, max(20, args.steps))
         log("prefill n=4096 at the 4B shape, 36 layers")
         extras["prefill_4b_n4096"] = measure_prefill_4b(torch, ops, tab)
+        log("decode matmuls (GpuMatMulQuant, n = 1)")
+        extras["matmul_decode_n1"] = measure_matmul_decode(torch, ops)
         log("gather Q4_K / Q6_K")
         extras["gather_q4k_n2811"] = measure_gather(torch, ops, ops.GGML_Q4_K, 144)
         extras["gather_q6k_n2811"] = measure_gather(torch, ops, ops.GGML_Q6_K, 210)

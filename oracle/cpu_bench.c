@@ -189,6 +189,40 @@ done:
   return result;
 }
 
+/* One thread: the oracle's float64 matmul restatement over a random [rows, cols]
+ * matrix of `type` times one fp32 vector; median of `reps` runs, in seconds. */
+double ora_bench_matmul(uint32_t type, int64_t rows, int64_t cols, int reps) {
+  const int64_t rb = ora_type_row_bytes(type, cols);
+  if (rb <= 0 || rows <= 0 || reps < 1 || reps > 64) return -1.0;
+  uint8_t* w = malloc((size_t)(rows * rb));
+  float* x = malloc((size_t)cols * 4);
+  double* out = malloc((size_t)rows * 8);
+  double result = -2.0;
+  if (!w || !x || !out) goto done;
+  {
+    uint64_t s = 12;
+    for (int64_t i = 0; i < rows * rb; i += 8) {
+      const uint64_t r = splitmix64(&s);
+      const int64_t m = rows * rb - i < 8 ? rows * rb - i : 8;
+      memcpy(w + i, &r, (size_t)m);
+    }
+    fill_uniform(x, cols, 13, -1.f, 1.f);
+    double times[64];
+    for (int r = 0; r < reps; ++r) {
+      const double t0 = now_s();
+      ora_matmul_quant_f64(type, w, rows, cols, x, 1, out, NULL);
+      times[r] = now_s() - t0;
+    }
+    qsort(times, (size_t)reps, sizeof(double), cmp_double);
+    result = times[reps / 2];
+  }
+done:
+  free(w);
+  free(x);
+  free(out);
+  return result;
+}
+
 double ora_bench_layer_chain(int threads, int64_t n, int64_t hidden, int32_t n_heads, int32_t n_kv_heads,
                              int64_t inter, int reps) {
   return ora_bench_layer_op(0, threads, n, hidden, n_heads, n_kv_heads, inter, reps);

@@ -103,6 +103,7 @@ double ora_bench_layer_op(int op, int threads, int64_t n, int64_t hidden, int32_
                           int64_t inter, int reps);
 /* Same for the embedding gather of `seq` ids from a rows x cols table of `type`. */
 double ora_bench_gather(int threads, uint32_t type, int64_t rows, int64_t cols, int64_t seq, int reps);
+double ora_bench_matmul(uint32_t type, int64_t rows, int64_t cols, int reps);
 
 #ifdef __cplusplus
 }

@@ -46,6 +46,7 @@ _SIGS = {
     "ora_bench_layer_chain": (_f64, [ctypes.c_int, _i64, _i64, _i32, _i32, _i64, ctypes.c_int]),
     "ora_bench_layer_op": (_f64, [ctypes.c_int, ctypes.c_int, _i64, _i64, _i32, _i32, _i64, ctypes.c_int]),
     "ora_bench_gather": (_f64, [ctypes.c_int, _u32, _i64, _i64, _i64, ctypes.c_int]),
+    "ora_bench_matmul": (_f64, [_u32, _i64, _i64, ctypes.c_int]),
 }
 
 _lib = None
@@ -269,3 +270,7 @@ def bench_layer_op(op, threads, n, hidden, n_heads, n_kv_heads, inter, reps) -> 
 
 def bench_gather(threads, ggml_type, rows, cols, seq, reps) -> float:
     return float(lib().ora_bench_gather(threads, ggml_type, rows, cols, seq, reps))
+
+
+def bench_matmul(ggml_type, rows, cols, reps) -> float:
+    return float(lib().ora_bench_matmul(ggml_type, rows, cols, reps))
