@@ -425,6 +425,20 @@ __device__ __forceinline__ float BlockDot(const LaneBytes& r, int s, const float
   }
 }
 
+// Sums of each lane's two 16-activation runs (Q4_K's low- and high-nibble runs).
+__device__ __forceinline__ void RunSums(const float (&xv)[32], float (&sx)[2]) {
+  float a = 0.0f, z = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    a += xv[i];
+    z += xv[16 + i];
+  }
+  sx[0] = a;
+  sx[1] = z;
+}
+
+// Each lane keeps the activations of its NX block groups in registers (rows of
+// up to 8 * NX blocks; used for NX == 1).
 template <uint32_t kType, int NX, int RI>
 __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(const uint8_t* __restrict__ w, int64_t rows,
                                                               int64_t row_bytes, int32_t nb,
@@ -433,6 +447,7 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(const uint8_t* __r
   const int lane = threadIdx.x & 63;
   const int c = lane / kGroupLanes;
   const int s = lane % kGroupLanes;
+
   // Row bookkeeping is uniform over the wave: keep it in scalar registers.
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kWavesPerBlock * RI;
   int64_t r0 = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(
@@ -452,14 +467,7 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(const uint8_t* __r
 #pragma unroll
       for (int i = 0; i < 32; ++i) xv[it][i] = 0.0f;
     }
-    float a = 0.0f, z = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      a += xv[it][i];
-      z += xv[it][16 + i];
-    }
-    sx[it][0] = a;
-    sx[it][1] = z;
+    RunSums(xv[it], sx[it]);
   }
 
   // Rows past the end are clamped to the last row (loads stay in bounds; results are dropped).
@@ -480,11 +488,12 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(const uint8_t* __r
     load(r0 + stride < rows ? r0 + stride : r0, nxt);
     float acc[RI];
 #pragma unroll
-    for (int r = 0; r < RI; ++r) {
-      acc[r] = 0.0f;
+    for (int r = 0; r < RI; ++r) acc[r] = 0.0f;
 #pragma unroll
-      for (int it = 0; it < NX; ++it) {
-        if (c + kGroups * it < nb) acc[r] += BlockDot<kType>(cur[r][it], s, xv[it], sx[it]);
+    for (int it = 0; it < NX; ++it) {
+      if (c + kGroups * it < nb) {
+#pragma unroll
+        for (int r = 0; r < RI; ++r) acc[r] += BlockDot<kType>(cur[r][it], s, xv[it], sx[it]);
       }
     }
     const float total = ReduceRows<RI>(acc, lane);
@@ -494,6 +503,86 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(const uint8_t* __r
     for (int r = 0; r < RI; ++r)
 #pragma unroll
       for (int it = 0; it < NX; ++it) cur[r][it] = nxt[r][it];
+  }
+}
+
+// Wide rows (9 to 64 blocks; e.g. ffn_down, 4B projections): the WS waves of a
+// workgroup share RI rows, wave q taking the block groups q, q + WS, ... (a
+// group is 8 consecutive blocks, one per lane group), so a matrix with few rows
+// still fills the chip. Each wave keeps the activations of its NXW groups in
+// registers and reduces its partial sums; the WS partials of a row meet in LDS
+// and wave 0 adds them in wave order, so results are deterministic.
+template <uint32_t kType, int WS, int NXW, int RI>
+__global__ __launch_bounds__(64 * WS) void MatVecSplitKernel(const uint8_t* __restrict__ w, int64_t rows,
+                                                             int64_t row_bytes, int32_t nb,
+                                                             const float* __restrict__ x, float* __restrict__ out) {
+  constexpr int64_t kBB = BlockBytesOf<kType>::value;
+  __shared__ float part[WS][RI];
+  const int lane = threadIdx.x & 63;
+  const int q = threadIdx.x >> 6;
+  const int c = lane / kGroupLanes;
+  const int s = lane % kGroupLanes;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * RI;
+  int64_t r0 = static_cast<int64_t>(blockIdx.x) * RI;  // uniform over the workgroup
+
+  float xv[NXW][32];
+  float sx[NXW][2];
+  int64_t lane_off[NXW];
+  bool valid[NXW];
+#pragma unroll
+  for (int it = 0; it < NXW; ++it) {
+    const int b = c + kGroups * (q + WS * it);
+    valid[it] = b < nb;
+    lane_off[it] = static_cast<int64_t>(valid[it] ? b : nb - 1) * kBB;
+    if (valid[it]) {
+      LoadLaneX<kType>(x, static_cast<int64_t>(b) * kQK_K, s, xv[it]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) xv[it][i] = 0.0f;
+    }
+    RunSums(xv[it], sx[it]);
+  }
+
+  auto load = [&](int64_t base_row, LaneBytes (&lb)[RI][NXW]) {
+#pragma unroll
+    for (int r = 0; r < RI; ++r) {
+      const int64_t row = base_row + r < rows ? base_row + r : rows - 1;
+      const uint8_t* rp = w + row * row_bytes;
+#pragma unroll
+      for (int it = 0; it < NXW; ++it) lb[r][it] = LoadLaneBytes<kType>(rp + lane_off[it], s);
+    }
+  };
+
+  LaneBytes cur[RI][NXW];
+  load(r0 < rows ? r0 : 0, cur);
+  for (; r0 < rows; r0 += stride) {
+    LaneBytes nxt[RI][NXW];
+    load(r0 + stride < rows ? r0 + stride : r0, nxt);
+    float acc[RI];
+#pragma unroll
+    for (int r = 0; r < RI; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int it = 0; it < NXW; ++it) {
+      if (valid[it]) {
+#pragma unroll
+        for (int r = 0; r < RI; ++r) acc[r] += BlockDot<kType>(cur[r][it], s, xv[it], sx[it]);
+      }
+    }
+    const float total = ReduceRows<RI>(acc, lane);
+    const int rr = ReducedRow<RI>(lane);
+    if ((lane & 15) == 0 && lane < 16 * RI) part[q][rr] = total;
+    __syncthreads();
+    if (q == 0 && lane < RI && r0 + lane < rows) {
+      float v = part[0][lane];
+#pragma unroll
+      for (int k = 1; k < WS; ++k) v += part[k][lane];
+      out[r0 + lane] = v;
+    }
+    __syncthreads();  // part is rewritten by the next row step
+#pragma unroll
+    for (int r = 0; r < RI; ++r)
+#pragma unroll
+      for (int it = 0; it < NXW; ++it) cur[r][it] = nxt[r][it];
   }
 }
 
@@ -536,12 +625,23 @@ void LaunchQuant(const char* name, const uint8_t* w, int64_t rows, int64_t row_b
 // or more), at most kDecodeGrid workgroups (16 waves per CU).
 constexpr int64_t kDecodeGrid = 1024;
 
-template <uint32_t kType, int NX, int RI>
+template <uint32_t kType, int RI>
 void LaunchDecode(const char* name, const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb, const float* x,
                   float* out) {
   const int64_t need = (rows + kWavesPerBlock * RI - 1) / (kWavesPerBlock * RI);
   const unsigned grid = static_cast<unsigned>(need < kDecodeGrid ? need : kDecodeGrid);
-  Launch(name, MatVecQuantKernel<kType, NX, RI>, dim3(grid), dim3(kMmBlock), w, rows, row_bytes, nb, x, out);
+  Launch(name, MatVecQuantKernel<kType, 1, RI>, dim3(grid), dim3(kMmBlock), w, rows, row_bytes, nb, x, out);
+}
+
+// Split decode: at most max_grid workgroups (rows are visited with a stride);
+// measured best at 4096 for one block group per wave, 1024 for two.
+template <uint32_t kType, int WS, int NXW, int RI>
+void LaunchSplit(const char* name, const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb, const float* x,
+                 float* out) {
+  const int64_t max_grid = NXW == 1 ? 4096 : 1024;
+  const int64_t need = (rows + RI - 1) / RI;
+  const unsigned grid = static_cast<unsigned>(need < max_grid ? need : max_grid);
+  Launch(name, MatVecSplitKernel<kType, WS, NXW, RI>, dim3(grid), dim3(64 * WS), w, rows, row_bytes, nb, x, out);
 }
 
 // Rows per wave: enough waves to cover the chip first (a wave per row below
@@ -549,14 +649,16 @@ void LaunchDecode(const char* name, const uint8_t* w, int64_t rows, int64_t row_
 template <uint32_t kType>
 void LaunchByShape(const char* name, const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb, const float* x,
                    int64_t cols, int64_t n_tokens, float* out) {
-  if (n_tokens == 1 && nb <= 2 * kGroups) {
-    const char* dname = kType == kGgmlQ4_K ? "MatVecQ4KKernel" : "MatVecQ6KKernel";
-    if (nb <= kGroups) {
-      if (kType == kGgmlQ4_K && rows >= 32768) return LaunchDecode<kType, 1, 4>(dname, w, rows, row_bytes, nb, x, out);
-      return LaunchDecode<kType, 1, 2>(dname, w, rows, row_bytes, nb, x, out);
-    }
-    return LaunchDecode<kType, 2, 2>(dname, w, rows, row_bytes, nb, x, out);
+  const char* dname = kType == kGgmlQ4_K ? "MatVecQ4KKernel" : "MatVecQ6KKernel";
+  const char* sname = kType == kGgmlQ4_K ? "MatVecSplitQ4KKernel" : "MatVecSplitQ6KKernel";
+  if (n_tokens == 1 && nb <= kGroups) {
+    if (kType == kGgmlQ4_K && rows >= 32768) return LaunchDecode<kType, 4>(dname, w, rows, row_bytes, nb, x, out);
+    return LaunchDecode<kType, 2>(dname, w, rows, row_bytes, nb, x, out);
   }
+  if (n_tokens == 1 && nb <= 2 * kGroups) return LaunchSplit<kType, 2, 1, 2>(sname, w, rows, row_bytes, nb, x, out);
+  if (n_tokens == 1 && nb <= 3 * kGroups) return LaunchSplit<kType, 3, 1, 2>(sname, w, rows, row_bytes, nb, x, out);
+  if (n_tokens == 1 && nb <= 4 * kGroups) return LaunchSplit<kType, 4, 1, 2>(sname, w, rows, row_bytes, nb, x, out);
+  if (n_tokens == 1 && nb <= 8 * kGroups) return LaunchSplit<kType, 4, 2, 1>(sname, w, rows, row_bytes, nb, x, out);
   if (n_tokens == 1) {
     if (rows >= 32768) return LaunchQuant<kType, 4, 1>(name, w, rows, row_bytes, nb, x, cols, n_tokens, out);
     if (rows >= 8192) return LaunchQuant<kType, 2, 1>(name, w, rows, row_bytes, nb, x, cols, n_tokens, out);

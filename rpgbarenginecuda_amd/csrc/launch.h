@@ -17,12 +17,14 @@
 
 namespace rpg {
 
+// The same with `shmem` bytes of dynamic LDS.
 template <typename... KArgs, typename... Args>
-inline void Launch(const char* name, void (*kernel)(KArgs...), dim3 grid, dim3 block, Args... args) {
+inline void LaunchShared(const char* name, void (*kernel)(KArgs...), dim3 grid, dim3 block, size_t shmem,
+                         Args... args) {
   static_assert(sizeof...(KArgs) == sizeof...(Args), "kernel argument count mismatch");
   const LaunchTiming* timing = NextLaunchTiming(name);
   if (timing == nullptr) {
-    kernel<<<grid, block, 0, EngineStream()>>>(static_cast<KArgs>(args)...);
+    kernel<<<grid, block, shmem, EngineStream()>>>(static_cast<KArgs>(args)...);
   } else {
     std::tuple<KArgs...> values{static_cast<KArgs>(args)...};
     void* ptrs[sizeof...(KArgs)];
@@ -32,10 +34,15 @@ inline void Launch(const char* name, void (*kernel)(KArgs...), dim3 grid, dim3 b
           ((ptrs[i++] = static_cast<void*>(&v)), ...);
         },
         values);
-    RPG_HIP_CHECK(hipExtLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, ptrs, 0, EngineStream(),
+    RPG_HIP_CHECK(hipExtLaunchKernel(reinterpret_cast<const void*>(kernel), grid, block, ptrs, shmem, EngineStream(),
                                      timing->start, timing->stop, 0));
   }
   CheckLaunch(name);
+}
+
+template <typename... KArgs, typename... Args>
+inline void Launch(const char* name, void (*kernel)(KArgs...), dim3 grid, dim3 block, Args... args) {
+  LaunchShared(name, kernel, grid, block, 0, args...);
 }
 
 }  // namespace rpg

@@ -62,7 +62,10 @@ SHAPES = [
     (14, 2048, 6144, 1),     # ffn_down (Q6_K)
     (12, 2048, 6144, 1),     # ffn_down (Q4_K)
     (12, 9728, 2560, 1),     # 4B ffn_gate: 10 blocks per row (not a multiple of 8), 2 rows per wave
-    (14, 2560, 9728, 1),     # 4B ffn_down: 38 blocks per row
+    (14, 2560, 9728, 1),     # 4B ffn_down: 38 blocks per row (activations staged in LDS)
+    (12, 2048, 6144, 1),     # 24 blocks per row, Q4_K run sums from LDS
+    (12, 300, 16384, 1),     # 64 blocks per row: the widest LDS-staged decode
+    (14, 100, 20480, 1),     # 80 blocks per row: the tiled kernel
     (12, 40000, 2048, 1),    # 4 rows per wave
     (14, 40001, 2048, 1),    # 4 rows per wave, ragged last wave
     (12, 2048, 2048, 2),
