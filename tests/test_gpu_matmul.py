@@ -8,8 +8,10 @@ with D the longest chain of roundings from one product to the result. Any
 kernel that keeps at least 8 independent partial sums of cols / 8 terms each and
 combines them by a tree of depth <= 7 has D <= cols / 8 + 7; the kernels here
 (at most 32 * ceil(cols / 2048) sequential fused multiply-adds per lane and a
-64-lane butterfly) stay well inside it. A dropped, doubled or misplaced term
-breaks the bound by many orders of magnitude.
+64-lane butterfly) stay well inside it. For Q4_K the decode kernels evaluate
+d1 * sum(q x) - m1 * sum(x) per run, whose two terms can partly cancel, so the
+bound there also counts sum_e (|d1 q_e| + |m1|) |x_e|. A dropped, doubled or
+misplaced term breaks the bound by many orders of magnitude.
 """
 from __future__ import annotations
 
@@ -45,8 +47,24 @@ def last_error(gpu) -> str:
     return msg.decode("utf-8", "replace") if msg else ""
 
 
-def check(got, exact, absdot, cols):
-    bound = (cols // 8 + 7) * U * absdot + 1e-37
+def factored_magnitude(ora, t, w, rows, cols, x):
+    """Q4_K only: sum_e (|d1 q_e| + |m1|) |x_e|, the scale of the error of the
+    factored form d1 * sum(q x) - m1 * sum(x) that the decode kernels use. A copy
+    of the matrix with every quant zeroed dequantises to -m1 exactly, and
+    w - (-m1) = d1 q."""
+    if t != 12:
+        return 0.0
+    z = np.array(w, copy=True).reshape(-1, 144)
+    z[:, 16:] = 0
+    n = rows * cols
+    wd = ora.dequantize_row(t, np.ascontiguousarray(w), n).reshape(rows, cols).astype(np.float64)
+    w0 = ora.dequantize_row(t, z.reshape(-1), n).reshape(rows, cols).astype(np.float64)
+    mag = np.abs(wd - w0) + np.abs(w0)
+    return np.abs(np.asarray(x, np.float64).reshape(-1, cols)) @ mag.T
+
+
+def check(got, exact, absdot, cols, extra=0.0):
+    bound = (cols // 8 + 7) * U * (absdot + extra) + 1e-37
     err = np.abs(got.astype(np.float64) - exact)
     worst = float(np.max(err / np.maximum(bound, 1e-300)))
     assert np.all(err <= bound), f"max error / bound = {worst:.3g}"
@@ -89,7 +107,7 @@ def test_matmul_quant_vs_f64(gpu, ora, t, rows, cols, n):
     out = torch.full((n, rows), np.nan, dtype=torch.float32, device="cuda")
     gpu.GpuMatMulQuant(gpu.GpuTensor(dev(w), t, rows, cols), dev(x), n, out)
     exact, absdot = ora.matmul_quant_f64(t, w, rows, cols, x)
-    check(host(out), exact, absdot, cols)
+    check(host(out), exact, absdot, cols, factored_magnitude(ora, t, w, rows, cols, x))
 
 
 def test_matmul_quant_lm_head_shape(gpu, ora):
@@ -134,7 +152,7 @@ def test_matmul_quant_generic_paths(gpu, ora, t, w_off, x_off):
                                                  out.data_ptr())
     assert rc == 0, last_error(gpu)
     exact, absdot = ora.matmul_quant_f64(t, w, rows, cols, x)
-    check(host(out), exact, absdot, cols)
+    check(host(out), exact, absdot, cols, factored_magnitude(ora, t, w, rows, cols, x))
 
 
 def test_matmul_quant_one_hot_selects_columns(gpu, ora):
