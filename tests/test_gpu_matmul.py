@@ -93,6 +93,12 @@ SHAPES = [
     (12, 777, 2048, 8),
     (14, 513, 2048, 13),     # two tiles of 8, the second ragged
     (12, 256, 256, 21),      # the CPU-runnable n = 21
+    (12, 2048, 2048, 64),    # matrix-core GEMM: one token tile, 16 row tiles
+    (14, 1024, 2048, 130),   # ragged token tiles
+    (12, 300, 2560, 200),    # ragged row tile, 10 blocks per row
+    (14, 777, 6144, 129),    # 24 blocks per row, ragged both ways
+    (14, 128, 256, 32),      # the smallest matrix-core case
+    (12, 64, 512, 31),       # just below it: the tiled kernel
 ]
 
 
