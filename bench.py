@@ -372,6 +372,48 @@ def measure_matmul_decode(torch, ops, reps=20, span=768 << 20):
                     "matmuls only"}
 
 
+def measure_matmul_prefill(torch, ops, n=N_PREFILL, reps=3):
+    """GpuMatMulQuant at prefill size (n = 2811) on the Qwen3-1.7B layer matrices:
+    the matrix-core GEMM. Reported as useful TFLOP/s (2 n rows cols) against
+    MI355X's dense bf16 peak; the kernel issues three bf16 products per fp32
+    multiply-add (the activations are split into three bf16 terms)."""
+    res = {}
+    layer_us = 0.0
+    for name, t, rows, cols in DECODE_MATRICES:
+        rb = (cols // 256) * (144 if t == 12 else 210)
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(40 + rows + cols + t)
+        blob = torch.randint(0, 256, (rows * rb,), dtype=torch.uint8, device="cuda", generator=gen)
+        blocks = blob.view(-1, 144 if t == 12 else 210)
+        if t == 12:
+            blocks[:, 1] &= 0x3B
+            blocks[:, 3] &= 0x3B
+        else:
+            blocks[:, 209] &= 0x3B
+        x = torch.randn((n, cols), dtype=torch.float32, device="cuda", generator=gen)
+        out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
+        mat = ops.GpuTensor(blob, t, rows, cols)
+        ops.GpuMatMulQuant(mat, x, n, out)
+        torch.cuda.synchronize()
+        ops.profile_start(reps)
+        for _ in range(reps):
+            ops.GpuMatMulQuant(mat, x, n, out)
+        ops.profile_stop()
+        kname, k = next(iter(ops.profile_report().items()))
+        us = k["avg_us"]
+        flops = 2.0 * n * rows * cols
+        res[name] = {"type": "Q4_K" if t == 12 else "Q6_K", "rows": rows, "cols": cols, "us": round(us, 1),
+                     "TFLOPs": round(flops / us / 1e6, 1), "kernel": kname}
+        layer_us += us
+        del blob, blocks, x, out, mat
+        torch.cuda.empty_cache()
+    total_flops = sum(2.0 * n * r * c for _, _, r, c in DECODE_MATRICES)
+    return {"n_tokens": n, "matrices": res, "layer_us": round(layer_us, 1),
+            "layer_TFLOPs": round(total_flops / layer_us / 1e6, 1),
+            "roofline": {"bound": "mfma", "peak": 2500.0, "unit": "TFLOP/s",
+                         "note": "useful fp32-accurate TFLOP/s; the bf16 units execute 3x that"}}
+
+
 def cpu_baseline():
     """The oracle's C restatement of one layer of the chain (n = 2811, 1.7B shape)
     on the host cores, median of 5; plus per-op and single-thread figures. A
@@ -475,6 +517,8 @@ def main():
         extras["prefill_4b_n4096"] = measure_prefill_4b(torch, ops, tab)
         log("decode matmuls (GpuMatMulQuant, n = 1)")
         extras["matmul_decode_n1"] = measure_matmul_decode(torch, ops)
+        log("prefill matmuls (GpuMatMulQuant, n = 2811)")
+        extras["matmul_prefill_n2811"] = measure_matmul_prefill(torch, ops)
         log("gather Q4_K / Q6_K")
         extras["gather_q4k_n2811"] = measure_gather(torch, ops, ops.GGML_Q4_K, 144)
         extras["gather_q6k_n2811"] = measure_gather(torch, ops, ops.GGML_Q6_K, 210)

@@ -48,8 +48,18 @@ __device__ __forceinline__ float HalfF(uint32_t bits) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
 }
 
+// Hides a packed-quant word's known-zero bits from the optimiser so bytes are
+// converted directly (v_cvt_f32_ubyte{0..3}) instead of extracted first. Emits
+// no instruction.
+__device__ __forceinline__ uint32_t Opaque(uint32_t w) {
+  __asm__("" : "+v"(w));
+  return w;
+}
+
 // Eight exact integers (as bytes, unsigned or signed) -> eight bf16 lanes.
 __device__ __forceinline__ Bf16x8 BytesToBf16U(uint32_t lo, uint32_t hi) {
+  lo = Opaque(lo);
+  hi = Opaque(hi);
   Bf16x8 v;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
