@@ -114,6 +114,21 @@ RPG_OPS_API int32_t rpg_op_vec_add_inplace(float* a, const float* b, int64_t n);
 RPG_OPS_API int32_t rpg_op_embedding_lookup(uint32_t type, const uint8_t* emb, int64_t rows, int64_t cols,
                                             const int32_t* toks, int64_t seq, float* x);
 
+/* Causal attention over one layer of the fp16 KV cache: q / out are
+ * [seq][n_heads][head_dim] fp32 (head_dim 128), k_layer / v_layer
+ * [n_kv_heads][max_seq][head_dim] fp16 bits; token t attends to positions
+ * [0, pos0 + t]. sh_positions > 0: position budget for graph capture.
+ * Replaces: GpuAttentionFromCache, src/kernels_gpu.h:113-116 (its ModelMeta
+ * argument flattened to the three head counts). */
+RPG_OPS_API int32_t rpg_op_attention_from_cache(const float* q, int32_t n_heads, int32_t n_kv_heads,
+                                                int32_t head_dim, int64_t pos0, int64_t seq,
+                                                const uint16_t* k_layer, const uint16_t* v_layer, int64_t max_seq,
+                                                float* out, int64_t sh_positions);
+
+/* Pre-sizes the attention's partials buffer for graph capture.
+ * Replaces: GpuAttentionWarmupShmem, src/kernels_gpu.h:128. */
+RPG_OPS_API int32_t rpg_op_attention_warmup(int64_t sh_positions);
+
 /* out[t * rows + r] = dot(row r of the [rows][cols] matrix w of `type`, row t of
  * x), i.e. OUT[n_tokens, rows] = X[n_tokens, cols] . W^T. Weights are dequantised
  * bit-exactly and summed in fp32.

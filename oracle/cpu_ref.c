@@ -183,6 +183,61 @@ int ora_dequantize_row(uint32_t type, const uint8_t* src, int64_t n_elems, float
   }
 }
 
+/* src/kernels_gpu.cu:737-823: softmax over the cached positions in double (the
+ * reference subtracts the max, exponentiates in fp32 and sums in double; here
+ * every step is double, the exact answer to compare against). */
+int ora_attention_f64(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t max_seq, int32_t n_heads,
+                      int32_t n_kv_heads, int32_t d, int64_t pos0, int64_t seq, double* out, double* smag,
+                      double* vmax) {
+  if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads != 0 || d <= 0 || pos0 < 0 || seq < 0 ||
+      pos0 + seq > max_seq)
+    return -1;
+  const int32_t group = n_heads / n_kv_heads;
+  const double scale = (double)(1.0f / sqrtf((float)d));
+  double* s = (double*)malloc((size_t)(pos0 + seq + 1) * sizeof(double));
+  if (s == NULL) return -1;
+  for (int64_t t = 0; t < seq; ++t) {
+    const int64_t pos = pos0 + t;
+    for (int32_t h = 0; h < n_heads; ++h) {
+      const int32_t kh = h / group;
+      const float* qt = q + (t * n_heads + h) * d;
+      const uint16_t* kb = kc + (int64_t)kh * max_seq * d;
+      const uint16_t* vb = vc + (int64_t)kh * max_seq * d;
+      double mx = -INFINITY, mag = 0.0, vm = 0.0;
+      for (int64_t j = 0; j <= pos; ++j) {
+        double acc = 0.0, a = 0.0;
+        for (int32_t e = 0; e < d; ++e) {
+          const double p = (double)qt[e] * (double)ora_f16_to_f32(kb[j * d + e]);
+          acc += p;
+          a += fabs(p);
+        }
+        s[j] = acc * scale;
+        if (s[j] > mx) mx = s[j];
+        if (a * scale > mag) mag = a * scale;
+        for (int32_t e = 0; e < d; ++e) {
+          const double v = fabs((double)ora_f16_to_f32(vb[j * d + e]));
+          if (v > vm) vm = v;
+        }
+      }
+      double sum = 0.0;
+      for (int64_t j = 0; j <= pos; ++j) {
+        s[j] = exp(s[j] - mx);
+        sum += s[j];
+      }
+      double* ot = out + (t * n_heads + h) * d;
+      for (int32_t e = 0; e < d; ++e) {
+        double acc = 0.0;
+        for (int64_t j = 0; j <= pos; ++j) acc += s[j] * (double)ora_f16_to_f32(vb[j * d + e]);
+        ot[e] = acc / sum;
+      }
+      if (smag != NULL) smag[t * n_heads + h] = mag;
+      if (vmax != NULL) vmax[t * n_heads + h] = vm;
+    }
+  }
+  free(s);
+  return 0;
+}
+
 /* src/kernels_gpu.cu:166-560 (MatMulQuantKernel and its Q4_K / Q6_K forms):
  * OUT[t * rows + r] = dot(dequantised row r of W, row t of X). The reference sums
  * in fp32 in a thread-strided order plus a tree; here every product is exact in

@@ -31,6 +31,9 @@
  *   ora_matmul_quant_f64 numpy float64 dot products (BLAS) of the dequantised
  *                        matrix, one-hot inputs select exact matrix columns,
  *                        linearity in X
+ *   ora_attention_f64    numpy float64 softmax attention, equal keys give the
+ *                        mean of v, a dominant score selects its v row,
+ *                        rows past the causal limit do not matter
  */
 #ifndef RPG_ORACLE_CPU_REF_H
 #define RPG_ORACLE_CPU_REF_H
@@ -56,6 +59,18 @@ int64_t ora_type_row_bytes(uint32_t type, int64_t n_elems); /* <0 if unsupported
 int ora_dequantize_row(uint32_t type, const uint8_t* src, int64_t n_elems, float* dst);
 int ora_embedding_lookup(uint32_t type, const uint8_t* emb, int64_t rows, int64_t cols, const int32_t* toks,
                          int64_t seq, float* x);
+
+/* ---- attention over the fp16 KV cache --------------------------------------- */
+/* src/kernels_gpu.cu:737-823 (AttentionFromCacheKernel) in double: for token t
+ * (position pos0 + t) and head h, kv head h / (n_heads / n_kv_heads):
+ * s_j = (q . k_j) * scale, scale = (double)(1.0f / sqrtf((float)d)), over j in
+ * [0, pos0 + t]; p = softmax(s); out = sum_j p_j v_j. q / out [seq][n_heads][d];
+ * caches [n_kv][max_seq][d] fp16 bits. Optional outputs per (t, h): smag =
+ * max_j scale * sum_d |q_d k_jd| (the scale of the scores' rounding) and
+ * vmax = max_j max_d |v_jd|. Returns 0, or -1 on bad arguments. */
+int ora_attention_f64(const float* q, const uint16_t* kc, const uint16_t* vc, int64_t max_seq, int32_t n_heads,
+                      int32_t n_kv_heads, int32_t d, int64_t pos0, int64_t seq, double* out, double* smag,
+                      double* vmax);
 
 /* ---- quantized matmul ------------------------------------------------------ */
 /* OUT[t][r] = sum_e W[r][e] * X[t][e] for the raw [rows][row_bytes] matrix W

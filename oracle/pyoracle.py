@@ -30,6 +30,7 @@ _SIGS = {
     "ora_dequantize_row": (ctypes.c_int, [_u32, _vp, _i64, _vp]),
     "ora_embedding_lookup": (ctypes.c_int, [_u32, _vp, _i64, _i64, _vp, _i64, _vp]),
     "ora_matmul_quant_f64": (ctypes.c_int, [_u32, _vp, _i64, _i64, _vp, _i64, _vp, _vp]),
+    "ora_attention_f64": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i64, _i64, _vp, _vp, _vp]),
     "ora_rms_norm": (None, [_vp, _vp, _i64, _i64, _i64, _f32, _vp]),
     "ora_build_rope_table": (None, [_i32, _f64, _i64, _vp]),
     "ora_rope": (None, [_vp, _i32, _i32, _vp, _i64, _i64]),
@@ -158,6 +159,20 @@ def matmul_quant_f64(ggml_type: int, w: np.ndarray, rows: int, cols: int, x: np.
     absdot = np.empty_like(out)
     assert lib().ora_matmul_quant_f64(ggml_type, _p(w), rows, cols, _p(x), x.shape[0], _p(out), _p(absdot)) == 0
     return out, absdot
+
+
+def attention_f64(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, max_seq: int, n_heads: int, n_kv_heads: int,
+                  d: int, pos0: int, seq: int):
+    """(out, smag, vmax) in float64: out [seq, n_heads, d]; smag / vmax [seq, n_heads]."""
+    q = np.ascontiguousarray(q, dtype=np.float32).reshape(-1)
+    kc = np.ascontiguousarray(kc, dtype=np.uint16).reshape(-1)
+    vc = np.ascontiguousarray(vc, dtype=np.uint16).reshape(-1)
+    out = np.empty((seq, n_heads, d), dtype=np.float64)
+    smag = np.empty((seq, n_heads), dtype=np.float64)
+    vmax = np.empty((seq, n_heads), dtype=np.float64)
+    assert lib().ora_attention_f64(_p(q), _p(kc), _p(vc), max_seq, n_heads, n_kv_heads, d, pos0, seq, _p(out),
+                                   _p(smag), _p(vmax)) == 0
+    return out, smag, vmax
 
 
 def ref_dequantize_row(ggml_type: int, raw: np.ndarray, n: int):

@@ -114,6 +114,22 @@ int32_t rpg_op_embedding_lookup(uint32_t type, const uint8_t* emb, int64_t rows,
   return Guard([&] { rpg::GpuEmbeddingLookupRaw(type, emb, rows, cols, toks, seq, x); });
 }
 
+int32_t rpg_op_attention_from_cache(const float* q, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                    int64_t pos0, int64_t seq, const uint16_t* k_layer, const uint16_t* v_layer,
+                                    int64_t max_seq, float* out, int64_t sh_positions) {
+  return Guard([&] {
+    rpg::ModelMeta c;
+    c.n_heads = n_heads;
+    c.n_kv_heads = n_kv_heads;
+    c.head_dim = head_dim;
+    rpg::GpuAttentionFromCache(c, pos0, q, seq, k_layer, v_layer, max_seq, out, sh_positions);
+  });
+}
+
+int32_t rpg_op_attention_warmup(int64_t sh_positions) {
+  return Guard([&] { rpg::GpuAttentionWarmupShmem(sh_positions); });
+}
+
 int32_t rpg_op_matmul_quant(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols, const float* x,
                             int64_t n_tokens, float* out) {
   return Guard([&] { rpg::GpuMatMulQuantRaw(type, w, rows, cols, x, n_tokens, out); });

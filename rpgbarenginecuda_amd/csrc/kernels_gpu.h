@@ -160,6 +160,24 @@ void GpuQkNormRopeKv(float* q, float* k, const float* v, const float* q_norm, co
 void GpuEmbeddingLookupRaw(uint32_t type, const uint8_t* emb_dev, int64_t rows, int64_t cols,
                            const int32_t* toks_dev, int64_t seq, float* x_dev);
 
+// ---------------------------------------------------------------- attention
+
+// Causal attention over the fp16 KV cache (src/kernels_gpu.h:113-116): for token
+// t (absolute position pos0 + t) and query head h, softmax((q . k_j) / sqrt(d))
+// over the cached positions j <= pos0 + t of kv head h / (n_heads / n_kv_heads),
+// then the weighted sum of the v rows. q and out are [seq][n_heads][head_dim]
+// fp32; k_layer / v_layer are one layer of the cache, [n_kv_heads][max_seq][d]
+// fp16 bits. sh_positions > 0 fixes the position budget (needed under graph
+// capture, where pos0 is read from the staging scalar at replay); otherwise
+// pos0 + seq. head_dim must be 128.
+void GpuAttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev, int64_t seq, const uint16_t* k_layer,
+                           const uint16_t* v_layer, int64_t max_seq, float* out_dev, int64_t sh_positions = -1);
+
+// Sizes the attention's partials buffer for up to sh_positions cached positions
+// (decode calls), so that a graph capture of the decode step allocates nothing
+// (src/kernels_gpu.h:128; there it raises the shared-memory limit instead).
+void GpuAttentionWarmupShmem(int64_t sh_positions);
+
 // ---------------------------------------------------------------- quantised matmul
 
 // OUT[t, r] = dot(row r of W, row t of X), i.e. OUT = X . W^T (src/kernels_gpu.h:42-49):

@@ -47,6 +47,8 @@ SIGNATURES = {
     "rpg_op_vec_add_inplace": (_i32, [_vp, _vp, _i64]),
     "rpg_op_embedding_lookup": (_i32, [_u32, _vp, _i64, _i64, _vp, _i64, _vp]),
     "rpg_op_matmul_quant": (_i32, [_u32, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "rpg_op_attention_from_cache": (_i32, [_vp, _i32, _i32, _i32, _i64, _i64, _vp, _vp, _i64, _vp, _i64]),
+    "rpg_op_attention_warmup": (_i32, [_i64]),
     "rpg_op_add_rms_norm": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _vp]),
     "rpg_op_qk_norm_rope_kv": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _i64, _f32,
                                       _vp, _vp, _i64, _i32]),
@@ -262,6 +264,23 @@ def GpuMatMulQuant(w: GpuTensor, x, n_tokens: int, out) -> None:
         w.type, _addr(w.buf, w.rows * w.row_bytes(), name="w"), w.rows, w.cols,
         _addr(x, 4 * n_tokens * w.cols, torch.float32, "x"), n_tokens,
         _addr(out, 4 * n_tokens * w.rows, torch.float32, "out")))
+
+
+def GpuAttentionFromCache(n_heads: int, n_kv_heads: int, head_dim: int, pos0: int, q, seq: int, k_layer, v_layer,
+                          max_seq: int, out, sh_positions: int = -1) -> None:
+    """Causal attention over one fp16 cache layer (reference GpuAttentionFromCache,
+    src/kernels_gpu.h:113-116, with ModelMeta flattened to the head counts)."""
+    torch = _t()
+    span = 4 * seq * n_heads * head_dim
+    cache = 2 * n_kv_heads * max_seq * head_dim
+    _check(load_library().rpg_op_attention_from_cache(
+        _addr(q, span, torch.float32, "q"), n_heads, n_kv_heads, head_dim, pos0, seq,
+        _addr(k_layer, cache, name="k_layer"), _addr(v_layer, cache, name="v_layer"), max_seq,
+        _addr(out, span, torch.float32, "out"), sh_positions))
+
+
+def GpuAttentionWarmupShmem(sh_positions: int) -> None:
+    _check(load_library().rpg_op_attention_warmup(sh_positions))
 
 
 # ----------------------------------------------------------------------------- fused operators

@@ -1,0 +1,150 @@
+"""Attention over the fp16 KV cache (GpuAttentionFromCache, src/kernels_gpu.h:113-116)
+on the GPU against the float64 oracle.
+
+Bar: the GPU computes each score as an fp32 dot product of 128 terms (plus the
+scale), so |s_gpu - s| <= delta = (d + 2) 2^-24 smag, with smag = max_j scale
+sum_d |q_d k_jd|. A perturbation of every score by at most delta changes each
+softmax weight by a factor within e^(+-2 delta), so the weighted sum of the v
+rows moves by at most (e^(2 delta) - 1) vmax. The exponentials, the running sums
+and the weighted sums add fp32 rounding over at most pos + 1 terms and one merge:
+(pos + 64) 2^-24 vmax more. A wrong row, head, scale or causal limit breaks the
+bound by orders of magnitude.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+U = 2.0 ** -24
+
+
+def case(name: str) -> None:
+    print(f"\n[case] {name}", flush=True)
+
+
+def dev(a):
+    import torch
+
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def host(t):
+    import torch
+
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def check(got, ref, smag, vmax, pos_max, d=128):
+    delta = (d + 2) * U * smag
+    bound = (np.expm1(2 * delta) + (pos_max + 64) * U) * vmax + 1e-30
+    err = np.max(np.abs(got.astype(np.float64) - ref), axis=-1)
+    assert np.all(err <= bound), f"max error / bound = {float(np.max(err / bound)):.3g}"
+
+
+def make(rng, nh, nkv, max_seq, seq, d=128, qscale=1.0):
+    q = rng.normal(0, qscale, (seq, nh, d)).astype(np.float32)
+    kc = rng.normal(0, 1, (nkv, max_seq, d)).astype(np.float16).view(np.uint16)
+    vc = rng.normal(0, 1, (nkv, max_seq, d)).astype(np.float16).view(np.uint16)
+    return q, kc, vc
+
+
+CASES = [
+    # (name, n_heads, n_kv_heads, max_seq, pos0, seq)
+    ("1.7B decode at 2731", 16, 8, 4096, 2731, 1),
+    ("1.7B decode at 0", 16, 8, 4096, 0, 1),
+    ("1.7B decode at 4095 (full cache)", 16, 8, 4096, 4095, 1),
+    ("4B decode at 1000", 32, 8, 4096, 1000, 1),
+    ("1.7B prefill n=21", 16, 8, 4096, 0, 21),
+    ("1.7B small batch continuation", 16, 8, 4096, 300, 3),
+    ("1.7B prefill n=512 after 100", 16, 8, 1024, 100, 512),
+    ("MHA, odd sizes", 4, 4, 200, 37, 70),
+]
+
+
+@pytest.mark.parametrize("name,nh,nkv,max_seq,pos0,seq", CASES)
+def test_attention_from_cache(gpu, ora, name, nh, nkv, max_seq, pos0, seq):
+    import torch
+
+    case(f"attention {name}")
+    rng = np.random.default_rng(1300 + pos0 + seq + nh)
+    q, kc, vc = make(rng, nh, nkv, max_seq, seq, qscale=0.5)
+    out = torch.full((seq, nh, 128), np.nan, dtype=torch.float32, device="cuda")
+    gpu.GpuAttentionFromCache(nh, nkv, 128, pos0, dev(q), seq, dev(kc), dev(vc), max_seq, out)
+    ref, smag, vmax = ora.attention_f64(q, kc, vc, max_seq, nh, nkv, 128, pos0, seq)
+    check(host(out), ref, smag[..., None], vmax[..., None], pos0 + seq)
+
+
+def test_attention_causal_limit_and_budget(gpu, ora):
+    """Cache rows past pos0 + t are never read into the result (garbage there
+    changes nothing, bit for bit); a larger position budget (the graph-capture
+    layout) gives the same bits as the default one."""
+    import torch
+
+    case("attention causal limit / budget")
+    nh, nkv, max_seq, pos0, seq = 16, 8, 4096, 1500, 1
+    rng = np.random.default_rng(1400)
+    q, kc, vc = make(rng, nh, nkv, max_seq, seq)
+    out1 = torch.empty((seq, nh, 128), dtype=torch.float32, device="cuda")
+    gpu.GpuAttentionFromCache(nh, nkv, 128, pos0, dev(q), seq, dev(kc), dev(vc), max_seq, out1)
+    kc2, vc2 = kc.copy().reshape(nkv, max_seq, 128), vc.copy().reshape(nkv, max_seq, 128)
+    kc2[:, pos0 + seq:] = np.float16(np.inf).view(np.uint16)
+    vc2[:, pos0 + seq:] = np.float16(np.nan).view(np.uint16)
+    out2 = torch.empty_like(out1)
+    gpu.GpuAttentionFromCache(nh, nkv, 128, pos0, dev(q), seq, dev(kc2), dev(vc2), max_seq, out2)
+    a = host(out1)
+    assert np.array_equal(a.view(np.uint32), host(out2).view(np.uint32))
+    # the graph layout: chunks planned for the whole cache, same positions used
+    gpu.GpuAttentionWarmupShmem(max_seq)
+    out3 = torch.empty_like(out1)
+    gpu.GpuAttentionFromCache(nh, nkv, 128, pos0, dev(q), seq, dev(kc), dev(vc), max_seq, out3, max_seq)
+    ref, smag, vmax = ora.attention_f64(q, kc, vc, max_seq, nh, nkv, 128, pos0, seq)
+    check(host(out3), ref, smag[..., None], vmax[..., None], pos0 + seq)
+
+
+def test_attention_graph_replay_reads_staged_pos0(gpu, ora):
+    """Decode attention captured in a HIP graph with the position budget of the
+    whole cache; each replay reads pos0 from the staging scalar."""
+    import torch
+
+    case("attention graph replay")
+    nh, nkv, max_seq = 16, 8, 1024
+    rng = np.random.default_rng(1500)
+    q, kc, vc = make(rng, nh, nkv, max_seq, 1)
+    qd, kd, vd = dev(q), dev(kc), dev(vc)
+    out = torch.empty((1, nh, 128), dtype=torch.float32, device="cuda")
+    gpu.init()
+    gpu.GpuAttentionWarmupShmem(max_seq)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with gpu.ScopedEngineStream(s):
+            g.capture_begin()
+            gpu.GpuAttentionFromCache(nh, nkv, 128, 5, qd, 1, kd, vd, max_seq, out, max_seq)
+            g.capture_end()
+    torch.cuda.synchronize()
+    for pos in (5, 17, 640, 1023, 64):
+        gpu.stage_pos0(pos)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        ref, smag, vmax = ora.attention_f64(q, kc, vc, max_seq, nh, nkv, 128, pos, 1)
+        check(host(out), ref, smag[..., None], vmax[..., None], pos + 1)
+
+
+def test_attention_rejects_bad_arguments(gpu):
+    import torch
+
+    case("attention host errors")
+    q = torch.zeros(128 * 16, dtype=torch.float32, device="cuda")
+    kc = torch.zeros(8 * 64 * 128, dtype=torch.int16, device="cuda")
+    out = torch.zeros_like(q)
+    with pytest.raises(gpu.RpgError, match="cache capacity"):
+        gpu.GpuAttentionFromCache(16, 8, 128, 64, q, 1, kc, kc, 64, out)
+    with pytest.raises(gpu.RpgError, match="multiple"):
+        gpu.GpuAttentionFromCache(16, 6, 128, 0, q, 1, kc, kc, 64, out)
+    with pytest.raises(gpu.RpgError, match="head_dim"):
+        gpu.GpuAttentionFromCache(16, 8, 64, 0, q, 1, kc, kc, 64, out)

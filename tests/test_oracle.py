@@ -283,6 +283,68 @@ def test_matmul_quant_f64_one_hot_and_linearity(ora):
         assert np.allclose(oc, 2.0 * oa + ob, rtol=1e-13, atol=1e-13 * np.max(np.abs(oc)))
 
 
+# ----------------------------------------------------------------------------- attention
+
+
+def _np_attention(q, kc, vc, max_seq, nh, nkv, d, pos0, seq):
+    """numpy float64 restatement used only to pin the C oracle."""
+    k = kc.view(np.float16).astype(np.float64).reshape(nkv, max_seq, d)
+    v = vc.view(np.float16).astype(np.float64).reshape(nkv, max_seq, d)
+    qq = q.astype(np.float64).reshape(seq, nh, d)
+    scale = float(np.float32(1.0) / np.sqrt(np.float32(d)))
+    out = np.zeros((seq, nh, d))
+    for t in range(seq):
+        for h in range(nh):
+            kh = h // (nh // nkv)
+            s = (k[kh, :pos0 + t + 1] @ qq[t, h]) * scale
+            p = np.exp(s - s.max())
+            out[t, h] = (p / p.sum()) @ v[kh, :pos0 + t + 1]
+    return out
+
+
+def _cache(rng, nkv, max_seq, d, scale=1.0):
+    return (rng.normal(0, scale, (nkv, max_seq, d)).astype(np.float16).view(np.uint16))
+
+
+def test_attention_f64_vs_numpy(ora):
+    rng = np.random.default_rng(900)
+    nh, nkv, d, max_seq, pos0, seq = 4, 2, 16, 40, 7, 5
+    q = rng.normal(0, 1, (seq, nh, d)).astype(np.float32)
+    kc, vc = _cache(rng, nkv, max_seq, d), _cache(rng, nkv, max_seq, d)
+    out, smag, vmax = ora.attention_f64(q, kc, vc, max_seq, nh, nkv, d, pos0, seq)
+    assert np.allclose(out, _np_attention(q, kc, vc, max_seq, nh, nkv, d, pos0, seq), rtol=1e-12, atol=1e-12)
+    vv = vc.view(np.float16).astype(np.float64).reshape(nkv, max_seq, d)
+    for t in range(seq):
+        for h in range(nh):
+            assert vmax[t, h] == np.max(np.abs(vv[h // 2, :pos0 + t + 1]))
+            assert smag[t, h] > 0
+
+
+def test_attention_f64_closed_forms_and_causality(ora):
+    rng = np.random.default_rng(901)
+    nh, nkv, d, max_seq, pos0, seq = 2, 1, 8, 20, 3, 4
+    q = rng.normal(0, 1, (seq, nh, d)).astype(np.float32)
+    # equal keys: uniform weights, the output is the mean of the visible v rows
+    kc = np.tile(_cache(rng, 1, 1, d), (1, max_seq, 1))
+    vc = _cache(rng, nkv, max_seq, d)
+    out, _, _ = ora.attention_f64(q, kc, vc, max_seq, nh, nkv, d, pos0, seq)
+    vv = vc.view(np.float16).astype(np.float64).reshape(max_seq, d)
+    for t in range(seq):
+        assert np.allclose(out[t], vv[:pos0 + t + 1].mean(axis=0), rtol=1e-12, atol=1e-12)
+    # a dominant score selects its v row
+    kc2 = np.zeros((1, max_seq, d), np.float16)
+    kc2[0, 2, 0] = 60.0
+    q2 = np.zeros((seq, nh, d), np.float32)
+    q2[..., 0] = 60.0
+    out2, _, _ = ora.attention_f64(q2, kc2.view(np.uint16), vc, max_seq, nh, nkv, d, pos0, seq)
+    assert np.allclose(out2, np.broadcast_to(vv[2], out2.shape), rtol=1e-9, atol=1e-9)
+    # rows past pos0 + t never matter
+    vc3 = vc.copy().reshape(max_seq, d)
+    vc3[pos0 + seq:] = np.float16(1000.0).view(np.uint16)
+    out3, _, _ = ora.attention_f64(q, kc, vc3, max_seq, nh, nkv, d, pos0, seq)
+    assert np.array_equal(out3, out)
+
+
 # ----------------------------------------------------------------------------- RMSNorm
 
 
