@@ -37,10 +37,14 @@ def host(t):
     return t.cpu().numpy()
 
 
-def check(got, ref, smag, vmax, pos_max, d=128):
+def check(got, ref, smag, vmax, pos0, d=128):
+    """got / ref [seq, heads, d]; smag / vmax [seq, heads]; token t sees pos0 + t + 1 keys."""
+    seq = ref.shape[0]
+    keys = (pos0 + 1 + np.arange(seq, dtype=np.float64))[:, None]
     delta = (d + 2) * U * smag
-    bound = (np.expm1(2 * delta) + (pos_max + 64) * U) * vmax + 1e-30
-    err = np.max(np.abs(got.astype(np.float64) - ref), axis=-1)
+    bound = (np.expm1(2 * delta) + (keys + 64) * U) * vmax + 1e-30
+    err = np.max(np.abs(got.reshape(ref.shape).astype(np.float64) - ref), axis=-1)
+    assert err.shape == bound.shape
     assert np.all(err <= bound), f"max error / bound = {float(np.max(err / bound)):.3g}"
 
 
@@ -74,7 +78,7 @@ def test_attention_from_cache(gpu, ora, name, nh, nkv, max_seq, pos0, seq):
     out = torch.full((seq, nh, 128), np.nan, dtype=torch.float32, device="cuda")
     gpu.GpuAttentionFromCache(nh, nkv, 128, pos0, dev(q), seq, dev(kc), dev(vc), max_seq, out)
     ref, smag, vmax = ora.attention_f64(q, kc, vc, max_seq, nh, nkv, 128, pos0, seq)
-    check(host(out), ref, smag[..., None], vmax[..., None], pos0 + seq)
+    check(host(out), ref, smag, vmax, pos0)
 
 
 def test_attention_causal_limit_and_budget(gpu, ora):
@@ -101,7 +105,7 @@ def test_attention_causal_limit_and_budget(gpu, ora):
     out3 = torch.empty_like(out1)
     gpu.GpuAttentionFromCache(nh, nkv, 128, pos0, dev(q), seq, dev(kc), dev(vc), max_seq, out3, max_seq)
     ref, smag, vmax = ora.attention_f64(q, kc, vc, max_seq, nh, nkv, 128, pos0, seq)
-    check(host(out3), ref, smag[..., None], vmax[..., None], pos0 + seq)
+    check(host(out3), ref, smag, vmax, pos0)
 
 
 def test_attention_graph_replay_reads_staged_pos0(gpu, ora):
@@ -132,7 +136,7 @@ def test_attention_graph_replay_reads_staged_pos0(gpu, ora):
         g.replay()
         torch.cuda.synchronize()
         ref, smag, vmax = ora.attention_f64(q, kc, vc, max_seq, nh, nkv, 128, pos, 1)
-        check(host(out), ref, smag[..., None], vmax[..., None], pos + 1)
+        check(host(out), ref, smag, vmax, pos)
 
 
 def test_attention_rejects_bad_arguments(gpu):
