@@ -126,13 +126,27 @@ __global__ __launch_bounds__(kBlockThreads) void AttnChunkKernel(
     o0 *= corr;
     o1 *= corr;
     m = mn;
+    // o += sum_j p_j v_j over the block: lane l reads dims 2l, 2l + 1 of each v
+    // row (one 256-byte row per wave load); 16 rows are requested before any is
+    // used so their latencies overlap.
     const int64_t nk = hi - base < 64 ? hi - base : 64;
     const uint32_t* vr = reinterpret_cast<const uint32_t*>(vb + base * kD) + lane;
-    for (int j = 0; j < nk; ++j) {
-      const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j));
-      const uint32_t vv = vr[static_cast<int64_t>(j) * (kD / 2)];
-      o0 = __builtin_fmaf(pj, HalfToF(vv & 0xFFFFu), o0);
-      o1 = __builtin_fmaf(pj, HalfToF(vv >> 16), o1);
+    for (int j0 = 0; j0 < 64; j0 += 16) {
+      if (j0 >= nk) break;
+      uint32_t vv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int j = j0 + i < nk ? j0 + i : static_cast<int>(nk) - 1;  // clamped: stays in the block
+        vv[i] = vr[static_cast<int64_t>(j) * (kD / 2)];
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        // p of a key past the block's end is 0 (invalid lanes), so the clamped
+        // duplicate rows add nothing
+        const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j0 + i));
+        o0 = __builtin_fmaf(pj, HalfToF(vv[i] & 0xFFFFu), o0);
+        o1 = __builtin_fmaf(pj, HalfToF(vv[i] >> 16), o1);
+      }
     }
   }
 
@@ -153,23 +167,37 @@ __global__ __launch_bounds__(kBlockThreads) void AttnChunkKernel(
 }
 
 // Merges the chunks of each (t, h): M = max m_c, L = sum l_c e^(m_c - M),
-// out = sum o_c e^(m_c - M) / L. One wave per (t, h).
+// out = sum o_c e^(m_c - M) / L. One wave per (t, h): lane c holds chunk c's
+// (m, l) and weight; the partial outputs are read 16 chunks at a time (lane l
+// owns dims 2l, 2l + 1). n_chunks <= 64.
 __global__ __launch_bounds__(kBlockThreads) void AttnMergeKernel(const float* __restrict__ part, int64_t pairs,
                                                                  int32_t n_chunks, float* __restrict__ out) {
   const int lane = threadIdx.x & 63;
   const int64_t th = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
   if (th >= pairs) return;
   const float* pp = part + th * n_chunks * kPartFloats;
-  float mx = -INFINITY;
-  for (int c = 0; c < n_chunks; ++c) mx = fmaxf(mx, pp[c * kPartFloats + kD]);
-  float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
-  for (int c = 0; c < n_chunks; ++c) {
-    const float* pc = pp + c * kPartFloats;
-    const float mc = pc[kD];
-    const float f = mc == -INFINITY ? 0.0f : expf(mc - mx);
-    L = __builtin_fmaf(pc[kD + 1], f, L);
-    o0 = __builtin_fmaf(pc[2 * lane], f, o0);
-    o1 = __builtin_fmaf(pc[2 * lane + 1], f, o1);
+  const bool has = lane < n_chunks;
+  const float mc = has ? pp[lane * kPartFloats + kD] : -INFINITY;
+  const float lc = has ? pp[lane * kPartFloats + kD + 1] : 0.0f;
+  const float mx = WaveMax(mc);
+  const float f = mc == -INFINITY ? 0.0f : expf(mc - mx);
+  const float L = WaveSumF(lc * f);
+  float o0 = 0.0f, o1 = 0.0f;
+  for (int c0 = 0; c0 < n_chunks; c0 += 16) {
+    float2 v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int c = c0 + i < n_chunks ? c0 + i : n_chunks - 1;  // clamped: its weight is used only if c0 + i < n
+      v[i] = *reinterpret_cast<const float2*>(pp + c * kPartFloats + 2 * lane);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float fc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), c0 + i));
+      if (c0 + i < n_chunks) {
+        o0 = __builtin_fmaf(v[i].x, fc, o0);
+        o1 = __builtin_fmaf(v[i].y, fc, o1);
+      }
+    }
   }
   const float inv = L > 0.0f ? 1.0f / L : 0.0f;
   out[th * kD + 2 * lane] = o0 * inv;
