@@ -43,19 +43,67 @@ constexpr int kPartFloats = kD + 2;  // o[128], m, l
 
 __device__ __forceinline__ int64_t ReadPos0(int64_t value, const int64_t* dev) { return dev != nullptr ? *dev : value; }
 
+// Wave reductions: DPP inside each 16-lane row (lane pairs xor 1, xor 2, then
+// mirrored halves and rows, which pair every lane with a partner of the other
+// half), then two cross-row exchanges.
+__device__ __forceinline__ float DppMov(float v, int ctrl_sel) {
+  int m;
+  switch (ctrl_sel) {
+    case 0: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false); break;   // quad_perm 1,0,3,2
+    case 1: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false); break;   // quad_perm 2,3,0,1
+    case 2: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false); break;  // row_half_mirror
+    default: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false); break; // row_mirror
+  }
+  return __int_as_float(m);
+}
 __device__ __forceinline__ float WaveMax(float v) {
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  return v;
+  for (int k = 0; k < 4; ++k) v = fmaxf(v, DppMov(v, k));
+  v = fmaxf(v, __shfl_xor(v, 16, 64));
+  return fmaxf(v, __shfl_xor(v, 32, 64));
 }
 __device__ __forceinline__ float WaveSumF(float v) {
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+  for (int k = 0; k < 4; ++k) v += DppMov(v, k);
+  v += __shfl_xor(v, 16, 64);
+  return v + __shfl_xor(v, 32, 64);
 }
 
 __device__ __forceinline__ float HalfToF(uint32_t bits) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
+}
+
+// Merges the chunks of one (t, h): M = max m_c, L = sum l_c e^(m_c - M),
+// out = sum o_c e^(m_c - M) / L. Lane c holds chunk c's (m, l) and weight; the
+// partial outputs are read 16 chunks at a time (lane l owns dims 2l, 2l + 1).
+// n_chunks <= 64.
+__device__ __forceinline__ void MergeChunks(const float* pp, int32_t n_chunks, int lane, float* ot) {
+  const bool has = lane < n_chunks;
+  const float mc = has ? pp[lane * kPartFloats + kD] : -INFINITY;
+  const float lc = has ? pp[lane * kPartFloats + kD + 1] : 0.0f;
+  const float mx = WaveMax(mc);
+  const float f = mc == -INFINITY ? 0.0f : expf(mc - mx);
+  const float L = WaveSumF(lc * f);
+  float o0 = 0.0f, o1 = 0.0f;
+  for (int c0 = 0; c0 < n_chunks; c0 += 16) {
+    float2 v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int c = c0 + i < n_chunks ? c0 + i : n_chunks - 1;  // clamped: its weight is used only if c0 + i < n
+      v[i] = *reinterpret_cast<const float2*>(pp + c * kPartFloats + 2 * lane);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float fc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), c0 + i));
+      if (c0 + i < n_chunks) {
+        o0 = __builtin_fmaf(v[i].x, fc, o0);
+        o1 = __builtin_fmaf(v[i].y, fc, o1);
+      }
+    }
+  }
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  ot[2 * lane] = o0 * inv;
+  ot[2 * lane + 1] = o1 * inv;
 }
 
 // One wave per (t, h, chunk). part == nullptr: a single chunk, the output is
@@ -105,18 +153,18 @@ __global__ __launch_bounds__(kBlockThreads) void AttnChunkKernel(
     float sc = -INFINITY;
     if (valid) {
       const uint4* kr = reinterpret_cast<const uint4*>(kb + s * kD);
-      float acc = 0.0f;
+      float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // four interleaved partial sums: a 32-deep chain
 #pragma unroll
       for (int i = 0; i < kD / 8; ++i) {
         const uint4 w = kr[i];
         const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          acc = __builtin_fmaf(qs[wv][8 * i + 2 * k], HalfToF(wd[k] & 0xFFFFu), acc);
-          acc = __builtin_fmaf(qs[wv][8 * i + 2 * k + 1], HalfToF(wd[k] >> 16), acc);
+          acc[k] = __builtin_fmaf(qs[wv][8 * i + 2 * k], HalfToF(wd[k] & 0xFFFFu), acc[k]);
+          acc[k] = __builtin_fmaf(qs[wv][8 * i + 2 * k + 1], HalfToF(wd[k] >> 16), acc[k]);
         }
       }
-      sc = acc * scale;
+      sc = ((acc[0] + acc[1]) + (acc[2] + acc[3])) * scale;
     }
     const float bm = WaveMax(sc);
     const float mn = fmaxf(m, bm);
@@ -166,48 +214,23 @@ __global__ __launch_bounds__(kBlockThreads) void AttnChunkKernel(
   }
 }
 
-// Merges the chunks of each (t, h): M = max m_c, L = sum l_c e^(m_c - M),
-// out = sum o_c e^(m_c - M) / L. One wave per (t, h): lane c holds chunk c's
-// (m, l) and weight; the partial outputs are read 16 chunks at a time (lane l
-// owns dims 2l, 2l + 1). n_chunks <= 64.
+// One wave per (t, h): merges its n_chunks partials into out. (A merge by the
+// last chunk to arrive would save this launch, but its device-scope release
+// fence writes the whole L2 back once per chunk, which costs more.)
 __global__ __launch_bounds__(kBlockThreads) void AttnMergeKernel(const float* __restrict__ part, int64_t pairs,
-                                                                 int32_t n_chunks, float* __restrict__ out) {
+                                                                  int32_t n_chunks, float* __restrict__ out) {
   const int lane = threadIdx.x & 63;
   const int64_t th = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
   if (th >= pairs) return;
-  const float* pp = part + th * n_chunks * kPartFloats;
-  const bool has = lane < n_chunks;
-  const float mc = has ? pp[lane * kPartFloats + kD] : -INFINITY;
-  const float lc = has ? pp[lane * kPartFloats + kD + 1] : 0.0f;
-  const float mx = WaveMax(mc);
-  const float f = mc == -INFINITY ? 0.0f : expf(mc - mx);
-  const float L = WaveSumF(lc * f);
-  float o0 = 0.0f, o1 = 0.0f;
-  for (int c0 = 0; c0 < n_chunks; c0 += 16) {
-    float2 v[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int c = c0 + i < n_chunks ? c0 + i : n_chunks - 1;  // clamped: its weight is used only if c0 + i < n
-      v[i] = *reinterpret_cast<const float2*>(pp + c * kPartFloats + 2 * lane);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float fc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), c0 + i));
-      if (c0 + i < n_chunks) {
-        o0 = __builtin_fmaf(v[i].x, fc, o0);
-        o1 = __builtin_fmaf(v[i].y, fc, o1);
-      }
-    }
-  }
-  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  out[th * kD + 2 * lane] = o0 * inv;
-  out[th * kD + 2 * lane + 1] = o1 * inv;
+  MergeChunks(part + th * n_chunks * kPartFloats, n_chunks, lane, out + th * kD);
 }
 
 // ---------------------------------------------------------------- partials buffer
 
 // Grow-only device buffer for the chunk partials. Deliberately never freed at
 // exit (a destructor running after the HIP runtime has shut down can hang).
+constexpr int64_t kMaxSplitPairs = 1024;
+
 struct PartialsBuffer {
   std::mutex mu;
   float* ptr = nullptr;
@@ -221,19 +244,20 @@ PartialsBuffer& Partials() {
 float* EnsurePartials(size_t floats) {
   PartialsBuffer& b = Partials();
   std::lock_guard<std::mutex> lock(b.mu);
-  if (b.floats >= floats) return b.ptr;
-  RPG_CHECK(!StreamIsCapturing(),
-            "attention needs a %zu-float partials buffer (have %zu), which cannot be allocated during graph "
-            "capture; call GpuAttentionWarmupShmem(max positions) before capturing",
-            floats, b.floats);
-  if (b.ptr != nullptr) {
-    RPG_HIP_CHECK(hipDeviceSynchronize());
-    RPG_HIP_CHECK(hipFree(b.ptr));
-    b.ptr = nullptr;
-    b.floats = 0;
+  if (b.floats < floats) {
+    RPG_CHECK(!StreamIsCapturing(),
+              "attention needs a %zu-float partials buffer (have %zu), which cannot be allocated during graph "
+              "capture; call GpuAttentionWarmupShmem(max positions) before capturing",
+              floats, b.floats);
+    if (b.ptr != nullptr) {
+      RPG_HIP_CHECK(hipDeviceSynchronize());
+      RPG_HIP_CHECK(hipFree(b.ptr));
+      b.ptr = nullptr;
+      b.floats = 0;
+    }
+    RPG_HIP_CHECK(hipMalloc(&b.ptr, floats * sizeof(float)));
+    b.floats = floats;
   }
-  RPG_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&b.ptr), floats * sizeof(float)));
-  b.floats = floats;
   return b.ptr;
 }
 
@@ -241,7 +265,7 @@ float* EnsurePartials(size_t floats) {
 // when the pairs alone fill the chip; otherwise enough chunks (of at least 64
 // keys, a multiple of 64) for ~2048 waves.
 void PlanChunks(int64_t pairs, int64_t positions, int32_t* n_chunks, int64_t* chunk_len) {
-  if (pairs >= 1024 || positions <= 64) {
+  if (pairs >= kMaxSplitPairs || positions <= 64) {
     *n_chunks = 1;
     *chunk_len = positions;
     return;
