@@ -56,6 +56,11 @@ RPG_OPS_API int32_t rpg_ops_init(void);
 RPG_OPS_API int32_t rpg_ops_set_stream(void* stream);
 RPG_OPS_API void* rpg_ops_get_stream(void);
 
+/* Device address of the pos0 staging scalar (allocating it on first use, so
+ * call it before any capture). The graph path's sampler reads its counter
+ * there. Replaces: PosStagingPtr, src/cuda_common.h:153. */
+RPG_OPS_API int64_t* rpg_ops_pos_staging_ptr(void);
+
 /* Writes pos into the pos0 scalar read by captured (graph) launches; a graph
  * replay loop calls it before each replay. Replaces: StagePos0,
  * src/cuda_common.h:154. */
@@ -136,6 +141,53 @@ RPG_OPS_API int32_t rpg_op_attention_warmup(int64_t sh_positions);
  * flattened to type / data / rows / cols). */
 RPG_OPS_API int32_t rpg_op_matmul_quant(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols,
                                         const float* x, int64_t n_tokens, float* out);
+
+/* ---------------------------------------------------------------- argmax and sampling
+ * n (the vocabulary) is at most 2^22 for all of these. Semantics: greedy
+ * (temperature <= 0) is argmax, ties to the smallest index; otherwise logits *
+ * (1/T), top_k threshold (k-th largest, ties kept), softmax with a double sum,
+ * top_p cut (largest key whose cumulative mass <= 1 - top_p, at least one
+ * token kept, renormalised), and the inverse transform (first running double
+ * sum > u). */
+
+/* *out_idx = index of the largest x[i] above -FLT_MAX (none: 0).
+ * Replaces: GpuArgMax, src/kernels_gpu.h:131-143. */
+RPG_OPS_API int32_t rpg_op_argmax(const float* x, int64_t n, int32_t* out_idx);
+
+/* Host-side counter-based random source: SplitMix64, H(seed, counter) and
+ * u = (H >> 40) * 2^-24 in [0, 1).
+ * Replaces: DevSplitMix64 / DevCounterRng / DevCounterUniform, src/sampler_gpu.h:71-73. */
+RPG_OPS_API uint64_t rpg_sample_split_mix64(uint64_t x);
+RPG_OPS_API uint64_t rpg_sample_counter_rng(uint64_t seed, uint64_t counter);
+RPG_OPS_API float rpg_sample_counter_uniform(uint64_t seed, uint64_t counter);
+
+/* probs[0..n) <- filtered, normalised distribution of logits.
+ * Replaces: GpuFilterToProbs, src/sampler_gpu.h:86-87 (SampleOptions flattened). */
+RPG_OPS_API int32_t rpg_op_filter_to_probs(const float* logits, int64_t n, float temperature, int32_t top_k,
+                                           float top_p, float* probs);
+
+/* *out_idx = first i whose running double sum of probs exceeds u (u in [0, 1));
+ * none: the first maximum. Not capturable.
+ * Replaces: GpuInverseSample, src/sampler_gpu.h:95-96. */
+RPG_OPS_API int32_t rpg_op_inverse_sample(const float* probs, int64_t n, float u, int32_t* out_idx);
+
+/* One token with u = CounterUniform(seed, counter); greedy is rpg_op_argmax.
+ * probs is scratch of n floats. Not capturable (use the _dev form).
+ * Replaces: GpuSampleToken, src/sampler_gpu.h:108-110. */
+RPG_OPS_API int32_t rpg_op_sample_token(const float* logits, int64_t n, float temperature, int32_t top_k,
+                                        float top_p, uint64_t seed, uint64_t counter, float* probs,
+                                        int32_t* out_idx);
+
+/* The same with the counter read on the device from counter_dev (the pos0
+ * staging scalar in the engine's graph path).
+ * Replaces: GpuSampleTokenDev, src/sampler_gpu.h:124-126. */
+RPG_OPS_API int32_t rpg_op_sample_token_dev(const float* logits, int64_t n, float temperature, int32_t top_k,
+                                            float top_p, uint64_t seed, const uint64_t* counter_dev, float* probs,
+                                            int32_t* out_idx);
+
+/* Allocates the sampler's scratch block (call before a graph capture that
+ * samples or takes an argmax). Replaces: GpuSamplerWarmup, src/sampler_gpu.h:130. */
+RPG_OPS_API int32_t rpg_op_sampler_warmup(void);
 
 /* ---------------------------------------------------------------- fused operators */
 

@@ -34,6 +34,15 @@
  *   ora_attention_f64    numpy float64 softmax attention, equal keys give the
  *                        mean of v, a dominant score selects its v row,
  *                        rows past the causal limit do not matter
+ *   ora_split_mix64 /    SplitMix64's published outputs for seed 0 (the first
+ *   ora_counter_rng      five), which CounterRng(0, c) reproduces for c = 0..4
+ *   ora_counter_uniform  24-bit grid, range [0, 1), mean over many counters
+ *   ora_argmax           numpy argmax (first maximum), the -FLT_MAX / -inf floors
+ *   ora_filter_to_probs  a numpy restatement by sorting (np.sort keys for top_k,
+ *                        float64 cumsum for top_p), one-hot for T <= 0, tie
+ *                        groups kept whole, the mass bounds that define the cut
+ *   ora_inverse_sample   np.cumsum (sequential float64) + searchsorted, exact
+ *                        boundaries, the no-crossing fallback
  */
 #ifndef RPG_ORACLE_CPU_REF_H
 #define RPG_ORACLE_CPU_REF_H
@@ -81,6 +90,17 @@ int ora_attention_f64(const float* q, const uint16_t* kc, const uint16_t* vc, in
  * summation error. Returns 0, or -1 for an unsupported type / shape. */
 int ora_matmul_quant_f64(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols, const float* x,
                          int64_t n_tokens, double* out, double* absdot);
+
+/* ---- argmax and sampling (cpu_sample.c) ------------------------------------ */
+uint64_t ora_split_mix64(uint64_t x);
+uint64_t ora_counter_rng(uint64_t seed, uint64_t counter);
+float ora_counter_uniform(uint64_t seed, uint64_t counter);
+int32_t ora_argmax(const float* x, int64_t n, float init);
+int ora_filter_to_probs(const float* logits, int64_t n, float temperature, int32_t top_k, float top_p, float* probs,
+                        double* margin);
+int32_t ora_inverse_sample(const float* probs, int64_t n, float u);
+int32_t ora_sample_token(const float* logits, int64_t n, float temperature, int32_t top_k, float top_p, uint64_t seed,
+                         uint64_t counter, float* probs);
 
 /* ---- layer ops, fp32 in the reference's op order -------------------------- */
 void ora_rms_norm(const float* x, const float* w, int64_t n_rows, int64_t n, int64_t stride, float eps, float* out);

@@ -31,6 +31,13 @@ _SIGS = {
     "ora_embedding_lookup": (ctypes.c_int, [_u32, _vp, _i64, _i64, _vp, _i64, _vp]),
     "ora_matmul_quant_f64": (ctypes.c_int, [_u32, _vp, _i64, _i64, _vp, _i64, _vp, _vp]),
     "ora_attention_f64": (ctypes.c_int, [_vp, _vp, _vp, _i64, _i32, _i32, _i32, _i64, _i64, _vp, _vp, _vp]),
+    "ora_split_mix64": (ctypes.c_uint64, [ctypes.c_uint64]),
+    "ora_counter_rng": (ctypes.c_uint64, [ctypes.c_uint64, ctypes.c_uint64]),
+    "ora_counter_uniform": (_f32, [ctypes.c_uint64, ctypes.c_uint64]),
+    "ora_argmax": (_i32, [_vp, _i64, _f32]),
+    "ora_filter_to_probs": (ctypes.c_int, [_vp, _i64, _f32, _i32, _f32, _vp, _vp]),
+    "ora_inverse_sample": (_i32, [_vp, _i64, _f32]),
+    "ora_sample_token": (_i32, [_vp, _i64, _f32, _i32, _f32, ctypes.c_uint64, ctypes.c_uint64, _vp]),
     "ora_rms_norm": (None, [_vp, _vp, _i64, _i64, _i64, _f32, _vp]),
     "ora_build_rope_table": (None, [_i32, _f64, _i64, _vp]),
     "ora_rope": (None, [_vp, _i32, _i32, _vp, _i64, _i64]),
@@ -186,6 +193,47 @@ def ref_dequantize_row(ggml_type: int, raw: np.ndarray, n: int):
 
 
 # ------------------------------------------------------------------------- layer ops (fp32)
+
+
+def split_mix64(x: int) -> int:
+    return int(lib().ora_split_mix64(x))
+
+
+def counter_rng(seed: int, counter: int) -> int:
+    return int(lib().ora_counter_rng(seed, counter))
+
+
+def counter_uniform(seed: int, counter: int) -> float:
+    return float(lib().ora_counter_uniform(seed, counter))
+
+
+def argmax(x: np.ndarray, init: float) -> int:
+    x = _f(x)
+    return int(lib().ora_argmax(_p(x), x.size, init))
+
+
+def filter_to_probs(logits: np.ndarray, temperature: float, top_k: int, top_p: float):
+    """(probs, margin): the filtered distribution and top_p's decision margin."""
+    logits = _f(logits)
+    probs = np.empty_like(logits)
+    margin = ctypes.c_double(0.0)
+    rc = lib().ora_filter_to_probs(_p(logits), logits.size, temperature, top_k, top_p, _p(probs),
+                                   ctypes.byref(margin))
+    if rc != 0:
+        raise ValueError("ora_filter_to_probs failed")
+    return probs, float(margin.value)
+
+
+def inverse_sample(probs: np.ndarray, u: float) -> int:
+    probs = _f(probs)
+    return int(lib().ora_inverse_sample(_p(probs), probs.size, u))
+
+
+def sample_token(logits: np.ndarray, temperature: float, top_k: int, top_p: float, seed: int, counter: int) -> int:
+    logits = _f(logits)
+    scratch = np.empty_like(logits)
+    return int(lib().ora_sample_token(_p(logits), logits.size, temperature, top_k, top_p, seed, counter,
+                                      _p(scratch)))
 
 
 def rms_norm(x: np.ndarray, w: np.ndarray, n_rows: int, n: int, stride: int, eps: float) -> np.ndarray:

@@ -11,6 +11,7 @@
 #include "common.h"
 #include "hip_common.h"
 #include "kernels_gpu.h"
+#include "sampler_gpu.h"
 
 namespace {
 
@@ -33,6 +34,14 @@ int32_t Guard(F&& f) {
   }
 }
 
+rpg::SampleOptions Options(float temperature, int32_t top_k, float top_p) {
+  rpg::SampleOptions o;
+  o.temperature = temperature;
+  o.top_k = top_k;
+  o.top_p = top_p;
+  return o;
+}
+
 }  // namespace
 
 extern "C" {
@@ -50,6 +59,12 @@ int32_t rpg_ops_set_stream(void* stream) {
 }
 
 void* rpg_ops_get_stream(void) { return static_cast<void*>(rpg::EngineStream()); }
+
+int64_t* rpg_ops_pos_staging_ptr(void) {
+  int64_t* p = nullptr;
+  if (Guard([&] { p = rpg::PosStagingPtr(); }) != RPG_OPS_OK) return nullptr;
+  return p;
+}
 
 int32_t rpg_ops_stage_pos0(int64_t pos) {
   return Guard([&] { rpg::StagePos0(pos); });
@@ -128,6 +143,42 @@ int32_t rpg_op_attention_from_cache(const float* q, int32_t n_heads, int32_t n_k
 
 int32_t rpg_op_attention_warmup(int64_t sh_positions) {
   return Guard([&] { rpg::GpuAttentionWarmupShmem(sh_positions); });
+}
+
+int32_t rpg_op_argmax(const float* x, int64_t n, int32_t* out_idx) {
+  return Guard([&] { rpg::GpuArgMax(x, n, out_idx); });
+}
+
+uint64_t rpg_sample_split_mix64(uint64_t x) { return rpg::DevSplitMix64(x); }
+
+uint64_t rpg_sample_counter_rng(uint64_t seed, uint64_t counter) { return rpg::DevCounterRng(seed, counter); }
+
+float rpg_sample_counter_uniform(uint64_t seed, uint64_t counter) { return rpg::DevCounterUniform(seed, counter); }
+
+int32_t rpg_op_filter_to_probs(const float* logits, int64_t n, float temperature, int32_t top_k, float top_p,
+                               float* probs) {
+  return Guard([&] { rpg::GpuFilterToProbs(logits, n, Options(temperature, top_k, top_p), probs); });
+}
+
+int32_t rpg_op_inverse_sample(const float* probs, int64_t n, float u, int32_t* out_idx) {
+  return Guard([&] { rpg::GpuInverseSample(probs, n, u, out_idx); });
+}
+
+int32_t rpg_op_sample_token(const float* logits, int64_t n, float temperature, int32_t top_k, float top_p,
+                            uint64_t seed, uint64_t counter, float* probs, int32_t* out_idx) {
+  return Guard(
+      [&] { rpg::GpuSampleToken(logits, n, Options(temperature, top_k, top_p), seed, counter, probs, out_idx); });
+}
+
+int32_t rpg_op_sample_token_dev(const float* logits, int64_t n, float temperature, int32_t top_k, float top_p,
+                                uint64_t seed, const uint64_t* counter_dev, float* probs, int32_t* out_idx) {
+  return Guard([&] {
+    rpg::GpuSampleTokenDev(logits, n, Options(temperature, top_k, top_p), seed, counter_dev, probs, out_idx);
+  });
+}
+
+int32_t rpg_op_sampler_warmup(void) {
+  return Guard([] { rpg::GpuSamplerWarmup(); });
 }
 
 int32_t rpg_op_matmul_quant(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols, const float* x,

@@ -191,6 +191,13 @@ void GpuMatMulQuant(const GpuTensor& w, const float* X_dev, int64_t n_tokens, fl
 void GpuMatMulQuantRaw(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_t cols, const float* x_dev,
                        int64_t n_tokens, float* out_dev);
 
+// ---------------------------------------------------------------- argmax
+
+// Index of the largest of x[0..n) (src/kernels_gpu.h:131-143): only values above
+// -FLT_MAX count (none -> 0), ties go to the smallest index, NaN never wins.
+// n <= kSamplerMaxVocab (sampler_gpu.h, which declares the sampler around it).
+void GpuArgMax(const float* x_dev, int64_t n, int32_t* out_idx_dev);
+
 // ---------------------------------------------------------------- measurement / verification
 
 // Streaming copy of `bytes` (multiple of 16) used to calibrate bandwidth and

@@ -36,6 +36,16 @@ SIGNATURES = {
     "rpg_ops_set_stream": (_i32, [_vp]),
     "rpg_ops_get_stream": (_vp, []),
     "rpg_ops_stage_pos0": (_i32, [_i64]),
+    "rpg_ops_pos_staging_ptr": (_vp, []),
+    "rpg_op_argmax": (_i32, [_vp, _i64, _vp]),
+    "rpg_sample_split_mix64": (ctypes.c_uint64, [ctypes.c_uint64]),
+    "rpg_sample_counter_rng": (ctypes.c_uint64, [ctypes.c_uint64, ctypes.c_uint64]),
+    "rpg_sample_counter_uniform": (_f32, [ctypes.c_uint64, ctypes.c_uint64]),
+    "rpg_op_filter_to_probs": (_i32, [_vp, _i64, _f32, _i32, _f32, _vp]),
+    "rpg_op_inverse_sample": (_i32, [_vp, _i64, _f32, _vp]),
+    "rpg_op_sample_token": (_i32, [_vp, _i64, _f32, _i32, _f32, ctypes.c_uint64, ctypes.c_uint64, _vp, _vp]),
+    "rpg_op_sample_token_dev": (_i32, [_vp, _i64, _f32, _i32, _f32, ctypes.c_uint64, _vp, _vp, _vp]),
+    "rpg_op_sampler_warmup": (_i32, []),
     "rpg_ops_device_info": (_i32, [ctypes.c_char_p, _i32]),
     "rpg_ops_type_row_bytes": (_i64, [_u32, _i64]),
     "rpg_ops_build_rope_table": (_i32, [_i32, _f64, _i64, _vp]),
@@ -168,6 +178,14 @@ def stage_pos0(pos: int) -> None:
     _check(load_library().rpg_ops_stage_pos0(int(pos)))
 
 
+def pos_staging_ptr() -> int:
+    """Device address of the pos0 staging scalar (reference PosStagingPtr, src/cuda_common.h:153)."""
+    p = load_library().rpg_ops_pos_staging_ptr()
+    if not p:
+        _check(-1)
+    return p
+
+
 def device_info() -> tuple[bool, str]:
     buf = ctypes.create_string_buffer(512)
     rc = _check(load_library().rpg_ops_device_info(buf, 512))
@@ -281,6 +299,73 @@ def GpuAttentionFromCache(n_heads: int, n_kv_heads: int, head_dim: int, pos0: in
 
 def GpuAttentionWarmupShmem(sh_positions: int) -> None:
     _check(load_library().rpg_op_attention_warmup(sh_positions))
+
+
+# ----------------------------------------------------------------------------- argmax and sampling
+
+
+class SampleOptions:
+    """Sampling parameters (reference SampleOptions, src/sampler.h:35-46)."""
+
+    def __init__(self, temperature: float = 1.0, top_k: int = 0, top_p: float = 1.0):
+        self.temperature = float(temperature)
+        self.top_k = int(top_k)
+        self.top_p = float(top_p)
+
+
+def GpuArgMax(x, n: int, out_idx) -> None:
+    """out_idx[0] = first index of the largest x[i] above -FLT_MAX (reference GpuArgMax, src/kernels_gpu.h:131-143)."""
+    torch = _t()
+    _check(load_library().rpg_op_argmax(_addr(x, 4 * n, torch.float32, "x"), n,
+                                        _addr(out_idx, 4, torch.int32, "out_idx")))
+
+
+def DevSplitMix64(x: int) -> int:
+    return int(load_library().rpg_sample_split_mix64(x))
+
+
+def DevCounterRng(seed: int, counter: int) -> int:
+    return int(load_library().rpg_sample_counter_rng(seed, counter))
+
+
+def DevCounterUniform(seed: int, counter: int) -> float:
+    return float(load_library().rpg_sample_counter_uniform(seed, counter))
+
+
+def GpuFilterToProbs(logits, n: int, opt: SampleOptions, probs) -> None:
+    """Filtered, normalised distribution (reference GpuFilterToProbs, src/sampler_gpu.h:86-87)."""
+    torch = _t()
+    _check(load_library().rpg_op_filter_to_probs(
+        _addr(logits, 4 * n, torch.float32, "logits"), n, opt.temperature, opt.top_k, opt.top_p,
+        _addr(probs, 4 * n, torch.float32, "probs")))
+
+
+def GpuInverseSample(probs, n: int, u: float, out_idx) -> None:
+    """Inverse transform at a host u (reference GpuInverseSample, src/sampler_gpu.h:95-96)."""
+    torch = _t()
+    _check(load_library().rpg_op_inverse_sample(_addr(probs, 4 * n, torch.float32, "probs"), n, u,
+                                                _addr(out_idx, 4, torch.int32, "out_idx")))
+
+
+def GpuSampleToken(logits, n: int, opt: SampleOptions, seed: int, counter: int, probs, out_idx) -> None:
+    """One token (reference GpuSampleToken, src/sampler_gpu.h:108-110)."""
+    torch = _t()
+    _check(load_library().rpg_op_sample_token(
+        _addr(logits, 4 * n, torch.float32, "logits"), n, opt.temperature, opt.top_k, opt.top_p, seed, counter,
+        _addr(probs, 4 * n, torch.float32, "probs"), _addr(out_idx, 4, torch.int32, "out_idx")))
+
+
+def GpuSampleTokenDev(logits, n: int, opt: SampleOptions, seed: int, counter_dev, probs, out_idx) -> None:
+    """One token with the counter read on the device (reference GpuSampleTokenDev, src/sampler_gpu.h:124-126)."""
+    torch = _t()
+    _check(load_library().rpg_op_sample_token_dev(
+        _addr(logits, 4 * n, torch.float32, "logits"), n, opt.temperature, opt.top_k, opt.top_p, seed,
+        _addr(counter_dev, 8, name="counter_dev"), _addr(probs, 4 * n, torch.float32, "probs"),
+        _addr(out_idx, 4, torch.int32, "out_idx")))
+
+
+def GpuSamplerWarmup() -> None:
+    _check(load_library().rpg_op_sampler_warmup())
 
 
 # ----------------------------------------------------------------------------- fused operators

@@ -108,3 +108,62 @@ def special_q6k_blocks() -> np.ndarray:
 
 def normal(rng: np.random.Generator, shape, mean=0.0, std=1.0) -> np.ndarray:
     return rng.normal(mean, std, size=shape).astype(np.float32)
+
+
+# ----------------------------------------------------------------------------- sampling
+
+# The reference's sampler case matrix (tools/sample_check.cu:48-61):
+# (temperature, top_k, top_p, seed, tie, description).
+SAMPLE_CASES = [
+    (0.0, 0, 1.0, 11, False, "greedy"),
+    (0.0, 8, 0.9, 12, False, "greedy, filters ignored"),
+    (1.0, 0, 1.0, 13, False, "plain distribution"),
+    (0.7, 40, 1.0, 14, False, "temperature + top_k 40"),
+    (1.3, 0, 0.9, 15, False, "temperature + top_p 0.9"),
+    (0.5, 20, 0.95, 16, False, "all three"),
+    (1.0, 2, 1.0, 17, False, "top_k 2"),
+    (1.0, 0, 0.05, 18, False, "top_p 0.05"),
+    (0.001, 0, 1.0, 19, False, "tiny temperature"),
+    (5.0, 0, 1.0, 20, False, "large temperature"),
+    (1.0, 8, 1.0, 21, True, "exact ties + top_k 8"),
+    (0.0, 0, 1.0, 22, True, "exact ties + greedy"),
+]
+SAMPLE_U_COUNT = 16  # u values drawn per case (tools/sample_check.cu:63)
+
+_M64 = np.uint64(0xFFFFFFFFFFFFFFFF)
+
+
+def split_mix64_np(x: np.ndarray) -> np.ndarray:
+    """SplitMix64 over a uint64 array (wrapping arithmetic)."""
+    with np.errstate(over="ignore"):
+        z = x.astype(np.uint64) + np.uint64(0x9E3779B97F4A7C15)
+        z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
+        z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
+        return z ^ (z >> np.uint64(31))
+
+
+def sample_logits(seed: int, tie: bool, n: int) -> np.ndarray:
+    """The reference's synthetic logits (tools/sample_check.cu:65-76): x in [0, 1)
+    from SplitMix64(seed * 1000003 + i) >> 40, v = (x - 0.5) * 16, with `tie`
+    rounded to multiples of 1/8 (exact ties)."""
+    with np.errstate(over="ignore"):
+        base = np.uint64(seed) * np.uint64(1000003)
+        h = split_mix64_np(base + np.arange(n, dtype=np.uint64))
+    x = (h >> np.uint64(40)).astype(np.float32) * np.float32(1.0 / 16777216.0)
+    v = (x - np.float32(0.5)) * np.float32(16.0)
+    if tie:  # std::round: halves away from zero (exact in float64 for float32 input)
+        y = (v * np.float32(8.0)).astype(np.float64)
+        r = (np.sign(y) * np.floor(np.abs(y) + 0.5)).astype(np.float32)
+        v = (r / np.float32(8.0)).astype(np.float32)
+    return v.astype(np.float32)
+
+
+def order_key_np(x: np.ndarray) -> np.ndarray:
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    return np.where(u & np.uint32(0x80000000), ~u, u | np.uint32(0x80000000)).astype(np.uint32)
+
+
+def from_order_key_np(k) -> np.ndarray:
+    k = np.asarray(k, dtype=np.uint32)
+    u = np.where(k & np.uint32(0x80000000), k & np.uint32(0x7FFFFFFF), ~k).astype(np.uint32)
+    return u.view(np.float32)

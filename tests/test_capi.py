@@ -31,7 +31,7 @@ def ops():
 
 def test_library_exports_exactly_the_header(ops):
     declared = header_symbols()
-    assert len(declared) == 27
+    assert len(declared) == 37
     out = subprocess.run(["nm", "-D", "--defined-only", ops.LIB_PATH], stdout=subprocess.PIPE, text=True,
                          check=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
@@ -148,3 +148,29 @@ def test_python_mirror_rejects_undersized_tensors(ops):
     x = torch.zeros(10)
     with pytest.raises(ops.RpgError, match="not on the GPU"):
         ops.GpuVecAddInPlace(x, x, 10)
+
+
+def test_host_random_source_matches_oracle(ops, ora):
+    """DevSplitMix64 / DevCounterRng / DevCounterUniform are host code: bit-exact
+    with the oracle (itself pinned to SplitMix64's published outputs)."""
+    for x in (0, 1, 0x9E3779B97F4A7C15, 2 ** 63 + 12345, 2 ** 64 - 1):
+        assert ops.DevSplitMix64(x) == ora.split_mix64(x)
+    for seed in (0, 11, 2 ** 40 + 7):
+        for c in (0, 1, 2, 4095, 2 ** 33):
+            assert ops.DevCounterRng(seed, c) == ora.counter_rng(seed, c)
+            assert ops.DevCounterUniform(seed, c) == ora.counter_uniform(seed, c)
+
+
+def test_sampler_host_argument_errors(ops):
+    lib = ops.load_library()
+    assert lib.rpg_op_argmax(None, 10, FAKE) < 0
+    assert "null" in ops.load_library().rpg_ops_last_error().decode()
+    assert lib.rpg_op_argmax(FAKE, 0, FAKE) < 0                               # empty vocabulary
+    assert lib.rpg_op_argmax(FAKE, (1 << 22) + 1, FAKE) < 0                   # beyond the sampler limit
+    assert "limit" in ops.load_library().rpg_ops_last_error().decode()
+    assert lib.rpg_op_inverse_sample(FAKE, 10, 1.0, FAKE) < 0                 # u outside [0, 1)
+    assert "[0,1)" in ops.load_library().rpg_ops_last_error().decode()
+    assert lib.rpg_op_inverse_sample(FAKE, 10, -0.5, FAKE) < 0
+    assert lib.rpg_op_filter_to_probs(FAKE, 10, 1.0, 0, 1.0, None) < 0
+    assert lib.rpg_op_sample_token_dev(FAKE, 10, 0.7, 0, 0.9, 1, None, FAKE, FAKE) < 0  # no device counter
+    assert "counter" in ops.load_library().rpg_ops_last_error().decode()
