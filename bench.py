@@ -414,6 +414,97 @@ def measure_matmul_prefill(torch, ops, n=N_PREFILL, reps=3):
                          "note": "useful fp32-accurate TFLOP/s; the bf16 units execute 3x that"}}
 
 
+def measure_attention(torch, ops, reps=20):
+    """GpuAttentionFromCache on the Qwen3-1.7B cache (16 q heads, 8 kv heads, d 128,
+    max_seq 4096). Decode (one token at pos0) over rotating cache copies whose
+    total exceeds 2x the Infinity Cache; bytes = the K and V rows read
+    (2 * n_kv * (pos0 + 1) * 128 * 2) plus q and out. Prefill n = 2811 from
+    position 0: useful TFLOP/s = 4 * d * heads * sum over tokens of keys."""
+    nh, nkv, d, max_seq = HQ, HKV, D, MAX_SEQ
+    layer_elems = nkv * max_seq * d
+    copies = 32
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(77)
+    kc = torch.randn((copies, layer_elems), generator=gen, device="cuda").half()
+    vc = torch.randn((copies, layer_elems), generator=gen, device="cuda").half()
+    out = {"decode": {}}
+    q1 = torch.randn((1, nh, d), generator=gen, device="cuda")
+    o1 = torch.empty_like(q1)
+    for pos0 in (511, 2047, 4095):
+        for i in range(4):
+            ops.GpuAttentionFromCache(nh, nkv, d, pos0, q1, 1, kc[i], vc[i], max_seq, o1)
+        torch.cuda.synchronize()
+        ops.profile_start(2 * reps)
+        for r in range(reps):
+            ops.GpuAttentionFromCache(nh, nkv, d, pos0, q1, 1, kc[r % copies], vc[r % copies], max_seq, o1)
+        ops.profile_stop()
+        rep = ops.profile_report()
+        us = sum(k["total_us"] for k in rep.values()) / reps
+        nbytes = 2 * nkv * (pos0 + 1) * d * 2 + 2 * 4 * nh * d
+        out["decode"][f"pos{pos0}"] = {"us": round(us, 2), "GBps": round(nbytes / us / 1e3, 1),
+                                       "pct_peak": round(nbytes / us / 1e3 / PEAK_GBPS * 100, 1),
+                                       "kernels": {n: round(k["avg_us"], 2) for n, k in rep.items()},
+                                       "bytes": nbytes}
+    n = N_PREFILL
+    qp = torch.randn((n, nh, d), generator=gen, device="cuda")
+    op = torch.empty_like(qp)
+    ops.GpuAttentionFromCache(nh, nkv, d, 0, qp, n, kc[0], vc[0], max_seq, op)
+    torch.cuda.synchronize()
+    ops.profile_start(6)
+    for r in range(3):
+        ops.GpuAttentionFromCache(nh, nkv, d, 0, qp, n, kc[r + 1], vc[r + 1], max_seq, op)
+    ops.profile_stop()
+    rep = ops.profile_report()
+    us = sum(k["total_us"] for k in rep.values()) / 3
+    flops = 4.0 * d * nh * (n * (n + 1) / 2)
+    out["prefill_n2811"] = {"us": round(us, 1), "TFLOPs": round(flops / us / 1e6, 2),
+                            "kernels": {n_: round(k["avg_us"], 1) for n_, k in rep.items()}}
+    del kc, vc
+    torch.cuda.empty_cache()
+    return out
+
+
+def measure_sampler(torch, ops, reps=50):
+    """Device argmax and sampling over Qwen3's vocabulary (151936 logits, the
+    reference's synthetic logits seed 5): kernel microseconds per call (sum of
+    the launches, dispatch-attached events) and the stream's wall time per call.
+    Latency-bound: a few MB of traffic per call."""
+    n = VOCAB
+    x = torch.rand(n, generator=torch.Generator(device="cuda").manual_seed(5), device="cuda") * 16 - 8
+    probs = torch.empty(n, device="cuda")
+    idx = torch.empty(1, dtype=torch.int32, device="cuda")
+    ops.GpuSamplerWarmup()
+    cases = {
+        "argmax": lambda: ops.GpuArgMax(x, n, idx),
+        "sample_T0.7_topp0.95": lambda: ops.GpuSampleToken(x, n, ops.SampleOptions(0.7, 0, 0.95), 1, 3, probs, idx),
+        "sample_T0.7_topk20_topp0.95": lambda: ops.GpuSampleToken(x, n, ops.SampleOptions(0.7, 20, 0.95), 1, 3,
+                                                                  probs, idx),
+        "sample_T1": lambda: ops.GpuSampleToken(x, n, ops.SampleOptions(1.0, 0, 1.0), 1, 3, probs, idx),
+    }
+    res = {}
+    for name, fn in cases.items():
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        ops.profile_start(16 * reps)
+        for _ in range(reps):
+            fn()
+        ops.profile_stop()
+        rep = ops.profile_report()
+        kus = sum(k["total_us"] for k in rep.values()) / reps
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        res[name] = {"kernel_us": round(kus, 2), "wall_us": round(e0.elapsed_time(e1) * 1e3 / reps, 2),
+                     "launches": int(sum(k["count"] for k in rep.values()) // reps),
+                     "kernels": {k_: round(v["avg_us"], 2) for k_, v in rep.items()}}
+    return {"vocab": n, **res}
+
+
 def cpu_baseline():
     """The oracle's C restatement of one layer of the chain (n = 2811, 1.7B shape)
     on the host cores, median of 5; plus per-op and single-thread figures. A
@@ -519,6 +610,10 @@ def main():
         extras["matmul_decode_n1"] = measure_matmul_decode(torch, ops)
         log("prefill matmuls (GpuMatMulQuant, n = 2811)")
         extras["matmul_prefill_n2811"] = measure_matmul_prefill(torch, ops)
+        log("attention from the fp16 cache (decode, prefill n=2811)")
+        extras["attention"] = measure_attention(torch, ops)
+        log("argmax / sampler over the 151936-entry vocabulary")
+        extras["sampler"] = measure_sampler(torch, ops)
         log("gather Q4_K / Q6_K")
         extras["gather_q4k_n2811"] = measure_gather(torch, ops, ops.GGML_Q4_K, 144)
         extras["gather_q6k_n2811"] = measure_gather(torch, ops, ops.GGML_Q6_K, 210)
