@@ -505,6 +505,60 @@ def measure_sampler(torch, ops, reps=50):
     return {"vocab": n, **res}
 
 
+def measure_gguf_upload(torch, ops, reps=3):
+    """GpuModel::Load of a Qwen3-1.7B-shaped Q4_K_M GGUF (1.15 GB, random bytes,
+    written to the local temp directory first): file bytes per second from the
+    start of the upload to the last byte on the device (page cache warm), against
+    the PCIe 5.0 x16 host link (64 GB/s per direction). Beside it, the
+    reference's way -- one synchronous pageable copy per tensor out of the
+    mapping (src/gpu_model.cu:40-50) -- done with torch on the same file."""
+    import tempfile
+
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import gguf_writer
+
+    kv, specs = gguf_writer.qwen3_1_7b_specs(tied=True)
+    rng = np.random.default_rng(9)
+    tmpdir = os.environ.get("TMPDIR") or tempfile.gettempdir()
+    path = os.path.join(tmpdir, "rpg_bench_qwen3_1_7b.gguf")
+    size = gguf_writer.write_file(path, kv, specs, lambda name, n: rng.bytes(n))
+    try:
+        runs = []
+        for _ in range(reps):
+            m = ops.GpuModel(path, 4096)
+            runs.append(m.upload_stats())
+            desc = m.describe()
+            m.free()
+            torch.cuda.synchronize()
+        best = min(runs, key=lambda r: r["upload_seconds"])
+        nbytes = best["bytes"]
+        # reference-style: per tensor, one pageable copy from the mapping
+        with ops.GgufFile(path) as g:
+            tensors = g.tensors()
+        ref_times = []
+        for _ in range(reps):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            mm = np.memmap(path, dtype=np.uint8, mode="r")  # mapped per load, as the reference does
+            outs = [torch.from_numpy(np.array(mm[t["file_offset"]:t["file_offset"] + t["n_bytes"]], copy=False))
+                    .to("cuda") for t in tensors]
+            torch.cuda.synchronize()
+            ref_times.append(time.perf_counter() - t0)
+            del outs, mm
+        torch.cuda.empty_cache()
+        gbps = nbytes / best["upload_seconds"] / 1e9
+        ref = sum(t["n_bytes"] for t in tensors) / min(ref_times) / 1e9
+        return {"file_bytes": size, "uploaded_bytes": nbytes, "upload_s": round(best["upload_seconds"], 4),
+                "parse_s": round(best["parse_seconds"], 4), "GBps": round(gbps, 2),
+                "pct_of_pcie5_x16": round(gbps / 64.0 * 100, 1),
+                "runs_s": [round(r["upload_seconds"], 4) for r in runs],
+                "per_tensor_pageable_GBps": round(ref, 2), "describe": desc}
+    finally:
+        os.remove(path)
+
+
 def cpu_baseline():
     """The oracle's C restatement of one layer of the chain (n = 2811, 1.7B shape)
     on the host cores, median of 5; plus per-op and single-thread figures. A
@@ -614,6 +668,8 @@ def main():
         extras["attention"] = measure_attention(torch, ops)
         log("argmax / sampler over the 151936-entry vocabulary")
         extras["sampler"] = measure_sampler(torch, ops)
+        log("GGUF upload (Qwen3-1.7B-shaped file)")
+        extras["gguf_upload"] = measure_gguf_upload(torch, ops)
         log("gather Q4_K / Q6_K")
         extras["gather_q4k_n2811"] = measure_gather(torch, ops, ops.GGML_Q4_K, 144)
         extras["gather_q6k_n2811"] = measure_gather(torch, ops, ops.GGML_Q6_K, 210)

@@ -142,6 +142,65 @@ RPG_OPS_API int32_t rpg_op_attention_warmup(int64_t sh_positions);
 RPG_OPS_API int32_t rpg_op_matmul_quant(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols,
                                         const float* x, int64_t n_tokens, float* out);
 
+/* ---------------------------------------------------------------- GGUF files and the device model
+ * rpg_gguf: a parsed GGUF file (host only, no GPU needed). rpg_model: a qwen3
+ * GGUF uploaded to the device (F32 / Q4_K / Q6_K tensors only): quantized
+ * matrices as raw GGUF bytes, norms as fp32, in one device arena, plus the RoPE
+ * table. Replaces: GgufFile (src/gguf.h:43-97), ReadModelMeta
+ * (src/model_meta.cc:11-78) and GpuModel::Load (src/gpu_model.cu:148-246). */
+typedef struct rpg_gguf rpg_gguf;
+typedef struct rpg_model rpg_model;
+
+/* ModelMeta (src/model_meta.h:27-65) as plain fields; booleans as 0 / 1. */
+typedef struct {
+  char arch[32];
+  char name[128];
+  int32_t n_layers, hidden, n_heads, n_kv_heads, head_dim, value_dim, intermediate, vocab, context_length;
+  float rope_theta, rms_eps;
+  int32_t tied_embeddings, bos_id, eos_id, pad_id, add_bos;
+  int64_t weight_bytes;
+} rpg_model_meta_t;
+
+/* A tensor: data is a host pointer into the file mapping (rpg_gguf) or a device
+ * pointer (rpg_model); dims[0] varies fastest; norms of a model are fp32. */
+typedef struct {
+  const void* data;
+  uint32_t type;
+  int32_t n_dims;
+  int64_t dims[4];
+  int64_t n_elements, n_bytes, file_offset;
+} rpg_tensor_info_t;
+
+RPG_OPS_API int32_t rpg_gguf_open(const char* path, rpg_gguf** out);
+RPG_OPS_API int32_t rpg_gguf_close(rpg_gguf* g);
+RPG_OPS_API int64_t rpg_gguf_tensor_count(const rpg_gguf* g);
+/* Tensor `index` in file order; its name is copied into name[cap]. */
+RPG_OPS_API int32_t rpg_gguf_tensor_info(const rpg_gguf* g, int64_t index, char* name, int32_t cap,
+                                         rpg_tensor_info_t* out);
+/* Metadata value of `key` (item < 0) or item `item` of an array value: *kind = 0
+ * absent, 1 number (*num), 2 bool (*num = 0 / 1), 3 string (copied into str[cap];
+ * the return value is its full length), 4 array (*n_items). */
+RPG_OPS_API int32_t rpg_gguf_meta(const rpg_gguf* g, const char* key, int64_t item, int32_t* kind, double* num,
+                                  char* str, int32_t cap, int64_t* n_items);
+/* ReadModelMeta of the file (qwen3 only). */
+RPG_OPS_API int32_t rpg_gguf_model_meta(const rpg_gguf* g, rpg_model_meta_t* out);
+/* One-line summary; returns its full length. */
+RPG_OPS_API int32_t rpg_gguf_describe(const rpg_gguf* g, char* buf, int32_t cap);
+
+/* Parses and uploads a qwen3 GGUF; max_pos = positions of the RoPE table. */
+RPG_OPS_API int32_t rpg_model_load(const char* path, int32_t max_pos, rpg_model** out);
+RPG_OPS_API int32_t rpg_model_free(rpg_model* m);
+RPG_OPS_API int32_t rpg_model_meta(const rpg_model* m, rpg_model_meta_t* out);
+/* The device tensor loaded from GGUF tensor `name` (output.weight is token_embd
+ * when the embeddings are tied). */
+RPG_OPS_API int32_t rpg_model_tensor(const rpg_model* m, const char* name, rpg_tensor_info_t* out);
+/* Device RoPE table [*n_pos][head_dim] fp32 (cos | sin per row). */
+RPG_OPS_API int32_t rpg_model_rope(const rpg_model* m, const float** tab, int64_t* n_pos);
+RPG_OPS_API int32_t rpg_model_describe(const rpg_model* m, char* buf, int32_t cap);
+/* File bytes moved to the device, and the parse / upload wall times. */
+RPG_OPS_API int32_t rpg_model_upload_stats(const rpg_model* m, int64_t* bytes, double* parse_seconds,
+                                           double* upload_seconds);
+
 /* ---------------------------------------------------------------- argmax and sampling
  * n (the vocabulary) is at most 2^22 for all of these. Semantics: greedy
  * (temperature <= 0) is argmax, ties to the smallest index; otherwise logits *

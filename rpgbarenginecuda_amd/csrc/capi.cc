@@ -3,6 +3,7 @@
 // thread-local-message convention.
 #include "../../include/rpg_ops.h"
 
+#include <algorithm>
 #include <cstring>
 #include <exception>
 #include <new>
@@ -11,6 +12,7 @@
 #include "common.h"
 #include "hip_common.h"
 #include "kernels_gpu.h"
+#include "gpu_model.h"
 #include "sampler_gpu.h"
 
 namespace {
@@ -34,6 +36,39 @@ int32_t Guard(F&& f) {
   }
 }
 
+int32_t CopyText(const std::string& text, char* buf, int32_t cap) {
+  if (buf != nullptr && cap > 0) {
+    const size_t n = std::min(text.size(), static_cast<size_t>(cap - 1));
+    std::memcpy(buf, text.data(), n);
+    buf[n] = '\0';
+  }
+  return static_cast<int32_t>(std::min<size_t>(text.size(), 0x7FFFFFFF));
+}
+
+void FillMeta(const rpg::ModelMeta& c, rpg_model_meta_t* out) {
+  RPG_CHECK(out != nullptr, "null output pointer");
+  std::memset(out, 0, sizeof(*out));
+  CopyText(c.arch, out->arch, sizeof(out->arch));
+  CopyText(c.name, out->name, sizeof(out->name));
+  out->n_layers = c.n_layers;
+  out->hidden = c.hidden;
+  out->n_heads = c.n_heads;
+  out->n_kv_heads = c.n_kv_heads;
+  out->head_dim = c.head_dim;
+  out->value_dim = c.value_dim;
+  out->intermediate = c.intermediate;
+  out->vocab = c.vocab;
+  out->context_length = c.context_length;
+  out->rope_theta = c.rope_theta;
+  out->rms_eps = c.rms_eps;
+  out->tied_embeddings = c.tied_embeddings ? 1 : 0;
+  out->bos_id = c.bos_id;
+  out->eos_id = c.eos_id;
+  out->pad_id = c.pad_id;
+  out->add_bos = c.add_bos ? 1 : 0;
+  out->weight_bytes = c.weight_bytes;
+}
+
 rpg::SampleOptions Options(float temperature, int32_t top_k, float top_p) {
   rpg::SampleOptions o;
   o.temperature = temperature;
@@ -43,6 +78,14 @@ rpg::SampleOptions Options(float temperature, int32_t top_k, float top_p) {
 }
 
 }  // namespace
+
+struct rpg_gguf {
+  rpg::GgufFile file;
+};
+
+struct rpg_model {
+  rpg::GpuModel model;
+};
 
 extern "C" {
 
@@ -143,6 +186,167 @@ int32_t rpg_op_attention_from_cache(const float* q, int32_t n_heads, int32_t n_k
 
 int32_t rpg_op_attention_warmup(int64_t sh_positions) {
   return Guard([&] { rpg::GpuAttentionWarmupShmem(sh_positions); });
+}
+
+int32_t rpg_gguf_open(const char* path, rpg_gguf** out) {
+  return Guard([&] {
+    RPG_CHECK(path != nullptr && out != nullptr, "null argument");
+    *out = nullptr;
+    auto* g = new rpg_gguf{rpg::GgufFile::Open(path)};
+    *out = g;
+  });
+}
+
+int32_t rpg_gguf_close(rpg_gguf* g) {
+  delete g;
+  return RPG_OPS_OK;
+}
+
+int64_t rpg_gguf_tensor_count(const rpg_gguf* g) {
+  if (g == nullptr) {
+    rpg::SetLastError("null GGUF handle");
+    return -1;
+  }
+  return static_cast<int64_t>(g->file.tensors().size());
+}
+
+int32_t rpg_gguf_tensor_info(const rpg_gguf* g, int64_t index, char* name, int32_t cap, rpg_tensor_info_t* out) {
+  return Guard([&] {
+    RPG_CHECK(g != nullptr && out != nullptr, "null argument");
+    const auto& ts = g->file.tensors();
+    RPG_CHECK(index >= 0 && index < static_cast<int64_t>(ts.size()), "tensor index %lld out of range (%zu)",
+              static_cast<long long>(index), ts.size());
+    const rpg::GgufTensor& t = ts[static_cast<size_t>(index)];
+    CopyText(t.name, name, cap);
+    std::memset(out, 0, sizeof(*out));
+    out->data = g->file.TensorBytes(t);
+    out->type = t.type;
+    out->n_dims = static_cast<int32_t>(t.dims.size());
+    for (size_t d = 0; d < t.dims.size(); ++d) out->dims[d] = t.dims[d];
+    out->n_elements = t.n_elements;
+    out->n_bytes = t.n_bytes;
+    out->file_offset = g->file.TensorFileOffset(t);
+  });
+}
+
+int32_t rpg_gguf_meta(const rpg_gguf* g, const char* key, int64_t item, int32_t* kind, double* num, char* str,
+                      int32_t cap, int64_t* n_items) {
+  int32_t len = 0;
+  const int32_t rc = Guard([&] {
+    RPG_CHECK(g != nullptr && key != nullptr && kind != nullptr, "null argument");
+    const rpg::GgufValue* v = &g->file.Meta(key);
+    if (item >= 0) {
+      RPG_CHECK(v->IsArray(), "metadata %s is not an array", key);
+      RPG_CHECK(item < static_cast<int64_t>(v->items.size()), "item %lld out of range for %s (%zu items)",
+                static_cast<long long>(item), key, v->items.size());
+      v = &v->items[static_cast<size_t>(item)];
+    }
+    if (num) *num = 0.0;
+    if (n_items) *n_items = 0;
+    switch (v->kind) {
+      case rpg::GgufValue::Kind::kNone: *kind = 0; break;
+      case rpg::GgufValue::Kind::kNumber:
+        *kind = 1;
+        if (num) *num = v->num;
+        break;
+      case rpg::GgufValue::Kind::kBool:
+        *kind = 2;
+        if (num) *num = v->flag ? 1.0 : 0.0;
+        break;
+      case rpg::GgufValue::Kind::kString:
+        *kind = 3;
+        len = CopyText(v->str, str, cap);
+        break;
+      case rpg::GgufValue::Kind::kArray:
+        *kind = 4;
+        if (n_items) *n_items = static_cast<int64_t>(v->items.size());
+        break;
+    }
+  });
+  return rc < 0 ? rc : len;
+}
+
+int32_t rpg_gguf_model_meta(const rpg_gguf* g, rpg_model_meta_t* out) {
+  return Guard([&] {
+    RPG_CHECK(g != nullptr, "null GGUF handle");
+    FillMeta(rpg::ReadModelMeta(g->file), out);
+  });
+}
+
+int32_t rpg_gguf_describe(const rpg_gguf* g, char* buf, int32_t cap) {
+  int32_t len = 0;
+  const int32_t rc = Guard([&] {
+    RPG_CHECK(g != nullptr, "null GGUF handle");
+    len = CopyText(g->file.Describe(), buf, cap);
+  });
+  return rc < 0 ? rc : len;
+}
+
+int32_t rpg_model_load(const char* path, int32_t max_pos, rpg_model** out) {
+  return Guard([&] {
+    RPG_CHECK(path != nullptr && out != nullptr, "null argument");
+    *out = nullptr;
+    auto* m = new rpg_model{rpg::GpuModel::Load(path, max_pos)};
+    *out = m;
+  });
+}
+
+int32_t rpg_model_free(rpg_model* m) {
+  delete m;
+  return RPG_OPS_OK;
+}
+
+int32_t rpg_model_meta(const rpg_model* m, rpg_model_meta_t* out) {
+  return Guard([&] {
+    RPG_CHECK(m != nullptr, "null model handle");
+    FillMeta(m->model.config(), out);
+  });
+}
+
+int32_t rpg_model_tensor(const rpg_model* m, const char* name, rpg_tensor_info_t* out) {
+  return Guard([&] {
+    RPG_CHECK(m != nullptr && name != nullptr && out != nullptr, "null argument");
+    const rpg::GpuTensor* t = m->model.FindTensor(name);
+    RPG_CHECK(t != nullptr && t->valid(), "the model has no tensor %s", name);
+    std::memset(out, 0, sizeof(*out));
+    out->data = t->buf.data();
+    out->type = t->type;
+    out->n_dims = t->matrix ? 2 : 1;
+    out->dims[0] = t->matrix ? t->cols : t->n_elements;
+    out->dims[1] = t->matrix ? t->rows : 1;
+    out->n_elements = t->n_elements;
+    out->n_bytes = t->bytes();
+    const rpg::GgufTensor* src = m->model.gguf().Find(
+        std::string(name) == "output.weight" && m->model.config().tied_embeddings ? "token_embd.weight" : name);
+    out->file_offset = src != nullptr ? m->model.gguf().TensorFileOffset(*src) : -1;
+  });
+}
+
+int32_t rpg_model_rope(const rpg_model* m, const float** tab, int64_t* n_pos) {
+  return Guard([&] {
+    RPG_CHECK(m != nullptr && tab != nullptr && n_pos != nullptr, "null argument");
+    *tab = m->model.rope_dev();
+    *n_pos = m->model.rope_positions();
+  });
+}
+
+int32_t rpg_model_describe(const rpg_model* m, char* buf, int32_t cap) {
+  int32_t len = 0;
+  const int32_t rc = Guard([&] {
+    RPG_CHECK(m != nullptr, "null model handle");
+    len = CopyText(m->model.Describe(), buf, cap);
+  });
+  return rc < 0 ? rc : len;
+}
+
+int32_t rpg_model_upload_stats(const rpg_model* m, int64_t* bytes, double* parse_seconds, double* upload_seconds) {
+  return Guard([&] {
+    RPG_CHECK(m != nullptr, "null model handle");
+    const rpg::UploadStats& s = m->model.upload_stats();
+    if (bytes) *bytes = s.bytes;
+    if (parse_seconds) *parse_seconds = s.parse_seconds;
+    if (upload_seconds) *upload_seconds = s.upload_seconds;
+  });
 }
 
 int32_t rpg_op_argmax(const float* x, int64_t n, int32_t* out_idx) {

@@ -80,9 +80,10 @@ std::string DescribeDevice(const DeviceInfo& d) {
 
 // ---------------------------------------------------------------- DeviceBuffer
 
-DeviceBuffer::DeviceBuffer(DeviceBuffer&& o) noexcept : ptr_(o.ptr_), bytes_(o.bytes_) {
+DeviceBuffer::DeviceBuffer(DeviceBuffer&& o) noexcept : ptr_(o.ptr_), bytes_(o.bytes_), owned_(o.owned_) {
   o.ptr_ = nullptr;
   o.bytes_ = 0;
+  o.owned_ = true;
 }
 
 DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& o) noexcept {
@@ -90,10 +91,20 @@ DeviceBuffer& DeviceBuffer::operator=(DeviceBuffer&& o) noexcept {
     Free();
     ptr_ = o.ptr_;
     bytes_ = o.bytes_;
+    owned_ = o.owned_;
     o.ptr_ = nullptr;
     o.bytes_ = 0;
+    o.owned_ = true;
   }
   return *this;
+}
+
+DeviceBuffer DeviceBuffer::View(void* p, size_t bytes) {
+  DeviceBuffer b;
+  b.ptr_ = p;
+  b.bytes_ = bytes;
+  b.owned_ = false;
+  return b;
 }
 
 void DeviceBuffer::Alloc(size_t bytes) {
@@ -101,16 +112,20 @@ void DeviceBuffer::Alloc(size_t bytes) {
   Free();
   RPG_HIP_CHECK(hipMalloc(&ptr_, bytes));
   bytes_ = bytes;
+  owned_ = true;
 }
 
 void DeviceBuffer::Free() {
   if (ptr_ == nullptr) return;
-  // Destructors must not throw; a failing free only happens once the runtime
-  // is already tearing down.
-  const hipError_t e = hipFree(ptr_);
-  if (e != hipSuccess) RPG_LOG_WARN("hipFree failed: %s", hipGetErrorString(e));
+  if (owned_) {
+    // Destructors must not throw; a failing free only happens once the runtime
+    // is already tearing down.
+    const hipError_t e = hipFree(ptr_);
+    if (e != hipSuccess) RPG_LOG_WARN("hipFree failed: %s", hipGetErrorString(e));
+  }
   ptr_ = nullptr;
   bytes_ = 0;
+  owned_ = true;
 }
 
 void DeviceBuffer::Upload(const void* src, size_t bytes) {

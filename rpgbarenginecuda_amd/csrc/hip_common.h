@@ -91,9 +91,14 @@ class DeviceBuffer {
   size_t size() const { return bytes_; }
   bool empty() const { return ptr_ == nullptr; }
 
+  // Non-owning view of `bytes` device bytes at `p` (a slice of an allocation
+  // someone else owns, e.g. the model's weight arena): Free() forgets it.
+  static DeviceBuffer View(void* p, size_t bytes);
+
  private:
   void* ptr_ = nullptr;
   size_t bytes_ = 0;
+  bool owned_ = true;
 };
 
 // ---------------------------------------------------------------- engine stream

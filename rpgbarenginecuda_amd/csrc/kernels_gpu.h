@@ -45,19 +45,38 @@ namespace rpg {
 
 // ---------------------------------------------------------------- shapes
 
-// The subset of the reference's model metadata (src/model_meta.h:27-65) that
-// the hot path reads.
+// Shapes and hyper-parameters of a model, with the reference's field names and
+// types (src/model_meta.h:27-65); filled from a GGUF by ReadModelMeta
+// (gpu_model.h) or by hand for single-operator use.
 struct ModelMeta {
+  std::string arch;  // "qwen3"
+  std::string name;
+
   int32_t n_layers = 0;
-  int64_t hidden = 0;
+  int32_t hidden = 0;
   int32_t n_heads = 0;
   int32_t n_kv_heads = 0;
-  int32_t head_dim = 0;
-  int64_t intermediate = 0;
-  int64_t vocab = 0;
-  int64_t context_length = 0;
+  int32_t head_dim = 0;   // qwen3.attention.key_length
+  int32_t value_dim = 0;  // qwen3.attention.value_length (== head_dim)
+  int32_t intermediate = 0;
+  int32_t vocab = 0;  // rows of token_embd
+  int32_t context_length = 0;
+
+  float rope_theta = 10000.0f;
   float rms_eps = 1e-6f;
-  double rope_theta = 1e6;
+
+  bool tied_embeddings = false;  // no output.weight / lm_head.weight: lm_head is token_embd
+
+  int32_t bos_id = -1;
+  int32_t eos_id = -1;
+  int32_t pad_id = -1;
+  bool add_bos = false;
+
+  int64_t weight_bytes = 0;  // sum of every tensor's bytes in the file
+
+  int32_t q_dim() const { return n_heads * head_dim; }
+  int32_t kv_dim() const { return n_kv_heads * head_dim; }
+  int32_t heads_per_kv() const { return n_kv_heads > 0 ? n_heads / n_kv_heads : 0; }
 };
 
 // A weight tensor resident in device memory as its raw GGUF bytes

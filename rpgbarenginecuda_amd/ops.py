@@ -37,6 +37,20 @@ SIGNATURES = {
     "rpg_ops_get_stream": (_vp, []),
     "rpg_ops_stage_pos0": (_i32, [_i64]),
     "rpg_ops_pos_staging_ptr": (_vp, []),
+    "rpg_gguf_open": (_i32, [ctypes.c_char_p, _vp]),
+    "rpg_gguf_close": (_i32, [_vp]),
+    "rpg_gguf_tensor_count": (_i64, [_vp]),
+    "rpg_gguf_tensor_info": (_i32, [_vp, _i64, ctypes.c_char_p, _i32, _vp]),
+    "rpg_gguf_meta": (_i32, [_vp, ctypes.c_char_p, _i64, _vp, _vp, ctypes.c_char_p, _i32, _vp]),
+    "rpg_gguf_model_meta": (_i32, [_vp, _vp]),
+    "rpg_gguf_describe": (_i32, [_vp, ctypes.c_char_p, _i32]),
+    "rpg_model_load": (_i32, [ctypes.c_char_p, _i32, _vp]),
+    "rpg_model_free": (_i32, [_vp]),
+    "rpg_model_meta": (_i32, [_vp, _vp]),
+    "rpg_model_tensor": (_i32, [_vp, ctypes.c_char_p, _vp]),
+    "rpg_model_rope": (_i32, [_vp, _vp, _vp]),
+    "rpg_model_describe": (_i32, [_vp, ctypes.c_char_p, _i32]),
+    "rpg_model_upload_stats": (_i32, [_vp, _vp, _vp, _vp]),
     "rpg_op_argmax": (_i32, [_vp, _i64, _vp]),
     "rpg_sample_split_mix64": (ctypes.c_uint64, [ctypes.c_uint64]),
     "rpg_sample_counter_rng": (ctypes.c_uint64, [ctypes.c_uint64, ctypes.c_uint64]),
@@ -299,6 +313,152 @@ def GpuAttentionFromCache(n_heads: int, n_kv_heads: int, head_dim: int, pos0: in
 
 def GpuAttentionWarmupShmem(sh_positions: int) -> None:
     _check(load_library().rpg_op_attention_warmup(sh_positions))
+
+
+# ----------------------------------------------------------------------------- GGUF and the device model
+
+
+class ModelMetaC(ctypes.Structure):
+    """rpg_model_meta_t (ModelMeta, reference src/model_meta.h:27-65)."""
+    _fields_ = [("arch", ctypes.c_char * 32), ("name", ctypes.c_char * 128), ("n_layers", _i32), ("hidden", _i32),
+                ("n_heads", _i32), ("n_kv_heads", _i32), ("head_dim", _i32), ("value_dim", _i32),
+                ("intermediate", _i32), ("vocab", _i32), ("context_length", _i32), ("rope_theta", _f32),
+                ("rms_eps", _f32), ("tied_embeddings", _i32), ("bos_id", _i32), ("eos_id", _i32), ("pad_id", _i32),
+                ("add_bos", _i32), ("weight_bytes", _i64)]
+
+    def as_dict(self) -> dict:
+        d = {k: getattr(self, k) for k, _ in self._fields_}
+        d["arch"] = self.arch.decode()
+        d["name"] = self.name.decode()
+        d["tied_embeddings"] = bool(self.tied_embeddings)
+        d["add_bos"] = bool(self.add_bos)
+        return d
+
+
+class TensorInfoC(ctypes.Structure):
+    """rpg_tensor_info_t."""
+    _fields_ = [("data", _vp), ("type", _u32), ("n_dims", _i32), ("dims", _i64 * 4), ("n_elements", _i64),
+                ("n_bytes", _i64), ("file_offset", _i64)]
+
+    def as_dict(self) -> dict:
+        return {"data": self.data or 0, "type": int(self.type), "dims": [int(self.dims[i]) for i in range(self.n_dims)],
+                "n_elements": int(self.n_elements), "n_bytes": int(self.n_bytes), "file_offset": int(self.file_offset)}
+
+
+class GgufFile:
+    """A parsed GGUF file (reference GgufFile, src/gguf.h:43-97); host only."""
+
+    def __init__(self, path: str):
+        h = ctypes.c_void_p()
+        _check(load_library().rpg_gguf_open(os.fsencode(path), ctypes.byref(h)))
+        self._h = h
+
+    def close(self) -> None:
+        if self._h:
+            load_library().rpg_gguf_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+        return False
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensors(self) -> list:
+        lib = load_library()
+        n = lib.rpg_gguf_tensor_count(self._h)
+        if n < 0:
+            _check(-1)
+        out = []
+        name = ctypes.create_string_buffer(512)
+        info = TensorInfoC()
+        for i in range(n):
+            _check(lib.rpg_gguf_tensor_info(self._h, i, name, 512, ctypes.byref(info)))
+            d = info.as_dict()
+            d["name"] = name.value.decode()
+            out.append(d)
+        return out
+
+    def meta(self, key: str, item: int = -1):
+        """None (absent), float, bool, str, or ("array", n_items)."""
+        lib = load_library()
+        kind, num, n_items = ctypes.c_int32(), ctypes.c_double(), ctypes.c_int64()
+        buf = ctypes.create_string_buffer(256)
+        n = _check(lib.rpg_gguf_meta(self._h, key.encode(), item, ctypes.byref(kind), ctypes.byref(num), buf, 256,
+                                     ctypes.byref(n_items)))
+        if kind.value == 3 and n >= 256:
+            buf = ctypes.create_string_buffer(n + 1)
+            _check(lib.rpg_gguf_meta(self._h, key.encode(), item, ctypes.byref(kind), ctypes.byref(num), buf, n + 1,
+                                     ctypes.byref(n_items)))
+        return {0: lambda: None, 1: lambda: num.value, 2: lambda: bool(num.value),
+                3: lambda: buf.raw[:n].decode("utf-8", "replace"), 4: lambda: ("array", n_items.value)}[kind.value]()
+
+    def model_meta(self) -> dict:
+        m = ModelMetaC()
+        _check(load_library().rpg_gguf_model_meta(self._h, ctypes.byref(m)))
+        return m.as_dict()
+
+    def describe(self) -> str:
+        buf = ctypes.create_string_buffer(1024)
+        _check(load_library().rpg_gguf_describe(self._h, buf, 1024))
+        return buf.value.decode()
+
+
+class GpuModel:
+    """A qwen3 GGUF on the device (reference GpuModel::Load, src/gpu_model.cu:148-246)."""
+
+    def __init__(self, path: str, max_pos: int = 4096):
+        h = ctypes.c_void_p()
+        _check(load_library().rpg_model_load(os.fsencode(path), max_pos, ctypes.byref(h)))
+        self._h = h
+
+    def free(self) -> None:
+        if self._h:
+            load_library().rpg_model_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+    def meta(self) -> dict:
+        m = ModelMetaC()
+        _check(load_library().rpg_model_meta(self._h, ctypes.byref(m)))
+        return m.as_dict()
+
+    def tensor(self, name: str) -> dict:
+        info = TensorInfoC()
+        _check(load_library().rpg_model_tensor(self._h, name.encode(), ctypes.byref(info)))
+        return info.as_dict()
+
+    def gpu_tensor(self, name: str) -> "GpuTensor":
+        """A GpuTensor view (for GpuMatMulQuant / GpuEmbeddingLookup) of a loaded matrix."""
+        t = self.tensor(name)
+        return GpuTensor(t["data"], t["type"], t["dims"][1], t["dims"][0])
+
+    def rope(self):
+        tab, n = ctypes.c_void_p(), ctypes.c_int64()
+        _check(load_library().rpg_model_rope(self._h, ctypes.byref(tab), ctypes.byref(n)))
+        return tab.value, n.value
+
+    def describe(self) -> str:
+        buf = ctypes.create_string_buffer(2048)
+        _check(load_library().rpg_model_describe(self._h, buf, 2048))
+        return buf.value.decode()
+
+    def upload_stats(self) -> dict:
+        b, p, u = ctypes.c_int64(), ctypes.c_double(), ctypes.c_double()
+        _check(load_library().rpg_model_upload_stats(self._h, ctypes.byref(b), ctypes.byref(p), ctypes.byref(u)))
+        return {"bytes": b.value, "parse_seconds": p.value, "upload_seconds": u.value}
 
 
 # ----------------------------------------------------------------------------- argmax and sampling
