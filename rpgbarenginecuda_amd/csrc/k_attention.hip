@@ -40,6 +40,7 @@ constexpr int kBlockThreads = 256;
 constexpr int kWaves = kBlockThreads / 64;
 constexpr int kMaxChunks = 64;
 constexpr int kPartFloats = kD + 2;  // o[128], m, l
+constexpr int64_t kFaMinTokens = 64;  // prefill calls with at least this many tokens run on the matrix cores
 
 __device__ __forceinline__ int64_t ReadPos0(int64_t value, const int64_t* dev) { return dev != nullptr ? *dev : value; }
 
@@ -225,6 +226,224 @@ __global__ __launch_bounds__(kBlockThreads) void AttnMergeKernel(const float* __
   MergeChunks(part + th * n_chunks * kPartFloats, n_chunks, lane, out + th * kD);
 }
 
+// ---------------------------------------------------------------- prefill on the matrix cores
+//
+// Flash attention with v_mfma_f32_32x32x16_f16. One workgroup = one query head
+// and 128 consecutive tokens, 4 waves of 32 tokens; keys in blocks of 64 staged
+// in LDS (K as [key][dim], V transposed to [dim][key]) and shared by the waves.
+// Per wave and block:
+//   S^T (64 keys x 32 queries) = K . Q^T    2 key tiles x 8 dim steps x 3 terms
+//   O^T (128 dims x 32 queries) += V^T . P^T  4 dim tiles x 4 key steps x 2 terms
+// Computing the transposes puts one query in each lane column: lane l owns query
+// l % 32 (its running max, sum and rescale are lane values; lanes l and l + 32
+// hold the two halves of the keys), and the S^T accumulator registers 0-7 / 8-15
+// are already the B operand of the P.V step for the keys they hold, provided
+// V^T is read in the same key order.
+// Exact operands: K and V are fp16 cache values. q (fp32) is scaled per row by
+// 2^e (max |q| into [64, 128)) and split into three fp16 terms h + m + l that
+// reproduce it to ~2^-33 relative; the probabilities p in [0, 1] are split into
+// two fp16 terms (to ~2^-22, plus an absolute 2^-25 below fp16's normal range).
+// The matrix core forms exact products and accumulates in fp32; the score is
+// rescaled by scale * 2^-e. Non-finite q gives NaN rows.
+typedef _Float16 F16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 F16x4 __attribute__((ext_vector_type(4)));
+typedef float F32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kFaTokens = 128;    // tokens (of one head) per workgroup
+constexpr int kFaKeys = 64;       // keys per LDS block
+constexpr int kFaKStride = 136;   // halves per K row in LDS (128 + 8: conflict-free 16-byte reads)
+constexpr int kFaVtStride = 68;   // halves per V^T row in LDS (64 + 4)
+
+__device__ __forceinline__ F16x8 SplitTerm(float (&x)[8]) {
+  // x <- x - fp16(x), returning fp16(x) (round to nearest even; the difference is exact in fp32)
+  F16x8 h;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    h[j] = static_cast<_Float16>(x[j]);
+    x[j] -= static_cast<float>(h[j]);
+  }
+  return h;
+}
+
+__global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
+    const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t max_seq,
+    int32_t n_heads, int32_t group, float scale, int64_t pos0_val, const int64_t* __restrict__ pos0_dev, int64_t seq,
+    float* __restrict__ out) {
+  __shared__ __attribute__((aligned(16))) _Float16 ks[kFaKeys * kFaKStride];
+  __shared__ __attribute__((aligned(16))) _Float16 vts[kD * kFaVtStride];
+  const int lane = threadIdx.x & 63;
+  const int wv = threadIdx.x >> 6;
+  const int hf = lane >> 5;    // which half of the keys / dims this lane holds
+  const int col = lane & 31;   // the lane's query within the wave
+  const int h = blockIdx.y;
+  const int kh = h / group;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kFaTokens;
+  const int64_t pos0 = ReadPos0(pos0_val, pos0_dev);
+  const int64_t tq = t0 + 32 * wv + col;
+  const bool qvalid = tq < seq;
+  const int64_t qpos = pos0 + tq;
+
+  // ---- q row: this lane holds dims 16 s + 8 hf + j (s = 0..7), the partner lane the rest
+  float qv[8][8];
+  const float* qrow = q + (tq * n_heads + h) * kD;
+  float amax = 0.0f;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
+    if (qvalid) {
+      a = *reinterpret_cast<const float4*>(qrow + 16 * s + 8 * hf);
+      b = *reinterpret_cast<const float4*>(qrow + 16 * s + 8 * hf + 4);
+    }
+    qv[s][0] = a.x; qv[s][1] = a.y; qv[s][2] = a.z; qv[s][3] = a.w;
+    qv[s][4] = b.x; qv[s][5] = b.y; qv[s][6] = b.z; qv[s][7] = b.w;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(qv[s][j]));
+  }
+  amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+  int e = 0;
+  if (amax > 0.0f && amax <= 3.0e38f) e = 6 - ilogbf(amax);  // max |q| * 2^e in [64, 128)
+  F16x8 qb[3][8];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qv[s][j] = ldexpf(qv[s][j], e);
+    qb[0][s] = SplitTerm(qv[s]);
+    qb[1][s] = SplitTerm(qv[s]);
+    qb[2][s] = SplitTerm(qv[s]);
+  }
+  const float sfac = scale * ldexpf(1.0f, -e);
+
+  F32x16 o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) o[dt] = F32x16{};
+  float m = -INFINITY, l = 0.0f;
+
+  const int64_t t_last = (t0 + kFaTokens < seq ? t0 + kFaTokens : seq) - 1;
+  const int64_t last_key = pos0 + t_last;                                   // the workgroup's causal limit
+  const int64_t wave_last = pos0 + (t0 + 32 * wv + 31 < seq ? t0 + 32 * wv + 31 : seq - 1);
+  const uint16_t* kbase = kc + static_cast<int64_t>(kh) * max_seq * kD;
+  const uint16_t* vbase = vc + static_cast<int64_t>(kh) * max_seq * kD;
+
+  for (int64_t kb = 0; kb <= last_key; kb += kFaKeys) {
+    __syncthreads();  // the previous block is consumed
+    {
+      // thread t: key t / 4, dims 32 (t % 4) .. + 31 of K and V
+      const int key = threadIdx.x >> 2;
+      const int part = threadIdx.x & 3;
+      const int64_t j = kb + key;
+      uint4 kw[4], vw[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        kw[i] = make_uint4(0, 0, 0, 0);
+        vw[i] = kw[i];
+      }
+      if (j <= last_key) {  // keys past the causal limit stay zero: p = 0 must meet finite v
+        const uint4* kr = reinterpret_cast<const uint4*>(kbase + j * kD + 32 * part);
+        const uint4* vr = reinterpret_cast<const uint4*>(vbase + j * kD + 32 * part);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          kw[i] = kr[i];
+          vw[i] = vr[i];
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&ks[key * kFaKStride + 32 * part + 8 * i]) = kw[i];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t w4[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const int d = 32 * part + 8 * i + 2 * k;
+          vts[d * kFaVtStride + key] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(w4[k] & 0xFFFFu));
+          vts[(d + 1) * kFaVtStride + key] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(w4[k] >> 16));
+        }
+      }
+    }
+    __syncthreads();
+    if (kb > wave_last) continue;  // every query of this wave is before the block (uniform per wave)
+
+    // ---- S^T = K . Q^T (the smallest term first)
+    F32x16 st[2] = {F32x16{}, F32x16{}};
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        const F16x8 a = *reinterpret_cast<const F16x8*>(&ks[(32 * mt + col) * kFaKStride + 16 * s + 8 * hf]);
+        st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[2][s], st[mt], 0, 0, 0);
+        st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[1][s], st[mt], 0, 0, 0);
+        st[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qb[0][s], st[mt], 0, 0, 0);
+      }
+    }
+
+    // ---- online softmax: register r of tile mt is key kb + 32 mt + (r % 4) + 8 (r / 4) + 4 hf
+    float bmax = -INFINITY;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t key = kb + 32 * mt + (r & 3) + 8 * (r >> 2) + 4 * hf;
+        const float sc = (qvalid && key <= qpos) ? st[mt][r] * sfac : -INFINITY;
+        st[mt][r] = sc;
+        bmax = fmaxf(bmax, sc);
+      }
+    }
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+    const float mn = fmaxf(m, bmax);
+    const float corr = mn == -INFINITY ? 1.0f : expf(m - mn);  // exp(-inf) = 0 on the first live block
+    float psum = 0.0f;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = st[mt][r] == -INFINITY ? 0.0f : expf(st[mt][r] - mn);
+        st[mt][r] = p;
+        psum += p;
+      }
+    }
+    psum += __shfl_xor(psum, 32, 64);
+    l = l * corr + psum;
+    m = mn;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) o[dt] *= corr;
+
+    // ---- O^T += V^T . P^T: key step ks takes registers 8 (ks % 2) .. + 7 of tile ks / 2
+#pragma unroll
+    for (int ks2 = 0; ks2 < 4; ++ks2) {
+      const int mt = ks2 >> 1;
+      const int rb = 8 * (ks2 & 1);
+      float pr[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pr[j] = st[mt][rb + j];
+      const F16x8 ph = SplitTerm(pr);
+      const F16x8 pl = SplitTerm(pr);
+      const int koff = 32 * mt + 16 * (ks2 & 1) + 4 * hf;  // keys koff + 0..3 and koff + 8..11
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const _Float16* vrow = &vts[(32 * dt + col) * kFaVtStride];
+        const F16x4 lo = *reinterpret_cast<const F16x4*>(vrow + koff);
+        const F16x4 hi = *reinterpret_cast<const F16x4*>(vrow + koff + 8);
+        const F16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pl, o[dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, ph, o[dt], 0, 0, 0);
+      }
+    }
+  }
+
+  // ---- out[tq][h][dim]: register r of tile dt is dim 32 dt + (r % 4) + 8 (r / 4) + 4 hf
+  if (!qvalid) return;
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  float* orow = out + (tq * n_heads + h) * kD;
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const float4 v = make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
+                                   o[dt][4 * g + 3] * inv);
+      *reinterpret_cast<float4*>(orow + 32 * dt + 8 * g + 4 * hf) = v;
+    }
+  }
+}
+
 // ---------------------------------------------------------------- partials buffer
 
 // Grow-only device buffer for the chunk partials. Deliberately never freed at
@@ -309,9 +528,16 @@ void GpuAttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev,
   int32_t n_chunks;
   int64_t chunk_len;
   PlanChunks(pairs, positions, &n_chunks, &chunk_len);
+  const Pos0Arg p0 = Pos0ForLaunch(pos0);
+  if (seq >= kFaMinTokens) {
+    Launch("AttnPrefillMfmaKernel", AttnPrefillMfmaKernel,
+           dim3(static_cast<unsigned>((seq + kFaTokens - 1) / kFaTokens), static_cast<unsigned>(c.n_heads)),
+           dim3(kBlockThreads), q_dev, k_layer, v_layer, max_seq, c.n_heads, c.n_heads / c.n_kv_heads, scale,
+           p0.value, p0.dev, seq, out_dev);
+    return;
+  }
   float* part = nullptr;
   if (n_chunks > 1) part = EnsurePartials(static_cast<size_t>(pairs) * n_chunks * kPartFloats);
-  const Pos0Arg p0 = Pos0ForLaunch(pos0);
   const int64_t units = pairs * n_chunks;
   Launch("AttnChunkKernel", AttnChunkKernel, dim3(GridFor(units, kWaves)), dim3(kBlockThreads), q_dev, k_layer,
          v_layer, max_seq, c.n_heads, c.n_heads / c.n_kv_heads, scale, p0.value, p0.dev, seq, n_chunks, chunk_len,

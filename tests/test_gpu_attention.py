@@ -65,6 +65,11 @@ CASES = [
     ("1.7B small batch continuation", 16, 8, 4096, 300, 3),
     ("1.7B prefill n=512 after 100", 16, 8, 1024, 100, 512),
     ("MHA, odd sizes", 4, 4, 200, 37, 70),
+    # matrix-core prefill (>= 64 tokens): tile edges, GQA groups, a long cached prefix
+    ("prefill n=64 (threshold)", 4, 2, 256, 0, 64),
+    ("prefill n=129 (tile edge)", 8, 2, 512, 5, 129),
+    ("1.7B prefill n=1024", 16, 8, 1024, 0, 1024),
+    ("4B prefill n=300 after 1000", 32, 8, 4096, 1000, 300),
 ]
 
 
@@ -79,6 +84,28 @@ def test_attention_from_cache(gpu, ora, name, nh, nkv, max_seq, pos0, seq):
     gpu.GpuAttentionFromCache(nh, nkv, 128, pos0, dev(q), seq, dev(kc), dev(vc), max_seq, out)
     ref, smag, vmax = ora.attention_f64(q, kc, vc, max_seq, nh, nkv, 128, pos0, seq)
     check(host(out), ref, smag, vmax, pos0)
+
+
+def test_attention_prefill_ignores_rows_past_the_limit(gpu, ora):
+    """Matrix-core prefill: cache rows past pos0 + seq - 1 (inf / NaN garbage) do
+    not change a bit of the result."""
+    import torch
+
+    case("attention prefill causal limit")
+    nh, nkv, max_seq, pos0, seq = 16, 8, 1024, 40, 200
+    rng = np.random.default_rng(1450)
+    q, kc, vc = make(rng, nh, nkv, max_seq, seq)
+    out1 = torch.empty((seq, nh, 128), dtype=torch.float32, device="cuda")
+    gpu.GpuAttentionFromCache(nh, nkv, 128, pos0, dev(q), seq, dev(kc), dev(vc), max_seq, out1)
+    kc2, vc2 = kc.copy().reshape(nkv, max_seq, 128), vc.copy().reshape(nkv, max_seq, 128)
+    kc2[:, pos0 + seq:] = np.float16(np.inf).view(np.uint16)
+    vc2[:, pos0 + seq:] = np.float16(np.nan).view(np.uint16)
+    out2 = torch.empty_like(out1)
+    gpu.GpuAttentionFromCache(nh, nkv, 128, pos0, dev(q), seq, dev(kc2.reshape(-1)), dev(vc2.reshape(-1)), max_seq,
+                              out2)
+    assert torch.equal(out1, out2)
+    ref, smag, vmax = ora.attention_f64(q, kc, vc, max_seq, nh, nkv, 128, pos0, seq)
+    check(host(out1), ref, smag, vmax, pos0)
 
 
 def test_attention_causal_limit_and_budget(gpu, ora):
