@@ -151,7 +151,7 @@ class StagedUploader {
     }
     cap_ = static_cast<size_t>(std::min<int64_t>(static_cast<int64_t>(kStagingBytes), std::max<int64_t>(total, 1)));
     const unsigned hw = std::max(1u, std::thread::hardware_concurrency());
-    threads_ = static_cast<int>(std::min(16u, hw));
+    threads_ = static_cast<int>(std::min(8u, hw));
   }
   ~StagedUploader() {
     if (stream_ != nullptr) (void)hipStreamSynchronize(stream_);  // the buffers are reused by the next load
