@@ -367,9 +367,57 @@ def measure_matmul_decode(torch, ops, reps=20, span=768 << 20):
         del blob, blocks, mats, x, out
         torch.cuda.empty_cache()
     token_us = LAYERS * layer_us + res[OUTPUT_MATRIX[0]]["us"]
+    grouped = measure_matmul_decode_grouped(torch, ops, reps, span)
     return {"matrices": res, "layer_us": round(layer_us, 2), "token_matmul_us": round(token_us, 1),
+            "grouped": grouped,
+            "token_matmul_us_grouped": round(LAYERS * grouped["layer_us"] + res[OUTPUT_MATRIX[0]]["us"], 1),
             "note": "n = 1, Qwen3-1.7B Q4_K_M layout; token_matmul_us = 28 layers + output projection, "
-                    "matmuls only"}
+                    "matmuls only; _grouped = with q/k and gate/up fused per layer (GpuMatMulQuantGroup)"}
+
+
+def measure_matmul_decode_grouped(torch, ops, reps, span):
+    """One 1.7B layer's decode matmuls as GpuMatMulQuantGroup launches: [q, k] (Q4_K),
+    [v] (Q6_K), [o], [gate, up], [down]; copies rotated past the Infinity Cache."""
+    mats = {name: (t, rows, cols) for name, t, rows, cols in DECODE_MATRICES}
+    groups = [["attn_q", "attn_k"], ["attn_v"], ["attn_output"], ["ffn_gate", "ffn_up"], ["ffn_down"]]
+    res, layer_us = {}, 0.0
+    for grp in groups:
+        specs = [mats[n] for n in grp]
+        sizes = [rows * (cols // 256) * (144 if t == 12 else 210) for t, rows, cols in specs]
+        copies = max(2, min(256, span // sum(sizes) + 1))
+        gen = torch.Generator(device="cuda")
+        gen.manual_seed(60 + sum(sizes))
+        sets = []
+        for _ in range(copies):
+            ts = []
+            for (t, rows, cols), nbytes in zip(specs, sizes):
+                blob = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda", generator=gen)
+                blocks = blob.view(-1, 144 if t == 12 else 210)
+                if t == 12:
+                    blocks[:, 1] &= 0x3B
+                    blocks[:, 3] &= 0x3B
+                else:
+                    blocks[:, 209] &= 0x3B
+                ts.append(ops.GpuTensor(blob, t, rows, cols))
+            sets.append(ts)
+        cols = specs[0][2]
+        x = torch.randn((1, cols), device="cuda", generator=gen)
+        outs = [torch.empty((1, rows), device="cuda") for _, rows, _ in specs]
+        for i in range(min(copies, 4)):
+            ops.GpuMatMulQuantGroup(sets[i], x, 1, outs)
+        torch.cuda.synchronize()
+        ops.profile_start(reps * len(grp))
+        for r in range(reps):
+            ops.GpuMatMulQuantGroup(sets[r % copies], x, 1, outs)
+        ops.profile_stop()
+        rep = ops.profile_report()
+        us = sum(k["total_us"] for k in rep.values()) / reps
+        res["+".join(grp)] = {"us": round(us, 2), "launches": int(sum(k["count"] for k in rep.values()) // reps),
+                              "GBps": round((sum(sizes) + 4 * cols + 4 * sum(r for _, r, _ in specs)) / us / 1e3, 1)}
+        layer_us += us
+        del sets, x, outs
+        torch.cuda.empty_cache()
+    return {"groups": res, "layer_us": round(layer_us, 2)}
 
 
 def measure_matmul_prefill(torch, ops, n=N_PREFILL, reps=3):

@@ -390,6 +390,28 @@ int32_t rpg_op_matmul_quant(uint32_t type, const uint8_t* w, int64_t rows, int64
   return Guard([&] { rpg::GpuMatMulQuantRaw(type, w, rows, cols, x, n_tokens, out); });
 }
 
+int32_t rpg_op_matmul_quant_group(int32_t n, const uint32_t* types, const uint8_t* const* ws, const int64_t* rows,
+                                  int64_t cols, const float* x, int64_t n_tokens, float* const* outs) {
+  return Guard([&] {
+    RPG_CHECK(n > 0 && n <= 64 && types && ws && rows && outs, "matmul group: bad arguments (n = %d)", n);
+    std::vector<rpg::GpuTensor> t(static_cast<size_t>(n));
+    std::vector<const rpg::GpuTensor*> p(static_cast<size_t>(n));
+    for (int32_t i = 0; i < n; ++i) {
+      RPG_CHECK(ws[i] != nullptr && rows[i] > 0 && cols > 0, "matmul group: matrix %d is empty", i);
+      rpg::GpuTensor& g = t[static_cast<size_t>(i)];
+      g.type = types[i];
+      g.matrix = true;
+      g.rows = rows[i];
+      g.cols = cols;
+      g.n_elements = rows[i] * cols;
+      g.buf = rpg::DeviceBuffer::View(const_cast<uint8_t*>(ws[i]),
+                                      static_cast<size_t>(rows[i] * rpg::TypeRowBytes(types[i], cols)));
+      p[static_cast<size_t>(i)] = &g;
+    }
+    rpg::GpuMatMulQuantGroup(p.data(), n, x, n_tokens, outs);
+  });
+}
+
 int32_t rpg_op_add_rms_norm(float* x, const float* d, const float* w, int64_t n_rows, int64_t n, float eps,
                             float* out) {
   return Guard([&] { rpg::GpuAddRmsNorm(x, d, w, n_rows, n, eps, out); });

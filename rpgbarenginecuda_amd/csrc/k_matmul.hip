@@ -28,6 +28,8 @@
 // matrices take a per-element generic kernel.
 #include <hip/hip_runtime.h>
 
+#include <climits>
+
 #include "dev_util.h"
 #include "kernels_gpu.h"
 #include "launch.h"
@@ -437,16 +439,32 @@ __device__ __forceinline__ void RunSums(const float (&xv)[32], float (&sx)[2]) {
   sx[1] = z;
 }
 
+// Up to kMaxSegs matrices of one type and width decoded as one row space: rows
+// [end[i-1], end[i]) are matrix i (w[i], out[i]); unused ends are INT64_MAX. A
+// single matrix is one segment.
+constexpr int kMaxSegs = 4;
+struct MatSegs {
+  const uint8_t* w[kMaxSegs];
+  float* out[kMaxSegs];
+  int64_t end[kMaxSegs];
+};
+
+// Segment of global row r (uniform over the wave, so scalar).
+__device__ __forceinline__ int SegOf(const MatSegs& sg, int64_t r) {
+  return (r >= sg.end[0]) + (r >= sg.end[1]) + (r >= sg.end[2]);
+}
+
 // Each lane keeps the activations of its NX block groups in registers (rows of
-// up to 8 * NX blocks; used for NX == 1).
+// up to 8 * NX blocks; used for NX == 1). Rows run over all segments; a row
+// group of RI rows never straddles two (segment sizes are multiples of RI).
 template <uint32_t kType, int NX, int RI>
-__global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(const uint8_t* __restrict__ w, int64_t rows,
-                                                              int64_t row_bytes, int32_t nb,
-                                                              const float* __restrict__ x, float* __restrict__ out) {
+__global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int32_t n_seg, int64_t row_bytes, int32_t nb,
+                                                              const float* __restrict__ x) {
   constexpr int64_t kBB = BlockBytesOf<kType>::value;
   const int lane = threadIdx.x & 63;
   const int c = lane / kGroupLanes;
   const int s = lane % kGroupLanes;
+  const int64_t rows = sg.end[n_seg - 1];
 
   // Row bookkeeping is uniform over the wave: keep it in scalar registers.
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kWavesPerBlock * RI;
@@ -472,10 +490,13 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(const uint8_t* __r
 
   // Rows past the end are clamped to the last row (loads stay in bounds; results are dropped).
   auto load = [&](int64_t base_row, LaneBytes (&lb)[RI][NX]) {
+    const int sgi = SegOf(sg, base_row);
+    const uint8_t* wseg = sg.w[sgi];
+    const int64_t first = sgi == 0 ? 0 : sg.end[sgi - 1];
 #pragma unroll
     for (int r = 0; r < RI; ++r) {
       const int64_t row = base_row + r < rows ? base_row + r : rows - 1;
-      const uint8_t* rp = w + row * row_bytes;
+      const uint8_t* rp = wseg + (row - first) * row_bytes;
 #pragma unroll
       for (int it = 0; it < NX; ++it) lb[r][it] = LoadLaneBytes<kType>(rp + lane_off[it], s);
     }
@@ -498,7 +519,9 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(const uint8_t* __r
     }
     const float total = ReduceRows<RI>(acc, lane);
     const int rr = ReducedRow<RI>(lane);
-    if ((lane & 15) == 0 && lane < 16 * RI && r0 + rr < rows) out[r0 + rr] = total;
+    const int sgi = SegOf(sg, r0);
+    const int64_t first = sgi == 0 ? 0 : sg.end[sgi - 1];
+    if ((lane & 15) == 0 && lane < 16 * RI && r0 + rr < rows) sg.out[sgi][r0 - first + rr] = total;
 #pragma unroll
     for (int r = 0; r < RI; ++r)
 #pragma unroll
@@ -626,11 +649,27 @@ void LaunchQuant(const char* name, const uint8_t* w, int64_t rows, int64_t row_b
 constexpr int64_t kDecodeGrid = 1024;
 
 template <uint32_t kType, int RI>
-void LaunchDecode(const char* name, const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb, const float* x,
-                  float* out) {
+void LaunchDecodeSegs(const char* name, const MatSegs& sg, int32_t n_seg, int64_t row_bytes, int32_t nb,
+                      const float* x) {
+  const int64_t rows = sg.end[n_seg - 1];
   const int64_t need = (rows + kWavesPerBlock * RI - 1) / (kWavesPerBlock * RI);
   const unsigned grid = static_cast<unsigned>(need < kDecodeGrid ? need : kDecodeGrid);
-  Launch(name, MatVecQuantKernel<kType, 1, RI>, dim3(grid), dim3(kMmBlock), w, rows, row_bytes, nb, x, out);
+  Launch(name, MatVecQuantKernel<kType, 1, RI>, dim3(grid), dim3(kMmBlock), sg, n_seg, row_bytes, nb, x);
+}
+
+MatSegs OneSeg(const uint8_t* w, int64_t rows, float* out) {
+  MatSegs sg{};
+  for (int i = 0; i < kMaxSegs; ++i) sg.end[i] = INT64_MAX;
+  sg.w[0] = w;
+  sg.out[0] = out;
+  sg.end[0] = rows;
+  return sg;
+}
+
+template <uint32_t kType, int RI>
+void LaunchDecode(const char* name, const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb, const float* x,
+                  float* out) {
+  LaunchDecodeSegs<kType, RI>(name, OneSeg(w, rows, out), 1, row_bytes, nb, x);
 }
 
 // Split decode: at most max_grid workgroups (rows are visited with a stride);
@@ -709,6 +748,61 @@ void GpuMatMulQuantRaw(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_
   const int64_t units = rows * n_tokens;
   Launch("MatMulGenericKernel", MatMulGenericKernel, dim3(GridFor(units, kWavesPerBlock)), dim3(kMmBlock), type,
          w_dev, rows, row_bytes, bs.elems, bs.bytes, x_dev, cols, n_tokens, out_dev);
+}
+
+void GpuMatMulQuantGroup(const GpuTensor* const* ws, int32_t n_mats, const float* x_dev, int64_t n_tokens,
+                         float* const* outs) {
+  RPG_CHECK(ws != nullptr && outs != nullptr && n_mats > 0, "GpuMatMulQuantGroup needs at least one matrix");
+  for (int32_t i = 0; i < n_mats; ++i) {
+    RPG_CHECK(ws[i] != nullptr && outs[i] != nullptr, "GpuMatMulQuantGroup got a null matrix or output");
+    RPG_CHECK(ws[i]->matrix && ws[i]->valid(), "GpuMatMulQuantGroup got a non-matrix or empty tensor");
+    RPG_CHECK(ws[i]->cols == ws[0]->cols, "GpuMatMulQuantGroup matrices must share their width (%lld vs %lld)",
+              static_cast<long long>(ws[i]->cols), static_cast<long long>(ws[0]->cols));
+    RPG_CHECK(ws[i]->buf.size() == static_cast<size_t>(ws[i]->rows * ws[i]->row_bytes()),
+              "tensor byte count does not match the [%lld, %lld] shape", static_cast<long long>(ws[i]->rows),
+              static_cast<long long>(ws[i]->cols));
+  }
+  // Decode rows fused per run of consecutive same-type matrices (the kernel of a
+  // single matrix, so every output is bit-identical to its GpuMatMulQuant);
+  // anything else goes matrix by matrix.
+  const int64_t cols = ws[0]->cols;
+  const int64_t nb = cols / kQK_K;
+  const bool decode = n_tokens == 1 && Aligned(x_dev, 16) && cols % kQK_K == 0 && nb <= kGroups;
+  int32_t i = 0;
+  while (i < n_mats) {
+    const uint32_t type = ws[i]->type;
+    int32_t j = i + 1;
+    while (j < n_mats && j - i < kMaxSegs && ws[j]->type == type) ++j;
+    const bool q4 = type == kGgmlQ4_K, q6 = type == kGgmlQ6_K;
+    int64_t total = 0;
+    bool fuse = decode && j - i > 1 && (q4 || q6);
+    for (int32_t k = i; k < j && fuse; ++k) {
+      fuse = ws[k]->rows % 2 == 0 && Aligned(ws[k]->buf.data(), q4 ? 16 : 2);
+      total += ws[k]->rows;
+    }
+    fuse = fuse && !(q4 && total >= 32768);  // the 4-rows-per-wave shape stays per matrix
+    if (!fuse) {
+      for (int32_t k = i; k < j; ++k) GpuMatMulQuant(*ws[k], x_dev, n_tokens, outs[k]);
+      i = j;
+      continue;
+    }
+    MatSegs sg{};
+    for (int s = 0; s < kMaxSegs; ++s) sg.end[s] = INT64_MAX;
+    int64_t end = 0;
+    for (int32_t k = i; k < j; ++k) {
+      sg.w[k - i] = static_cast<const uint8_t*>(ws[k]->buf.data());
+      sg.out[k - i] = outs[k];
+      end += ws[k]->rows;
+      sg.end[k - i] = end;
+    }
+    const int64_t row_bytes = TypeRowBytes(type, cols);
+    if (q4) {
+      LaunchDecodeSegs<kGgmlQ4_K, 2>("MatVecQ4KKernel", sg, j - i, row_bytes, static_cast<int32_t>(nb), x_dev);
+    } else {
+      LaunchDecodeSegs<kGgmlQ6_K, 2>("MatVecQ6KKernel", sg, j - i, row_bytes, static_cast<int32_t>(nb), x_dev);
+    }
+    i = j;
+  }
 }
 
 void GpuMatMulQuant(const GpuTensor& w, const float* X_dev, int64_t n_tokens, float* OUT_dev) {

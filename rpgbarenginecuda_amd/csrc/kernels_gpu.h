@@ -206,6 +206,14 @@ void GpuAttentionWarmupShmem(int64_t sh_positions);
 // Weights are dequantised bit-exactly and accumulated in fp32 (fused multiply-add).
 void GpuMatMulQuant(const GpuTensor& w, const float* X_dev, int64_t n_tokens, float* OUT_dev);
 
+// GpuMatMulQuant over several matrices that read the same X (a layer's q / k / v,
+// or gate / up): OUT_i = X . W_i^T. At n_tokens = 1, each run of consecutive
+// same-type matrices (up to 4) is decoded in one launch, with every output
+// bit-identical to its own GpuMatMulQuant call; otherwise one call per matrix.
+// No counterpart in the reference (which launches once per matrix).
+void GpuMatMulQuantGroup(const GpuTensor* const* ws, int32_t n_mats, const float* X_dev, int64_t n_tokens,
+                         float* const* OUTs);
+
 // The same on a raw (non-owning) weight pointer; GpuMatMulQuant forwards here.
 void GpuMatMulQuantRaw(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_t cols, const float* x_dev,
                        int64_t n_tokens, float* out_dev);

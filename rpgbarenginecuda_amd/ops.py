@@ -51,6 +51,7 @@ SIGNATURES = {
     "rpg_model_rope": (_i32, [_vp, _vp, _vp]),
     "rpg_model_describe": (_i32, [_vp, ctypes.c_char_p, _i32]),
     "rpg_model_upload_stats": (_i32, [_vp, _vp, _vp, _vp]),
+    "rpg_op_matmul_quant_group": (_i32, [_i32, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
     "rpg_op_argmax": (_i32, [_vp, _i64, _vp]),
     "rpg_sample_split_mix64": (ctypes.c_uint64, [ctypes.c_uint64]),
     "rpg_sample_counter_rng": (ctypes.c_uint64, [ctypes.c_uint64, ctypes.c_uint64]),
@@ -296,6 +297,24 @@ def GpuMatMulQuant(w: GpuTensor, x, n_tokens: int, out) -> None:
         w.type, _addr(w.buf, w.rows * w.row_bytes(), name="w"), w.rows, w.cols,
         _addr(x, 4 * n_tokens * w.cols, torch.float32, "x"), n_tokens,
         _addr(out, 4 * n_tokens * w.rows, torch.float32, "out")))
+
+
+def GpuMatMulQuantGroup(ws: list, x, n_tokens: int, outs: list) -> None:
+    """OUT_i = X . W_i^T for matrices sharing X, same-type runs fused at n = 1 (no reference counterpart)."""
+    torch = _t()
+    n = len(ws)
+    if n == 0 or n != len(outs):
+        raise RpgError("GpuMatMulQuantGroup needs one output per matrix and at least one matrix")
+    cols = ws[0].cols
+    if any(w.cols != cols for w in ws):
+        raise RpgError(f"GpuMatMulQuantGroup matrices must share their width ({[w.cols for w in ws]})")
+    types = (ctypes.c_uint32 * n)(*[w.type for w in ws])
+    ptrs = (ctypes.c_void_p * n)(*[_addr(w.buf, w.rows * w.row_bytes(), name="w") for w in ws])
+    rows = (ctypes.c_int64 * n)(*[w.rows for w in ws])
+    optrs = (ctypes.c_void_p * n)(*[_addr(o, 4 * n_tokens * w.rows, torch.float32, "out") for o, w in zip(outs, ws)])
+    _check(load_library().rpg_op_matmul_quant_group(n, types, ptrs, rows, cols,
+                                                    _addr(x, 4 * n_tokens * cols, torch.float32, "x"), n_tokens,
+                                                    optrs))
 
 
 def GpuAttentionFromCache(n_heads: int, n_kv_heads: int, head_dim: int, pos0: int, q, seq: int, k_layer, v_layer,

@@ -198,3 +198,53 @@ def test_matmul_quant_rejects_bad_shapes(gpu):
     assert "multiple of the block size" in last_error(gpu)
     assert L.rpg_op_matmul_quant(12, w.data_ptr(), 2, 512, x.data_ptr(), 0, out.data_ptr()) != 0
     assert L.rpg_op_matmul_quant(99, w.data_ptr(), 2, 512, x.data_ptr(), 1, out.data_ptr()) != 0
+
+
+GROUPS = [
+    # (label, [(type, rows)], cols, n_tokens)
+    ("q/k/v of a 1.7B layer", [(12, 2048), (12, 1024), (14, 1024)], 2048, 1),
+    ("gate/up", [(12, 6144), (12, 6144)], 2048, 1),
+    ("four Q6_K", [(14, 256), (14, 512), (14, 130), (14, 1000)], 1024, 1),
+    ("mixed runs", [(14, 300), (12, 200), (12, 128), (14, 64), (14, 64)], 512, 1),
+    ("odd rows (not fused)", [(12, 1001), (12, 7)], 256, 1),
+    ("Q4_K of 32768+ rows (own shape)", [(12, 20000), (12, 16000)], 256, 1),
+    ("prefill (one call per matrix)", [(12, 256), (14, 128)], 512, 40),
+    ("small batch", [(12, 256), (12, 256)], 512, 3),
+]
+
+
+@pytest.mark.parametrize("label,mats,cols,n", GROUPS, ids=[g[0] for g in GROUPS])
+def test_matmul_group_equals_separate_calls(gpu, ora, label, mats, cols, n):
+    """GpuMatMulQuantGroup: every output bit-identical to its own GpuMatMulQuant,
+    and within the matmul bound of the float64 oracle."""
+    import torch
+
+    case(f"matmul group {label}")
+    rng = np.random.default_rng(900 + cols + n + len(mats))
+    ws, outs, want = [], [], []
+    x = rng.normal(0, 1, (n, cols)).astype(np.float32)
+    xd = dev(x)
+    for t, rows in mats:
+        w = synth.quant_table(rng, t, rows, cols)
+        g = gpu.GpuTensor(dev(w), t, rows, cols)
+        ws.append((g, w))
+        outs.append(torch.full((n, rows), np.nan, dtype=torch.float32, device="cuda"))
+        ref = torch.full((n, rows), np.nan, dtype=torch.float32, device="cuda")
+        gpu.GpuMatMulQuant(g, xd, n, ref)
+        want.append(ref)
+    gpu.GpuMatMulQuantGroup([g for g, _ in ws], xd, n, outs)
+    for (g, w), o, r, (t, rows) in zip(ws, outs, want, mats):
+        assert torch.equal(o, r), (label, t, rows)
+        exact, absdot = ora.matmul_quant_f64(t, w, rows, cols, x)
+        check(host(o), exact, absdot, cols, factored_magnitude(ora, t, w, rows, cols, x))
+
+
+def test_matmul_group_rejects_mixed_widths(gpu):
+    import torch
+
+    case("matmul group host errors")
+    a = gpu.GpuTensor(torch.zeros(256 * 144 // 256 * 4, dtype=torch.uint8, device="cuda"), 12, 4, 256)
+    b = gpu.GpuTensor(torch.zeros(512 * 144 // 256 * 4, dtype=torch.uint8, device="cuda"), 12, 4, 512)
+    x = torch.zeros(512, device="cuda")
+    with pytest.raises(gpu.RpgError, match="width"):
+        gpu.GpuMatMulQuantGroup([a, b], x, 1, [torch.zeros(4, device="cuda"), torch.zeros(4, device="cuda")])
