@@ -13,6 +13,9 @@
 //     LDS), then the wave keeps a running max m, a running sum l of
 //     exp(s - m) and a running output o (lane l owns dims 2l, 2l + 1), rescaled
 //     when the max grows;
+//   * decode and short prefills with a GQA group of 1, 2 or 4 use one wave per
+//     (token, kv head, chunk) for the whole group (AttnDecodeGroupKernel), other
+//     shapes one wave per query head (AttnChunkKernel);
 //   * prefill (many (t, h) pairs) uses a single chunk per pair and writes the
 //     normalised output directly; decode (few pairs) splits the keys into up to
 //     kMaxChunks chunks so the whole chip streams the cache, each chunk storing
@@ -224,6 +227,167 @@ __global__ __launch_bounds__(kBlockThreads) void AttnMergeKernel(const float* __
   const int64_t th = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
   if (th >= pairs) return;
   MergeChunks(part + th * n_chunks * kPartFloats, n_chunks, lane, out + th * kD);
+}
+
+// ---------------------------------------------------------------- decode, one wave per kv head
+//
+// One wave per (token, kv head, key chunk) serves all G query heads of the GQA
+// group, so each K/V row is read once. Keys go 32 at a time: lane l covers dims
+// 8 (l % 16) .. + 7 of key base + 4 i + l / 16 (i = 0..7), so one load
+// instruction reads four whole 256-byte rows. The 8 partial dot products a lane
+// holds per head are reduced over its 16-lane row by a transposing butterfly
+// (xor 8, 4, 2, then 1): afterwards lanes 2i and 2i + 1 of row r both hold the
+// score of key base + 4 i + r. The online softmax then runs over the wave (each
+// key counted once), and V rows are accumulated with the probability of key
+// base + 4 i + r taken from lane 16 r + 2 i; the four rows' partial outputs are
+// summed at the end.
+template <int G>
+__global__ __launch_bounds__(kBlockThreads) void AttnDecodeGroupKernel(
+    const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t max_seq,
+    int32_t n_heads, int32_t n_kv_heads, float scale, int64_t pos0_val, const int64_t* __restrict__ pos0_dev,
+    int64_t seq, int32_t n_chunks, int64_t chunk_len, float* __restrict__ out, float* __restrict__ part) {
+  const int lane = threadIdx.x & 63;
+  const int64_t unit = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
+  if (unit >= seq * n_kv_heads * n_chunks) return;  // no barriers below
+  const int64_t tk = unit / n_chunks;
+  const int32_t c = static_cast<int32_t>(unit - tk * n_chunks);
+  const int64_t t = tk / n_kv_heads;
+  const int32_t kh = static_cast<int32_t>(tk - t * n_kv_heads);
+  const int64_t pos = ReadPos0(pos0_val, pos0_dev) + t;
+  const int64_t lo = static_cast<int64_t>(c) * chunk_len;
+  int64_t hi = lo + chunk_len;
+  if (hi > pos + 1) hi = pos + 1;
+  if (hi > max_seq) hi = max_seq;  // only reachable through a replayed graph with a bad staged pos0
+  const int rho = lane & 15;
+  const int r = lane >> 4;
+
+  float qv[G][8];
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) {
+    const float* qr = q + (t * n_heads + kh * G + hh) * kD + 8 * rho;
+    const float4 a = *reinterpret_cast<const float4*>(qr);
+    const float4 b = *reinterpret_cast<const float4*>(qr + 4);
+    qv[hh][0] = a.x; qv[hh][1] = a.y; qv[hh][2] = a.z; qv[hh][3] = a.w;
+    qv[hh][4] = b.x; qv[hh][5] = b.y; qv[hh][6] = b.z; qv[hh][7] = b.w;
+  }
+  float m[G], l[G], o[G][8];
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) {
+    m[hh] = -INFINITY;
+    l[hh] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[hh][j] = 0.0f;
+  }
+  const uint16_t* kb = kc + static_cast<int64_t>(kh) * max_seq * kD + 8 * rho;
+  const uint16_t* vb = vc + static_cast<int64_t>(kh) * max_seq * kD + 8 * rho;
+
+  for (int64_t base = lo; base < hi; base += 32) {
+    uint4 kw[8], vw[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int64_t key = base + 4 * i + r;
+      key = key < hi ? key : hi - 1;  // clamped rows get probability 0
+      kw[i] = *reinterpret_cast<const uint4*>(kb + key * kD);
+      vw[i] = *reinterpret_cast<const uint4*>(vb + key * kD);
+    }
+    const int64_t skey = base + 4 * (rho >> 1) + r;  // the key whose score this lane ends with
+    const bool valid = skey < hi;
+    float p[G];
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) {
+      float sp[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t wd[4] = {kw[i].x, kw[i].y, kw[i].z, kw[i].w};
+        float a0 = qv[hh][0] * HalfToF(wd[0] & 0xFFFFu);
+        float a1 = qv[hh][1] * HalfToF(wd[0] >> 16);
+        a0 = __builtin_fmaf(qv[hh][2], HalfToF(wd[1] & 0xFFFFu), a0);
+        a1 = __builtin_fmaf(qv[hh][3], HalfToF(wd[1] >> 16), a1);
+        a0 = __builtin_fmaf(qv[hh][4], HalfToF(wd[2] & 0xFFFFu), a0);
+        a1 = __builtin_fmaf(qv[hh][5], HalfToF(wd[2] >> 16), a1);
+        a0 = __builtin_fmaf(qv[hh][6], HalfToF(wd[3] & 0xFFFFu), a0);
+        a1 = __builtin_fmaf(qv[hh][7], HalfToF(wd[3] >> 16), a1);
+        sp[i] = a0 + a1;
+      }
+      // transposing butterfly over the 16-lane row
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const bool up = rho & 8;
+        const float mine = up ? sp[j + 4] : sp[j];
+        const float other = up ? sp[j] : sp[j + 4];
+        sp[j] = mine + __shfl_xor(other, 8, 16);
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const bool up = rho & 4;
+        const float mine = up ? sp[j + 2] : sp[j];
+        const float other = up ? sp[j] : sp[j + 2];
+        sp[j] = mine + __shfl_xor(other, 4, 16);
+      }
+      {
+        const bool up = rho & 2;
+        const float mine = up ? sp[1] : sp[0];
+        const float other = up ? sp[0] : sp[1];
+        sp[0] = mine + __shfl_xor(other, 2, 16);
+      }
+      sp[0] += __shfl_xor(sp[0], 1, 16);
+      const float sc = valid ? sp[0] * scale : -INFINITY;
+      const float bm = WaveMax(sc);
+      const float mn = fmaxf(m[hh], bm);
+      const float corr = mn == -INFINITY ? 1.0f : expf(m[hh] - mn);
+      p[hh] = valid ? expf(sc - mn) : 0.0f;
+      l[hh] = l[hh] * corr + WaveSumF((rho & 1) ? 0.0f : p[hh]);  // each key once
+      m[hh] = mn;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[hh][j] *= corr;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t wd[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
+      float vf[8];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        vf[2 * k] = HalfToF(wd[k] & 0xFFFFu);
+        vf[2 * k + 1] = HalfToF(wd[k] >> 16);
+      }
+#pragma unroll
+      for (int hh = 0; hh < G; ++hh) {
+        const float pi = __shfl(p[hh], 16 * r + 2 * i, 64);  // probability of key base + 4 i + r
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[hh][j] = __builtin_fmaf(pi, vf[j], o[hh][j]);
+      }
+    }
+  }
+
+  // the four rows' partial outputs
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      o[hh][j] += __shfl_xor(o[hh][j], 16, 64);
+      o[hh][j] += __shfl_xor(o[hh][j], 32, 64);
+    }
+  }
+  if (r != 0) return;
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) {
+    const int64_t th = t * n_heads + kh * G + hh;
+    float* dst;
+    float f = 1.0f;
+    if (part == nullptr) {
+      dst = out + th * kD;
+      f = l[hh] > 0.0f ? 1.0f / l[hh] : 0.0f;
+    } else {
+      float* pp = part + (th * n_chunks + c) * kPartFloats;
+      dst = pp;
+      if (rho == 0) {
+        pp[kD] = m[hh];
+        pp[kD + 1] = l[hh];
+      }
+    }
+    *reinterpret_cast<float4*>(dst + 8 * rho) = make_float4(o[hh][0] * f, o[hh][1] * f, o[hh][2] * f, o[hh][3] * f);
+    *reinterpret_cast<float4*>(dst + 8 * rho + 4) = make_float4(o[hh][4] * f, o[hh][5] * f, o[hh][6] * f, o[hh][7] * f);
+  }
 }
 
 // ---------------------------------------------------------------- prefill on the matrix cores
@@ -497,13 +661,44 @@ void PlanChunks(int64_t pairs, int64_t positions, int32_t* n_chunks, int64_t* ch
   *n_chunks = static_cast<int32_t>((positions + len - 1) / len);
 }
 
-// Partials needed for decode-sized calls with up to `positions` keys (seq 1,
-// up to 64 heads), the worst case a decode graph replays.
-size_t WarmupFloats(int64_t positions) {
+// The same for the grouped decode kernel: `units` (token, kv head) pairs, chunks
+// of a multiple of 32 keys, enough for ~2048 waves.
+void PlanGroupChunks(int64_t units, int64_t positions, int32_t* n_chunks, int64_t* chunk_len) {
+  if (units >= 2048 || positions <= 32) {
+    *n_chunks = 1;
+    *chunk_len = positions;
+    return;
+  }
+  int64_t want = (2048 + units - 1) / units;
+  if (want > kMaxChunks) want = kMaxChunks;
+  int64_t len = (positions + want - 1) / want;
+  len = (len + 31) / 32 * 32;
+  *chunk_len = len;
+  *n_chunks = static_cast<int32_t>((positions + len - 1) / len);
+}
+
+// Partials needed by any decode-sized call (seq 1, up to 64 heads, at most
+// kMaxChunks chunks): what a captured decode graph may replay.
+size_t WarmupFloats(int64_t /*positions*/) { return static_cast<size_t>(64) * kMaxChunks * kPartFloats; }
+
+template <int G>
+void LaunchDecodeGroup(const ModelMeta& c, const Pos0Arg& p0, const float* q_dev, int64_t seq,
+                       const uint16_t* k_layer, const uint16_t* v_layer, int64_t max_seq, float scale,
+                       int64_t positions, float* out_dev) {
   int32_t n_chunks;
-  int64_t len;
-  PlanChunks(64, positions, &n_chunks, &len);
-  return static_cast<size_t>(64) * n_chunks * kPartFloats;
+  int64_t chunk_len;
+  PlanGroupChunks(seq * c.n_kv_heads, positions, &n_chunks, &chunk_len);
+  const int64_t pairs = seq * c.n_heads;
+  float* part = nullptr;
+  if (n_chunks > 1) part = EnsurePartials(static_cast<size_t>(pairs) * n_chunks * kPartFloats);
+  const int64_t units = seq * c.n_kv_heads * n_chunks;
+  Launch("AttnDecodeGroupKernel", AttnDecodeGroupKernel<G>, dim3(GridFor(units, kWaves)), dim3(kBlockThreads), q_dev,
+         k_layer, v_layer, max_seq, c.n_heads, c.n_kv_heads, scale, p0.value, p0.dev, seq, n_chunks, chunk_len,
+         out_dev, part);
+  if (n_chunks > 1) {
+    Launch("AttnMergeKernel", AttnMergeKernel, dim3(GridFor(pairs, kWaves)), dim3(kBlockThreads), part, pairs,
+           n_chunks, out_dev);
+  }
 }
 
 }  // namespace
@@ -536,6 +731,19 @@ void GpuAttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev,
            p0.value, p0.dev, seq, out_dev);
     return;
   }
+  const int group = c.n_heads / c.n_kv_heads;
+  const bool aligned = (reinterpret_cast<uintptr_t>(q_dev) & 15u) == 0 &&
+                       (reinterpret_cast<uintptr_t>(v_layer) & 15u) == 0;
+  if (aligned && group == 1) {
+    return LaunchDecodeGroup<1>(c, p0, q_dev, seq, k_layer, v_layer, max_seq, scale, positions, out_dev);
+  }
+  if (aligned && group == 2) {
+    return LaunchDecodeGroup<2>(c, p0, q_dev, seq, k_layer, v_layer, max_seq, scale, positions, out_dev);
+  }
+  if (aligned && group == 4) {
+    return LaunchDecodeGroup<4>(c, p0, q_dev, seq, k_layer, v_layer, max_seq, scale, positions, out_dev);
+  }
+  // other group sizes / alignments: one wave per query head
   float* part = nullptr;
   if (n_chunks > 1) part = EnsurePartials(static_cast<size_t>(pairs) * n_chunks * kPartFloats);
   const int64_t units = pairs * n_chunks;

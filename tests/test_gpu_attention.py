@@ -65,6 +65,10 @@ CASES = [
     ("1.7B small batch continuation", 16, 8, 4096, 300, 3),
     ("1.7B prefill n=512 after 100", 16, 8, 1024, 100, 512),
     ("MHA, odd sizes", 4, 4, 200, 37, 70),
+    # group sizes the grouped decode kernel does not take (one wave per query head)
+    ("GQA group 8 decode", 64, 8, 1024, 700, 1),
+    ("GQA group 3, two tokens", 12, 4, 512, 300, 2),
+    ("MHA decode (group 1)", 8, 8, 2048, 1999, 1),
     # matrix-core prefill (>= 64 tokens): tile edges, GQA groups, a long cached prefix
     ("prefill n=64 (threshold)", 4, 2, 256, 0, 64),
     ("prefill n=129 (tile edge)", 8, 2, 512, 5, 129),
