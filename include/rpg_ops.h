@@ -211,6 +211,73 @@ RPG_OPS_API int32_t rpg_model_describe(const rpg_model* m, char* buf, int32_t ca
 RPG_OPS_API int32_t rpg_model_upload_stats(const rpg_model* m, int64_t* bytes, double* parse_seconds,
                                            double* upload_seconds);
 
+/* ---------------------------------------------------------------- forward and generation
+ * The Qwen3 layer chain over the operators above, for a loaded rpg_model.
+ * rpg_kv: the fp16 KV cache [n_layers][n_kv_heads][max_seq][head_dim], allocated
+ * in full at creation (Replaces: GpuKvCache, src/kv_cache_gpu.h:50-100).
+ * rpg_scratch: the grow-only device activations of a forward plus the captured
+ * decode graph (Replaces: GpuScratch, src/qwen3_gpu.h:47-113). A model, its caches
+ * and scratches are used from one host thread at a time. */
+typedef struct rpg_kv rpg_kv;
+typedef struct rpg_scratch rpg_scratch;
+
+RPG_OPS_API int32_t rpg_kv_create(const rpg_model* m, int64_t max_seq, rpg_kv** out);
+RPG_OPS_API int32_t rpg_kv_free(rpg_kv* kv);
+/* Current length (positions filled), capacity and K + V bytes. */
+RPG_OPS_API int32_t rpg_kv_info(const rpg_kv* kv, int64_t* len, int64_t* max_seq, int64_t* bytes);
+/* Sets the length (0 <= len <= max_seq); 0 is GpuKvCache::Reset, src/kv_cache_gpu.h:75. */
+RPG_OPS_API int32_t rpg_kv_set_len(rpg_kv* kv, int64_t len);
+/* Device bases of one layer's K and V (fp16 bits). */
+RPG_OPS_API int32_t rpg_kv_layer(rpg_kv* kv, int32_t layer, uint16_t** k, uint16_t** v);
+
+RPG_OPS_API int32_t rpg_scratch_create(rpg_scratch** out);
+RPG_OPS_API int32_t rpg_scratch_free(rpg_scratch* s);
+/* Device address of the scratch's logits [seq, vocab] (valid after a forward),
+ * and of its sampled-token slot (int32). */
+RPG_OPS_API int32_t rpg_scratch_logits(rpg_scratch* s, const float** logits_dev, const int32_t** token_dev);
+
+/* Forward of `seq` host token ids. kv == NULL: the no-cache path (attention over
+ * the segment's fp32 k / v); otherwise the segment is appended at the cache's
+ * length and attends to the whole cache, whose length then grows by seq.
+ * layer_limit > 0 runs only that many layers (no logits then). logits (host,
+ * [seq, vocab]) and hidden (host, [n_use + 1, seq, hidden]: the residual stream
+ * after the embedding and after each layer) are optional (NULL).
+ * Replaces: GpuForwardFull, src/qwen3_gpu.h:136-139. */
+RPG_OPS_API int32_t rpg_forward_full(const rpg_model* m, const int32_t* tokens, int64_t seq, rpg_scratch* s,
+                                     float* logits, int32_t layer_limit, float* hidden, rpg_kv* kv);
+/* One token at pos == the cache length; logits (host [vocab]) optional.
+ * Replaces: GpuForwardStep, src/qwen3_gpu.h:145-146. */
+RPG_OPS_API int32_t rpg_forward_step(const rpg_model* m, int32_t token, int64_t pos, rpg_kv* kv, rpg_scratch* s,
+                                     float* logits);
+/* The same with the token id on the device; logits stay in the scratch.
+ * Replaces: GpuForwardStepDev, src/qwen3_gpu.h:151-152. */
+RPG_OPS_API int32_t rpg_forward_step_dev(const rpg_model* m, const int32_t* token_dev, int64_t pos, rpg_kv* kv,
+                                         rpg_scratch* s);
+
+/* Generation options (GpuGenerateOptions, src/qwen3_gpu.h:156-181). temperature
+ * <= 0 is greedy; step_logits (host, step_logits_cap floats, or NULL) receives
+ * the distribution each token was drawn from; use_graph replays the decode step
+ * as a HIP graph (ignored when step_logits is set). */
+typedef struct {
+  int32_t max_tokens;
+  const int32_t* stop_ids;
+  int32_t n_stop;
+  float temperature;
+  int32_t top_k;
+  float top_p;
+  uint64_t seed;
+  int32_t use_graph;
+  float* step_logits;
+  int64_t step_logits_cap;
+} rpg_generate_opts_t;
+
+/* Generates from the distribution at first_logits_dev ([vocab], device; e.g.
+ * the last row of rpg_scratch_logits after a prefill), writing up to out_cap
+ * ids and *n_out. Every returned token (the stop token included) is in the cache
+ * afterwards. Replaces: GpuGenerate, src/qwen3_gpu.h:197-199. */
+RPG_OPS_API int32_t rpg_generate(const rpg_model* m, rpg_kv* kv, rpg_scratch* s, const float* first_logits_dev,
+                                 const rpg_generate_opts_t* opts, int32_t* out_ids, int32_t out_cap, int32_t* n_out);
+
 /* ---------------------------------------------------------------- argmax and sampling
  * n (the vocabulary) is at most 2^22 for all of these. Semantics: greedy
  * (temperature <= 0) is argmax, ties to the smallest index; otherwise logits *

@@ -27,7 +27,7 @@ LIB_PATH = os.path.join(PKG_DIR, "librpg_ops.so")
 ARCHIVE_PATH = os.path.join(PKG_DIR, "librpg_ops_objs.a")
 
 HIP_SOURCES = ["k_norm.hip", "k_rope_kv.hip", "k_elementwise.hip", "k_dequant.hip", "k_matmul.hip", "k_matmul_mfma.hip", "k_attention.hip", "k_sample.hip"]
-HOST_SOURCES = ["common.cc", "hip_common.cc", "quant_types.cc", "kv_cache.cc", "gguf.cc", "gpu_model.cc", "capi.cc"]
+HOST_SOURCES = ["common.cc", "hip_common.cc", "quant_types.cc", "kv_cache.cc", "gguf.cc", "gpu_model.cc", "qwen3_gpu.cc", "capi.cc"]
 
 COMMON_FLAGS = [
     "-O3",

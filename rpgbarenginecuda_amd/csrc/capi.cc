@@ -13,6 +13,7 @@
 #include "hip_common.h"
 #include "kernels_gpu.h"
 #include "gpu_model.h"
+#include "qwen3_gpu.h"
 #include "sampler_gpu.h"
 
 namespace {
@@ -85,6 +86,14 @@ struct rpg_gguf {
 
 struct rpg_model {
   rpg::GpuModel model;
+};
+
+struct rpg_kv {
+  rpg::GpuKvCache kv;
+};
+
+struct rpg_scratch {
+  rpg::GpuScratch s;
 };
 
 extern "C" {
@@ -346,6 +355,135 @@ int32_t rpg_model_upload_stats(const rpg_model* m, int64_t* bytes, double* parse
     if (bytes) *bytes = s.bytes;
     if (parse_seconds) *parse_seconds = s.parse_seconds;
     if (upload_seconds) *upload_seconds = s.upload_seconds;
+  });
+}
+
+int32_t rpg_kv_create(const rpg_model* m, int64_t max_seq, rpg_kv** out) {
+  return Guard([&] {
+    RPG_CHECK(m != nullptr && out != nullptr, "null argument");
+    *out = nullptr;
+    *out = new rpg_kv{rpg::GpuKvCache(m->model.config(), max_seq)};
+  });
+}
+
+int32_t rpg_kv_free(rpg_kv* kv) {
+  delete kv;
+  return RPG_OPS_OK;
+}
+
+int32_t rpg_kv_info(const rpg_kv* kv, int64_t* len, int64_t* max_seq, int64_t* bytes) {
+  return Guard([&] {
+    RPG_CHECK(kv != nullptr, "null cache handle");
+    if (len) *len = kv->kv.len();
+    if (max_seq) *max_seq = kv->kv.max_seq();
+    if (bytes) *bytes = kv->kv.bytes();
+  });
+}
+
+int32_t rpg_kv_set_len(rpg_kv* kv, int64_t len) {
+  return Guard([&] {
+    RPG_CHECK(kv != nullptr, "null cache handle");
+    kv->kv.SetLen(len);
+  });
+}
+
+int32_t rpg_kv_layer(rpg_kv* kv, int32_t layer, uint16_t** k, uint16_t** v) {
+  return Guard([&] {
+    RPG_CHECK(kv != nullptr && k != nullptr && v != nullptr, "null argument");
+    *k = kv->kv.k_layer(layer);
+    *v = kv->kv.v_layer(layer);
+  });
+}
+
+int32_t rpg_scratch_create(rpg_scratch** out) {
+  return Guard([&] {
+    RPG_CHECK(out != nullptr, "null argument");
+    *out = new rpg_scratch();
+  });
+}
+
+int32_t rpg_scratch_free(rpg_scratch* s) {
+  delete s;
+  return RPG_OPS_OK;
+}
+
+int32_t rpg_scratch_logits(rpg_scratch* s, const float** logits_dev, const int32_t** token_dev) {
+  return Guard([&] {
+    RPG_CHECK(s != nullptr, "null scratch handle");
+    RPG_CHECK(!s->s.logits.empty(), "the scratch holds no logits yet (run a forward first)");
+    if (logits_dev) *logits_dev = static_cast<const float*>(s->s.logits.data());
+    if (token_dev) *token_dev = static_cast<const int32_t*>(s->s.argmax_idx.data());
+  });
+}
+
+int32_t rpg_forward_full(const rpg_model* m, const int32_t* tokens, int64_t seq, rpg_scratch* s, float* logits,
+                         int32_t layer_limit, float* hidden, rpg_kv* kv) {
+  return Guard([&] {
+    RPG_CHECK(m != nullptr && s != nullptr, "null model or scratch handle");
+    RPG_CHECK(layer_limit >= 0, "layer_limit must not be negative");
+    const rpg::ModelMeta& c = m->model.config();
+    RPG_CHECK(logits == nullptr || layer_limit == 0 || layer_limit >= c.n_layers,
+              "logits were requested from a truncated forward (layer_limit %d of %d layers)", layer_limit,
+              c.n_layers);
+    std::vector<float> hid;
+    std::vector<float> lg;
+    rpg::GpuForwardOptions opt;
+    opt.layer_limit = layer_limit;
+    if (hidden != nullptr) opt.capture_hidden = &hid;
+    rpg::GpuForwardFull(m->model, tokens, seq, &s->s, logits != nullptr ? &lg : nullptr, opt,
+                        kv != nullptr ? &kv->kv : nullptr);
+    if (hidden != nullptr) std::memcpy(hidden, hid.data(), hid.size() * sizeof(float));
+    if (logits != nullptr) std::memcpy(logits, lg.data(), lg.size() * sizeof(float));
+  });
+}
+
+int32_t rpg_forward_step(const rpg_model* m, int32_t token, int64_t pos, rpg_kv* kv, rpg_scratch* s, float* logits) {
+  return Guard([&] {
+    RPG_CHECK(m != nullptr && s != nullptr && kv != nullptr, "null handle");
+    std::vector<float> lg;
+    rpg::GpuForwardStep(m->model, token, pos, &kv->kv, &s->s, logits != nullptr ? &lg : nullptr);
+    if (logits != nullptr) std::memcpy(logits, lg.data(), lg.size() * sizeof(float));
+  });
+}
+
+int32_t rpg_forward_step_dev(const rpg_model* m, const int32_t* token_dev, int64_t pos, rpg_kv* kv, rpg_scratch* s) {
+  return Guard([&] {
+    RPG_CHECK(m != nullptr && s != nullptr && kv != nullptr, "null handle");
+    rpg::GpuForwardStepDev(m->model, token_dev, pos, &kv->kv, &s->s);
+  });
+}
+
+int32_t rpg_generate(const rpg_model* m, rpg_kv* kv, rpg_scratch* s, const float* first_logits_dev,
+                     const rpg_generate_opts_t* opts, int32_t* out_ids, int32_t out_cap, int32_t* n_out) {
+  return Guard([&] {
+    RPG_CHECK(m != nullptr && s != nullptr && kv != nullptr && opts != nullptr, "null handle");
+    RPG_CHECK(out_ids != nullptr && n_out != nullptr, "null output");
+    *n_out = 0;
+    RPG_CHECK(opts->max_tokens > 0 && opts->max_tokens <= out_cap, "max_tokens (%d) must be in [1, out_cap = %d]",
+              opts->max_tokens, out_cap);
+    RPG_CHECK(opts->n_stop >= 0 && (opts->n_stop == 0 || opts->stop_ids != nullptr), "bad stop id list");
+    const int64_t vocab = m->model.config().vocab;
+    rpg::GpuGenerateOptions g;
+    g.max_tokens = opts->max_tokens;
+    g.stop_ids.assign(opts->stop_ids, opts->stop_ids + opts->n_stop);
+    g.sample.temperature = opts->temperature;
+    g.sample.top_k = opts->top_k;
+    g.sample.top_p = opts->top_p;
+    g.seed = opts->seed;
+    g.use_graph = opts->use_graph != 0;
+    std::vector<float> steps;
+    if (opts->step_logits != nullptr) {
+      RPG_CHECK(opts->step_logits_cap >= static_cast<int64_t>(opts->max_tokens) * vocab,
+                "step_logits holds %lld floats, max_tokens x vocab = %lld are needed",
+                static_cast<long long>(opts->step_logits_cap),
+                static_cast<long long>(static_cast<int64_t>(opts->max_tokens) * vocab));
+      g.step_logits = &steps;
+    }
+    std::vector<int32_t> ids;
+    rpg::GpuGenerate(m->model, &kv->kv, &s->s, first_logits_dev, g, &ids);
+    std::memcpy(out_ids, ids.data(), ids.size() * sizeof(int32_t));
+    if (opts->step_logits != nullptr) std::memcpy(opts->step_logits, steps.data(), steps.size() * sizeof(float));
+    *n_out = static_cast<int32_t>(ids.size());
   });
 }
 

@@ -13,6 +13,8 @@
 //     LDS), then the wave keeps a running max m, a running sum l of
 //     exp(s - m) and a running output o (lane l owns dims 2l, 2l + 1), rescaled
 //     when the max grows;
+//   * the no-cache path (GpuCausalAttention, fp32 k / v rows of the segment)
+//     runs the per-query-head kernel on fp32 rows;
 //   * decode and short prefills with a GQA group of 1, 2 or 4 use one wave per
 //     (token, kv head, chunk) for the whole group (AttnDecodeGroupKernel), other
 //     shapes one wave per query head (AttnChunkKernel);
@@ -110,12 +112,42 @@ __device__ __forceinline__ void MergeChunks(const float* pp, int32_t n_chunks, i
   ot[2 * lane + 1] = o1 * inv;
 }
 
+// Key / value rows: the fp16 cache ([kv head][position][d], 16-bit bits) or
+// fp32 rows of the current segment ([token][kv head][d], the no-cache path).
+// Load8 converts elements 8 i .. 8 i + 7 of a row, Load2 elements 2 l, 2 l + 1.
+__device__ __forceinline__ void Load8(const uint16_t* row, int i, float f[8]) {
+  const uint4 w = reinterpret_cast<const uint4*>(row)[i];
+  const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    f[2 * k] = HalfToF(wd[k] & 0xFFFFu);
+    f[2 * k + 1] = HalfToF(wd[k] >> 16);
+  }
+}
+__device__ __forceinline__ void Load8(const float* row, int i, float f[8]) {
+  const float4 a = reinterpret_cast<const float4*>(row)[2 * i];
+  const float4 b = reinterpret_cast<const float4*>(row)[2 * i + 1];
+  f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+  f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+__device__ __forceinline__ float2 Load2(const uint16_t* row, int lane) {
+  const uint32_t w = reinterpret_cast<const uint32_t*>(row)[lane];
+  return make_float2(HalfToF(w & 0xFFFFu), HalfToF(w >> 16));
+}
+__device__ __forceinline__ float2 Load2(const float* row, int lane) {
+  return reinterpret_cast<const float2*>(row)[lane];
+}
+
 // One wave per (t, h, chunk). part == nullptr: a single chunk, the output is
-// written normalised; otherwise (m, l, o) of the chunk go to part.
+// written normalised; otherwise (m, l, o) of the chunk go to part. Row s of kv
+// head kh starts at kh * head_stride + s * pos_stride elements; positions at or
+// past max_seq are never read.
+template <typename KV>
 __global__ __launch_bounds__(kBlockThreads) void AttnChunkKernel(
-    const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t max_seq,
-    int32_t n_heads, int32_t group, float scale, int64_t pos0_val, const int64_t* __restrict__ pos0_dev, int64_t seq,
-    int32_t n_chunks, int64_t chunk_len, float* __restrict__ out, float* __restrict__ part) {
+    const float* __restrict__ q, const KV* __restrict__ kc, const KV* __restrict__ vc, int64_t head_stride,
+    int64_t pos_stride, int64_t max_seq, int32_t n_heads, int32_t group, float scale, int64_t pos0_val,
+    const int64_t* __restrict__ pos0_dev, int64_t seq, int32_t n_chunks, int64_t chunk_len, float* __restrict__ out,
+    float* __restrict__ part) {
   __shared__ float qs[kWaves][kD];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
@@ -144,8 +176,8 @@ __global__ __launch_bounds__(kBlockThreads) void AttnChunkKernel(
   if (hi > pos + 1) hi = pos + 1;
   if (hi > max_seq) hi = max_seq;  // only reachable through a replayed graph with a bad staged pos0
 
-  const uint16_t* kb = kc + static_cast<int64_t>(kh) * max_seq * kD;
-  const uint16_t* vb = vc + static_cast<int64_t>(kh) * max_seq * kD;
+  const KV* kb = kc + static_cast<int64_t>(kh) * head_stride;
+  const KV* vb = vc + static_cast<int64_t>(kh) * head_stride;
   float m = -INFINITY;
   float l = 0.0f;
   float o0 = 0.0f, o1 = 0.0f;
@@ -153,19 +185,19 @@ __global__ __launch_bounds__(kBlockThreads) void AttnChunkKernel(
   for (int64_t base = lo; base < hi; base += 64) {
     const int64_t s = base + lane;
     const bool valid = s < hi;
-    // score of key s: its 256-byte row against q
+    // score of key s: its row against q
     float sc = -INFINITY;
     if (valid) {
-      const uint4* kr = reinterpret_cast<const uint4*>(kb + s * kD);
+      const KV* kr = kb + s * pos_stride;
       float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // four interleaved partial sums: a 32-deep chain
 #pragma unroll
       for (int i = 0; i < kD / 8; ++i) {
-        const uint4 w = kr[i];
-        const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+        float f[8];
+        Load8(kr, i, f);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          acc[k] = __builtin_fmaf(qs[wv][8 * i + 2 * k], HalfToF(wd[k] & 0xFFFFu), acc[k]);
-          acc[k] = __builtin_fmaf(qs[wv][8 * i + 2 * k + 1], HalfToF(wd[k] >> 16), acc[k]);
+          acc[k] = __builtin_fmaf(qs[wv][8 * i + 2 * k], f[2 * k], acc[k]);
+          acc[k] = __builtin_fmaf(qs[wv][8 * i + 2 * k + 1], f[2 * k + 1], acc[k]);
         }
       }
       sc = ((acc[0] + acc[1]) + (acc[2] + acc[3])) * scale;
@@ -179,25 +211,25 @@ __global__ __launch_bounds__(kBlockThreads) void AttnChunkKernel(
     o1 *= corr;
     m = mn;
     // o += sum_j p_j v_j over the block: lane l reads dims 2l, 2l + 1 of each v
-    // row (one 256-byte row per wave load); 16 rows are requested before any is
-    // used so their latencies overlap.
+    // row (one row per wave load); 16 rows are requested before any is used so
+    // their latencies overlap.
     const int64_t nk = hi - base < 64 ? hi - base : 64;
-    const uint32_t* vr = reinterpret_cast<const uint32_t*>(vb + base * kD) + lane;
+    const KV* vr = vb + base * pos_stride;
     for (int j0 = 0; j0 < 64; j0 += 16) {
       if (j0 >= nk) break;
-      uint32_t vv[16];
+      float2 vv[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int j = j0 + i < nk ? j0 + i : static_cast<int>(nk) - 1;  // clamped: stays in the block
-        vv[i] = vr[static_cast<int64_t>(j) * (kD / 2)];
+        vv[i] = Load2(vr + static_cast<int64_t>(j) * pos_stride, lane);
       }
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         // p of a key past the block's end is 0 (invalid lanes), so the clamped
         // duplicate rows add nothing
         const float pj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p), j0 + i));
-        o0 = __builtin_fmaf(pj, HalfToF(vv[i] & 0xFFFFu), o0);
-        o1 = __builtin_fmaf(pj, HalfToF(vv[i] >> 16), o1);
+        o0 = __builtin_fmaf(pj, vv[i].x, o0);
+        o1 = __builtin_fmaf(pj, vv[i].y, o1);
       }
     }
   }
@@ -610,7 +642,9 @@ __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
 
 // ---------------------------------------------------------------- partials buffer
 
-// Grow-only device buffer for the chunk partials. Deliberately never freed at
+// Grow-only device buffer for the chunk partials. A buffer that is outgrown is
+// retired, not freed: a HIP graph captured earlier keeps its address and may
+// still replay (the sizes involved are a few MiB). Deliberately never freed at
 // exit (a destructor running after the HIP runtime has shut down can hang).
 constexpr int64_t kMaxSplitPairs = 1024;
 
@@ -632,14 +666,11 @@ float* EnsurePartials(size_t floats) {
               "attention needs a %zu-float partials buffer (have %zu), which cannot be allocated during graph "
               "capture; call GpuAttentionWarmupShmem(max positions) before capturing",
               floats, b.floats);
-    if (b.ptr != nullptr) {
-      RPG_HIP_CHECK(hipDeviceSynchronize());
-      RPG_HIP_CHECK(hipFree(b.ptr));
-      b.ptr = nullptr;
-      b.floats = 0;
-    }
-    RPG_HIP_CHECK(hipMalloc(&b.ptr, floats * sizeof(float)));
-    b.floats = floats;
+    const size_t grow = floats > 2 * b.floats ? floats : 2 * b.floats;  // geometric: few retired buffers
+    float* p = nullptr;
+    RPG_HIP_CHECK(hipMalloc(&p, grow * sizeof(float)));
+    b.ptr = p;  // the previous buffer stays allocated (see above)
+    b.floats = grow;
   }
   return b.ptr;
 }
@@ -747,9 +778,36 @@ void GpuAttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev,
   float* part = nullptr;
   if (n_chunks > 1) part = EnsurePartials(static_cast<size_t>(pairs) * n_chunks * kPartFloats);
   const int64_t units = pairs * n_chunks;
-  Launch("AttnChunkKernel", AttnChunkKernel, dim3(GridFor(units, kWaves)), dim3(kBlockThreads), q_dev, k_layer,
-         v_layer, max_seq, c.n_heads, c.n_heads / c.n_kv_heads, scale, p0.value, p0.dev, seq, n_chunks, chunk_len,
-         out_dev, part);
+  Launch("AttnChunkKernel", AttnChunkKernel<uint16_t>, dim3(GridFor(units, kWaves)), dim3(kBlockThreads), q_dev,
+         k_layer, v_layer, max_seq * kD, static_cast<int64_t>(kD), max_seq, c.n_heads, c.n_heads / c.n_kv_heads,
+         scale, p0.value, p0.dev, seq, n_chunks, chunk_len, out_dev, part);
+  if (n_chunks > 1) {
+    Launch("AttnMergeKernel", AttnMergeKernel, dim3(GridFor(pairs, kWaves)), dim3(kBlockThreads), part, pairs,
+           n_chunks, out_dev);
+  }
+}
+
+void GpuCausalAttention(const ModelMeta& c, const float* q_dev, const float* k_dev, const float* v_dev, int64_t seq,
+                        float* out_dev) {
+  RPG_CHECK(seq > 0, "attention seq must be positive");
+  RPG_CHECK(c.n_heads > 0 && c.n_kv_heads > 0 && c.n_heads % c.n_kv_heads == 0,
+            "n_heads (%d) must be a positive multiple of n_kv_heads (%d)", c.n_heads, c.n_kv_heads);
+  RPG_CHECK(c.head_dim == kD, "attention supports head_dim %d (got %d)", kD, c.head_dim);
+  RPG_CHECK(q_dev && k_dev && v_dev && out_dev, "attention got a null pointer");
+  RPG_CHECK((reinterpret_cast<uintptr_t>(k_dev) & 15u) == 0 && (reinterpret_cast<uintptr_t>(v_dev) & 7u) == 0,
+            "k / v rows must be 16-byte / 8-byte aligned");
+  const float scale = 1.0f / sqrtf(static_cast<float>(c.head_dim));
+  const int64_t pairs = seq * c.n_heads;
+  int32_t n_chunks;
+  int64_t chunk_len;
+  PlanChunks(pairs, seq, &n_chunks, &chunk_len);
+  float* part = nullptr;
+  if (n_chunks > 1) part = EnsurePartials(static_cast<size_t>(pairs) * n_chunks * kPartFloats);
+  const int64_t units = pairs * n_chunks;
+  const int64_t row = static_cast<int64_t>(c.n_kv_heads) * kD;  // one token's k (or v) row
+  Launch("AttnChunkKernel<f32>", AttnChunkKernel<float>, dim3(GridFor(units, kWaves)), dim3(kBlockThreads), q_dev,
+         k_dev, v_dev, static_cast<int64_t>(kD), row, seq, c.n_heads, c.n_heads / c.n_kv_heads, scale,
+         static_cast<int64_t>(0), static_cast<const int64_t*>(nullptr), seq, n_chunks, chunk_len, out_dev, part);
   if (n_chunks > 1) {
     Launch("AttnMergeKernel", AttnMergeKernel, dim3(GridFor(pairs, kWaves)), dim3(kBlockThreads), part, pairs,
            n_chunks, out_dev);

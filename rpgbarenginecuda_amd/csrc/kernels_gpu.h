@@ -192,6 +192,13 @@ void GpuEmbeddingLookupRaw(uint32_t type, const uint8_t* emb_dev, int64_t rows, 
 void GpuAttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev, int64_t seq, const uint16_t* k_layer,
                            const uint16_t* v_layer, int64_t max_seq, float* out_dev, int64_t sh_positions = -1);
 
+// Causal attention without a cache (src/kernels_gpu.h:82-84): the same maths
+// over the segment's own fp32 rows, k / v [seq][n_kv_heads][head_dim], token t
+// attending to tokens 0..t. The no-cache forward uses it; the difference from
+// GpuAttentionFromCache on the same tokens is the fp16 rounding of k and v only.
+void GpuCausalAttention(const ModelMeta& c, const float* q_dev, const float* k_dev, const float* v_dev, int64_t seq,
+                        float* out_dev);
+
 // Sizes the attention's partials buffer for up to sh_positions cached positions
 // (decode calls), so that a graph capture of the decode step allocates nothing
 // (src/kernels_gpu.h:128; there it raises the shared-memory limit instead).

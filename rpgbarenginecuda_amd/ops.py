@@ -51,6 +51,18 @@ SIGNATURES = {
     "rpg_model_rope": (_i32, [_vp, _vp, _vp]),
     "rpg_model_describe": (_i32, [_vp, ctypes.c_char_p, _i32]),
     "rpg_model_upload_stats": (_i32, [_vp, _vp, _vp, _vp]),
+    "rpg_kv_create": (_i32, [_vp, _i64, _vp]),
+    "rpg_kv_free": (_i32, [_vp]),
+    "rpg_kv_info": (_i32, [_vp, _vp, _vp, _vp]),
+    "rpg_kv_set_len": (_i32, [_vp, _i64]),
+    "rpg_kv_layer": (_i32, [_vp, _i32, _vp, _vp]),
+    "rpg_scratch_create": (_i32, [_vp]),
+    "rpg_scratch_free": (_i32, [_vp]),
+    "rpg_scratch_logits": (_i32, [_vp, _vp, _vp]),
+    "rpg_forward_full": (_i32, [_vp, _vp, _i64, _vp, _vp, _i32, _vp, _vp]),
+    "rpg_forward_step": (_i32, [_vp, _i32, _i64, _vp, _vp, _vp]),
+    "rpg_forward_step_dev": (_i32, [_vp, _vp, _i64, _vp, _vp]),
+    "rpg_generate": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp]),
     "rpg_op_matmul_quant_group": (_i32, [_i32, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
     "rpg_op_argmax": (_i32, [_vp, _i64, _vp]),
     "rpg_sample_split_mix64": (ctypes.c_uint64, [ctypes.c_uint64]),
@@ -478,6 +490,168 @@ class GpuModel:
         b, p, u = ctypes.c_int64(), ctypes.c_double(), ctypes.c_double()
         _check(load_library().rpg_model_upload_stats(self._h, ctypes.byref(b), ctypes.byref(p), ctypes.byref(u)))
         return {"bytes": b.value, "parse_seconds": p.value, "upload_seconds": u.value}
+
+
+# ----------------------------------------------------------------------------- forward and generation
+
+
+class _Handle:
+    _free_fn = ""
+
+    def free(self) -> None:
+        if getattr(self, "_h", None):
+            getattr(load_library(), self._free_fn)(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class GpuKvCache(_Handle):
+    """fp16 KV cache of a model, allocated in full (reference GpuKvCache, src/kv_cache_gpu.h:50-100)."""
+    _free_fn = "rpg_kv_free"
+
+    def __init__(self, model: GpuModel, max_seq: int):
+        h = ctypes.c_void_p()
+        _check(load_library().rpg_kv_create(model._h, max_seq, ctypes.byref(h)))
+        self._h = h
+
+    def _info(self):
+        n, cap, b = ctypes.c_int64(), ctypes.c_int64(), ctypes.c_int64()
+        _check(load_library().rpg_kv_info(self._h, ctypes.byref(n), ctypes.byref(cap), ctypes.byref(b)))
+        return n.value, cap.value, b.value
+
+    def len(self) -> int:
+        return self._info()[0]
+
+    def max_seq(self) -> int:
+        return self._info()[1]
+
+    def bytes(self) -> int:
+        return self._info()[2]
+
+    def set_len(self, n: int) -> None:
+        _check(load_library().rpg_kv_set_len(self._h, n))
+
+    def reset(self) -> None:
+        self.set_len(0)
+
+    def layer(self, layer: int):
+        """(k, v) device addresses of one layer ([n_kv_heads][max_seq][head_dim] fp16)."""
+        k, v = ctypes.c_void_p(), ctypes.c_void_p()
+        _check(load_library().rpg_kv_layer(self._h, layer, ctypes.byref(k), ctypes.byref(v)))
+        return k.value, v.value
+
+
+class GpuScratch(_Handle):
+    """Grow-only forward activations and the decode graph (reference GpuScratch, src/qwen3_gpu.h:47-113)."""
+    _free_fn = "rpg_scratch_free"
+
+    def __init__(self):
+        h = ctypes.c_void_p()
+        _check(load_library().rpg_scratch_create(ctypes.byref(h)))
+        self._h = h
+
+    def logits_dev(self) -> int:
+        """Device address of the logits [seq, vocab] of the last forward."""
+        p = ctypes.c_void_p()
+        _check(load_library().rpg_scratch_logits(self._h, ctypes.byref(p), None))
+        return p.value
+
+    def token_dev(self) -> int:
+        """Device address of the sampled-token slot (int32)."""
+        p = ctypes.c_void_p()
+        _check(load_library().rpg_scratch_logits(self._h, None, ctypes.byref(p)))
+        return p.value
+
+
+def GpuForwardFull(m: GpuModel, tokens, s: GpuScratch, want_logits: bool = True, layer_limit: int = 0,
+                   capture_hidden: bool = False, kv: Optional[GpuKvCache] = None):
+    """Forward of host token ids (reference GpuForwardFull, src/qwen3_gpu.h:136-139).
+    Returns (logits [seq, vocab] or None, hidden [n_use + 1, seq, hidden] or None) as numpy float32."""
+    import numpy as np
+
+    toks = np.ascontiguousarray(np.asarray(tokens, dtype=np.int32).reshape(-1))
+    seq = int(toks.size)
+    meta = m.meta()
+    n_use = layer_limit if 0 < layer_limit < meta["n_layers"] else meta["n_layers"]
+    logits = np.empty((seq, meta["vocab"]), np.float32) if want_logits and seq > 0 else None
+    hidden = np.empty((n_use + 1, seq, meta["hidden"]), np.float32) if capture_hidden and seq > 0 else None
+    _check(load_library().rpg_forward_full(
+        m._h, toks.ctypes.data_as(ctypes.c_void_p), seq, s._h,
+        logits.ctypes.data_as(ctypes.c_void_p) if logits is not None else None, layer_limit,
+        hidden.ctypes.data_as(ctypes.c_void_p) if hidden is not None else None, kv._h if kv is not None else None))
+    return logits, hidden
+
+
+def GpuForwardStep(m: GpuModel, token: int, pos: int, kv: GpuKvCache, s: GpuScratch, want_logits: bool = True):
+    """One token at pos == kv.len() (reference GpuForwardStep, src/qwen3_gpu.h:145-146)."""
+    import numpy as np
+
+    logits = np.empty(m.meta()["vocab"], np.float32) if want_logits else None
+    _check(load_library().rpg_forward_step(m._h, int(token), pos, kv._h, s._h,
+                                           logits.ctypes.data_as(ctypes.c_void_p) if logits is not None else None))
+    return logits
+
+
+def GpuForwardStepDev(m: GpuModel, token_dev, pos: int, kv: GpuKvCache, s: GpuScratch) -> None:
+    """One token whose id is on the device (reference GpuForwardStepDev, src/qwen3_gpu.h:151-152)."""
+    torch = _t()
+    _check(load_library().rpg_forward_step_dev(m._h, _addr(token_dev, 4, torch.int32, "token_dev"), pos, kv._h,
+                                               s._h))
+
+
+class _GenerateOptsC(ctypes.Structure):
+    _fields_ = [("max_tokens", ctypes.c_int32), ("stop_ids", ctypes.c_void_p), ("n_stop", ctypes.c_int32),
+                ("temperature", ctypes.c_float), ("top_k", ctypes.c_int32), ("top_p", ctypes.c_float),
+                ("seed", ctypes.c_uint64), ("use_graph", ctypes.c_int32), ("step_logits", ctypes.c_void_p),
+                ("step_logits_cap", ctypes.c_int64)]
+
+
+class GpuGenerateOptions:
+    """Reference GpuGenerateOptions (src/qwen3_gpu.h:156-181): temperature 0 is greedy."""
+
+    def __init__(self, max_tokens: int = 64, stop_ids=(), sample: Optional["SampleOptions"] = None, seed: int = 0,
+                 step_logits: bool = False, use_graph: bool = False):
+        self.max_tokens = int(max_tokens)
+        self.stop_ids = [int(x) for x in stop_ids]
+        self.sample = sample if sample is not None else SampleOptions(temperature=0.0)
+        self.seed = int(seed)
+        self.step_logits = bool(step_logits)
+        self.use_graph = bool(use_graph)
+
+
+def GpuGenerate(m: GpuModel, kv: GpuKvCache, s: GpuScratch, first_logits_dev, opt: GpuGenerateOptions):
+    """Generates from the distribution at first_logits_dev (reference GpuGenerate,
+    src/qwen3_gpu.h:197-199). Returns (ids, step_logits [n, vocab] or None)."""
+    import numpy as np
+
+    torch = _t()
+    vocab = m.meta()["vocab"]
+    stops = np.asarray(opt.stop_ids, dtype=np.int32)
+    out = np.empty(max(opt.max_tokens, 1), np.int32)
+    steps = np.empty((max(opt.max_tokens, 1), vocab), np.float32) if opt.step_logits else None
+    c = _GenerateOptsC(opt.max_tokens, stops.ctypes.data if stops.size else None, int(stops.size),
+                       opt.sample.temperature, opt.sample.top_k, opt.sample.top_p, opt.seed & (2 ** 64 - 1),
+                       int(opt.use_graph), steps.ctypes.data if steps is not None else None,
+                       steps.size if steps is not None else 0)
+    n = ctypes.c_int32()
+    _check(load_library().rpg_generate(m._h, kv._h, s._h, _addr(first_logits_dev, 4 * vocab, torch.float32,
+                                                                 "first_logits"),
+                                       ctypes.byref(c), out.ctypes.data_as(ctypes.c_void_p), out.size,
+                                       ctypes.byref(n)))
+    ids = out[:n.value].tolist()
+    return ids, (steps[:n.value].copy() if steps is not None else None)
+
+
+def GpuGenerateGreedy(m: GpuModel, kv: GpuKvCache, s: GpuScratch, first_logits_dev, opt: GpuGenerateOptions):
+    """GpuGenerate with temperature 0 (reference src/qwen3_gpu.h:207-210)."""
+    g = GpuGenerateOptions(opt.max_tokens, opt.stop_ids, SampleOptions(0.0, opt.sample.top_k, opt.sample.top_p),
+                           opt.seed, opt.step_logits, opt.use_graph)
+    return GpuGenerate(m, kv, s, first_logits_dev, g)
 
 
 # ----------------------------------------------------------------------------- argmax and sampling

@@ -81,9 +81,13 @@ def build(kv, tensors, version: int = 3, alignment: int = 32, offsets=None, pad_
     return bytes(out + data + b"\0" * pad_data)
 
 
-def random_tensor(rng: np.random.Generator, ggml_type: int, dims) -> bytes:
+def random_tensor(rng: np.random.Generator, ggml_type: int, dims, model_like: bool = False) -> bytes:
+    """Random tensor bytes. model_like: matrices with zero-mean, trained-weight-like
+    values (synth.model_table) instead of the benchmark's uniform blocks."""
     rows = int(np.prod(dims[1:])) if len(dims) > 1 else 1
     cols = int(dims[0])
+    if model_like and len(dims) > 1 and ggml_type in (GGML_F32, GGML_Q4_K, GGML_Q6_K):
+        return synth.model_table(rng, ggml_type, rows, cols).tobytes()
     if ggml_type == GGML_F32:
         return rng.normal(1.0, 0.1, size=rows * cols).astype(np.float32).tobytes()
     if ggml_type == GGML_F16:
@@ -95,9 +99,10 @@ def random_tensor(rng: np.random.Generator, ggml_type: int, dims) -> bytes:
 
 def qwen3_model(rng: np.random.Generator, n_layers=2, hidden=256, n_heads=2, n_kv_heads=1, head_dim=128,
                 inter=512, vocab=1000, tied=False, version=3, alignment=32, mat_type=None, norm_type=GGML_F32,
-                key_length=True, extra_kv=(), drop=(), override=None):
+                key_length=True, extra_kv=(), drop=(), override=None, model_like=False):
     """(bytes, tensors, kv) of a synthetic qwen3 GGUF with Q4_K / Q6_K matrices
-    (Q4_K_M-like: attn_v, ffn_down and the embeddings Q6_K, the rest Q4_K)."""
+    (Q4_K_M-like: attn_v, ffn_down and the embeddings Q6_K, the rest Q4_K).
+    model_like: zero-mean weights of trained-model size, for forward tests."""
     kv = [("general.architecture", STR, "qwen3"), ("general.name", STR, "synthetic-qwen3"),
           ("qwen3.block_count", U32, n_layers), ("qwen3.embedding_length", U32, hidden),
           ("qwen3.attention.head_count", U32, n_heads), ("qwen3.attention.head_count_kv", U32, n_kv_heads),
@@ -133,7 +138,7 @@ def qwen3_model(rng: np.random.Generator, n_layers=2, hidden=256, n_heads=2, n_k
                   (p + "ffn_gate.weight", [hidden, inter], mt(p + "ffn_gate.weight", GGML_Q4_K)),
                   (p + "ffn_up.weight", [hidden, inter], mt(p + "ffn_up.weight", GGML_Q4_K)),
                   (p + "ffn_down.weight", [inter, hidden], mt(p + "ffn_down.weight", GGML_Q6_K))]
-    tensors = [(n, d, t, random_tensor(rng, t, d)) for n, d, t in specs if n not in drop]
+    tensors = [(n, d, t, random_tensor(rng, t, d, model_like)) for n, d, t in specs if n not in drop]
     return build(kv, tensors, version=version, alignment=alignment), tensors, kv
 
 

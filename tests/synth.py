@@ -43,6 +43,54 @@ def q6k_blocks(rng: np.random.Generator, n_blocks: int) -> np.ndarray:
     return b
 
 
+def pack_q4k_scales(sc: np.ndarray, m: np.ndarray) -> np.ndarray:
+    """[n, 8] 6-bit scales and mins -> the 12 packed bytes of a Q4_K block (the
+    inverse of the format's get_scale_min_k4: entries 0-3 in the low 6 bits of
+    bytes 0-3 / 4-7, entries 4-7 split over bytes 8-11 and the top 2 bits)."""
+    sc = sc.astype(np.uint8)
+    m = m.astype(np.uint8)
+    out = np.zeros((sc.shape[0], 12), np.uint8)
+    out[:, 0:4] = sc[:, 0:4] | ((sc[:, 4:8] >> 4) << 6)
+    out[:, 4:8] = m[:, 0:4] | ((m[:, 4:8] >> 4) << 6)
+    out[:, 8:12] = (sc[:, 4:8] & 0xF) | ((m[:, 4:8] & 0xF) << 4)
+    return out
+
+
+def model_q4k_blocks(rng: np.random.Generator, n_blocks: int, d: float = 0.002) -> np.ndarray:
+    """Q4_K blocks whose values look like trained weights: zero mean, std ~ 10 d.
+    Scales uniform over 1..8 with the min m = round(7.5 sc), so d (sc q - m)
+    centres q = 0..15 on zero."""
+    b = rng.integers(0, 256, size=(n_blocks, Q4K_BYTES), dtype=np.uint8)
+    dd = f16_bits(np.full(n_blocks, d) * rng.uniform(0.5, 1.5, n_blocks))
+    b[:, 0:2] = dd.view(np.uint8).reshape(n_blocks, 2)
+    b[:, 2:4] = dd.view(np.uint8).reshape(n_blocks, 2)  # dmin = d
+    sc = rng.integers(1, 9, size=(n_blocks, 8))
+    m = np.rint(7.5 * sc).astype(np.int64)
+    b[:, 4:16] = pack_q4k_scales(sc, m)
+    return b
+
+
+def model_q6k_blocks(rng: np.random.Generator, n_blocks: int, d: float = 1e-4) -> np.ndarray:
+    """Q6_K blocks with trained-weight-like values: d sc (q - 32), zero mean."""
+    b = rng.integers(0, 256, size=(n_blocks, Q6K_BYTES), dtype=np.uint8)
+    b[:, 192:208] = rng.integers(-32, 32, size=(n_blocks, 16)).astype(np.int8).view(np.uint8)
+    dd = f16_bits(np.full(n_blocks, d) * rng.uniform(0.5, 1.5, n_blocks))
+    b[:, 208:210] = dd.view(np.uint8).reshape(n_blocks, 2)
+    return b
+
+
+def model_table(rng: np.random.Generator, ggml_type: int, rows: int, cols: int) -> np.ndarray:
+    """quant_table with model_q4k_blocks / model_q6k_blocks (F32: N(0, 0.02))."""
+    nb = cols // 256
+    if ggml_type == 12:
+        return model_q4k_blocks(rng, rows * nb).reshape(-1)
+    if ggml_type == 14:
+        return model_q6k_blocks(rng, rows * nb).reshape(-1)
+    if ggml_type == 0:
+        return rng.normal(0.0, 0.02, rows * cols).astype(np.float32).view(np.uint8)
+    raise ValueError(ggml_type)
+
+
 def quant_table(rng: np.random.Generator, ggml_type: int, rows: int, cols: int) -> np.ndarray:
     """A [rows, cols] table as raw bytes, shape [rows * row_bytes] uint8."""
     nb = cols // 256
