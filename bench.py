@@ -609,6 +609,97 @@ def measure_gguf_upload(torch, ops, reps=3):
         os.remove(path)
 
 
+def measure_model_e2e(torch, ops, reps=3, decode_tokens=128):
+    """The whole Qwen3-1.7B through the library: a Q4_K_M-layout GGUF with
+    zero-mean, trained-weight-sized synthetic weights (tied embeddings), loaded
+    with rpg_model_load, then
+      * prefill (GpuForwardFull with the cache, logits for every position as the
+        reference computes them) of 21 and 2811 tokens;
+      * greedy decoding (GpuGenerate) after those prompts, with the HIP-graph loop
+        and with per-step launches; one sampled run (T 0.7, top_k 40, top_p 0.9).
+    Wall-clock times with the device synchronised; medians of `reps`."""
+    import tempfile
+
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(REPO, "tests"))
+    import gguf_writer
+
+    kv_meta, specs = gguf_writer.qwen3_1_7b_specs(tied=True)
+    shapes = {name: (dims, t) for name, dims, t in specs}
+    rng = np.random.default_rng(17)
+
+    def fill(name, n):
+        dims, t = shapes[name]
+        raw = gguf_writer.random_tensor(rng, t, dims, model_like=True)
+        assert len(raw) == n, (name, len(raw), n)
+        return raw
+
+    tmpdir = os.environ.get("TMPDIR") or tempfile.gettempdir()
+    path = os.path.join(tmpdir, "rpg_bench_qwen3_1_7b_model.gguf")
+    t0 = time.perf_counter()
+    gguf_writer.write_file(path, kv_meta, specs, fill, chunk=1 << 40)
+    gen_s = time.perf_counter() - t0
+    try:
+        m = ops.GpuModel(path, 4096)
+        vocab = m.meta()["vocab"]
+        s = ops.GpuScratch()
+        kv = ops.GpuKvCache(m, 4096)
+        out = {"model": "Qwen3-1.7B shape, 28 layers, Q4_K_M layout (Q6_K token_embd / attn_v / ffn_down), tied",
+               "weights": "synthetic zero-mean Q4_K / Q6_K blocks (std ~0.04), N(1, 0.1) norms",
+               "file_gen_s": round(gen_s, 1), "device_bytes": m.upload_stats()["bytes"]}
+
+        def prefill(n):
+            toks = np.random.default_rng(n).integers(0, vocab, size=n).astype(np.int32)
+            times = []
+            for _ in range(reps + 1):
+                kv.reset()
+                torch.cuda.synchronize()
+                t = time.perf_counter()
+                ops.GpuForwardFull(m, toks, s, want_logits=False, kv=kv)
+                torch.cuda.synchronize()
+                times.append(time.perf_counter() - t)
+            return float(np.median(times[1:]))
+
+        def decode(n_prompt, use_graph, sample=None):
+            prompt_s = prefill(n_prompt)
+            first = s.logits_dev() + 4 * vocab * (n_prompt - 1)
+            opt = ops.GpuGenerateOptions(max_tokens=decode_tokens, use_graph=use_graph, seed=7,
+                                         sample=sample or ops.SampleOptions(0.0))
+            times = []
+            for _ in range(reps + 1):
+                kv.set_len(n_prompt)
+                torch.cuda.synchronize()
+                t = time.perf_counter()
+                ids, _ = ops.GpuGenerate(m, kv, s, first, opt)
+                torch.cuda.synchronize()
+                times.append(time.perf_counter() - t)
+                assert len(ids) == decode_tokens
+            sec = float(np.median(times[1:]))
+            return prompt_s, sec
+
+        for n in (21, N_PREFILL):
+            sec = prefill(n)
+            out[f"prefill_n{n}"] = {"ms": round(sec * 1e3, 2), "tok_per_s": round(n / sec, 1)}
+        for n_prompt in (21, N_PREFILL):
+            for use_graph in (True, False):
+                _, sec = decode(n_prompt, use_graph)
+                out[f"decode_after_{n_prompt}_{'graph' if use_graph else 'per_step'}"] = {
+                    "tokens": decode_tokens, "ms_per_token": round(sec / decode_tokens * 1e3, 3),
+                    "tok_per_s": round(decode_tokens / sec, 1)}
+        _, sec = decode(21, True, ops.SampleOptions(0.7, 40, 0.9))
+        out["decode_after_21_graph_sampled"] = {"tokens": decode_tokens,
+                                                "ms_per_token": round(sec / decode_tokens * 1e3, 3),
+                                                "tok_per_s": round(decode_tokens / sec, 1)}
+        kv.free()
+        s.free()
+        m.free()
+        torch.cuda.empty_cache()
+        return out
+    finally:
+        os.remove(path)
+
+
 def cpu_baseline():
     """The oracle's C restatement of one layer of the chain (n = 2811, 1.7B shape)
     on the host cores, median of 5; plus per-op and single-thread figures. A
@@ -718,6 +809,8 @@ def main():
         extras["attention"] = measure_attention(torch, ops)
         log("argmax / sampler over the 151936-entry vocabulary")
         extras["sampler"] = measure_sampler(torch, ops)
+        log("whole model: Qwen3-1.7B prefill and decode through rpg_forward / rpg_generate")
+        extras["model_e2e"] = measure_model_e2e(torch, ops)
         log("GGUF upload (Qwen3-1.7B-shaped file)")
         extras["gguf_upload"] = measure_gguf_upload(torch, ops)
         log("gather Q4_K / Q6_K")

@@ -33,6 +33,7 @@
 #include "dev_util.h"
 #include "kernels_gpu.h"
 #include "launch.h"
+#include "matmul_mfma.h"
 #include "quant_dev.h"
 
 namespace rpg {
@@ -710,13 +711,20 @@ void LaunchByShape(const char* name, const uint8_t* w, int64_t rows, int64_t row
 
 }  // namespace
 
-// Prefill GEMM on the matrix cores (k_matmul_mfma.hip).
-void LaunchMatMulMfma(uint32_t type, const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb, const float* x,
-                      int64_t cols, int64_t n_tokens, float* out);
-
 // Token count from which the matrix-core GEMM replaces the tiled kernel (measured
 // at 6144 x 2048 Q4_K: 99 us vs ~55 us at 16 tokens, 116 us vs 173 us at 64).
 constexpr int64_t kMfmaMinTokens = 32;
+
+namespace {
+
+// The matrix-core GEMM takes Q4_K / Q6_K matrices with enough tokens, 16-byte
+// aligned activations and rows at the alignment its quant loads assume.
+bool MfmaEligible(uint32_t type, const uint8_t* w_dev, const float* x_dev, int64_t cols, int64_t n_tokens) {
+  return (type == kGgmlQ4_K || type == kGgmlQ6_K) && n_tokens >= kMfmaMinTokens && Aligned(x_dev, 16) &&
+         cols % kQK_K == 0 && Aligned(w_dev, type == kGgmlQ4_K ? 16 : 2) && cols / kQK_K <= 0x7FFFFFFF;
+}
+
+}  // namespace
 
 void GpuMatMulQuantRaw(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_t cols, const float* x_dev,
                        int64_t n_tokens, float* out_dev) {
@@ -730,8 +738,7 @@ void GpuMatMulQuantRaw(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_
   const int64_t row_bytes = TypeRowBytes(type, cols);
   const bool x_ok = Aligned(x_dev, 16) && cols % 4 == 0;
   const int64_t nb = cols / kQK_K;
-  if ((type == kGgmlQ4_K || type == kGgmlQ6_K) && n_tokens >= kMfmaMinTokens && x_ok &&
-      Aligned(w_dev, type == kGgmlQ4_K ? 16 : 2) && nb <= 0x7FFFFFFF) {
+  if (MfmaEligible(type, w_dev, x_dev, cols, n_tokens)) {
     LaunchMatMulMfma(type, w_dev, rows, row_bytes, static_cast<int32_t>(nb), x_dev, cols, n_tokens, out_dev);
     return;
   }
@@ -762,10 +769,24 @@ void GpuMatMulQuantGroup(const GpuTensor* const* ws, int32_t n_mats, const float
               "tensor byte count does not match the [%lld, %lld] shape", static_cast<long long>(ws[i]->rows),
               static_cast<long long>(ws[i]->cols));
   }
+  const int64_t cols = ws[0]->cols;
+  // Prefill: the activations are split once for all the matrices (each output
+  // bit-identical to its own GpuMatMulQuant call, which splits the same way).
+  bool mfma = true;
+  for (int32_t i = 0; i < n_mats && mfma; ++i) {
+    mfma = MfmaEligible(ws[i]->type, static_cast<const uint8_t*>(ws[i]->buf.data()), x_dev, cols, n_tokens);
+  }
+  if (mfma) {
+    const SplitActivations sa = SplitForMfma(x_dev, n_tokens, cols);
+    for (int32_t i = 0; i < n_mats; ++i) {
+      LaunchMatMulMfmaSplit(ws[i]->type, static_cast<const uint8_t*>(ws[i]->buf.data()), ws[i]->rows,
+                            ws[i]->row_bytes(), static_cast<int32_t>(cols / kQK_K), sa, outs[i]);
+    }
+    return;
+  }
   // Decode rows fused per run of consecutive same-type matrices (the kernel of a
   // single matrix, so every output is bit-identical to its GpuMatMulQuant);
   // anything else goes matrix by matrix.
-  const int64_t cols = ws[0]->cols;
   const int64_t nb = cols / kQK_K;
   const bool decode = n_tokens == 1 && Aligned(x_dev, 16) && cols % kQK_K == 0 && nb <= kGroups;
   int32_t i = 0;

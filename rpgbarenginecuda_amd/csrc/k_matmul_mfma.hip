@@ -1,31 +1,43 @@
-// Prefill GEMM for the quantised matmul on the bf16 matrix cores of gfx950:
+// Prefill GEMM for the quantised matmul on the fp16 matrix cores of gfx950:
 // OUT[t][r] = sum_e W[r][e] * X[t][e] for n_tokens large enough to fill a tile.
 //
-// Exactness of the operands:
-//   * weights: the MFMA sees only the integer quants (Q4_K: q in 0..15; Q6_K:
-//     q - 32 in -32..31), exact in bf16; the block scales are applied afterwards
-//     in fp32, per sub-block (Q4_K, 32 elements: d1 * sum(q x) - m1 * sum(x)) or
-//     per 16-element group (Q6_K: d * sc * sum((q - 32) x)), with d1 = d * sc,
-//     m1 = dmin * m and d * sc exact in fp32 (11-bit fp16 times a 6/8-bit integer);
-//   * activations: each fp32 x is split into three bf16 terms h + m + l (each the
-//     round-to-nearest of what is left), which reproduce x to within 2^-27 |x|;
-//     the three products with the same quant are accumulated by the matrix core
-//     in fp32, like the fp32 fused multiply-adds of the other kernels.
-// The activation run sums of Q4_K are summed in fp32 from the unsplit x.
+// Operands (every product the matrix core forms is exact; it accumulates in fp32):
+//   * activations: per token t a power of two s_t brings max |x_t| into
+//     [2^13, 2^14); x s_t is split into two fp16 terms hi + lo (round to
+//     nearest, then the rest), which reproduce x to ~2^-22 |x|. The pre-pass
+//     (SplitActivationsKernel) does this once per input; the result is divided
+//     by s_t at the end (exact);
+//   * Q4_K weights: the matrix core sees sc_j * q (6-bit scale times 4-bit quant,
+//     at most 945, exact in fp16), so a whole 256-element block accumulates in
+//     one register set and the block scale d is applied once per block; the min
+//     term dmin * sum_j m_j * sum(x over sub-block j) is one more 16-deep MFMA
+//     step per block, over the token's 8 run sums (fp32 sums of x, times s_t 2^-6,
+//     split in two fp16 terms) against m_j 2^6 (exact);
+//   * Q6_K weights: sc * (q - 32) can need 12 significant bits, so it is fed as
+//     two exact operands, (sc with its low bit cleared) * (q - 32) (an even
+//     integer of magnitude <= 4096) and (sc & 1) * (q - 32); d once per block.
+// Exact operand values are built from the quant bytes with a byte permute
+// against 0x64 (the fp16 bits of 1024 + q) and one packed fp16 fma or add.
 //
 // Tiling: a 256-thread workgroup computes 128 tokens x 128 weight rows; wave
 // (wm, wn) owns tokens 64 wm + [0, 64) and rows 64 wn + [0, 64) as 2 x 2 tiles
-// of v_mfma_f32_32x32x16_bf16 (A = activations [token][k], B = quants [k][row],
+// of v_mfma_f32_32x32x16_f16 (A = activations [token][k], B = weights [k][row],
 // so each lane's outputs for one register are 32 consecutive rows of one token:
-// coalesced stores). The K loop walks 64-column chunks: the workgroup stages the
-// chunk's activations as three bf16 planes plus the per-(token, sub-block) run
-// sums in LDS, while each lane fetches the quant bytes its B operands need for
-// the chunk straight from global memory.
+// coalesced stores). The K loop walks 64-column chunks: each thread stages 32
+// columns of one token's activation planes and decodes 32 weights of one row
+// into LDS, then the waves run the chunk's MFMAs from LDS only, while the next
+// chunk's global loads (held in registers, branch-free) are in flight. The LDS
+// image is kept under 80 KB and the registers under 256 so that two
+// workgroups share a CU and cover each other's barriers and LDS latency.
 #include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <mutex>
 
 #include "dev_util.h"
 #include "kernels_gpu.h"
 #include "launch.h"
+#include "matmul_mfma.h"
 #include "quant_dev.h"
 
 namespace rpg {
@@ -34,48 +46,50 @@ namespace {
 using dev::ByteOf;
 using dev::ScaleMinK4;
 
-typedef __bf16 Bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 F16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 H2 __attribute__((ext_vector_type(2)));
 typedef float F32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kTileT = 128;       // tokens per workgroup
 constexpr int kTileR = 128;       // weight rows per workgroup
 constexpr int kChunk = 64;        // K columns staged per step
-constexpr int kPad = 8;           // bf16 padding per staged row (breaks LDS bank conflicts)
+constexpr int kPad = 8;           // fp16 padding per staged row (breaks LDS bank conflicts)
 constexpr int kRowStride = kChunk + kPad;
 constexpr int kThreads = 256;
+constexpr int kPlanes = 2;        // fp16 terms per activation
+constexpr int kSumShift = 6;      // run sums stored times 2^-6, m_j times 2^6
+constexpr uint32_t kMagic = 0x64646464u;  // byte 0x64 above a quant byte q: fp16 bits of 1024 + q
 
 __device__ __forceinline__ float HalfF(uint32_t bits) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
 }
 
-// Hides a packed-quant word's known-zero bits from the optimiser so bytes are
-// converted directly (v_cvt_f32_ubyte{0..3}) instead of extracted first. Emits
-// no instruction.
-__device__ __forceinline__ uint32_t Opaque(uint32_t w) {
-  __asm__("" : "+v"(w));
-  return w;
+// fp16 pairs (1024 + q0, 1024 + q1) and (1024 + q2, 1024 + q3) of the four bytes of w.
+__device__ __forceinline__ H2 MagicLo(uint32_t w) { return __builtin_bit_cast(H2, __builtin_amdgcn_perm(kMagic, w, 0x04010400u)); }
+__device__ __forceinline__ H2 MagicHi(uint32_t w) { return __builtin_bit_cast(H2, __builtin_amdgcn_perm(kMagic, w, 0x04030402u)); }
+
+__device__ __forceinline__ F16x8 Join(H2 a, H2 b, H2 c, H2 d) {
+  F16x8 v;
+  v[0] = a[0]; v[1] = a[1]; v[2] = b[0]; v[3] = b[1];
+  v[4] = c[0]; v[5] = c[1]; v[6] = d[0]; v[7] = d[1];
+  return v;
 }
 
-// Eight exact integers (as bytes, unsigned or signed) -> eight bf16 lanes.
-__device__ __forceinline__ Bf16x8 BytesToBf16U(uint32_t lo, uint32_t hi) {
-  lo = Opaque(lo);
-  hi = Opaque(hi);
-  Bf16x8 v;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    v[j] = static_cast<__bf16>(static_cast<float>((lo >> (8 * j)) & 0xFFu));
-    v[4 + j] = static_cast<__bf16>(static_cast<float>((hi >> (8 * j)) & 0xFFu));
-  }
-  return v;
+// sc * q for eight nibble bytes (q in 0..15, sc in 0..63): (1024 + q) sc - 1024 sc
+// in one fused step, exact.
+__device__ __forceinline__ F16x8 ScaledQ4(uint2 q, _Float16 sc) {
+  const H2 s2 = {sc, sc};
+  const _Float16 o = static_cast<_Float16>(-1024.0f) * sc;
+  const H2 o2 = {o, o};
+  return Join(__builtin_elementwise_fma(MagicLo(q.x), s2, o2), __builtin_elementwise_fma(MagicHi(q.x), s2, o2),
+              __builtin_elementwise_fma(MagicLo(q.y), s2, o2), __builtin_elementwise_fma(MagicHi(q.y), s2, o2));
 }
-__device__ __forceinline__ Bf16x8 BytesToBf16S(uint32_t lo, uint32_t hi) {
-  Bf16x8 v;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    v[j] = static_cast<__bf16>(static_cast<float>(static_cast<int8_t>(static_cast<uint8_t>(lo >> (8 * j)))));
-    v[4 + j] = static_cast<__bf16>(static_cast<float>(static_cast<int8_t>(static_cast<uint8_t>(hi >> (8 * j)))));
-  }
-  return v;
+
+// q - 32 for eight 6-bit quant bytes, exact.
+__device__ __forceinline__ F16x8 CenteredQ6(uint2 q) {
+  const _Float16 c = static_cast<_Float16>(-1056.0f);
+  const H2 c2 = {c, c};
+  return Join(MagicLo(q.x) + c2, MagicHi(q.x) + c2, MagicLo(q.y) + c2, MagicHi(q.y) + c2);
 }
 
 // 8 bytes starting `sh` (0 or 2) bytes into three aligned dwords.
@@ -91,89 +105,303 @@ __device__ __forceinline__ uint2 Load8Aligned2(const uint8_t* p) {
   return Window8x(a[0], a[1], a[1 + (sh >> 1)], sh);
 }
 
-// The per-chunk quant bytes and scales one lane needs for one weight row.
-// Q4_K: q8[ks] = the 8 quants (as nibble bytes) for K-step ks; scale/min of the
-// chunk's two sub-blocks. Q6_K: q8[ks] = the 8 signed quants (q - 32) for K-step
-// ks; ds[ks] = d * sc of the group K-step ks falls in.
-struct ChunkQuants {
-  uint2 q8[4];
-  float sc[4];   // Q4_K: d1 of sub-block 0, 1 in [0], [1]; Q6_K: d * sc per K-step
-  float mn[2];   // Q4_K: m1 of sub-block 0, 1
-};
-
-// Q4_K chunk kc (0..3) of block blk; lane half h selects k = 8h .. 8h + 7 of
-// each 16-wide K-step. Sub-block of K-step ks: 2 kc + ks / 2.
-__device__ __forceinline__ ChunkQuants LoadChunkQ4K(const uint8_t* __restrict__ blk, int kc, int h) {
-  ChunkQuants c;
-  const uint4 hdr = *reinterpret_cast<const uint4*>(blk);
-  const float d = HalfF(hdr.x & 0xFFFFu);
-  const float dmin = HalfF(hdr.x >> 16);
+// 32 bytes at a 2-byte aligned address, from nine aligned dwords (Q6_K rows
+// are 210-byte blocks; the dwords around the field stay inside the tensor's pages).
+__device__ __forceinline__ void Load32Aligned2(const uint8_t* p, uint32_t out[8]) {
+  const uint32_t sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3u);
+  const uint32_t* a = reinterpret_cast<const uint32_t*>(p - sh);
+  uint32_t w[9];
 #pragma unroll
-  for (int s2 = 0; s2 < 2; ++s2) {
-    uint32_t sc, m;
-    ScaleMinK4(2 * kc + s2, hdr.y, hdr.z, hdr.w, &sc, &m);
-    c.sc[s2] = d * static_cast<float>(sc);
-    c.mn[s2] = dmin * static_cast<float>(m);
-  }
-  c.sc[2] = c.sc[3] = 0.0f;
-  // elements of sub-block j live in qs[32 (j / 2) + l], nibble j & 1; both
-  // sub-blocks of a chunk share the same 32 qs bytes (j = 2kc, 2kc + 1).
-  const uint8_t* qs = blk + 16 + 32 * kc;
+  for (int i = 0; i < 8; ++i) w[i] = a[i];
+  w[8] = sh != 0 ? a[8] : 0u;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const uint2 raw = *reinterpret_cast<const uint2*>(qs + 16 * (ks & 1) + 8 * h);
-    const int shift = (ks >> 1) * 4;  // K-steps 0, 1: low nibbles (sub-block 2kc); 2, 3: high
-    c.q8[ks] = make_uint2((raw.x >> shift) & 0x0F0F0F0Fu, (raw.y >> shift) & 0x0F0F0F0Fu);
-  }
-  return c;
+  for (int i = 0; i < 8; ++i) out[i] = __builtin_amdgcn_alignbyte(w[i + 1], w[i], sh);
 }
 
-// Q6_K chunk kc (0..3) of block blk (2-byte aligned): elements 64 kc + [0, 64)
-// = half kc / 2, quarters 2 (kc % 2) and 2 (kc % 2) + 1.
-__device__ __forceinline__ ChunkQuants LoadChunkQ6K(const uint8_t* __restrict__ blk, int kc, int h) {
-  ChunkQuants c;
-  const int half = kc >> 1;
-  const int q0 = 2 * (kc & 1);
-  const float d = HalfF(*reinterpret_cast<const uint16_t*>(blk + 208));
-  const uint2 scw = Load8Aligned2(blk + 192 + 8 * half);
-  uint2 qh[2];
+// Raw weight bytes one staging thread decodes per chunk: row `row`, 32 of the
+// chunk's 64 columns (half hf).
+//   Q4_K: hdr = d | dmin | 12 scale bytes of the block; q[0..3] = qs bytes
+//         32 kc + 16 hf .. + 15 (low nibbles: sub-block 2 kc, columns 16 hf + i;
+//         high nibbles: sub-block 2 kc + 1, columns 32 + 16 hf + i).
+//   Q6_K: hdr.x = d, hdr.y = the two scales of the 16-groups of these 32 columns;
+//         q[0..7] = ql bytes, q[8..15] = qh bytes of quarter 2 (kc & 1) + hf.
+struct StageRaw {
+  uint4 hdr;
+  uint32_t q[16];
+};
+
+__device__ __forceinline__ StageRaw FetchStageQ4K(const uint8_t* __restrict__ blk, int kc, int hf) {
+  StageRaw r;
+  r.hdr = *reinterpret_cast<const uint4*>(blk);
+  const uint4 v = *reinterpret_cast<const uint4*>(blk + 16 + 32 * kc + 16 * hf);
+  r.q[0] = v.x; r.q[1] = v.y; r.q[2] = v.z; r.q[3] = v.w;
 #pragma unroll
-  for (int r = 0; r < 2; ++r) qh[r] = Load8Aligned2(blk + 128 + 32 * half + 16 * r + 8 * h);
+  for (int i = 4; i < 16; ++i) r.q[i] = 0u;
+  return r;
+}
+
+__device__ __forceinline__ StageRaw FetchStageQ6K(const uint8_t* __restrict__ blk, int kc, int hf) {
+  StageRaw r;
+  const int half = kc >> 1;
+  const int quarter = 2 * (kc & 1) + hf;
+  const uint8_t* sc = blk + 192 + 4 * kc + 2 * hf;  // 2-byte aligned: one aligned dword holds both
+  const uint32_t scw = *reinterpret_cast<const uint32_t*>(sc - (reinterpret_cast<uintptr_t>(sc) & 3u));
+  const uint32_t scs = (reinterpret_cast<uintptr_t>(sc) & 2u) ? (scw >> 16) : (scw & 0xFFFFu);
+  r.hdr = make_uint4(*reinterpret_cast<const uint16_t*>(blk + 208), scs, 0u, 0u);
+  Load32Aligned2(blk + 64 * half + 32 * (quarter & 1), r.q);
+  Load32Aligned2(blk + 128 + 32 * half, r.q + 8);
+  return r;
+}
+
+// Activation pre-pass: one workgroup per token row.
+__global__ __launch_bounds__(kThreads) void SplitActivationsKernel(const float* __restrict__ x, int64_t cols,
+                                                                   int64_t plane_elems, int64_t sum_elems,
+                                                                   _Float16* __restrict__ planes,
+                                                                   _Float16* __restrict__ sum_planes,
+                                                                   float* __restrict__ inv_scale) {
+  __shared__ float red[kThreads / 64];
+  const int64_t t = blockIdx.x;
+  const float* row = x + t * cols;
+  const int64_t runs = cols / 32;
+  const int tid = threadIdx.x;
+  float mx = 0.0f;
+  for (int64_t r = tid; r < runs; r += kThreads) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float4 f = *reinterpret_cast<const float4*>(row + 32 * r + 4 * k);
+      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)), fmaxf(fabsf(f.z), fabsf(f.w))));
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  // s = 2^e with max |x| s in [2^13, 2^14); 1 for an all-zero or non-finite row
+  int e = 0;
+  if (mx > 0.0f && mx <= 3.4e38f) {
+    int ex;
+    (void)frexpf(mx, &ex);  // mx = f 2^ex, f in [0.5, 1)
+    e = 14 - ex;
+    e = e < -120 ? -120 : (e > 120 ? 120 : e);
+  }
+  const float s = ldexpf(1.0f, e);
+  const float ss = ldexpf(1.0f, e - kSumShift);
+  if (tid == 0) inv_scale[t] = ldexpf(1.0f, -e);
+  for (int64_t r = tid; r < runs; r += kThreads) {
+    float v[32];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float4 f = *reinterpret_cast<const float4*>(row + 32 * r + 4 * k);
+      v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
+    }
+    float sum = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 32; ++k) sum += v[k];
+    const int64_t e0 = t * cols + 32 * r;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      F16x8 hi, lo;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float y = v[8 * g + j] * s;
+        const _Float16 a = static_cast<_Float16>(y);
+        hi[j] = a;
+        lo[j] = static_cast<_Float16>(y - static_cast<float>(a));
+      }
+      *reinterpret_cast<F16x8*>(planes + e0 + 8 * g) = hi;
+      *reinterpret_cast<F16x8*>(planes + plane_elems + e0 + 8 * g) = lo;
+    }
+    const float ys = sum * ss;
+    const _Float16 a = static_cast<_Float16>(ys);
+    const int64_t si = t * runs + r;
+    sum_planes[si] = a;
+    sum_planes[sum_elems + si] = static_cast<_Float16>(ys - static_cast<float>(a));
+  }
+}
+
+// LDS image of the workgroup's operands: two buffers of activation planes
+// and decoded weights, plus the per-block values used at each block's end.
+template <int kWOps>
+struct GemmLds {
+  _Float16 xs[kPlanes][kTileT][kRowStride];
+  _Float16 ws[kWOps][kTileR][kRowStride];
+  _Float16 ss[kWOps == 1 ? kPlanes : 1][kTileT][8];  // Q4_K: the block's run sums of each token
+  _Float16 sm[kWOps == 1 ? kTileR : 1][8];           // Q4_K: m_j 2^6 of each row
+  float sd[kTileR][2];                               // d, dmin of each row's block
+};
+
+// One chunk's global loads, held in registers until the chunk is staged.
+struct ChunkLoads {
+  uint4 x[kPlanes][4];
+  uint4 sum;
+  StageRaw raw;
+};
+
+// Branch-free: a token past n_tokens reads token 0 (a valid address) and the
+// value is replaced by zero.
+template <bool kQ4>
+__device__ __forceinline__ void FetchChunk(ChunkLoads& f, int c, const _Float16* st_src, const _Float16* st_sum,
+                                           int64_t plane_elems, bool st_ok, const uint8_t* st_w, int st_hf) {
+  constexpr int64_t kBB = kQ4 ? kQ4KBlockBytes : kQ6KBlockBytes;
+  const uint32_t keep = st_ok ? 0xFFFFFFFFu : 0u;
+#pragma unroll
+  for (int p = 0; p < kPlanes; ++p)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint4 v = *reinterpret_cast<const uint4*>(st_src + p * plane_elems + kChunk * c + 8 * g);
+      f.x[p][g] = make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
+    }
+  if (kQ4) {
+    const uint4 v = *reinterpret_cast<const uint4*>(st_sum + 8 * (c >> 2));
+    f.sum = make_uint4(v.x & keep, v.y & keep, v.z & keep, v.w & keep);
+  }
+  const uint8_t* blk = st_w + (c >> 2) * kBB;
+  f.raw = kQ4 ? FetchStageQ4K(blk, c & 3, st_hf) : FetchStageQ6K(blk, c & 3, st_hf);
+}
+
+// Chunk c (held in f) -> LDS.
+template <bool kQ4, int kWOps>
+__device__ __forceinline__ void StageChunk(GemmLds<kWOps>& L, const ChunkLoads& f, int c, int st_i, int st_hf) {
+  const int kc = c & 3;
+#pragma unroll
+  for (int p = 0; p < kPlanes; ++p)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) *reinterpret_cast<uint4*>(&L.xs[p][st_i][32 * st_hf + 8 * g]) = f.x[p][g];
+  const StageRaw& raw = f.raw;
+  if (kQ4) {
+    const uint32_t s0 = raw.hdr.y, s1 = raw.hdr.z, s2 = raw.hdr.w;
+    uint32_t scl, ml, sch, mh;
+    ScaleMinK4(2 * kc, s0, s1, s2, &scl, &ml);
+    ScaleMinK4(2 * kc + 1, s0, s1, s2, &sch, &mh);
+    const _Float16 fl = static_cast<_Float16>(static_cast<float>(scl));
+    const _Float16 fh = static_cast<_Float16>(static_cast<float>(sch));
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {  // low nibbles: sub-block 2 kc; high: 2 kc + 1
+      const uint32_t bx = raw.q[2 * g], by = raw.q[2 * g + 1];
+      *reinterpret_cast<F16x8*>(&L.ws[0][st_i][16 * st_hf + 8 * g]) =
+          ScaledQ4(make_uint2(bx & 0x0F0F0F0Fu, by & 0x0F0F0F0Fu), fl);
+      *reinterpret_cast<F16x8*>(&L.ws[0][st_i][32 + 16 * st_hf + 8 * g]) =
+          ScaledQ4(make_uint2((bx >> 4) & 0x0F0F0F0Fu, (by >> 4) & 0x0F0F0F0Fu), fh);
+    }
+    if (kc == 3) {  // used by this chunk's block end only
+      *reinterpret_cast<uint4*>(&L.ss[st_hf][st_i][0]) = f.sum;
+      if (st_hf == 0) {
+        F16x8 mv;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          uint32_t scj, mj;
+          ScaleMinK4(j, s0, s1, s2, &scj, &mj);
+          mv[j] = static_cast<_Float16>(static_cast<float>(mj << kSumShift));
+        }
+        *reinterpret_cast<F16x8*>(&L.sm[st_i][0]) = mv;
+        L.sd[st_i][0] = HalfF(raw.hdr.x & 0xFFFFu);
+        L.sd[st_i][1] = HalfF(raw.hdr.x >> 16);
+      }
+    }
+  } else {
+    const int quarter = 2 * (kc & 1) + st_hf;
+    const int nshift = quarter < 2 ? 0 : 4;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {  // columns 32 st_hf + 8 g .. + 7: 16-group g / 2
+      const uint32_t lx = raw.q[2 * g], ly = raw.q[2 * g + 1];
+      const uint32_t hx = raw.q[8 + 2 * g], hy = raw.q[8 + 2 * g + 1];
+      const uint2 q = make_uint2(((lx >> nshift) & 0x0F0F0F0Fu) | (((hx >> (2 * quarter)) & 0x03030303u) << 4),
+                                 ((ly >> nshift) & 0x0F0F0F0Fu) | (((hy >> (2 * quarter)) & 0x03030303u) << 4));
+      const F16x8 qc = CenteredQ6(q);
+      const int sc = static_cast<int8_t>(ByteOf(raw.hdr.y, g >> 1));
+      const _Float16 se = static_cast<_Float16>(static_cast<float>(sc & ~1));
+      const _Float16 so = static_cast<_Float16>(static_cast<float>(sc & 1));
+      *reinterpret_cast<F16x8*>(&L.ws[0][st_i][32 * st_hf + 8 * g]) = qc * se;
+      *reinterpret_cast<F16x8*>(&L.ws[kWOps - 1][st_i][32 * st_hf + 8 * g]) = qc * so;
+    }
+    if (kc == 3 && st_hf == 0) L.sd[st_i][0] = HalfF(raw.hdr.x & 0xFFFFu);
+  }
+}
+
+// Chunk c on the matrix cores, one 16-deep K-step at a time (the other
+// workgroup on the CU covers the LDS latency); at a block's end the block
+// scale (and for Q4_K the min term) moves part into acc.
+template <bool kQ4, int kWOps>
+__device__ __forceinline__ void ComputeChunk(const GemmLds<kWOps>& L, int c, int wm, int wn, int li, int h,
+                                             F32x16 (&acc)[2][2], F32x16 (&part)[2][2]) {
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    const int quarter = q0 + (ks >> 1);
-    const int lq = 16 * (ks & 1) + 8 * h;  // element index inside the 32-run of the quarter
-    const uint2 ql = Load8Aligned2(blk + 64 * half + 32 * (quarter & 1) + lq);
-    const int nshift = quarter < 2 ? 0 : 4;
-    const uint2 hb = qh[ks & 1];
-    uint32_t w[2];
+    const int kcol = 16 * ks + 8 * h;
+    F16x8 af[2][kPlanes], bf[2][kWOps];
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const uint32_t qlw = k == 0 ? ql.x : ql.y;
-      const uint32_t qhw = k == 0 ? hb.x : hb.y;
-      const uint32_t nib = (qlw >> nshift) & 0x0F0F0F0Fu;
-      const uint32_t hi2 = ((qhw >> (2 * quarter)) & 0x03030303u) << 4;
-      w[k] = (nib | hi2) ^ 0x20202020u;  // 6-bit q - 32, two's complement in 6 bits
-      // sign-extend each 6-bit field to a byte: bit 5 -> bits 6, 7
-      w[k] |= ((w[k] & 0x20202020u) >> 5) * 0xC0u;
-    }
-    c.q8[ks] = make_uint2(w[0], w[1]);
-    const int si = (lq >> 4) + 2 * quarter;  // index inside the half's 8 scales
-    const int8_t sc = static_cast<int8_t>(ByteOf(si < 4 ? scw.x : scw.y, si & 3));
-    c.sc[ks] = d * static_cast<float>(sc);
+    for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+      for (int o = 0; o < kWOps; ++o)
+        bf[nt][o] = *reinterpret_cast<const F16x8*>(&L.ws[o][64 * wn + 32 * nt + li][kcol]);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int p = 0; p < kPlanes; ++p)
+        af[mt][p] = *reinterpret_cast<const F16x8*>(&L.xs[p][64 * wm + 32 * mt + li][kcol]);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int p = 0; p < kPlanes; ++p)
+#pragma unroll
+        for (int nt = 0; nt < 2; ++nt)
+#pragma unroll
+          for (int o = 0; o < kWOps; ++o)
+            part[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[mt][p], bf[nt][o], part[mt][nt], 0, 0, 0);
   }
-  c.mn[0] = c.mn[1] = 0.0f;
-  return c;
+  if ((c & 3) != 3) return;
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const float d = L.sd[64 * wn + 32 * nt + li][0];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        acc[mt][nt][i] = __builtin_fmaf(d, part[mt][nt][i], acc[mt][nt][i]);
+        part[mt][nt][i] = 0.0f;
+      }
+  }
+  if (!kQ4) return;
+  F16x8 bm[2];
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const F16x8 v = *reinterpret_cast<const F16x8*>(&L.sm[64 * wn + 32 * nt + li][0]);
+    const F16x8 z = {};
+    bm[nt] = h == 0 ? v : z;  // k 8..15 carry zero weights
+  }
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int p = 0; p < kPlanes; ++p) {
+      const F16x8 a = *reinterpret_cast<const F16x8*>(&L.ss[p][64 * wm + 32 * mt + li][0]);
+#pragma unroll
+      for (int nt = 0; nt < 2; ++nt)
+        part[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bm[nt], part[mt][nt], 0, 0, 0);
+    }
+#pragma unroll
+  for (int nt = 0; nt < 2; ++nt) {
+    const float dmin = L.sd[64 * wn + 32 * nt + li][1];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        acc[mt][nt][i] = __builtin_fmaf(-dmin, part[mt][nt][i], acc[mt][nt][i]);
+        part[mt][nt][i] = 0.0f;
+      }
+  }
 }
 
 template <uint32_t kType>
-__global__ __launch_bounds__(kThreads) void MatMulMfmaKernel(const uint8_t* __restrict__ w, int64_t rows,
+__global__ __launch_bounds__(kThreads, 2) void MatMulMfmaKernel(const uint8_t* __restrict__ w, int64_t rows,
                                                              int64_t row_bytes, int32_t nb,
-                                                             const float* __restrict__ x, int64_t cols,
+                                                             const _Float16* __restrict__ planes,
+                                                             const _Float16* __restrict__ sum_planes,
+                                                             int64_t sum_stride,
+                                                             const float* __restrict__ inv_scale, int64_t cols,
                                                              int64_t n_tokens, float* __restrict__ out) {
-  constexpr int64_t kBB = kType == kGgmlQ4_K ? kQ4KBlockBytes : kQ6KBlockBytes;
-  __shared__ __attribute__((aligned(16))) __bf16 xs[3][kTileT][kRowStride];
-  __shared__ float xsum[kTileT][2];
+  constexpr bool kQ4 = kType == kGgmlQ4_K;
+  constexpr int kWOps = kQ4 ? 1 : 2;  // weight operands per column (Q6_K: even and odd scale parts)
+  __shared__ __attribute__((aligned(16))) GemmLds<kWOps> L;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -185,170 +413,55 @@ __global__ __launch_bounds__(kThreads) void MatMulMfmaKernel(const uint8_t* __re
   const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kTileT;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kTileR;
 
-  // the two weight rows of this lane (clamped: loads stay in bounds, results dropped)
-  const uint8_t* wrow[2];
-#pragma unroll
-  for (int nt = 0; nt < 2; ++nt) {
-    const int64_t r = r0 + 64 * wn + 32 * nt + li;
-    wrow[nt] = w + (r < rows ? r : rows - 1) * row_bytes;
-  }
-
-  F32x16 acc[2][2];
+  F32x16 acc[2][2], part[2][2];
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
     for (int nt = 0; nt < 2; ++nt)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) acc[mt][nt][i] = 0.0f;
-
-  // staging map: thread -> (token tok, sub-block half sh of the chunk: 32 columns)
-  const int st_tok = tid >> 1;
-  const int st_half = tid & 1;
-  const int64_t st_t = t0 + st_tok;
-
-  for (int b = 0; b < nb; ++b) {
-    for (int kc = 0; kc < 4; ++kc) {
-      // this chunk's quants for both weight rows (in flight during the staging)
-      ChunkQuants cq[2];
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-        cq[nt] = kType == kGgmlQ4_K ? LoadChunkQ4K(wrow[nt] + b * kBB, kc, h) : LoadChunkQ6K(wrow[nt] + b * kBB, kc, h);
-
-      // stage 128 tokens x 64 columns: three bf16 planes and fp32 run sums
-      {
-        float v[32];
-        if (st_t < n_tokens) {
-          const float* src = x + st_t * cols + static_cast<int64_t>(b) * kQK_K + kChunk * kc + 32 * st_half;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) {
-            const float4 f = *reinterpret_cast<const float4*>(src + 4 * i);
-            v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
-          }
-        } else {
-#pragma unroll
-          for (int i = 0; i < 32; ++i) v[i] = 0.0f;
-        }
-        float s = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 32; ++i) s += v[i];
-        xsum[st_tok][st_half] = s;
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          Bf16x8 ph, pm, pl;
-#pragma unroll
-          for (int j = 0; j < 8; ++j) {
-            const float xv = v[8 * g + j];
-            const __bf16 bh = static_cast<__bf16>(xv);
-            const float r1 = xv - static_cast<float>(bh);
-            const __bf16 bm = static_cast<__bf16>(r1);
-            const float r2 = r1 - static_cast<float>(bm);
-            ph[j] = bh;
-            pm[j] = bm;
-            pl[j] = static_cast<__bf16>(r2);
-          }
-          const int col = 32 * st_half + 8 * g;
-          *reinterpret_cast<Bf16x8*>(&xs[0][st_tok][col]) = ph;
-          *reinterpret_cast<Bf16x8*>(&xs[1][st_tok][col]) = pm;
-          *reinterpret_cast<Bf16x8*>(&xs[2][st_tok][col]) = pl;
-        }
+      for (int i = 0; i < 16; ++i) {
+        acc[mt][nt][i] = 0.0f;
+        part[mt][nt][i] = 0.0f;
       }
-      __syncthreads();
 
-      if (kType == kGgmlQ4_K) {
-        // two sub-blocks per chunk, two K-steps each
-#pragma unroll
-        for (int sb = 0; sb < 2; ++sb) {
-          F32x16 part[2][2];
-#pragma unroll
-          for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-              for (int i = 0; i < 16; ++i) part[mt][nt][i] = 0.0f;
-#pragma unroll
-          for (int k2 = 0; k2 < 2; ++k2) {
-            const int ks = 2 * sb + k2;
-            Bf16x8 bq[2];
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt) bq[nt] = BytesToBf16U(cq[nt].q8[ks].x, cq[nt].q8[ks].y);
-            const int kcol = 16 * (ks & 1) + 32 * sb + 8 * h;
-#pragma unroll
-            for (int mt = 0; mt < 2; ++mt) {
-              const int tok = 64 * wm + 32 * mt + li;
-#pragma unroll
-              for (int p = 0; p < 3; ++p) {
-                const Bf16x8 a = *reinterpret_cast<const Bf16x8*>(&xs[p][tok][kcol]);
-#pragma unroll
-                for (int nt = 0; nt < 2; ++nt)
-                  part[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq[nt], part[mt][nt], 0, 0, 0);
-              }
-            }
-          }
-          // acc += d1 * part - m1 * sum(x over the sub-block), per (token, row)
-#pragma unroll
-          for (int mt = 0; mt < 2; ++mt) {
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              const int tok = 64 * wm + 32 * mt + (i & 3) + 8 * (i >> 2) + 4 * h;
-              const float sx = xsum[tok][sb];
-#pragma unroll
-              for (int nt = 0; nt < 2; ++nt) {
-                float a = __builtin_fmaf(cq[nt].sc[sb], part[mt][nt][i], acc[mt][nt][i]);
-                acc[mt][nt][i] = __builtin_fmaf(-cq[nt].mn[sb], sx, a);
-              }
-            }
-          }
-        }
-      } else {
-        // one scale group per K-step
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          F32x16 part[2][2];
-#pragma unroll
-          for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-              for (int i = 0; i < 16; ++i) part[mt][nt][i] = 0.0f;
-          Bf16x8 bq[2];
-#pragma unroll
-          for (int nt = 0; nt < 2; ++nt) bq[nt] = BytesToBf16S(cq[nt].q8[ks].x, cq[nt].q8[ks].y);
-          const int kcol = 16 * ks + 8 * h;
-#pragma unroll
-          for (int mt = 0; mt < 2; ++mt) {
-            const int tok = 64 * wm + 32 * mt + li;
-#pragma unroll
-            for (int p = 0; p < 3; ++p) {
-              const Bf16x8 a = *reinterpret_cast<const Bf16x8*>(&xs[p][tok][kcol]);
-#pragma unroll
-              for (int nt = 0; nt < 2; ++nt)
-                part[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, bq[nt], part[mt][nt], 0, 0, 0);
-            }
-          }
-#pragma unroll
-          for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-            for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-              for (int i = 0; i < 16; ++i)
-                acc[mt][nt][i] = __builtin_fmaf(cq[nt].sc[ks], part[mt][nt][i], acc[mt][nt][i]);
-        }
-      }
-      __syncthreads();  // the next chunk overwrites xs / xsum
-    }
+  // staging map: thread -> (tile row st_i, 32-column half st_hf of the chunk):
+  // activations of token t0 + st_i, weights of row r0 + st_i (both clamped to
+  // valid rows; an activation past n_tokens is zeroed)
+  const int st_i = tid >> 1;
+  const int st_hf = tid & 1;
+  const int64_t st_t = t0 + st_i;
+  const bool st_ok = st_t < n_tokens;
+  const int64_t st_tc = st_ok ? st_t : 0;
+  const int64_t runs = cols / 32;
+  const int64_t plane_elems = n_tokens * cols;
+  const _Float16* st_src = planes + st_tc * cols + 32 * st_hf;
+  const _Float16* st_sum = sum_planes + st_hf * sum_stride + st_tc * runs;
+  const int64_t st_r = r0 + st_i;
+  const uint8_t* st_w = w + (st_r < rows ? st_r : rows - 1) * row_bytes;
+
+  const int n_chunks = 4 * nb;
+  ChunkLoads f;
+  FetchChunk<kQ4>(f, 0, st_src, st_sum, plane_elems, st_ok, st_w, st_hf);
+  for (int c = 0; c < n_chunks; ++c) {
+    if (c > 0) __syncthreads();  // every wave is done with chunk c - 1's operands
+    StageChunk<kQ4, kWOps>(L, f, c, st_i, st_hf);
+    __syncthreads();
+    if (c + 1 < n_chunks) FetchChunk<kQ4>(f, c + 1, st_src, st_sum, plane_elems, st_ok, st_w, st_hf);
+    ComputeChunk<kQ4, kWOps>(L, c, wm, wn, li, h, acc, part);
   }
 
   // D[i][j]: j = lane % 32 (weight row), i = (r % 4) + 8 (r / 4) + 4 (lane / 32) (token)
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
-    for (int nt = 0; nt < 2; ++nt) {
-      const int64_t row = r0 + 64 * wn + 32 * nt + li;
-      if (row >= rows) continue;
+    for (int i = 0; i < 16; ++i) {
+      const int64_t tok = t0 + 64 * wm + 32 * mt + (i & 3) + 8 * (i >> 2) + 4 * h;
+      if (tok >= n_tokens) continue;
+      const float inv = inv_scale[tok];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int64_t tok = t0 + 64 * wm + 32 * mt + (i & 3) + 8 * (i >> 2) + 4 * h;
-        if (tok < n_tokens) out[tok * rows + row] = acc[mt][nt][i];
+      for (int nt = 0; nt < 2; ++nt) {
+        const int64_t row = r0 + 64 * wn + 32 * nt + li;
+        if (row < rows) out[tok * rows + row] = acc[mt][nt][i] * inv;
       }
     }
   }
@@ -356,23 +469,91 @@ __global__ __launch_bounds__(kThreads) void MatMulMfmaKernel(const uint8_t* __re
 
 }  // namespace
 
-// Launched by GpuMatMulQuantRaw for Q4_K / Q6_K with enough tokens; the caller
-// has checked the type, the alignment (Q4_K 16 bytes, Q6_K 2 bytes, x 16 bytes)
-// and cols % 256 == 0.
-void LaunchMatMulMfma(uint32_t type, const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb, const float* x,
-                      int64_t cols, int64_t n_tokens, float* out) {
-  const int64_t gy = (n_tokens + kTileT - 1) / kTileT;
+namespace {
+
+// ---------------------------------------------------------------- split-activation buffer
+//
+// Grow-only, library-owned. An outgrown buffer is retired, not freed: a graph
+// captured earlier keeps its address (growth during a capture is refused).
+// Never freed at exit (a destructor running after the HIP runtime has shut down
+// can hang).
+struct SplitBuffer {
+  std::mutex mu;
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+SplitBuffer& Splits() {
+  static SplitBuffer* b = new SplitBuffer();
+  return *b;
+}
+
+void* EnsureSplitBuffer(size_t bytes) {
+  SplitBuffer& b = Splits();
+  std::lock_guard<std::mutex> lock(b.mu);
+  if (b.bytes < bytes) {
+    RPG_CHECK(!StreamIsCapturing(),
+              "the prefill matmul needs a %zu-byte activation buffer (have %zu), which cannot be allocated during "
+              "graph capture; run the same shape once before capturing",
+              bytes, b.bytes);
+    const size_t grow = bytes > 2 * b.bytes ? bytes : 2 * b.bytes;
+    void* p = nullptr;
+    RPG_HIP_CHECK(hipMalloc(&p, grow));
+    b.ptr = p;  // the previous buffer stays allocated (see above)
+    b.bytes = grow;
+  }
+  return b.ptr;
+}
+
+}  // namespace
+
+SplitActivations SplitForMfma(const float* x, int64_t n_tokens, int64_t cols) {
+  RPG_CHECK(n_tokens > 0 && cols > 0 && cols % 32 == 0, "invalid activation split [%lld, %lld]",
+            static_cast<long long>(n_tokens), static_cast<long long>(cols));
+  RPG_CHECK(n_tokens <= 0x7FFFFFFF, "too many tokens for the activation split: %lld", static_cast<long long>(n_tokens));
+  const int64_t elems = n_tokens * cols;
+  const int64_t sum_elems = elems / 32;
+  const size_t plane_bytes = static_cast<size_t>(elems) * sizeof(_Float16);
+  const size_t sum_bytes = (static_cast<size_t>(sum_elems) * sizeof(_Float16) + 255) / 256 * 256;
+  const size_t bytes = kPlanes * plane_bytes + kPlanes * sum_bytes + static_cast<size_t>(n_tokens) * sizeof(float);
+  uint8_t* base = static_cast<uint8_t*>(EnsureSplitBuffer(bytes));
+  SplitActivations sa;
+  sa.planes = base;
+  sa.sums = base + kPlanes * plane_bytes;
+  sa.inv_scale = reinterpret_cast<float*>(base + kPlanes * plane_bytes + kPlanes * sum_bytes);
+  sa.sum_stride = static_cast<int64_t>(sum_bytes / sizeof(_Float16));
+  sa.n_tokens = n_tokens;
+  sa.cols = cols;
+  Launch("SplitActivationsKernel", SplitActivationsKernel, dim3(static_cast<unsigned>(n_tokens)), dim3(kThreads), x,
+         cols, elems, sa.sum_stride, static_cast<_Float16*>(sa.planes), static_cast<_Float16*>(sa.sums), sa.inv_scale);
+  return sa;
+}
+
+// Launched by GpuMatMulQuantRaw / GpuMatMulQuantGroup for Q4_K / Q6_K with
+// enough tokens; the caller has checked the type, the alignment (Q4_K 16 bytes,
+// Q6_K 2 bytes) and cols % 256 == 0, and split the activations.
+void LaunchMatMulMfmaSplit(uint32_t type, const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb,
+                           const SplitActivations& sa, float* out) {
+  const int64_t gy = (sa.n_tokens + kTileT - 1) / kTileT;
   const int64_t gx = (rows + kTileR - 1) / kTileR;
   RPG_CHECK(gy <= 65535 && gx <= 0x7FFFFFFF, "matmul grid too large: %lld x %lld", static_cast<long long>(gx),
             static_cast<long long>(gy));
+  RPG_CHECK(static_cast<int64_t>(nb) * kQK_K == sa.cols, "split activations have %lld columns, the matrix %lld",
+            static_cast<long long>(sa.cols), static_cast<long long>(nb) * kQK_K);
   const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+  const _Float16* planes = static_cast<const _Float16*>(sa.planes);
+  const _Float16* sums = static_cast<const _Float16*>(sa.sums);
   if (type == kGgmlQ4_K) {
-    Launch("MatMulMfmaQ4KKernel", MatMulMfmaKernel<kGgmlQ4_K>, grid, dim3(kThreads), w, rows, row_bytes, nb, x, cols,
-           n_tokens, out);
+    Launch("MatMulMfmaQ4KKernel", MatMulMfmaKernel<kGgmlQ4_K>, grid, dim3(kThreads), w, rows, row_bytes, nb, planes,
+           sums, sa.sum_stride, sa.inv_scale, sa.cols, sa.n_tokens, out);
   } else {
-    Launch("MatMulMfmaQ6KKernel", MatMulMfmaKernel<kGgmlQ6_K>, grid, dim3(kThreads), w, rows, row_bytes, nb, x, cols,
-           n_tokens, out);
+    Launch("MatMulMfmaQ6KKernel", MatMulMfmaKernel<kGgmlQ6_K>, grid, dim3(kThreads), w, rows, row_bytes, nb, planes,
+           sums, sa.sum_stride, sa.inv_scale, sa.cols, sa.n_tokens, out);
   }
+}
+
+void LaunchMatMulMfma(uint32_t type, const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb, const float* x,
+                      int64_t cols, int64_t n_tokens, float* out) {
+  LaunchMatMulMfmaSplit(type, w, rows, row_bytes, nb, SplitForMfma(x, n_tokens, cols), out);
 }
 
 }  // namespace rpg
