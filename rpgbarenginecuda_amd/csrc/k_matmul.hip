@@ -711,17 +711,23 @@ void LaunchByShape(const char* name, const uint8_t* w, int64_t rows, int64_t row
 
 }  // namespace
 
-// Token count from which the matrix-core GEMM replaces the tiled kernel (measured
-// at 6144 x 2048 Q4_K: 99 us vs ~55 us at 16 tokens, 116 us vs 173 us at 64).
+// Token counts from which the matrix-core GEMM replaces the tiled kernel
+// (measured on Qwen3-1.7B matrices: at 16 tokens 26 us vs 50 us for 6144 x 2048
+// Q4_K, 362 us vs 622 us for the 151936-row lm_head, but 22 us vs 19 us for
+// 2048 x 2048; from 32 tokens it wins for every shape).
 constexpr int64_t kMfmaMinTokens = 32;
+constexpr int64_t kMfmaMinTokensWide = 16;  // matrices of at least kMfmaWideRows rows
+constexpr int64_t kMfmaWideRows = 4096;
 
 namespace {
 
 // The matrix-core GEMM takes Q4_K / Q6_K matrices with enough tokens, 16-byte
 // aligned activations and rows at the alignment its quant loads assume.
-bool MfmaEligible(uint32_t type, const uint8_t* w_dev, const float* x_dev, int64_t cols, int64_t n_tokens) {
-  return (type == kGgmlQ4_K || type == kGgmlQ6_K) && n_tokens >= kMfmaMinTokens && Aligned(x_dev, 16) &&
-         cols % kQK_K == 0 && Aligned(w_dev, type == kGgmlQ4_K ? 16 : 2) && cols / kQK_K <= 0x7FFFFFFF;
+bool MfmaEligible(uint32_t type, const uint8_t* w_dev, const float* x_dev, int64_t rows, int64_t cols,
+                  int64_t n_tokens) {
+  const bool enough = n_tokens >= kMfmaMinTokens || (n_tokens >= kMfmaMinTokensWide && rows >= kMfmaWideRows);
+  return (type == kGgmlQ4_K || type == kGgmlQ6_K) && enough && Aligned(x_dev, 16) && cols % kQK_K == 0 &&
+         Aligned(w_dev, type == kGgmlQ4_K ? 16 : 2) && cols / kQK_K <= 0x7FFFFFFF;
 }
 
 }  // namespace
@@ -738,7 +744,7 @@ void GpuMatMulQuantRaw(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_
   const int64_t row_bytes = TypeRowBytes(type, cols);
   const bool x_ok = Aligned(x_dev, 16) && cols % 4 == 0;
   const int64_t nb = cols / kQK_K;
-  if (MfmaEligible(type, w_dev, x_dev, cols, n_tokens)) {
+  if (MfmaEligible(type, w_dev, x_dev, rows, cols, n_tokens)) {
     LaunchMatMulMfma(type, w_dev, rows, row_bytes, static_cast<int32_t>(nb), x_dev, cols, n_tokens, out_dev);
     return;
   }
@@ -774,7 +780,8 @@ void GpuMatMulQuantGroup(const GpuTensor* const* ws, int32_t n_mats, const float
   // bit-identical to its own GpuMatMulQuant call, which splits the same way).
   bool mfma = true;
   for (int32_t i = 0; i < n_mats && mfma; ++i) {
-    mfma = MfmaEligible(ws[i]->type, static_cast<const uint8_t*>(ws[i]->buf.data()), x_dev, cols, n_tokens);
+    mfma = MfmaEligible(ws[i]->type, static_cast<const uint8_t*>(ws[i]->buf.data()), x_dev, ws[i]->rows, cols,
+                        n_tokens);
   }
   if (mfma) {
     const SplitActivations sa = SplitForMfma(x_dev, n_tokens, cols);

@@ -391,6 +391,9 @@ __device__ __forceinline__ void ComputeChunk(const GemmLds<kWOps>& L, int c, int
   }
 }
 
+// Blocks [z bps, min(nb, (z + 1) bps)) of K for z = blockIdx.z; with one
+// split (partial == nullptr) the result goes to out, otherwise the K-slice's
+// partial tile to partial[z] for MatMulSplitReduceKernel.
 template <uint32_t kType>
 __global__ __launch_bounds__(kThreads, 2) void MatMulMfmaKernel(const uint8_t* __restrict__ w, int64_t rows,
                                                              int64_t row_bytes, int32_t nb,
@@ -398,7 +401,8 @@ __global__ __launch_bounds__(kThreads, 2) void MatMulMfmaKernel(const uint8_t* _
                                                              const _Float16* __restrict__ sum_planes,
                                                              int64_t sum_stride,
                                                              const float* __restrict__ inv_scale, int64_t cols,
-                                                             int64_t n_tokens, float* __restrict__ out) {
+                                                             int64_t n_tokens, int32_t blocks_per_split,
+                                                             float* __restrict__ out, float* __restrict__ partial) {
   constexpr bool kQ4 = kType == kGgmlQ4_K;
   constexpr int kWOps = kQ4 ? 1 : 2;  // weight operands per column (Q6_K: even and odd scale parts)
   __shared__ __attribute__((aligned(16))) GemmLds<kWOps> L;
@@ -434,12 +438,14 @@ __global__ __launch_bounds__(kThreads, 2) void MatMulMfmaKernel(const uint8_t* _
   const int64_t st_tc = st_ok ? st_t : 0;
   const int64_t runs = cols / 32;
   const int64_t plane_elems = n_tokens * cols;
-  const _Float16* st_src = planes + st_tc * cols + 32 * st_hf;
-  const _Float16* st_sum = sum_planes + st_hf * sum_stride + st_tc * runs;
+  const int b0 = static_cast<int>(blockIdx.z) * blocks_per_split;  // first block of this K-slice
+  const int n_blk = nb - b0 < blocks_per_split ? nb - b0 : blocks_per_split;
+  const _Float16* st_src = planes + st_tc * cols + 32 * st_hf + static_cast<int64_t>(kQK_K) * b0;
+  const _Float16* st_sum = sum_planes + st_hf * sum_stride + st_tc * runs + 8 * b0;
   const int64_t st_r = r0 + st_i;
-  const uint8_t* st_w = w + (st_r < rows ? st_r : rows - 1) * row_bytes;
+  const uint8_t* st_w = w + (st_r < rows ? st_r : rows - 1) * row_bytes + static_cast<int64_t>(b0) * (kQ4 ? kQ4KBlockBytes : kQ6KBlockBytes);
 
-  const int n_chunks = 4 * nb;
+  const int n_chunks = 4 * n_blk;
   ChunkLoads f;
   FetchChunk<kQ4>(f, 0, st_src, st_sum, plane_elems, st_ok, st_w, st_hf);
   for (int c = 0; c < n_chunks; ++c) {
@@ -451,6 +457,7 @@ __global__ __launch_bounds__(kThreads, 2) void MatMulMfmaKernel(const uint8_t* _
   }
 
   // D[i][j]: j = lane % 32 (weight row), i = (r % 4) + 8 (r / 4) + 4 (lane / 32) (token)
+  float* dst = partial != nullptr ? partial + static_cast<int64_t>(blockIdx.z) * n_tokens * rows : out;
 #pragma unroll
   for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
@@ -461,10 +468,20 @@ __global__ __launch_bounds__(kThreads, 2) void MatMulMfmaKernel(const uint8_t* _
 #pragma unroll
       for (int nt = 0; nt < 2; ++nt) {
         const int64_t row = r0 + 64 * wn + 32 * nt + li;
-        if (row < rows) out[tok * rows + row] = acc[mt][nt][i] * inv;
+        if (row < rows) dst[tok * rows + row] = acc[mt][nt][i] * inv;
       }
     }
   }
+}
+
+// out[e] = sum over z = 0 .. splits - 1 of partial[z][e], in that order.
+__global__ __launch_bounds__(kThreads) void MatMulSplitReduceKernel(const float* __restrict__ partial, int64_t elems,
+                                                                     int32_t splits, float* __restrict__ out) {
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (e >= elems) return;
+  float v = partial[e];
+  for (int32_t z = 1; z < splits; ++z) v += partial[z * elems + e];
+  out[e] = v;
 }
 
 }  // namespace
@@ -504,6 +521,29 @@ void* EnsureSplitBuffer(size_t bytes) {
   return b.ptr;
 }
 
+SplitBuffer& PartialTiles() {
+  static SplitBuffer* b = new SplitBuffer();
+  return *b;
+}
+
+// Grow-only buffer of the K-slices' partial tiles (same policy as the split buffer).
+void* EnsurePartialTiles(size_t bytes) {
+  SplitBuffer& b = PartialTiles();
+  std::lock_guard<std::mutex> lock(b.mu);
+  if (b.bytes < bytes) {
+    RPG_CHECK(!StreamIsCapturing(),
+              "the prefill matmul needs a %zu-byte partial-tile buffer (have %zu), which cannot be allocated during "
+              "graph capture; run the same shape once before capturing",
+              bytes, b.bytes);
+    const size_t grow = bytes > 2 * b.bytes ? bytes : 2 * b.bytes;
+    void* p = nullptr;
+    RPG_HIP_CHECK(hipMalloc(&p, grow));
+    b.ptr = p;  // the previous buffer stays allocated
+    b.bytes = grow;
+  }
+  return b.ptr;
+}
+
 }  // namespace
 
 SplitActivations SplitForMfma(const float* x, int64_t n_tokens, int64_t cols) {
@@ -530,7 +570,11 @@ SplitActivations SplitForMfma(const float* x, int64_t n_tokens, int64_t cols) {
 
 // Launched by GpuMatMulQuantRaw / GpuMatMulQuantGroup for Q4_K / Q6_K with
 // enough tokens; the caller has checked the type, the alignment (Q4_K 16 bytes,
-// Q6_K 2 bytes) and cols % 256 == 0, and split the activations.
+// Q6_K 2 bytes) and cols % 256 == 0, and split the activations. When the output
+// tiles cannot give every CU a workgroup, K is divided
+// into slices of whole blocks whose partial tiles are summed afterwards in a
+// fixed order (deterministic). Between one and two workgroups per CU the
+// extra pass costs more than the second workgroup slot gains.
 void LaunchMatMulMfmaSplit(uint32_t type, const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb,
                            const SplitActivations& sa, float* out) {
   const int64_t gy = (sa.n_tokens + kTileT - 1) / kTileT;
@@ -539,15 +583,28 @@ void LaunchMatMulMfmaSplit(uint32_t type, const uint8_t* w, int64_t rows, int64_
             static_cast<long long>(gy));
   RPG_CHECK(static_cast<int64_t>(nb) * kQK_K == sa.cols, "split activations have %lld columns, the matrix %lld",
             static_cast<long long>(sa.cols), static_cast<long long>(nb) * kQK_K);
-  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy));
+  constexpr int64_t kFill = 256;
+  const int64_t tiles = gx * gy;
+  int64_t want = tiles >= kFill ? 1 : (kFill + tiles - 1) / tiles;
+  if (want > nb) want = nb;
+  const int32_t bps = static_cast<int32_t>((nb + want - 1) / want);
+  const int32_t splits = static_cast<int32_t>((nb + bps - 1) / bps);
+  float* partial = nullptr;
+  const int64_t elems = sa.n_tokens * rows;
+  if (splits > 1) partial = static_cast<float*>(EnsurePartialTiles(static_cast<size_t>(splits) * elems * sizeof(float)));
+  const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy), static_cast<unsigned>(splits));
   const _Float16* planes = static_cast<const _Float16*>(sa.planes);
   const _Float16* sums = static_cast<const _Float16*>(sa.sums);
   if (type == kGgmlQ4_K) {
     Launch("MatMulMfmaQ4KKernel", MatMulMfmaKernel<kGgmlQ4_K>, grid, dim3(kThreads), w, rows, row_bytes, nb, planes,
-           sums, sa.sum_stride, sa.inv_scale, sa.cols, sa.n_tokens, out);
+           sums, sa.sum_stride, sa.inv_scale, sa.cols, sa.n_tokens, bps, out, partial);
   } else {
     Launch("MatMulMfmaQ6KKernel", MatMulMfmaKernel<kGgmlQ6_K>, grid, dim3(kThreads), w, rows, row_bytes, nb, planes,
-           sums, sa.sum_stride, sa.inv_scale, sa.cols, sa.n_tokens, out);
+           sums, sa.sum_stride, sa.inv_scale, sa.cols, sa.n_tokens, bps, out, partial);
+  }
+  if (splits > 1) {
+    Launch("MatMulSplitReduceKernel", MatMulSplitReduceKernel, dim3(GridFor(elems, kThreads)), dim3(kThreads),
+           static_cast<const float*>(partial), elems, splits, out);
   }
 }
 

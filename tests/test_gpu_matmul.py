@@ -99,6 +99,9 @@ SHAPES = [
     (14, 777, 6144, 129),    # 24 blocks per row, ragged both ways
     (14, 128, 256, 32),      # the smallest matrix-core case
     (12, 64, 512, 31),       # just below it: the tiled kernel
+    (12, 6144, 2048, 17),    # wide matrix: matrix cores from 16 tokens, K split 8 ways
+    (14, 4096, 2560, 16),    # ... Q6_K, 10 blocks per row split one each
+    (12, 4095, 2048, 16),    # one row short of wide: the tiled kernel
 ]
 
 
