@@ -422,11 +422,14 @@ def measure_matmul_decode_grouped(torch, ops, reps, span):
 
 def measure_matmul_prefill(torch, ops, n=N_PREFILL, reps=3):
     """GpuMatMulQuant at prefill size (n = 2811) on the Qwen3-1.7B layer matrices:
-    the matrix-core GEMM. Reported as useful TFLOP/s (2 n rows cols) against
-    MI355X's dense bf16 peak; the kernel issues three bf16 products per fp32
-    multiply-add (the activations are split into three bf16 terms)."""
+    the matrix-core GEMM. Each matrix alone (its own activation split), then the
+    layer as the forward runs it (GpuMatMulQuantGroup: q / k / v and gate / up
+    share one split). Reported as useful TFLOP/s (2 n rows cols) against
+    MI355X's dense fp16 peak; the matrix cores execute 2x that for Q4_K (two
+    fp16 activation terms) and 4x for Q6_K (two weight terms as well)."""
     res = {}
     layer_us = 0.0
+    mats = {}
     for name, t, rows, cols in DECODE_MATRICES:
         rb = (cols // 256) * (144 if t == 12 else 210)
         gen = torch.Generator(device="cuda")
@@ -441,6 +444,7 @@ def measure_matmul_prefill(torch, ops, n=N_PREFILL, reps=3):
         x = torch.randn((n, cols), dtype=torch.float32, device="cuda", generator=gen)
         out = torch.empty((n, rows), dtype=torch.float32, device="cuda")
         mat = ops.GpuTensor(blob, t, rows, cols)
+        mats[name] = (mat, blob, x, out)
         ops.GpuMatMulQuant(mat, x, n, out)
         torch.cuda.synchronize()
         ops.profile_start(4 * reps)
@@ -454,14 +458,33 @@ def measure_matmul_prefill(torch, ops, n=N_PREFILL, reps=3):
                      "TFLOPs": round(flops / us / 1e6, 1),
                      "kernels": {kn: round(k["avg_us"], 1) for kn, k in rep.items()}}
         layer_us += us
-        del blob, blocks, x, out, mat
-        torch.cuda.empty_cache()
+    groups = (("attn_q", "attn_k", "attn_v"), ("attn_output",), ("ffn_gate", "ffn_up"), ("ffn_down",))
+
+    def layer():
+        for g in groups:
+            x = mats[g[0]][2]
+            ops.GpuMatMulQuantGroup([mats[k][0] for k in g], x, n, [mats[k][3] for k in g])
+
+    layer()
+    torch.cuda.synchronize()
+    ops.profile_start(32 * reps)
+    for _ in range(reps):
+        layer()
+    ops.profile_stop()
+    rep = ops.profile_report()
+    grouped_us = sum(k["total_us"] for k in rep.values()) / reps
+    del mats
+    torch.cuda.empty_cache()
     total_flops = sum(2.0 * n * r * c for _, _, r, c in DECODE_MATRICES)
-    return {"n_tokens": n, "matrices": res, "layer_us": round(layer_us, 1),
-            "layer_TFLOPs": round(total_flops / layer_us / 1e6, 1),
+    return {"n_tokens": n, "matrices": res, "layer_us": round(grouped_us, 1),
+            "layer_TFLOPs": round(total_flops / grouped_us / 1e6, 1),
+            "layer_us_matrix_by_matrix": round(layer_us, 1),
+            "layer_kernels": {kn: {"count": k["count"] // reps, "avg_us": round(k["avg_us"], 1)}
+                              for kn, k in rep.items()},
             "roofline": {"bound": "mfma", "peak": 2500.0, "unit": "TFLOP/s",
-                         "note": "useful fp32-accurate TFLOP/s; the bf16 matrix cores execute 3x that (three "
-                                 "activation terms)"}}
+                         "note": "useful fp32-accurate TFLOP/s against the dense fp16 peak; the matrix cores "
+                                 "execute 2x that for Q4_K (two fp16 activation terms) and 4x for Q6_K (even / odd "
+                                 "scale parts as well)"}}
 
 
 def measure_attention(torch, ops, reps=20):
@@ -731,6 +754,16 @@ def cpu_baseline():
                              "restatement, one thread"}
 
 
+# Secondary measurements that --only can run alone.
+SECTIONS = {
+    "model_e2e": lambda torch, ops: measure_model_e2e(torch, ops),
+    "matmul_prefill_n2811": lambda torch, ops: measure_matmul_prefill(torch, ops),
+    "matmul_decode_n1": lambda torch, ops: measure_matmul_decode(torch, ops),
+    "attention": lambda torch, ops: measure_attention(torch, ops),
+    "sampler": lambda torch, ops: measure_sampler(torch, ops),
+}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -738,6 +771,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extras", action="store_true", help="only the headline prefill workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", choices=sorted(SECTIONS), default=None,
+                    help="run one secondary measurement alone and print its JSON (for profiling runs); "
+                         "not the benchmark line")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -753,6 +789,9 @@ def main():
     ops.set_stream(torch.cuda.current_stream())
     ok, desc = ops.device_info()
     log(desc)
+    if args.only is not None:
+        print(json.dumps({args.only: SECTIONS[args.only](torch, ops)}), flush=True)
+        return
 
     tab = torch.from_numpy(ops.build_rope_table(D, THETA, MAX_SEQ)).cuda()
 

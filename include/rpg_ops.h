@@ -152,6 +152,15 @@ RPG_OPS_API int32_t rpg_op_matmul_quant_group(int32_t n, const uint32_t* types, 
                                               const int64_t* rows, int64_t cols, const float* x, int64_t n_tokens,
                                               float* const* outs);
 
+/* A layer's gate / up projections and SwiGLU: gate <- silu(x . w_gate^T) *
+ * (x . w_up^T), both matrices [rows][cols] of `type`; up is scratch. At n_tokens
+ * = 1 (<= 2048 columns) one launch forms the SwiGLU from each row pair's totals.
+ * Bit-identical to rpg_op_matmul_quant_group + rpg_op_silu_mul_inplace. No
+ * counterpart in the reference (src/qwen3_gpu.cu:104-106 makes three calls). */
+RPG_OPS_API int32_t rpg_op_matmul_quant_swiglu(uint32_t type, const uint8_t* w_gate, const uint8_t* w_up,
+                                               int64_t rows, int64_t cols, const float* x, int64_t n_tokens,
+                                               float* gate, float* up);
+
 /* ---------------------------------------------------------------- GGUF files and the device model
  * rpg_gguf: a parsed GGUF file (host only, no GPU needed). rpg_model: a qwen3
  * GGUF uploaded to the device (F32 / Q4_K / Q6_K tensors only): quantized

@@ -7,6 +7,7 @@
 #include <cstring>
 #include <exception>
 #include <new>
+#include <utility>
 #include <vector>
 
 #include "common.h"
@@ -526,6 +527,27 @@ int32_t rpg_op_sampler_warmup(void) {
 int32_t rpg_op_matmul_quant(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols, const float* x,
                             int64_t n_tokens, float* out) {
   return Guard([&] { rpg::GpuMatMulQuantRaw(type, w, rows, cols, x, n_tokens, out); });
+}
+
+int32_t rpg_op_matmul_quant_swiglu(uint32_t type, const uint8_t* w_gate, const uint8_t* w_up, int64_t rows,
+                                   int64_t cols, const float* x, int64_t n_tokens, float* gate, float* up) {
+  return Guard([&] {
+    RPG_CHECK(w_gate != nullptr && w_up != nullptr, "null weight pointer");
+    RPG_CHECK(rows > 0 && cols > 0, "invalid matrix shape [%lld, %lld]", static_cast<long long>(rows),
+              static_cast<long long>(cols));
+    const int64_t rb = rpg::TypeRowBytes(type, cols);
+    RPG_CHECK(rb > 0, "unsupported matrix type %u or width %lld", type, static_cast<long long>(cols));
+    rpg::GpuTensor g, u;
+    for (auto [t, p] : {std::pair<rpg::GpuTensor*, const uint8_t*>{&g, w_gate}, {&u, w_up}}) {
+      t->buf = rpg::DeviceBuffer::View(const_cast<uint8_t*>(p), static_cast<size_t>(rows * rb));
+      t->type = type;
+      t->matrix = true;
+      t->rows = rows;
+      t->cols = cols;
+      t->n_elements = rows * cols;
+    }
+    rpg::GpuMatMulQuantSwiGLU(g, u, x, n_tokens, gate, up);
+  });
 }
 
 int32_t rpg_op_matmul_quant_group(int32_t n, const uint32_t* types, const uint8_t* const* ws, const int64_t* rows,

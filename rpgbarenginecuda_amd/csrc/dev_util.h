@@ -133,6 +133,11 @@ __device__ __forceinline__ void StoreStreamHalf4(uint16_t* p, uint2 v) {
   __builtin_nontemporal_store(w, reinterpret_cast<U32x2*>(p));
 }
 
+// SwiGLU element (src/kernels_gpu.cu:868): silu(g) * u = (g / (1 + e^-g)) * u,
+// IEEE division. Shared by SiluMulKernel and the gate / up matvec that applies
+// it to its two row totals, so both produce the same bits.
+__device__ __forceinline__ float SiluMul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+
 }  // namespace dev
 }  // namespace rpg
 

@@ -30,7 +30,7 @@ constexpr int kBlock = 512;
 
 bool Aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-__device__ __forceinline__ float SiluMul(float g, float u) { return (g / (1.0f + expf(-g))) * u; }
+using dev::SiluMul;
 
 __global__ __launch_bounds__(kBlock) void SiluMulKernel(float* gate, const float* __restrict__ up, int64_t n4,
                                                         int64_t n) {

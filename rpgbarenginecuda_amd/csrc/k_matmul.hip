@@ -458,7 +458,11 @@ __device__ __forceinline__ int SegOf(const MatSegs& sg, int64_t r) {
 // Each lane keeps the activations of its NX block groups in registers (rows of
 // up to 8 * NX blocks; used for NX == 1). Rows run over all segments; a row
 // group of RI rows never straddles two (segment sizes are multiples of RI).
-template <uint32_t kType, int NX, int RI>
+// kPaired (RI == 2): the layer's gate / up pair. Virtual rows 2p and 2p + 1 are
+// row p of w[0] (gate) and of w[1] (up), and out[0][p] = silu(gate) * up, the
+// SwiGLU formed from the two row totals (each total the same bits as an
+// unpaired launch computes for that row).
+template <uint32_t kType, int NX, int RI, bool kPaired = false>
 __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int32_t n_seg, int64_t row_bytes, int32_t nb,
                                                               const float* __restrict__ x) {
   constexpr int64_t kBB = BlockBytesOf<kType>::value;
@@ -491,6 +495,16 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int32_
 
   // Rows past the end are clamped to the last row (loads stay in bounds; results are dropped).
   auto load = [&](int64_t base_row, LaneBytes (&lb)[RI][NX]) {
+    if (kPaired) {
+      const int64_t p = (base_row < rows ? base_row : rows - 2) >> 1;
+#pragma unroll
+      for (int r = 0; r < RI; ++r) {
+        const uint8_t* rp = sg.w[r] + p * row_bytes;
+#pragma unroll
+        for (int it = 0; it < NX; ++it) lb[r][it] = LoadLaneBytes<kType>(rp + lane_off[it], s);
+      }
+      return;
+    }
     const int sgi = SegOf(sg, base_row);
     const uint8_t* wseg = sg.w[sgi];
     const int64_t first = sgi == 0 ? 0 : sg.end[sgi - 1];
@@ -519,10 +533,17 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int32_
       }
     }
     const float total = ReduceRows<RI>(acc, lane);
-    const int rr = ReducedRow<RI>(lane);
-    const int sgi = SegOf(sg, r0);
-    const int64_t first = sgi == 0 ? 0 : sg.end[sgi - 1];
-    if ((lane & 15) == 0 && lane < 16 * RI && r0 + rr < rows) sg.out[sgi][r0 - first + rr] = total;
+    if (kPaired) {
+      // lanes 0 and 16 hold the gate and up totals of pair r0 / 2
+      const float g = __shfl(total, 0, 64);
+      const float u = __shfl(total, 16, 64);
+      if (lane == 0) sg.out[0][r0 >> 1] = dev::SiluMul(g, u);
+    } else {
+      const int rr = ReducedRow<RI>(lane);
+      const int sgi = SegOf(sg, r0);
+      const int64_t first = sgi == 0 ? 0 : sg.end[sgi - 1];
+      if ((lane & 15) == 0 && lane < 16 * RI && r0 + rr < rows) sg.out[sgi][r0 - first + rr] = total;
+    }
 #pragma unroll
     for (int r = 0; r < RI; ++r)
 #pragma unroll
@@ -649,13 +670,13 @@ void LaunchQuant(const char* name, const uint8_t* w, int64_t rows, int64_t row_b
 // or more), at most kDecodeGrid workgroups (16 waves per CU).
 constexpr int64_t kDecodeGrid = 1024;
 
-template <uint32_t kType, int RI>
+template <uint32_t kType, int RI, bool kPaired = false>
 void LaunchDecodeSegs(const char* name, const MatSegs& sg, int32_t n_seg, int64_t row_bytes, int32_t nb,
                       const float* x) {
   const int64_t rows = sg.end[n_seg - 1];
   const int64_t need = (rows + kWavesPerBlock * RI - 1) / (kWavesPerBlock * RI);
   const unsigned grid = static_cast<unsigned>(need < kDecodeGrid ? need : kDecodeGrid);
-  Launch(name, MatVecQuantKernel<kType, 1, RI>, dim3(grid), dim3(kMmBlock), sg, n_seg, row_bytes, nb, x);
+  Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired>, dim3(grid), dim3(kMmBlock), sg, n_seg, row_bytes, nb, x);
 }
 
 MatSegs OneSeg(const uint8_t* w, int64_t rows, float* out) {
@@ -831,6 +852,45 @@ void GpuMatMulQuantGroup(const GpuTensor* const* ws, int32_t n_mats, const float
     }
     i = j;
   }
+}
+
+void GpuMatMulQuantSwiGLU(const GpuTensor& w_gate, const GpuTensor& w_up, const float* x_dev, int64_t n_tokens,
+                          float* gate_dev, float* up_dev) {
+  RPG_CHECK(w_gate.matrix && w_gate.valid() && w_up.matrix && w_up.valid(),
+            "GpuMatMulQuantSwiGLU got a non-matrix or empty tensor");
+  RPG_CHECK(w_gate.rows == w_up.rows && w_gate.cols == w_up.cols,
+            "gate [%lld, %lld] and up [%lld, %lld] must have the same shape", static_cast<long long>(w_gate.rows),
+            static_cast<long long>(w_gate.cols), static_cast<long long>(w_up.rows), static_cast<long long>(w_up.cols));
+  RPG_CHECK(n_tokens > 0, "n_tokens must be positive");
+  RPG_CHECK(x_dev != nullptr && gate_dev != nullptr && up_dev != nullptr, "GpuMatMulQuantSwiGLU got a null pointer");
+  const int64_t cols = w_gate.cols;
+  const uint32_t type = w_gate.type;
+  const bool q4 = type == kGgmlQ4_K, q6 = type == kGgmlQ6_K;
+  const uint8_t* wg = static_cast<const uint8_t*>(w_gate.buf.data());
+  const uint8_t* wu = static_cast<const uint8_t*>(w_up.buf.data());
+  if (n_tokens == 1 && w_up.type == type && (q4 || q6) && Aligned(x_dev, 16) && cols % kQK_K == 0 &&
+      cols / kQK_K <= kGroups && Aligned(wg, q4 ? 16 : 2) && Aligned(wu, q4 ? 16 : 2) &&
+      w_gate.buf.size() == static_cast<size_t>(w_gate.rows * w_gate.row_bytes()) &&
+      w_up.buf.size() == static_cast<size_t>(w_up.rows * w_up.row_bytes())) {
+    MatSegs sg{};
+    for (int i = 0; i < kMaxSegs; ++i) sg.end[i] = INT64_MAX;
+    sg.w[0] = wg;
+    sg.w[1] = wu;
+    sg.out[0] = gate_dev;
+    sg.end[0] = 2 * w_gate.rows;  // virtual rows: (gate p, up p) pairs
+    const int32_t nb = static_cast<int32_t>(cols / kQK_K);
+    const int64_t row_bytes = TypeRowBytes(type, cols);
+    if (q4) {
+      LaunchDecodeSegs<kGgmlQ4_K, 2, true>("MatVecSwiGLUQ4KKernel", sg, 1, row_bytes, nb, x_dev);
+    } else {
+      LaunchDecodeSegs<kGgmlQ6_K, 2, true>("MatVecSwiGLUQ6KKernel", sg, 1, row_bytes, nb, x_dev);
+    }
+    return;
+  }
+  const GpuTensor* mats[2] = {&w_gate, &w_up};
+  float* outs[2] = {gate_dev, up_dev};
+  GpuMatMulQuantGroup(mats, 2, x_dev, n_tokens, outs);
+  GpuSiluMulInPlace(gate_dev, up_dev, n_tokens * w_gate.rows);
 }
 
 void GpuMatMulQuant(const GpuTensor& w, const float* X_dev, int64_t n_tokens, float* OUT_dev) {

@@ -215,11 +215,22 @@ void GpuMatMulQuant(const GpuTensor& w, const float* X_dev, int64_t n_tokens, fl
 
 // GpuMatMulQuant over several matrices that read the same X (a layer's q / k / v,
 // or gate / up): OUT_i = X . W_i^T. At n_tokens = 1, each run of consecutive
-// same-type matrices (up to 4) is decoded in one launch, with every output
-// bit-identical to its own GpuMatMulQuant call; otherwise one call per matrix.
-// No counterpart in the reference (which launches once per matrix).
+// same-type matrices (up to 4) is decoded in one launch; on the matrix-core path
+// X is split once for all the matrices; otherwise one call per matrix. Every
+// output is bit-identical to its own GpuMatMulQuant call. No counterpart in the
+// reference (which launches once per matrix).
 void GpuMatMulQuantGroup(const GpuTensor* const* ws, int32_t n_mats, const float* X_dev, int64_t n_tokens,
                          float* const* OUTs);
+
+// The layer's gate / up projections and SwiGLU (src/qwen3_gpu.cu:104-106):
+// gate <- silu(X . W_gate^T) * (X . W_up^T); up is scratch (it holds X . W_up^T
+// after a multi-token call, and is left untouched at one token). At one token on
+// same-type matrices of <= 2048 columns it is one launch: each wave computes
+// row p of both matrices and writes the SwiGLU of the two totals. Bit-identical
+// to GpuMatMulQuantGroup({gate, up}) + GpuSiluMulInPlace. No counterpart in the
+// reference.
+void GpuMatMulQuantSwiGLU(const GpuTensor& w_gate, const GpuTensor& w_up, const float* X_dev, int64_t n_tokens,
+                          float* gate_dev, float* up_dev);
 
 // The same on a raw (non-owning) weight pointer; GpuMatMulQuant forwards here.
 void GpuMatMulQuantRaw(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_t cols, const float* x_dev,

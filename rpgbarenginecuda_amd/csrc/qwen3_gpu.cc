@@ -95,12 +95,7 @@ void ForwardLayer(const GpuModel& m, int32_t layer, int64_t pos0, GpuScratch* s,
   res->Defer();
 
   res->NormInto(static_cast<const float*>(w.ffn_norm.buf.data()));
-  {
-    const GpuTensor* mats[2] = {&w.ffn_gate, &w.ffn_up};
-    float* outs[2] = {F(s->gate), F(s->up)};
-    GpuMatMulQuantGroup(mats, 2, h, seq, outs);
-  }
-  GpuSiluMulInPlace(F(s->gate), F(s->up), seq * c.intermediate);
+  GpuMatMulQuantSwiGLU(w.ffn_gate, w.ffn_up, h, seq, F(s->gate), F(s->up));  // gate <- silu(gate) * up
   GpuMatMulQuant(w.ffn_down, F(s->gate), seq, F(s->proj));
   res->Defer();
 }

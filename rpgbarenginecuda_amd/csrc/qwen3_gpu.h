@@ -17,8 +17,10 @@
 //     the output norm), so x is read and written once per sub-layer;
 //   * q / k RMSNorm, RoPE and the fp16 K/V store run as one pass
 //     (GpuQkNormRopeKv) on the cache path;
-//   * q / k / v and gate / up go through GpuMatMulQuantGroup (at one token one
-//     launch per same-type run, bit-identical to separate calls);
+//   * q / k / v go through GpuMatMulQuantGroup (at one token one launch per
+//     same-type run, bit-identical to separate calls), and gate / up with the
+//     SwiGLU through GpuMatMulQuantSwiGLU (at one token one launch that writes
+//     silu(gate) * up from each row pair's totals);
 //   * the decode graph reads the sampled token straight from the sampler's
 //     output slot instead of copying it into the token buffer first.
 // The no-cache path keeps the reference's separate norm / RoPE steps and runs

@@ -64,6 +64,7 @@ SIGNATURES = {
     "rpg_forward_step_dev": (_i32, [_vp, _vp, _i64, _vp, _vp]),
     "rpg_generate": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp]),
     "rpg_op_matmul_quant_group": (_i32, [_i32, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
+    "rpg_op_matmul_quant_swiglu": (_i32, [_u32, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp]),
     "rpg_op_argmax": (_i32, [_vp, _i64, _vp]),
     "rpg_sample_split_mix64": (ctypes.c_uint64, [ctypes.c_uint64]),
     "rpg_sample_counter_rng": (ctypes.c_uint64, [ctypes.c_uint64, ctypes.c_uint64]),
@@ -311,8 +312,23 @@ def GpuMatMulQuant(w: GpuTensor, x, n_tokens: int, out) -> None:
         _addr(out, 4 * n_tokens * w.rows, torch.float32, "out")))
 
 
+def GpuMatMulQuantSwiGLU(w_gate: GpuTensor, w_up: GpuTensor, x, n_tokens: int, gate, up) -> None:
+    """gate <- silu(x . W_gate^T) * (x . W_up^T), up is scratch (the layer's gate / up + SwiGLU; no reference
+    counterpart). Bit-identical to GpuMatMulQuantGroup + GpuSiluMulInPlace."""
+    torch = _t()
+    if (w_gate.type, w_gate.rows, w_gate.cols) != (w_up.type, w_up.rows, w_up.cols):
+        raise RpgError("GpuMatMulQuantSwiGLU: gate and up must have the same type and shape")
+    nbytes = w_gate.rows * w_gate.row_bytes()
+    no = 4 * n_tokens * w_gate.rows
+    _check(load_library().rpg_op_matmul_quant_swiglu(
+        w_gate.type, _addr(w_gate.buf, nbytes, name="w_gate"), _addr(w_up.buf, nbytes, name="w_up"), w_gate.rows,
+        w_gate.cols, _addr(x, 4 * n_tokens * w_gate.cols, torch.float32, "x"), n_tokens,
+        _addr(gate, no, torch.float32, "gate"), _addr(up, no, torch.float32, "up")))
+
+
 def GpuMatMulQuantGroup(ws: list, x, n_tokens: int, outs: list) -> None:
-    """OUT_i = X . W_i^T for matrices sharing X, same-type runs fused at n = 1 (no reference counterpart)."""
+    """OUT_i = X . W_i^T for matrices sharing X (no reference counterpart): same-type runs fused at n = 1, one
+    activation split for all matrices on the matrix-core path; outputs bit-identical to GpuMatMulQuant calls."""
     torch = _t()
     n = len(ws)
     if n == 0 or n != len(outs):

@@ -242,6 +242,38 @@ def test_matmul_group_equals_separate_calls(gpu, ora, label, mats, cols, n):
         check(host(o), exact, absdot, cols, factored_magnitude(ora, t, w, rows, cols, x))
 
 
+SWIGLU = [
+    (12, 6144, 2048, 1),   # Qwen3-1.7B gate / up (Q4_K): one paired launch
+    (14, 6144, 2048, 1),   # the same in Q6_K
+    (12, 9728, 2560, 1),   # Qwen3-4B: 10 blocks per row, not a paired shape
+    (12, 300, 512, 1),     # small paired shape, ragged last wave
+    (12, 6144, 2048, 3),   # several tokens: group matmul, then SwiGLU
+    (12, 6144, 2048, 40),  # the matrix-core path
+]
+
+
+@pytest.mark.parametrize("t,rows,cols,n", SWIGLU)
+def test_matmul_swiglu_equals_group_then_silu(gpu, t, rows, cols, n):
+    """GpuMatMulQuantSwiGLU: gate bit-identical to GpuMatMulQuantGroup({gate, up})
+    followed by GpuSiluMulInPlace (the paired kernel forms each row pair's totals
+    exactly as the unpaired kernel does, and the same SwiGLU expression)."""
+    import torch
+
+    case(f"matmul swiglu type={t} rows={rows} cols={cols} n={n}")
+    rng = np.random.default_rng(1300 + rows + cols + n + t)
+    wg = gpu.GpuTensor(dev(synth.quant_table(rng, t, rows, cols)), t, rows, cols)
+    wu = gpu.GpuTensor(dev(synth.quant_table(rng, t, rows, cols)), t, rows, cols)
+    x = dev(rng.normal(0, 1, (n, cols)).astype(np.float32))
+    g1 = torch.full((n, rows), np.nan, dtype=torch.float32, device="cuda")
+    u1 = torch.full_like(g1, np.nan)
+    gpu.GpuMatMulQuantGroup([wg, wu], x, n, [g1, u1])
+    gpu.GpuSiluMulInPlace(g1, u1, n * rows)
+    g2 = torch.full_like(g1, np.nan)
+    u2 = torch.full_like(g1, np.nan)
+    gpu.GpuMatMulQuantSwiGLU(wg, wu, x, n, g2, u2)
+    assert torch.equal(g2, g1)
+
+
 def test_matmul_group_rejects_mixed_widths(gpu):
     import torch
 
