@@ -771,6 +771,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-extras", action="store_true", help="only the headline prefill workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-model", action="store_true",
+                    help="skip the whole-model measurement (~1M kernel launches; for kernel-trace runs)")
     ap.add_argument("--only", choices=sorted(SECTIONS), default=None,
                     help="run one secondary measurement alone and print its JSON (for profiling runs); "
                          "not the benchmark line")
@@ -848,8 +850,9 @@ def main():
         extras["attention"] = measure_attention(torch, ops)
         log("argmax / sampler over the 151936-entry vocabulary")
         extras["sampler"] = measure_sampler(torch, ops)
-        log("whole model: Qwen3-1.7B prefill and decode through rpg_forward / rpg_generate")
-        extras["model_e2e"] = measure_model_e2e(torch, ops)
+        if not args.no_model:
+            log("whole model: Qwen3-1.7B prefill and decode through rpg_forward / rpg_generate")
+            extras["model_e2e"] = measure_model_e2e(torch, ops)
         log("GGUF upload (Qwen3-1.7B-shaped file)")
         extras["gguf_upload"] = measure_gguf_upload(torch, ops)
         log("gather Q4_K / Q6_K")

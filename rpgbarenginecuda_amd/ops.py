@@ -620,7 +620,7 @@ def GpuForwardStepDev(m: GpuModel, token_dev, pos: int, kv: GpuKvCache, s: GpuSc
                                                s._h))
 
 
-class _GenerateOptsC(ctypes.Structure):
+class GenerateOptsC(ctypes.Structure):
     _fields_ = [("max_tokens", ctypes.c_int32), ("stop_ids", ctypes.c_void_p), ("n_stop", ctypes.c_int32),
                 ("temperature", ctypes.c_float), ("top_k", ctypes.c_int32), ("top_p", ctypes.c_float),
                 ("seed", ctypes.c_uint64), ("use_graph", ctypes.c_int32), ("step_logits", ctypes.c_void_p),
@@ -650,7 +650,7 @@ def GpuGenerate(m: GpuModel, kv: GpuKvCache, s: GpuScratch, first_logits_dev, op
     stops = np.asarray(opt.stop_ids, dtype=np.int32)
     out = np.empty(max(opt.max_tokens, 1), np.int32)
     steps = np.empty((max(opt.max_tokens, 1), vocab), np.float32) if opt.step_logits else None
-    c = _GenerateOptsC(opt.max_tokens, stops.ctypes.data if stops.size else None, int(stops.size),
+    c = GenerateOptsC(opt.max_tokens, stops.ctypes.data if stops.size else None, int(stops.size),
                        opt.sample.temperature, opt.sample.top_k, opt.sample.top_p, opt.seed & (2 ** 64 - 1),
                        int(opt.use_graph), steps.ctypes.data if steps is not None else None,
                        steps.size if steps is not None else 0)
