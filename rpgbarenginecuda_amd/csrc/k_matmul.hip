@@ -448,6 +448,8 @@ struct MatSegs {
   const uint8_t* w[kMaxSegs];
   float* out[kMaxSegs];
   int64_t end[kMaxSegs];
+  uint32_t b_mask;      // segments of the kernel's second type (bit i: segment i)
+  int64_t row_bytes_b;  // row bytes of those segments
 };
 
 // Segment of global row r (uniform over the wave, so scalar).
@@ -462,10 +464,17 @@ __device__ __forceinline__ int SegOf(const MatSegs& sg, int64_t r) {
 // row p of w[0] (gate) and of w[1] (up), and out[0][p] = silu(gate) * up, the
 // SwiGLU formed from the two row totals (each total the same bits as an
 // unpaired launch computes for that row).
-template <uint32_t kType, int NX, int RI, bool kPaired = false>
+// kTypeB != kType: segments in sg.b_mask are matrices of kTypeB (a layer's
+// Q6_K attn_v beside its Q4_K q / k in Q4_K_M files). Each lane then holds its
+// activations in both types' lane orders, and a row pair takes the path of its
+// segment's type (uniform over the wave): every row the same bits as a launch
+// of its own type.
+template <uint32_t kType, int NX, int RI, bool kPaired = false, uint32_t kTypeB = kType>
 __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int32_t n_seg, int64_t row_bytes, int32_t nb,
                                                               const float* __restrict__ x) {
   constexpr int64_t kBB = BlockBytesOf<kType>::value;
+  constexpr bool kMixed = kTypeB != kType;
+  constexpr int64_t kBBB = BlockBytesOf<kTypeB>::value;
   const int lane = threadIdx.x & 63;
   const int c = lane / kGroupLanes;
   const int s = lane % kGroupLanes;
@@ -480,6 +489,9 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int32_
   float xv[NX][32];
   float sx[NX][2];
   int64_t lane_off[NX];  // byte offset of this lane's block inside a row (clamped to the last block)
+  float xvb[kMixed ? NX : 1][32];  // the same activations in kTypeB's lane order
+  float sxb[kMixed ? NX : 1][2];
+  int64_t lane_off_b[kMixed ? NX : 1];
 #pragma unroll
   for (int it = 0; it < NX; ++it) {
     const int b = c + kGroups * it;
@@ -491,6 +503,16 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int32_
       for (int i = 0; i < 32; ++i) xv[it][i] = 0.0f;
     }
     RunSums(xv[it], sx[it]);
+    if (kMixed) {
+      lane_off_b[it] = static_cast<int64_t>(b < nb ? b : nb - 1) * kBBB;
+      if (b < nb) {
+        LoadLaneX<kTypeB>(x, static_cast<int64_t>(b) * kQK_K, s, xvb[it]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) xvb[it][i] = 0.0f;
+      }
+      RunSums(xvb[it], sxb[it]);
+    }
   }
 
   // Rows past the end are clamped to the last row (loads stay in bounds; results are dropped).
@@ -508,6 +530,16 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int32_
     const int sgi = SegOf(sg, base_row);
     const uint8_t* wseg = sg.w[sgi];
     const int64_t first = sgi == 0 ? 0 : sg.end[sgi - 1];
+    if (kMixed && ((sg.b_mask >> sgi) & 1u)) {
+#pragma unroll
+      for (int r = 0; r < RI; ++r) {
+        const int64_t row = base_row + r < rows ? base_row + r : rows - 1;
+        const uint8_t* rp = wseg + (row - first) * sg.row_bytes_b;
+#pragma unroll
+        for (int it = 0; it < NX; ++it) lb[r][it] = LoadLaneBytes<kTypeB>(rp + lane_off_b[it], s);
+      }
+      return;
+    }
 #pragma unroll
     for (int r = 0; r < RI; ++r) {
       const int64_t row = base_row + r < rows ? base_row + r : rows - 1;
@@ -525,11 +557,17 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int32_
     float acc[RI];
 #pragma unroll
     for (int r = 0; r < RI; ++r) acc[r] = 0.0f;
+    const bool row_b = kMixed && ((sg.b_mask >> SegOf(sg, r0)) & 1u);
 #pragma unroll
     for (int it = 0; it < NX; ++it) {
       if (c + kGroups * it < nb) {
+        if (row_b) {
 #pragma unroll
-        for (int r = 0; r < RI; ++r) acc[r] += BlockDot<kType>(cur[r][it], s, xv[it], sx[it]);
+          for (int r = 0; r < RI; ++r) acc[r] += BlockDot<kTypeB>(cur[r][it], s, xvb[it], sxb[it]);
+        } else {
+#pragma unroll
+          for (int r = 0; r < RI; ++r) acc[r] += BlockDot<kType>(cur[r][it], s, xv[it], sx[it]);
+        }
       }
     }
     const float total = ReduceRows<RI>(acc, lane);
@@ -670,13 +708,14 @@ void LaunchQuant(const char* name, const uint8_t* w, int64_t rows, int64_t row_b
 // or more), at most kDecodeGrid workgroups (16 waves per CU).
 constexpr int64_t kDecodeGrid = 1024;
 
-template <uint32_t kType, int RI, bool kPaired = false>
+template <uint32_t kType, int RI, bool kPaired = false, uint32_t kTypeB = kType>
 void LaunchDecodeSegs(const char* name, const MatSegs& sg, int32_t n_seg, int64_t row_bytes, int32_t nb,
                       const float* x) {
   const int64_t rows = sg.end[n_seg - 1];
   const int64_t need = (rows + kWavesPerBlock * RI - 1) / (kWavesPerBlock * RI);
   const unsigned grid = static_cast<unsigned>(need < kDecodeGrid ? need : kDecodeGrid);
-  Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired>, dim3(grid), dim3(kMmBlock), sg, n_seg, row_bytes, nb, x);
+  Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB>, dim3(grid), dim3(kMmBlock), sg, n_seg, row_bytes, nb,
+         x);
 }
 
 MatSegs OneSeg(const uint8_t* w, int64_t rows, float* out) {
@@ -817,6 +856,35 @@ void GpuMatMulQuantGroup(const GpuTensor* const* ws, int32_t n_mats, const float
   // anything else goes matrix by matrix.
   const int64_t nb = cols / kQK_K;
   const bool decode = n_tokens == 1 && Aligned(x_dev, 16) && cols % kQK_K == 0 && nb <= kGroups;
+  // Q4_K and Q6_K matrices together (a Q4_K_M layer's q, k and v): one launch
+  // when no Q4_K matrix needs its own 4-rows-per-wave shape.
+  if (decode && n_mats > 1 && n_mats <= kMaxSegs) {
+    bool ok = true, any4 = false, any6 = false;
+    int64_t total4 = 0;
+    for (int32_t k = 0; k < n_mats && ok; ++k) {
+      const bool q4 = ws[k]->type == kGgmlQ4_K, q6 = ws[k]->type == kGgmlQ6_K;
+      ok = (q4 || q6) && ws[k]->rows % 2 == 0 && Aligned(ws[k]->buf.data(), q4 ? 16 : 2);
+      any4 = any4 || q4;
+      any6 = any6 || q6;
+      if (q4) total4 += ws[k]->rows;
+    }
+    if (ok && any4 && any6 && total4 < 32768) {
+      MatSegs sg{};
+      for (int k = 0; k < kMaxSegs; ++k) sg.end[k] = INT64_MAX;
+      int64_t end = 0;
+      for (int32_t k = 0; k < n_mats; ++k) {
+        sg.w[k] = static_cast<const uint8_t*>(ws[k]->buf.data());
+        sg.out[k] = outs[k];
+        end += ws[k]->rows;
+        sg.end[k] = end;
+        if (ws[k]->type == kGgmlQ6_K) sg.b_mask |= 1u << k;
+      }
+      sg.row_bytes_b = TypeRowBytes(kGgmlQ6_K, cols);
+      LaunchDecodeSegs<kGgmlQ4_K, 2, false, kGgmlQ6_K>("MatVecQ4KQ6KKernel", sg, n_mats,
+                                                       TypeRowBytes(kGgmlQ4_K, cols), static_cast<int32_t>(nb), x_dev);
+      return;
+    }
+  }
   int32_t i = 0;
   while (i < n_mats) {
     const uint32_t type = ws[i]->type;

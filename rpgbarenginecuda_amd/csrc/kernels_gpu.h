@@ -214,8 +214,9 @@ void GpuAttentionWarmupShmem(int64_t sh_positions);
 void GpuMatMulQuant(const GpuTensor& w, const float* X_dev, int64_t n_tokens, float* OUT_dev);
 
 // GpuMatMulQuant over several matrices that read the same X (a layer's q / k / v,
-// or gate / up): OUT_i = X . W_i^T. At n_tokens = 1, each run of consecutive
-// same-type matrices (up to 4) is decoded in one launch; on the matrix-core path
+// or gate / up): OUT_i = X . W_i^T. At n_tokens = 1, up to 4 Q4_K / Q6_K
+// matrices (either type or both) are decoded in one launch, else each run of
+// consecutive same-type matrices is; on the matrix-core path
 // X is split once for all the matrices; otherwise one call per matrix. Every
 // output is bit-identical to its own GpuMatMulQuant call. No counterpart in the
 // reference (which launches once per matrix).

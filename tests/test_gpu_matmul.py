@@ -209,6 +209,8 @@ GROUPS = [
     ("gate/up", [(12, 6144), (12, 6144)], 2048, 1),
     ("four Q6_K", [(14, 256), (14, 512), (14, 130), (14, 1000)], 1024, 1),
     ("mixed runs", [(14, 300), (12, 200), (12, 128), (14, 64), (14, 64)], 512, 1),
+    ("Q6_K first, mixed launch", [(14, 300), (12, 200), (12, 128), (14, 64)], 512, 1),
+    ("mixed, one Q6_K of odd rows (not fused)", [(12, 256), (14, 7)], 256, 1),
     ("odd rows (not fused)", [(12, 1001), (12, 7)], 256, 1),
     ("Q4_K of 32768+ rows (own shape)", [(12, 20000), (12, 16000)], 256, 1),
     ("prefill (one call per matrix)", [(12, 256), (14, 128)], 512, 40),
