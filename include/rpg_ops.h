@@ -161,6 +161,29 @@ RPG_OPS_API int32_t rpg_op_matmul_quant_swiglu(uint32_t type, const uint8_t* w_g
                                                int64_t rows, int64_t cols, const float* x, int64_t n_tokens,
                                                float* gate, float* up);
 
+/* One token: v = x + d (d may be NULL: v = x), h = RMSNorm(v) * norm_w (the
+ * rpg_op_add_rms_norm maths) formed inside the matmul launches that read it,
+ * then out[i] = h . w[i]^T as rpg_op_matmul_quant_group. x_out (may be NULL)
+ * receives v, bit-exact; it must not alias x or d. x, d, norm_w, x_out hold
+ * cols floats, 16-byte aligned. *fused = 1 when launched; 0 when the group has
+ * no fused form (a matrix not Q4_K / Q6_K, cols > 2048), in which case nothing
+ * ran and the caller runs rpg_op_add_rms_norm + rpg_op_matmul_quant_group. h can
+ * differ from rpg_op_add_rms_norm's in the last fp32 bit (the double sum of
+ * squares is taken in another order). No counterpart in the reference
+ * (GpuVecAddInPlace, GpuRmsNorm and the matmuls are separate launches,
+ * src/qwen3_gpu.cu:69-76,100-104,168). */
+RPG_OPS_API int32_t rpg_op_norm_matmul_quant_group(int32_t n, const uint32_t* types, const uint8_t* const* ws,
+                                                   const int64_t* rows, int64_t cols, const float* x, const float* d,
+                                                   const float* norm_w, float eps, float* x_out, float* const* outs,
+                                                   int32_t* fused);
+
+/* The same in front of rpg_op_matmul_quant_swiglu (gate <- silu(h . w_gate^T) *
+ * (h . w_up^T); up is left untouched). No counterpart in the reference. */
+RPG_OPS_API int32_t rpg_op_norm_matmul_quant_swiglu(uint32_t type, const uint8_t* w_gate, const uint8_t* w_up,
+                                                    int64_t rows, int64_t cols, const float* x, const float* d,
+                                                    const float* norm_w, float eps, float* x_out, float* gate,
+                                                    float* up, int32_t* fused);
+
 /* ---------------------------------------------------------------- GGUF files and the device model
  * rpg_gguf: a parsed GGUF file (host only, no GPU needed). rpg_model: a qwen3
  * GGUF uploaded to the device (F32 / Q4_K / Q6_K tensors only): quantized

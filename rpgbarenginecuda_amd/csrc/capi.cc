@@ -550,25 +550,69 @@ int32_t rpg_op_matmul_quant_swiglu(uint32_t type, const uint8_t* w_gate, const u
   });
 }
 
+namespace {
+
+// Non-owning GpuTensor views of n matrices of one width (the group entry points).
+void GroupViews(int32_t n, const uint32_t* types, const uint8_t* const* ws, const int64_t* rows, int64_t cols,
+                std::vector<rpg::GpuTensor>* t, std::vector<const rpg::GpuTensor*>* p) {
+  RPG_CHECK(n > 0 && n <= 64 && types && ws && rows, "matmul group: bad arguments (n = %d)", n);
+  t->resize(static_cast<size_t>(n));
+  p->resize(static_cast<size_t>(n));
+  for (int32_t i = 0; i < n; ++i) {
+    RPG_CHECK(ws[i] != nullptr && rows[i] > 0 && cols > 0, "matmul group: matrix %d is empty", i);
+    const int64_t rb = rpg::TypeRowBytes(types[i], cols);
+    RPG_CHECK(rb > 0, "matmul group: unsupported type %u or width %lld", types[i], static_cast<long long>(cols));
+    rpg::GpuTensor& g = (*t)[static_cast<size_t>(i)];
+    g.type = types[i];
+    g.matrix = true;
+    g.rows = rows[i];
+    g.cols = cols;
+    g.n_elements = rows[i] * cols;
+    g.buf = rpg::DeviceBuffer::View(const_cast<uint8_t*>(ws[i]), static_cast<size_t>(rows[i] * rb));
+    (*p)[static_cast<size_t>(i)] = &g;
+  }
+}
+
+}  // namespace
+
 int32_t rpg_op_matmul_quant_group(int32_t n, const uint32_t* types, const uint8_t* const* ws, const int64_t* rows,
                                   int64_t cols, const float* x, int64_t n_tokens, float* const* outs) {
   return Guard([&] {
-    RPG_CHECK(n > 0 && n <= 64 && types && ws && rows && outs, "matmul group: bad arguments (n = %d)", n);
-    std::vector<rpg::GpuTensor> t(static_cast<size_t>(n));
-    std::vector<const rpg::GpuTensor*> p(static_cast<size_t>(n));
-    for (int32_t i = 0; i < n; ++i) {
-      RPG_CHECK(ws[i] != nullptr && rows[i] > 0 && cols > 0, "matmul group: matrix %d is empty", i);
-      rpg::GpuTensor& g = t[static_cast<size_t>(i)];
-      g.type = types[i];
-      g.matrix = true;
-      g.rows = rows[i];
-      g.cols = cols;
-      g.n_elements = rows[i] * cols;
-      g.buf = rpg::DeviceBuffer::View(const_cast<uint8_t*>(ws[i]),
-                                      static_cast<size_t>(rows[i] * rpg::TypeRowBytes(types[i], cols)));
-      p[static_cast<size_t>(i)] = &g;
-    }
+    RPG_CHECK(outs != nullptr, "matmul group: null output array");
+    std::vector<rpg::GpuTensor> t;
+    std::vector<const rpg::GpuTensor*> p;
+    GroupViews(n, types, ws, rows, cols, &t, &p);
     rpg::GpuMatMulQuantGroup(p.data(), n, x, n_tokens, outs);
+  });
+}
+
+int32_t rpg_op_norm_matmul_quant_group(int32_t n, const uint32_t* types, const uint8_t* const* ws,
+                                       const int64_t* rows, int64_t cols, const float* x, const float* d,
+                                       const float* norm_w, float eps, float* x_out, float* const* outs,
+                                       int32_t* fused) {
+  return Guard([&] {
+    RPG_CHECK(outs != nullptr && fused != nullptr, "norm matmul group: null output array or flag");
+    *fused = 0;
+    std::vector<rpg::GpuTensor> t;
+    std::vector<const rpg::GpuTensor*> p;
+    GroupViews(n, types, ws, rows, cols, &t, &p);
+    *fused = rpg::GpuNormMatMulQuantGroup(rpg::GpuNormIn{x, d, norm_w, eps, x_out}, p.data(), n, outs) ? 1 : 0;
+  });
+}
+
+int32_t rpg_op_norm_matmul_quant_swiglu(uint32_t type, const uint8_t* w_gate, const uint8_t* w_up, int64_t rows,
+                                        int64_t cols, const float* x, const float* d, const float* norm_w, float eps,
+                                        float* x_out, float* gate, float* up, int32_t* fused) {
+  return Guard([&] {
+    RPG_CHECK(fused != nullptr, "norm matmul swiglu: null flag");
+    *fused = 0;
+    const uint32_t types[2] = {type, type};
+    const uint8_t* ws[2] = {w_gate, w_up};
+    const int64_t rs[2] = {rows, rows};
+    std::vector<rpg::GpuTensor> t;
+    std::vector<const rpg::GpuTensor*> p;
+    GroupViews(2, types, ws, rs, cols, &t, &p);
+    *fused = rpg::GpuNormMatMulQuantSwiGLU(rpg::GpuNormIn{x, d, norm_w, eps, x_out}, t[0], t[1], gate, up) ? 1 : 0;
   });
 }
 

@@ -452,6 +452,17 @@ struct MatSegs {
   int64_t row_bytes_b;  // row bytes of those segments
 };
 
+// Residual + RMSNorm in front of a one-token matvec: the activations a wave
+// holds are h = RMSNorm(x + d) * w instead of x. d == nullptr: h = RMSNorm(x) * w.
+// x_out != nullptr: the first workgroup also writes x + d there (the updated residual
+// stream; it must not alias x or d, which other waves are still reading).
+struct NormPrologue {
+  const float* d;
+  const float* w;
+  float* x_out;
+  float eps;
+};
+
 // Segment of global row r (uniform over the wave, so scalar).
 __device__ __forceinline__ int SegOf(const MatSegs& sg, int64_t r) {
   return (r >= sg.end[0]) + (r >= sg.end[1]) + (r >= sg.end[2]);
@@ -469,9 +480,16 @@ __device__ __forceinline__ int SegOf(const MatSegs& sg, int64_t r) {
 // activations in both types' lane orders, and a row pair takes the path of its
 // segment's type (uniform over the wave): every row the same bits as a launch
 // of its own type.
-template <uint32_t kType, int NX, int RI, bool kPaired = false, uint32_t kTypeB = kType>
+// kNorm (rows of at most kGroups blocks): x is the residual stream and each
+// workgroup forms h = RMSNorm(x + nrm.d) * nrm.w itself, the GpuAddRmsNorm
+// maths (double sum of squares, float(1 / sqrt(ss / n + eps)), then
+// (v * scale) * w), before the dot products; the sum of squares is taken in
+// another order than GpuAddRmsNorm's, so the scale can differ from it in the
+// last bit of the double sum.
+template <uint32_t kType, int NX, int RI, bool kPaired = false, uint32_t kTypeB = kType, bool kNorm = false>
 __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int32_t n_seg, int64_t row_bytes, int32_t nb,
-                                                              const float* __restrict__ x) {
+                                                              const float* __restrict__ x, NormPrologue nrm) {
+  static_assert(!kNorm || NX == 1, "the norm prologue needs the whole row in one wave");
   constexpr int64_t kBB = BlockBytesOf<kType>::value;
   constexpr bool kMixed = kTypeB != kType;
   constexpr int64_t kBBB = BlockBytesOf<kTypeB>::value;
@@ -484,7 +502,7 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int32_
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kWavesPerBlock * RI;
   int64_t r0 = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(
                    static_cast<int>(blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6)))) * RI;
-  if (r0 >= rows) return;
+  if (!kNorm && r0 >= rows) return;
 
   float xv[NX][32];
   float sx[NX][2];
@@ -492,8 +510,65 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int32_
   float xvb[kMixed ? NX : 1][32];  // the same activations in kTypeB's lane order
   float sxb[kMixed ? NX : 1][2];
   int64_t lane_off_b[kMixed ? NX : 1];
+  if (kNorm) {
+    // The workgroup forms h once: each thread takes 4-float slices of the row,
+    // the sum of squares meets in LDS (waves added in a fixed order), and h is
+    // staged in LDS, from where each wave reads its lanes' elements.
+    __shared__ float hs[kGroups * kQK_K];
+    __shared__ double part[kWavesPerBlock];
+    const int n = nb * kQK_K;  // <= kGroups * kQK_K = 4 * kMmBlock * 2
+    float4 v[2], wv[2];
+    double ss = 0.0;
 #pragma unroll
-  for (int it = 0; it < NX; ++it) {
+    for (int j = 0; j < 2; ++j) {
+      const int i = 4 * static_cast<int>(threadIdx.x) + 4 * kMmBlock * j;
+      if (i < n) {
+        v[j] = dev::Load4(x + i);
+        if (nrm.d != nullptr) {
+          const float4 dd = dev::Load4(nrm.d + i);
+          v[j] = make_float4(v[j].x + dd.x, v[j].y + dd.y, v[j].z + dd.z, v[j].w + dd.w);
+        }
+        wv[j] = dev::Load4(nrm.w + i);
+        ss = dev::AddSquares(ss, v[j]);
+        if (nrm.x_out != nullptr && blockIdx.x == 0) dev::Store4(nrm.x_out + i, v[j]);
+      }
+    }
+    ss = dev::WaveSum(ss);
+    if (lane == 0) part[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    double total = part[0];
+#pragma unroll
+    for (int q = 1; q < kWavesPerBlock; ++q) total += part[q];
+    const float scale = dev::RmsScale(total, n, nrm.eps);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int i = 4 * static_cast<int>(threadIdx.x) + 4 * kMmBlock * j;
+      if (i < n) dev::Store4(hs + i, dev::ScaleMul(v[j], scale, wv[j]));
+    }
+    __syncthreads();
+    const bool live = c < nb;
+    lane_off[0] = static_cast<int64_t>(live ? c : nb - 1) * kBB;
+    if (live) {
+      LoadLaneX<kType>(hs, static_cast<int64_t>(c) * kQK_K, s, xv[0]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) xv[0][i] = 0.0f;
+    }
+    RunSums(xv[0], sx[0]);
+    if (kMixed) {
+      lane_off_b[0] = static_cast<int64_t>(live ? c : nb - 1) * kBBB;
+      if (live) {
+        LoadLaneX<kTypeB>(hs, static_cast<int64_t>(c) * kQK_K, s, xvb[0]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) xvb[0][i] = 0.0f;
+      }
+      RunSums(xvb[0], sxb[0]);
+    }
+    if (r0 >= rows) return;  // after the workgroup's barriers
+  }
+#pragma unroll
+  for (int it = 0; it < (kNorm ? 0 : NX); ++it) {
     const int b = c + kGroups * it;
     lane_off[it] = static_cast<int64_t>(b < nb ? b : nb - 1) * kBB;
     if (b < nb) {
@@ -708,14 +783,23 @@ void LaunchQuant(const char* name, const uint8_t* w, int64_t rows, int64_t row_b
 // or more), at most kDecodeGrid workgroups (16 waves per CU).
 constexpr int64_t kDecodeGrid = 1024;
 
+// nrm != nullptr: the launch forms the norm itself (x is then the residual
+// stream); nrm->x_out is cleared afterwards, so a group of launches writes the
+// updated residual once.
 template <uint32_t kType, int RI, bool kPaired = false, uint32_t kTypeB = kType>
 void LaunchDecodeSegs(const char* name, const MatSegs& sg, int32_t n_seg, int64_t row_bytes, int32_t nb,
-                      const float* x) {
+                      const float* x, NormPrologue* nrm = nullptr) {
   const int64_t rows = sg.end[n_seg - 1];
   const int64_t need = (rows + kWavesPerBlock * RI - 1) / (kWavesPerBlock * RI);
   const unsigned grid = static_cast<unsigned>(need < kDecodeGrid ? need : kDecodeGrid);
+  if (nrm != nullptr) {
+    Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB, true>, dim3(grid), dim3(kMmBlock), sg, n_seg,
+           row_bytes, nb, x, *nrm);
+    nrm->x_out = nullptr;
+    return;
+  }
   Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB>, dim3(grid), dim3(kMmBlock), sg, n_seg, row_bytes, nb,
-         x);
+         x, NormPrologue{});
 }
 
 MatSegs OneSeg(const uint8_t* w, int64_t rows, float* out) {
@@ -823,8 +907,128 @@ void GpuMatMulQuantRaw(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_
          w_dev, rows, row_bytes, bs.elems, bs.bytes, x_dev, cols, n_tokens, out_dev);
 }
 
-void GpuMatMulQuantGroup(const GpuTensor* const* ws, int32_t n_mats, const float* x_dev, int64_t n_tokens,
-                         float* const* outs) {
+namespace {
+
+// Whether every matrix of a group runs on the one-token decode kernels (Q4_K /
+// Q6_K rows of at most kGroups blocks at their load alignment).
+bool DecodeEligible(const GpuTensor* const* ws, int32_t n_mats, const float* x_dev, int64_t n_tokens) {
+  const int64_t cols = ws[0]->cols;
+  if (n_tokens != 1 || !Aligned(x_dev, 16) || cols % kQK_K != 0 || cols / kQK_K > kGroups) return false;
+  for (int32_t k = 0; k < n_mats; ++k) {
+    const bool q4 = ws[k]->type == kGgmlQ4_K, q6 = ws[k]->type == kGgmlQ6_K;
+    if (!(q4 || q6) || !Aligned(ws[k]->buf.data(), q4 ? 16 : 2)) return false;
+  }
+  return true;
+}
+
+// The one-token launches of an eligible group: Q4_K and Q6_K together in one
+// launch when no Q4_K matrix needs its own 4-rows-per-wave shape; otherwise one
+// launch per run of consecutive same-type matrices, and matrices with odd rows
+// or the 4-rows shape each on their own (the kernel of a single matrix, so every
+// output is bit-identical to its GpuMatMulQuant). nrm: see LaunchDecodeSegs.
+void DecodeGroup(const GpuTensor* const* ws, int32_t n_mats, const float* x_dev, float* const* outs,
+                 NormPrologue* nrm) {
+  const int64_t cols = ws[0]->cols;
+  const int32_t nb = static_cast<int32_t>(cols / kQK_K);
+  if (n_mats > 1 && n_mats <= kMaxSegs) {
+    bool even = true, any4 = false, any6 = false;
+    int64_t total4 = 0;
+    for (int32_t k = 0; k < n_mats; ++k) {
+      const bool q4 = ws[k]->type == kGgmlQ4_K;
+      even = even && ws[k]->rows % 2 == 0;
+      any4 = any4 || q4;
+      any6 = any6 || !q4;
+      if (q4) total4 += ws[k]->rows;
+    }
+    if (even && any4 && any6 && total4 < 32768) {
+      MatSegs sg{};
+      for (int k = 0; k < kMaxSegs; ++k) sg.end[k] = INT64_MAX;
+      int64_t end = 0;
+      for (int32_t k = 0; k < n_mats; ++k) {
+        sg.w[k] = static_cast<const uint8_t*>(ws[k]->buf.data());
+        sg.out[k] = outs[k];
+        end += ws[k]->rows;
+        sg.end[k] = end;
+        if (ws[k]->type == kGgmlQ6_K) sg.b_mask |= 1u << k;
+      }
+      sg.row_bytes_b = TypeRowBytes(kGgmlQ6_K, cols);
+      LaunchDecodeSegs<kGgmlQ4_K, 2, false, kGgmlQ6_K>(nrm ? "NormMatVecQ4KQ6KKernel" : "MatVecQ4KQ6KKernel", sg,
+                                                       n_mats, TypeRowBytes(kGgmlQ4_K, cols), nb, x_dev, nrm);
+      return;
+    }
+  }
+  int32_t i = 0;
+  while (i < n_mats) {
+    const uint32_t type = ws[i]->type;
+    const bool q4 = type == kGgmlQ4_K;
+    const int64_t row_bytes = TypeRowBytes(type, cols);
+    int32_t j = i + 1;
+    while (j < n_mats && j - i < kMaxSegs && ws[j]->type == type) ++j;
+    int64_t total = 0;
+    bool fuse = j - i > 1;
+    for (int32_t k = i; k < j && fuse; ++k) {
+      fuse = ws[k]->rows % 2 == 0;
+      total += ws[k]->rows;
+    }
+    fuse = fuse && !(q4 && total >= 32768);  // the 4-rows-per-wave shape stays per matrix
+    const int32_t n_launch = fuse ? 1 : j - i;
+    for (int32_t l = 0; l < n_launch; ++l) {
+      const int32_t first = i + l, last = fuse ? j : i + l + 1;
+      MatSegs sg{};
+      for (int s = 0; s < kMaxSegs; ++s) sg.end[s] = INT64_MAX;
+      int64_t end = 0;
+      for (int32_t k = first; k < last; ++k) {
+        sg.w[k - first] = static_cast<const uint8_t*>(ws[k]->buf.data());
+        sg.out[k - first] = outs[k];
+        end += ws[k]->rows;
+        sg.end[k - first] = end;
+      }
+      if (q4 && end >= 32768) {  // a single matrix (a run that large is not fused)
+        LaunchDecodeSegs<kGgmlQ4_K, 4>(nrm ? "NormMatVecQ4KKernel" : "MatVecQ4KKernel", sg, 1, row_bytes, nb, x_dev,
+                                       nrm);
+      } else if (q4) {
+        LaunchDecodeSegs<kGgmlQ4_K, 2>(nrm ? "NormMatVecQ4KKernel" : "MatVecQ4KKernel", sg, last - first, row_bytes,
+                                       nb, x_dev, nrm);
+      } else {
+        LaunchDecodeSegs<kGgmlQ6_K, 2>(nrm ? "NormMatVecQ6KKernel" : "MatVecQ6KKernel", sg, last - first, row_bytes,
+                                       nb, x_dev, nrm);
+      }
+    }
+    i = j;
+  }
+}
+
+// The gate / up pair of GpuMatMulQuantSwiGLU on the paired one-token kernel.
+bool SwiGLUDecodeEligible(const GpuTensor& w_gate, const GpuTensor& w_up, const float* x_dev, int64_t n_tokens) {
+  const int64_t cols = w_gate.cols;
+  const uint32_t type = w_gate.type;
+  const bool q4 = type == kGgmlQ4_K, q6 = type == kGgmlQ6_K;
+  return n_tokens == 1 && w_up.type == type && (q4 || q6) && Aligned(x_dev, 16) && cols % kQK_K == 0 &&
+         cols / kQK_K <= kGroups && Aligned(w_gate.buf.data(), q4 ? 16 : 2) && Aligned(w_up.buf.data(), q4 ? 16 : 2) &&
+         w_gate.buf.size() == static_cast<size_t>(w_gate.rows * w_gate.row_bytes()) &&
+         w_up.buf.size() == static_cast<size_t>(w_up.rows * w_up.row_bytes());
+}
+
+void DecodeSwiGLU(const GpuTensor& w_gate, const GpuTensor& w_up, const float* x_dev, float* gate_dev,
+                  NormPrologue* nrm) {
+  MatSegs sg{};
+  for (int i = 0; i < kMaxSegs; ++i) sg.end[i] = INT64_MAX;
+  sg.w[0] = static_cast<const uint8_t*>(w_gate.buf.data());
+  sg.w[1] = static_cast<const uint8_t*>(w_up.buf.data());
+  sg.out[0] = gate_dev;
+  sg.end[0] = 2 * w_gate.rows;  // virtual rows: (gate p, up p) pairs
+  const int32_t nb = static_cast<int32_t>(w_gate.cols / kQK_K);
+  const int64_t row_bytes = TypeRowBytes(w_gate.type, w_gate.cols);
+  if (w_gate.type == kGgmlQ4_K) {
+    LaunchDecodeSegs<kGgmlQ4_K, 2, true>(nrm ? "NormMatVecSwiGLUQ4KKernel" : "MatVecSwiGLUQ4KKernel", sg, 1,
+                                         row_bytes, nb, x_dev, nrm);
+  } else {
+    LaunchDecodeSegs<kGgmlQ6_K, 2, true>(nrm ? "NormMatVecSwiGLUQ6KKernel" : "MatVecSwiGLUQ6KKernel", sg, 1,
+                                         row_bytes, nb, x_dev, nrm);
+  }
+}
+
+void CheckGroup(const GpuTensor* const* ws, int32_t n_mats, float* const* outs) {
   RPG_CHECK(ws != nullptr && outs != nullptr && n_mats > 0, "GpuMatMulQuantGroup needs at least one matrix");
   for (int32_t i = 0; i < n_mats; ++i) {
     RPG_CHECK(ws[i] != nullptr && outs[i] != nullptr, "GpuMatMulQuantGroup got a null matrix or output");
@@ -835,6 +1039,26 @@ void GpuMatMulQuantGroup(const GpuTensor* const* ws, int32_t n_mats, const float
               "tensor byte count does not match the [%lld, %lld] shape", static_cast<long long>(ws[i]->rows),
               static_cast<long long>(ws[i]->cols));
   }
+}
+
+// The norm prologue of a fused call, or false when the call has no fused form.
+bool MakeNorm(const GpuNormIn& in, int64_t cols, NormPrologue* nrm) {
+  RPG_CHECK(in.x != nullptr && in.w != nullptr, "norm-fused matmul needs x and the norm weights");
+  RPG_CHECK(in.x_out == nullptr || (in.x_out != in.x && in.x_out != in.d),
+            "norm-fused matmul: x_out must not alias x or d (other waves are still reading them)");
+  if (!Aligned(in.w, 16) || (in.d != nullptr && !Aligned(in.d, 16)) ||
+      (in.x_out != nullptr && !Aligned(in.x_out, 16)) || cols % kQK_K != 0 || cols / kQK_K > kGroups) {
+    return false;
+  }
+  *nrm = NormPrologue{in.d, in.w, in.x_out, in.eps};
+  return true;
+}
+
+}  // namespace
+
+void GpuMatMulQuantGroup(const GpuTensor* const* ws, int32_t n_mats, const float* x_dev, int64_t n_tokens,
+                         float* const* outs) {
+  CheckGroup(ws, n_mats, outs);
   const int64_t cols = ws[0]->cols;
   // Prefill: the activations are split once for all the matrices (each output
   // bit-identical to its own GpuMatMulQuant call, which splits the same way).
@@ -851,75 +1075,11 @@ void GpuMatMulQuantGroup(const GpuTensor* const* ws, int32_t n_mats, const float
     }
     return;
   }
-  // Decode rows fused per run of consecutive same-type matrices (the kernel of a
-  // single matrix, so every output is bit-identical to its GpuMatMulQuant);
-  // anything else goes matrix by matrix.
-  const int64_t nb = cols / kQK_K;
-  const bool decode = n_tokens == 1 && Aligned(x_dev, 16) && cols % kQK_K == 0 && nb <= kGroups;
-  // Q4_K and Q6_K matrices together (a Q4_K_M layer's q, k and v): one launch
-  // when no Q4_K matrix needs its own 4-rows-per-wave shape.
-  if (decode && n_mats > 1 && n_mats <= kMaxSegs) {
-    bool ok = true, any4 = false, any6 = false;
-    int64_t total4 = 0;
-    for (int32_t k = 0; k < n_mats && ok; ++k) {
-      const bool q4 = ws[k]->type == kGgmlQ4_K, q6 = ws[k]->type == kGgmlQ6_K;
-      ok = (q4 || q6) && ws[k]->rows % 2 == 0 && Aligned(ws[k]->buf.data(), q4 ? 16 : 2);
-      any4 = any4 || q4;
-      any6 = any6 || q6;
-      if (q4) total4 += ws[k]->rows;
-    }
-    if (ok && any4 && any6 && total4 < 32768) {
-      MatSegs sg{};
-      for (int k = 0; k < kMaxSegs; ++k) sg.end[k] = INT64_MAX;
-      int64_t end = 0;
-      for (int32_t k = 0; k < n_mats; ++k) {
-        sg.w[k] = static_cast<const uint8_t*>(ws[k]->buf.data());
-        sg.out[k] = outs[k];
-        end += ws[k]->rows;
-        sg.end[k] = end;
-        if (ws[k]->type == kGgmlQ6_K) sg.b_mask |= 1u << k;
-      }
-      sg.row_bytes_b = TypeRowBytes(kGgmlQ6_K, cols);
-      LaunchDecodeSegs<kGgmlQ4_K, 2, false, kGgmlQ6_K>("MatVecQ4KQ6KKernel", sg, n_mats,
-                                                       TypeRowBytes(kGgmlQ4_K, cols), static_cast<int32_t>(nb), x_dev);
-      return;
-    }
+  if (DecodeEligible(ws, n_mats, x_dev, n_tokens)) {
+    DecodeGroup(ws, n_mats, x_dev, outs, nullptr);
+    return;
   }
-  int32_t i = 0;
-  while (i < n_mats) {
-    const uint32_t type = ws[i]->type;
-    int32_t j = i + 1;
-    while (j < n_mats && j - i < kMaxSegs && ws[j]->type == type) ++j;
-    const bool q4 = type == kGgmlQ4_K, q6 = type == kGgmlQ6_K;
-    int64_t total = 0;
-    bool fuse = decode && j - i > 1 && (q4 || q6);
-    for (int32_t k = i; k < j && fuse; ++k) {
-      fuse = ws[k]->rows % 2 == 0 && Aligned(ws[k]->buf.data(), q4 ? 16 : 2);
-      total += ws[k]->rows;
-    }
-    fuse = fuse && !(q4 && total >= 32768);  // the 4-rows-per-wave shape stays per matrix
-    if (!fuse) {
-      for (int32_t k = i; k < j; ++k) GpuMatMulQuant(*ws[k], x_dev, n_tokens, outs[k]);
-      i = j;
-      continue;
-    }
-    MatSegs sg{};
-    for (int s = 0; s < kMaxSegs; ++s) sg.end[s] = INT64_MAX;
-    int64_t end = 0;
-    for (int32_t k = i; k < j; ++k) {
-      sg.w[k - i] = static_cast<const uint8_t*>(ws[k]->buf.data());
-      sg.out[k - i] = outs[k];
-      end += ws[k]->rows;
-      sg.end[k - i] = end;
-    }
-    const int64_t row_bytes = TypeRowBytes(type, cols);
-    if (q4) {
-      LaunchDecodeSegs<kGgmlQ4_K, 2>("MatVecQ4KKernel", sg, j - i, row_bytes, static_cast<int32_t>(nb), x_dev);
-    } else {
-      LaunchDecodeSegs<kGgmlQ6_K, 2>("MatVecQ6KKernel", sg, j - i, row_bytes, static_cast<int32_t>(nb), x_dev);
-    }
-    i = j;
-  }
+  for (int32_t i = 0; i < n_mats; ++i) GpuMatMulQuant(*ws[i], x_dev, n_tokens, outs[i]);
 }
 
 void GpuMatMulQuantSwiGLU(const GpuTensor& w_gate, const GpuTensor& w_up, const float* x_dev, int64_t n_tokens,
@@ -931,34 +1091,34 @@ void GpuMatMulQuantSwiGLU(const GpuTensor& w_gate, const GpuTensor& w_up, const 
             static_cast<long long>(w_gate.cols), static_cast<long long>(w_up.rows), static_cast<long long>(w_up.cols));
   RPG_CHECK(n_tokens > 0, "n_tokens must be positive");
   RPG_CHECK(x_dev != nullptr && gate_dev != nullptr && up_dev != nullptr, "GpuMatMulQuantSwiGLU got a null pointer");
-  const int64_t cols = w_gate.cols;
-  const uint32_t type = w_gate.type;
-  const bool q4 = type == kGgmlQ4_K, q6 = type == kGgmlQ6_K;
-  const uint8_t* wg = static_cast<const uint8_t*>(w_gate.buf.data());
-  const uint8_t* wu = static_cast<const uint8_t*>(w_up.buf.data());
-  if (n_tokens == 1 && w_up.type == type && (q4 || q6) && Aligned(x_dev, 16) && cols % kQK_K == 0 &&
-      cols / kQK_K <= kGroups && Aligned(wg, q4 ? 16 : 2) && Aligned(wu, q4 ? 16 : 2) &&
-      w_gate.buf.size() == static_cast<size_t>(w_gate.rows * w_gate.row_bytes()) &&
-      w_up.buf.size() == static_cast<size_t>(w_up.rows * w_up.row_bytes())) {
-    MatSegs sg{};
-    for (int i = 0; i < kMaxSegs; ++i) sg.end[i] = INT64_MAX;
-    sg.w[0] = wg;
-    sg.w[1] = wu;
-    sg.out[0] = gate_dev;
-    sg.end[0] = 2 * w_gate.rows;  // virtual rows: (gate p, up p) pairs
-    const int32_t nb = static_cast<int32_t>(cols / kQK_K);
-    const int64_t row_bytes = TypeRowBytes(type, cols);
-    if (q4) {
-      LaunchDecodeSegs<kGgmlQ4_K, 2, true>("MatVecSwiGLUQ4KKernel", sg, 1, row_bytes, nb, x_dev);
-    } else {
-      LaunchDecodeSegs<kGgmlQ6_K, 2, true>("MatVecSwiGLUQ6KKernel", sg, 1, row_bytes, nb, x_dev);
-    }
+  if (SwiGLUDecodeEligible(w_gate, w_up, x_dev, n_tokens)) {
+    DecodeSwiGLU(w_gate, w_up, x_dev, gate_dev, nullptr);
     return;
   }
   const GpuTensor* mats[2] = {&w_gate, &w_up};
   float* outs[2] = {gate_dev, up_dev};
   GpuMatMulQuantGroup(mats, 2, x_dev, n_tokens, outs);
   GpuSiluMulInPlace(gate_dev, up_dev, n_tokens * w_gate.rows);
+}
+
+bool GpuNormMatMulQuantGroup(const GpuNormIn& in, const GpuTensor* const* ws, int32_t n_mats, float* const* outs) {
+  CheckGroup(ws, n_mats, outs);
+  NormPrologue nrm;
+  if (!MakeNorm(in, ws[0]->cols, &nrm) || !DecodeEligible(ws, n_mats, in.x, 1)) return false;
+  DecodeGroup(ws, n_mats, in.x, outs, &nrm);
+  return true;
+}
+
+bool GpuNormMatMulQuantSwiGLU(const GpuNormIn& in, const GpuTensor& w_gate, const GpuTensor& w_up, float* gate_dev,
+                              float* up_dev) {
+  RPG_CHECK(w_gate.matrix && w_gate.valid() && w_up.matrix && w_up.valid(),
+            "GpuNormMatMulQuantSwiGLU got a non-matrix or empty tensor");
+  RPG_CHECK(w_gate.rows == w_up.rows && w_gate.cols == w_up.cols, "gate and up must have the same shape");
+  RPG_CHECK(gate_dev != nullptr && up_dev != nullptr, "GpuNormMatMulQuantSwiGLU got a null output");
+  NormPrologue nrm;
+  if (!MakeNorm(in, w_gate.cols, &nrm) || !SwiGLUDecodeEligible(w_gate, w_up, in.x, 1)) return false;
+  DecodeSwiGLU(w_gate, w_up, in.x, gate_dev, &nrm);
+  return true;
 }
 
 void GpuMatMulQuant(const GpuTensor& w, const float* X_dev, int64_t n_tokens, float* OUT_dev) {

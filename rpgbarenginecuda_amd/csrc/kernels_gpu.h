@@ -233,6 +233,33 @@ void GpuMatMulQuantGroup(const GpuTensor* const* ws, int32_t n_mats, const float
 void GpuMatMulQuantSwiGLU(const GpuTensor& w_gate, const GpuTensor& w_up, const float* X_dev, int64_t n_tokens,
                           float* gate_dev, float* up_dev);
 
+// The sub-layer norm in front of a one-token matmul (the reference runs
+// GpuVecAddInPlace, GpuRmsNorm and the matmul as separate launches,
+// src/qwen3_gpu.cu:69-76,100-104,168): v = x + d (d == nullptr: v = x),
+// h = RMSNorm(v) * w as GpuAddRmsNorm computes it, and the matmul of h. Each
+// launch forms h itself, so no h buffer is written; x_out (optional) receives v,
+// bit-exact, and must not alias x or d. The scale's double sum of squares is
+// taken in another order than GpuAddRmsNorm's, so h can differ from it in the
+// last fp32 bit. All of x, d, w, x_out 16-byte aligned.
+struct GpuNormIn {
+  const float* x;
+  const float* d;
+  const float* w;
+  float eps;
+  float* x_out;
+};
+
+// GpuMatMulQuantGroup at one token on RMSNorm(x + d) * w. Returns false, having
+// launched nothing, when the group has no fused form (a matrix that is not
+// Q4_K / Q6_K, more than 2048 columns, misaligned pointers); the caller then
+// runs GpuAddRmsNorm and GpuMatMulQuantGroup. No counterpart in the reference.
+bool GpuNormMatMulQuantGroup(const GpuNormIn& in, const GpuTensor* const* ws, int32_t n_mats, float* const* OUTs);
+
+// GpuMatMulQuantSwiGLU at one token on RMSNorm(x + d) * w; false as above. No
+// counterpart in the reference.
+bool GpuNormMatMulQuantSwiGLU(const GpuNormIn& in, const GpuTensor& w_gate, const GpuTensor& w_up, float* gate_dev,
+                              float* up_dev);
+
 // The same on a raw (non-owning) weight pointer; GpuMatMulQuant forwards here.
 void GpuMatMulQuantRaw(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_t cols, const float* x_dev,
                        int64_t n_tokens, float* out_dev);

@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstring>
+#include <utility>
 
 namespace rpg {
 namespace {
@@ -23,8 +24,26 @@ void Need(DeviceBuffer& b, int64_t floats) {
 // GpuVecAddInPlace (one IEEE add per element).
 class Residual {
  public:
-  Residual(float* x, float* proj, float* h, int64_t seq, int64_t hidden, float eps)
-      : x_(x), proj_(proj), h_(h), seq_(seq), hidden_(hidden), eps_(eps) {}
+  Residual(float* x, float* x_alt, float* proj, float* h, int64_t seq, int64_t hidden, float eps)
+      : x_(x), alt_(x_alt), proj_(proj), h_(h), seq_(seq), hidden_(hidden), eps_(eps) {}
+
+  // The residual stream (x or x_alt: a fused norm writes x + proj to the other).
+  float* x() const { return x_; }
+
+  // At one token the norm runs inside the matmul that reads it (GpuNormIn):
+  // the sum x + proj, when pending, goes to the other buffer (keep) or nowhere
+  // (the output norm, after which x is not read). Returns the fused call's
+  // result; false leaves everything as it was, for NormInto.
+  template <typename Call>
+  bool Fused(const float* w, bool keep, Call&& call) {
+    if (seq_ != 1) return false;
+    const bool write = pending_ && keep;
+    const GpuNormIn in{x_, pending_ ? proj_ : nullptr, w, eps_, write ? alt_ : nullptr};
+    if (!call(in)) return false;
+    if (write) std::swap(x_, alt_);
+    pending_ = false;
+    return true;
+  }
 
   void NormInto(const float* w) {
     if (pending_) {
@@ -44,6 +63,7 @@ class Residual {
 
  private:
   float* x_;
+  float* alt_;
   float* proj_;
   float* h_;
   int64_t seq_;
@@ -69,11 +89,14 @@ void ForwardLayer(const GpuModel& m, int32_t layer, int64_t pos0, GpuScratch* s,
   float* attn = F(s->attn);
   float* h = F(s->h);
 
-  res->NormInto(static_cast<const float*>(w.attn_norm.buf.data()));
   {
+    const float* nw = static_cast<const float*>(w.attn_norm.buf.data());
     const GpuTensor* mats[3] = {&w.attn_q, &w.attn_k, &w.attn_v};
     float* outs[3] = {q, k, v};
-    GpuMatMulQuantGroup(mats, 3, h, seq, outs);
+    if (!res->Fused(nw, true, [&](const GpuNormIn& in) { return GpuNormMatMulQuantGroup(in, mats, 3, outs); })) {
+      res->NormInto(nw);
+      GpuMatMulQuantGroup(mats, 3, h, seq, outs);
+    }
   }
   const float* qn = static_cast<const float*>(w.q_norm.buf.data());
   const float* kn = static_cast<const float*>(w.k_norm.buf.data());
@@ -94,8 +117,14 @@ void ForwardLayer(const GpuModel& m, int32_t layer, int64_t pos0, GpuScratch* s,
   GpuMatMulQuant(w.attn_o, attn, seq, F(s->proj));
   res->Defer();
 
-  res->NormInto(static_cast<const float*>(w.ffn_norm.buf.data()));
-  GpuMatMulQuantSwiGLU(w.ffn_gate, w.ffn_up, h, seq, F(s->gate), F(s->up));  // gate <- silu(gate) * up
+  // gate <- silu(gate) * up
+  const float* fw = static_cast<const float*>(w.ffn_norm.buf.data());
+  if (!res->Fused(fw, true, [&](const GpuNormIn& in) {
+        return GpuNormMatMulQuantSwiGLU(in, w.ffn_gate, w.ffn_up, F(s->gate), F(s->up));
+      })) {
+    res->NormInto(fw);
+    GpuMatMulQuantSwiGLU(w.ffn_gate, w.ffn_up, h, seq, F(s->gate), F(s->up));
+  }
   GpuMatMulQuant(w.ffn_down, F(s->gate), seq, F(s->proj));
   res->Defer();
 }
@@ -119,12 +148,12 @@ void ForwardCore(const GpuModel& m, int64_t seq, GpuScratch* s, const int32_t* t
   GpuEmbeddingLookup(m.token_embd(), toks_dev, seq, F(s->x));
   if (opt.capture_hidden != nullptr) s->x.Download(opt.capture_hidden->data(), row_floats * sizeof(float));
 
-  Residual res(F(s->x), F(s->proj), F(s->h), seq, hidden, c.rms_eps);
+  Residual res(F(s->x), F(s->x_alt), F(s->proj), F(s->h), seq, hidden, c.rms_eps);
   for (int32_t l = 0; l < n_use; ++l) {
     ForwardLayer(m, l, pos0, s, seq, kv, attn_sh_positions, &res);
     if (opt.capture_hidden != nullptr) {
       res.Settle();
-      s->x.Download(opt.capture_hidden->data() + static_cast<size_t>(l + 1) * row_floats, row_floats * sizeof(float));
+      (res.x() == F(s->x) ? s->x : s->x_alt).Download(opt.capture_hidden->data() + static_cast<size_t>(l + 1) * row_floats, row_floats * sizeof(float));
     }
   }
   if (n_use < c.n_layers) {
@@ -134,8 +163,13 @@ void ForwardCore(const GpuModel& m, int64_t seq, GpuScratch* s, const int32_t* t
     return;
   }
   // Always computed, also when logits == nullptr: decoding reads s->logits.
-  res.NormInto(static_cast<const float*>(m.output_norm().buf.data()));
-  GpuMatMulQuant(m.lm_head(), F(s->h), seq, F(s->logits));
+  const float* ow = static_cast<const float*>(m.output_norm().buf.data());
+  const GpuTensor* head[1] = {&m.lm_head()};
+  float* head_out[1] = {F(s->logits)};
+  if (!res.Fused(ow, false, [&](const GpuNormIn& in) { return GpuNormMatMulQuantGroup(in, head, 1, head_out); })) {
+    res.NormInto(ow);
+    GpuMatMulQuant(m.lm_head(), F(s->h), seq, F(s->logits));
+  }
   if (logits == nullptr) return;
   logits->assign(static_cast<size_t>(seq) * static_cast<size_t>(c.vocab), 0.0f);
   s->logits.Download(logits->data(), logits->size() * sizeof(float));
@@ -167,6 +201,7 @@ void CheckCache(const GpuModel& m, const GpuKvCache* kv) {
 void GpuScratch::Ensure(const ModelMeta& c, int64_t seq) {
   RPG_CHECK(seq > 0, "scratch needs a positive segment length");
   Need(x, seq * c.hidden);
+  Need(x_alt, c.hidden);
   Need(h, seq * c.hidden);
   Need(q, seq * c.q_dim());
   Need(k, seq * c.kv_dim());
@@ -184,7 +219,7 @@ void GpuScratch::Ensure(const ModelMeta& c, int64_t seq) {
 
 int64_t GpuScratch::bytes() const {
   int64_t n = 0;
-  for (const DeviceBuffer* b : {&x, &h, &q, &k, &v, &attn, &proj, &gate, &up, &toks, &logits, &probs, &argmax_idx}) {
+  for (const DeviceBuffer* b : {&x, &x_alt, &h, &q, &k, &v, &attn, &proj, &gate, &up, &toks, &logits, &probs, &argmax_idx}) {
     n += static_cast<int64_t>(b->size());
   }
   return n;
@@ -261,7 +296,7 @@ uint64_t MakeGraphKey(const GpuModel& m, GpuKvCache* kv, const GpuScratch* s, co
   mix(reinterpret_cast<uintptr_t>(kv));
   mix(reinterpret_cast<uintptr_t>(kv->k_layer(0)));
   mix(reinterpret_cast<uintptr_t>(kv->v_layer(0)));
-  for (const DeviceBuffer* b : {&s->x, &s->h, &s->q, &s->k, &s->v, &s->attn, &s->proj, &s->gate, &s->up, &s->logits,
+  for (const DeviceBuffer* b : {&s->x, &s->x_alt, &s->h, &s->q, &s->k, &s->v, &s->attn, &s->proj, &s->gate, &s->up, &s->logits,
                                 &s->probs, &s->argmax_idx}) {
     mix(reinterpret_cast<uintptr_t>(b->data()));
   }

@@ -14,7 +14,10 @@
 // What differs from the reference layer (src/qwen3_gpu.cu:47-109), same maths:
 //   * the residual add of each sub-layer is folded into the RMSNorm that reads
 //     the sum next (GpuAddRmsNorm: the next layer's attn_norm, the ffn_norm, or
-//     the output norm), so x is read and written once per sub-layer;
+//     the output norm), so x is read and written once per sub-layer; at one
+//     token the add and the norm run inside the matmul that reads the norm
+//     (GpuNormMatMulQuantGroup / GpuNormMatMulQuantSwiGLU), and the residual
+//     alternates between x and x_alt;
 //   * q / k RMSNorm, RoPE and the fp16 K/V store run as one pass
 //     (GpuQkNormRopeKv) on the cache path;
 //   * q / k / v go through GpuMatMulQuantGroup (at one token one launch per
@@ -55,6 +58,7 @@ class GpuScratch {
   int64_t bytes() const;
 
   DeviceBuffer x;       // [seq, hidden] residual stream
+  DeviceBuffer x_alt;   // [hidden] the residual stream's second buffer at one token
   DeviceBuffer h;       // [seq, hidden] normalised input of a sub-layer
   DeviceBuffer q;       // [seq, q_dim]
   DeviceBuffer k;       // [seq, kv_dim]

@@ -65,6 +65,9 @@ SIGNATURES = {
     "rpg_generate": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp]),
     "rpg_op_matmul_quant_group": (_i32, [_i32, _vp, _vp, _vp, _i64, _vp, _i64, _vp]),
     "rpg_op_matmul_quant_swiglu": (_i32, [_u32, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp]),
+    "rpg_op_norm_matmul_quant_group": (_i32, [_i32, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _f32, _vp, _vp, _vp]),
+    "rpg_op_norm_matmul_quant_swiglu": (_i32, [_u32, _vp, _vp, _i64, _i64, _vp, _vp, _vp, _f32, _vp, _vp, _vp,
+                                               _vp]),
     "rpg_op_argmax": (_i32, [_vp, _i64, _vp]),
     "rpg_sample_split_mix64": (ctypes.c_uint64, [ctypes.c_uint64]),
     "rpg_sample_counter_rng": (ctypes.c_uint64, [ctypes.c_uint64, ctypes.c_uint64]),
@@ -343,6 +346,47 @@ def GpuMatMulQuantGroup(ws: list, x, n_tokens: int, outs: list) -> None:
     _check(load_library().rpg_op_matmul_quant_group(n, types, ptrs, rows, cols,
                                                     _addr(x, 4 * n_tokens * cols, torch.float32, "x"), n_tokens,
                                                     optrs))
+
+
+def GpuNormMatMulQuantGroup(x, d, norm_w, eps: float, x_out, ws: list, outs: list) -> bool:
+    """One token: OUT_i = (RMSNorm(x + d) * norm_w) . W_i^T with the norm formed inside the matmul launches, and
+    x_out <- x + d (no reference counterpart). Returns False, having launched nothing, when the group has no fused
+    form (the caller then runs GpuAddRmsNorm + GpuMatMulQuantGroup)."""
+    torch = _t()
+    n = len(ws)
+    if n == 0 or n != len(outs):
+        raise RpgError("GpuNormMatMulQuantGroup needs one output per matrix and at least one matrix")
+    cols = ws[0].cols
+    if any(w.cols != cols for w in ws):
+        raise RpgError(f"GpuNormMatMulQuantGroup matrices must share their width ({[w.cols for w in ws]})")
+    types = (ctypes.c_uint32 * n)(*[w.type for w in ws])
+    ptrs = (ctypes.c_void_p * n)(*[_addr(w.buf, w.rows * w.row_bytes(), name="w") for w in ws])
+    rows = (ctypes.c_int64 * n)(*[w.rows for w in ws])
+    optrs = (ctypes.c_void_p * n)(*[_addr(o, 4 * w.rows, torch.float32, "out") for o, w in zip(outs, ws)])
+    fused = ctypes.c_int32(0)
+    row = 4 * cols
+    _check(load_library().rpg_op_norm_matmul_quant_group(
+        n, types, ptrs, rows, cols, _addr(x, row, torch.float32, "x"), _addr(d, row, torch.float32, "d"),
+        _addr(norm_w, row, torch.float32, "norm_w"), eps, _addr(x_out, row, torch.float32, "x_out"), optrs,
+        ctypes.byref(fused)))
+    return bool(fused.value)
+
+
+def GpuNormMatMulQuantSwiGLU(x, d, norm_w, eps: float, x_out, w_gate: GpuTensor, w_up: GpuTensor, gate, up) -> bool:
+    """GpuNormMatMulQuantGroup in front of GpuMatMulQuantSwiGLU (one token; no reference counterpart)."""
+    torch = _t()
+    if (w_gate.type, w_gate.rows, w_gate.cols) != (w_up.type, w_up.rows, w_up.cols):
+        raise RpgError("GpuNormMatMulQuantSwiGLU: gate and up must have the same type and shape")
+    nbytes = w_gate.rows * w_gate.row_bytes()
+    row = 4 * w_gate.cols
+    fused = ctypes.c_int32(0)
+    _check(load_library().rpg_op_norm_matmul_quant_swiglu(
+        w_gate.type, _addr(w_gate.buf, nbytes, name="w_gate"), _addr(w_up.buf, nbytes, name="w_up"), w_gate.rows,
+        w_gate.cols, _addr(x, row, torch.float32, "x"), _addr(d, row, torch.float32, "d"),
+        _addr(norm_w, row, torch.float32, "norm_w"), eps, _addr(x_out, row, torch.float32, "x_out"),
+        _addr(gate, 4 * w_gate.rows, torch.float32, "gate"), _addr(up, 4 * w_gate.rows, torch.float32, "up"),
+        ctypes.byref(fused)))
+    return bool(fused.value)
 
 
 def GpuAttentionFromCache(n_heads: int, n_kv_heads: int, head_dim: int, pos0: int, q, seq: int, k_layer, v_layer,

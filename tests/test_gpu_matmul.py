@@ -285,3 +285,107 @@ def test_matmul_group_rejects_mixed_widths(gpu):
     x = torch.zeros(512, device="cuda")
     with pytest.raises(gpu.RpgError, match="width"):
         gpu.GpuMatMulQuantGroup([a, b], x, 1, [torch.zeros(4, device="cuda"), torch.zeros(4, device="cuda")])
+
+
+# The sub-layer norm inside the one-token matmul (GpuNormMatMulQuantGroup /
+# GpuNormMatMulQuantSwiGLU). Reference path: GpuAddRmsNorm (or GpuRmsNorm with no
+# delta) into h, then the plain call on h. The fused kernels take the double sum
+# of squares in another order, so h could differ in the last fp32 bit only if
+# the double sum fell within ~2^-29 (relative) of an fp32 rounding boundary of
+# the scale; for these seeded inputs it does not, so the outputs must be
+# bit-identical to the two-step path (and both within the matmul bound of the
+# float64 oracle on h).
+NORM_GROUPS = [
+    # (label, [(type, rows)], cols, with_d, with_x_out)
+    ("q/k/v of a 1.7B layer, pending residual", [(12, 2048), (12, 1024), (14, 1024)], 2048, True, True),
+    ("first layer: no residual delta", [(12, 2048), (12, 1024), (14, 1024)], 2048, False, False),
+    ("output norm + Q6_K head, residual not kept", [(14, 5000)], 2048, True, False),
+    ("Q4_K of 32768+ rows (4 rows per wave)", [(12, 33000)], 256, True, True),
+    ("runs, odd rows", [(14, 300), (12, 200), (12, 7), (14, 64), (14, 64)], 512, True, True),
+    ("three blocks per row", [(12, 128), (14, 96)], 768, True, True),
+]
+
+
+def _norm_inputs(gpu, rng, cols, with_d, eps=1e-6):
+    import torch
+
+    x = dev(rng.normal(0, 1, cols).astype(np.float32))
+    d = dev(rng.normal(0, 1, cols).astype(np.float32)) if with_d else None
+    w = dev(rng.normal(1, 0.1, cols).astype(np.float32))
+    xr = x.clone()
+    h = torch.full_like(x, np.nan)
+    if with_d:
+        gpu.GpuAddRmsNorm(xr, d, w, 1, cols, eps, h)
+    else:
+        gpu.GpuRmsNorm(xr, w, 1, cols, cols, eps, h)
+    return x, d, w, xr, h
+
+
+@pytest.mark.parametrize("label,mats,cols,with_d,with_x_out", NORM_GROUPS, ids=[g[0] for g in NORM_GROUPS])
+def test_norm_matmul_group_equals_two_step(gpu, ora, label, mats, cols, with_d, with_x_out):
+    import torch
+
+    case(f"norm matmul group {label}")
+    rng = np.random.default_rng(1700 + cols + len(mats))
+    eps = 1e-6
+    x, d, w, xr, h = _norm_inputs(gpu, rng, cols, with_d, eps)
+    ws, want, outs = [], [], []
+    for t, rows in mats:
+        wq = synth.quant_table(rng, t, rows, cols)
+        ws.append((gpu.GpuTensor(dev(wq), t, rows, cols), wq))
+        want.append(torch.full((1, rows), np.nan, dtype=torch.float32, device="cuda"))
+        outs.append(torch.full((1, rows), np.nan, dtype=torch.float32, device="cuda"))
+    gpu.GpuMatMulQuantGroup([g for g, _ in ws], h, 1, want)
+    x_out = torch.full_like(x, np.nan) if with_x_out else None
+    x0 = x.clone()
+    assert gpu.GpuNormMatMulQuantGroup(x, d, w, eps, x_out, [g for g, _ in ws], outs)
+    assert torch.equal(x, x0)
+    if with_x_out:
+        assert torch.equal(x_out, xr)  # x + d, one IEEE add
+    hh = host(h)[None, :]
+    for (g, wq), o, r, (t, rows) in zip(ws, outs, want, mats):
+        assert torch.equal(o, r), (label, t, rows)
+        exact, absdot = ora.matmul_quant_f64(t, wq, rows, cols, hh)
+        check(host(o), exact, absdot, cols, factored_magnitude(ora, t, wq, rows, cols, hh))
+
+
+@pytest.mark.parametrize("t,rows,cols", [(12, 6144, 2048), (14, 6144, 2048), (12, 130, 1024)])
+def test_norm_matmul_swiglu_equals_two_step(gpu, t, rows, cols):
+    import torch
+
+    case(f"norm matmul swiglu type={t} rows={rows} cols={cols}")
+    rng = np.random.default_rng(1800 + rows + cols + t)
+    eps = 1e-6
+    x, d, w, xr, h = _norm_inputs(gpu, rng, cols, True, eps)
+    wg = gpu.GpuTensor(dev(synth.quant_table(rng, t, rows, cols)), t, rows, cols)
+    wu = gpu.GpuTensor(dev(synth.quant_table(rng, t, rows, cols)), t, rows, cols)
+    g1 = torch.full((1, rows), np.nan, dtype=torch.float32, device="cuda")
+    u1 = torch.full_like(g1, np.nan)
+    gpu.GpuMatMulQuantSwiGLU(wg, wu, h, 1, g1, u1)
+    g2 = torch.full_like(g1, np.nan)
+    u2 = torch.full_like(g1, np.nan)
+    x_out = torch.full_like(x, np.nan)
+    assert gpu.GpuNormMatMulQuantSwiGLU(x, d, w, eps, x_out, wg, wu, g2, u2)
+    assert torch.equal(g2, g1)
+    assert torch.equal(x_out, xr)
+
+
+def test_norm_matmul_without_fused_form(gpu):
+    """Rows wider than 2048 columns (the 4B hidden size) have no fused form: the
+    call launches nothing and says so; an x_out aliasing x is refused."""
+    import torch
+
+    case("norm matmul group: no fused form, aliasing")
+    rng = np.random.default_rng(1900)
+    cols = 2560
+    x, d, w, _, _ = _norm_inputs(gpu, rng, cols, True)
+    g = gpu.GpuTensor(dev(synth.quant_table(rng, 12, 64, cols)), 12, 64, cols)
+    out = torch.full((1, 64), np.nan, dtype=torch.float32, device="cuda")
+    x_out = torch.full_like(x, np.nan)
+    assert not gpu.GpuNormMatMulQuantGroup(x, d, w, 1e-6, x_out, [g], [out])
+    torch.cuda.synchronize()
+    assert torch.isnan(out).all() and torch.isnan(x_out).all()
+    g2 = gpu.GpuTensor(dev(synth.quant_table(rng, 12, 64, 2048)), 12, 64, 2048)
+    x2 = torch.zeros(2048, device="cuda")
+    with pytest.raises(gpu.RpgError, match="alias"):
+        gpu.GpuNormMatMulQuantGroup(x2, x2.clone(), x2.clone(), 1e-6, x2, [g2], [out])
