@@ -130,6 +130,21 @@ RPG_OPS_API int32_t rpg_op_attention_from_cache(const float* q, int32_t n_heads,
                                                 const uint16_t* k_layer, const uint16_t* v_layer, int64_t max_seq,
                                                 float* out, int64_t sh_positions);
 
+/* One token at pos0: rpg_op_qk_norm_rope_kv (q / k per-head RMSNorm with q_norm /
+ * k_norm and eps, RoPE from rope_tab at pos0, k and v stored as fp16 at pos0)
+ * followed by rpg_op_attention_from_cache, in one decode launch, bit-identical
+ * to the two calls. q, k, v are the raw projections ([n_heads] / [n_kv_heads]
+ * rows of 128 floats) and are not modified. *fused = 0 when the shape has no
+ * fused kernel (head_dim != 128, n_heads / n_kv_heads not 1, 2 or 4, pointers
+ * not 16-byte aligned): nothing ran. No counterpart in the reference
+ * (src/qwen3_gpu.cu:77-96 runs these as separate launches). */
+RPG_OPS_API int32_t rpg_op_qk_norm_rope_kv_attention(const float* q, const float* k, const float* v,
+                                                     const float* q_norm, const float* k_norm, int32_t n_heads,
+                                                     int32_t n_kv_heads, int32_t head_dim, const float* rope_tab,
+                                                     int64_t rope_rows, int64_t pos0, float eps, uint16_t* k_layer,
+                                                     uint16_t* v_layer, int64_t max_seq, float* out,
+                                                     int64_t sh_positions, int32_t* fused);
+
 /* Pre-sizes the attention's partials buffer for graph capture.
  * Replaces: GpuAttentionWarmupShmem, src/kernels_gpu.h:128. */
 RPG_OPS_API int32_t rpg_op_attention_warmup(int64_t sh_positions);

@@ -194,6 +194,26 @@ int32_t rpg_op_attention_from_cache(const float* q, int32_t n_heads, int32_t n_k
   });
 }
 
+int32_t rpg_op_qk_norm_rope_kv_attention(const float* q, const float* k, const float* v, const float* q_norm,
+                                         const float* k_norm, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                         const float* rope_tab, int64_t rope_rows, int64_t pos0, float eps,
+                                         uint16_t* k_layer, uint16_t* v_layer, int64_t max_seq, float* out,
+                                         int64_t sh_positions, int32_t* fused) {
+  return Guard([&] {
+    RPG_CHECK(fused != nullptr, "qk_norm_rope_kv_attention: null flag");
+    *fused = 0;
+    rpg::ModelMeta c;
+    c.n_heads = n_heads;
+    c.n_kv_heads = n_kv_heads;
+    c.head_dim = head_dim;
+    c.rms_eps = eps;
+    *fused = rpg::GpuQkNormRopeKvAttention(c, pos0, q, k, v, q_norm, k_norm, rope_tab, rope_rows, k_layer, v_layer,
+                                           max_seq, out, sh_positions)
+                 ? 1
+                 : 0;
+  });
+}
+
 int32_t rpg_op_attention_warmup(int64_t sh_positions) {
   return Guard([&] { rpg::GpuAttentionWarmupShmem(sh_positions); });
 }

@@ -34,6 +34,7 @@
 #include <mutex>
 
 #include "dev_util.h"
+#include "head_row.h"
 #include "kernels_gpu.h"
 #include "launch.h"
 
@@ -289,11 +290,40 @@ __global__ __launch_bounds__(kBlockThreads) void AttnMergeKernel(const float* __
 // key counted once), and V rows are accumulated with the probability of key
 // base + 4 i + r taken from lane 16 r + 2 i; the four rows' partial outputs are
 // summed at the end.
-template <int G>
+//
+// kPrep (one token): q, k and v arrive as the projections' raw rows and the
+// wave first does what QkNormRopeKvKernel does for its kv head, with the same
+// routines on the same 8-lane head layout (so the same bits): 8-lane group g
+// < G takes query head kh G + g, group G the k row, group G + 1 the v row;
+// q and k get the per-head RMSNorm and the RoPE rotation at pos, k and v are
+// rounded to fp16. The wave of the chunk that holds pos stores the new K / V
+// rows into the cache and uses them for that key straight from LDS (the store
+// need not be visible to its own loads); the other chunks never read key pos.
+struct DecodePrep {
+  const float* k;
+  const float* v;
+  const float* q_norm;
+  const float* k_norm;
+  const float* tab;
+  int64_t rope_rows;
+  float eps;
+  uint16_t* k_store;
+  uint16_t* v_store;
+};
+
+template <int G, bool kPrep = false>
 __global__ __launch_bounds__(kBlockThreads) void AttnDecodeGroupKernel(
     const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t max_seq,
     int32_t n_heads, int32_t n_kv_heads, float scale, int64_t pos0_val, const int64_t* __restrict__ pos0_dev,
-    int64_t seq, int32_t n_chunks, int64_t chunk_len, float* __restrict__ out, float* __restrict__ part) {
+    int64_t seq, int32_t n_chunks, int64_t chunk_len, float* __restrict__ out, float* __restrict__ part,
+    DecodePrep prep) {
+  static_assert(!kPrep || G + 2 <= 8, "q heads, k and v: one 8-lane group each");
+  struct PrepLds {
+    float q[G][kD];
+    uint16_t k[kD];
+    uint16_t v[kD];
+  };
+  __shared__ __attribute__((aligned(16))) PrepLds prep_lds[kPrep ? kWaves : 1];
   const int lane = threadIdx.x & 63;
   const int64_t unit = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
   if (unit >= seq * n_kv_heads * n_chunks) return;  // no barriers below
@@ -311,15 +341,62 @@ __global__ __launch_bounds__(kBlockThreads) void AttnDecodeGroupKernel(
   if (hi > max_seq) hi = max_seq;  // only reachable through a replayed graph with a bad staged pos0
   const int rho = lane & 15;
   const int r = lane >> 4;
+  const bool writer = kPrep && c == live - 1;  // the chunk that holds key pos
 
   float qv[G][8];
+  uint4 knew = make_uint4(0u, 0u, 0u, 0u), vnew = make_uint4(0u, 0u, 0u, 0u);
+  if (kPrep) {
+    PrepLds& P = prep_lds[threadIdx.x >> 6];
+    const int g = lane >> 3;
+    const int hl = lane & 7;
+    const bool is_q = g < G, is_k = g == G, is_v = g > G;
+    const float* src = is_q ? q + (t * n_heads + kh * G + g) * kD
+                            : (is_k ? prep.k : prep.v) + (t * n_kv_heads + kh) * kD;
+    const bool rope_ok = pos >= 0 && pos < prep.rope_rows;
+    dev::HeadRow row = dev::LoadHeadVec(src, hl);
+    const dev::HeadRow trig = dev::LoadHeadVec(prep.tab + (rope_ok ? pos : 0) * kD, hl);
+    const dev::HeadRow w = dev::LoadHeadVec(is_q ? prep.q_norm : prep.k_norm, hl);
+    if (!is_v) {  // uniform over each 8-lane group
+      dev::NormHeadRow(row, w, prep.eps);
+      dev::RotateHeadRow(row, trig, rope_ok);
+    }
+    if (is_q) {
 #pragma unroll
-  for (int hh = 0; hh < G; ++hh) {
-    const float* qr = q + (t * n_heads + kh * G + hh) * kD + 8 * rho;
-    const float4 a = *reinterpret_cast<const float4*>(qr);
-    const float4 b = *reinterpret_cast<const float4*>(qr + 4);
-    qv[hh][0] = a.x; qv[hh][1] = a.y; qv[hh][2] = a.z; qv[hh][3] = a.w;
-    qv[hh][4] = b.x; qv[hh][5] = b.y; qv[hh][6] = b.z; qv[hh][7] = b.w;
+      for (int cc = 0; cc < 2; ++cc) {
+        *reinterpret_cast<float4*>(&P.q[g][dev::HeadOffset(hl, cc)]) = row.a[cc];
+        *reinterpret_cast<float4*>(&P.q[g][64 + dev::HeadOffset(hl, cc)]) = row.b[cc];
+      }
+    } else if (g <= G + 1) {
+      uint16_t* dst = is_k ? P.k : P.v;
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        *reinterpret_cast<uint2*>(&dst[dev::HeadOffset(hl, cc)]) = dev::PackHalf4(row.a[cc]);
+        *reinterpret_cast<uint2*>(&dst[64 + dev::HeadOffset(hl, cc)]) = dev::PackHalf4(row.b[cc]);
+      }
+      if (writer && pos >= 0 && pos < max_seq) {
+        uint16_t* cache = (is_k ? prep.k_store : prep.v_store) + (static_cast<int64_t>(kh) * max_seq + pos) * kD;
+        dev::StoreHeadRowHalf(cache, hl, row);
+      }
+    }
+    // the wave's own LDS writes, read back by other lanes of the same wave
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) {
+      const float4 a = *reinterpret_cast<const float4*>(&P.q[hh][8 * rho]);
+      const float4 b = *reinterpret_cast<const float4*>(&P.q[hh][8 * rho + 4]);
+      qv[hh][0] = a.x; qv[hh][1] = a.y; qv[hh][2] = a.z; qv[hh][3] = a.w;
+      qv[hh][4] = b.x; qv[hh][5] = b.y; qv[hh][6] = b.z; qv[hh][7] = b.w;
+    }
+    knew = *reinterpret_cast<const uint4*>(&P.k[8 * rho]);
+    vnew = *reinterpret_cast<const uint4*>(&P.v[8 * rho]);
+  } else {
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) {
+      const float* qr = q + (t * n_heads + kh * G + hh) * kD + 8 * rho;
+      const float4 a = *reinterpret_cast<const float4*>(qr);
+      const float4 b = *reinterpret_cast<const float4*>(qr + 4);
+      qv[hh][0] = a.x; qv[hh][1] = a.y; qv[hh][2] = a.z; qv[hh][3] = a.w;
+      qv[hh][4] = b.x; qv[hh][5] = b.y; qv[hh][6] = b.z; qv[hh][7] = b.w;
+    }
   }
   float m[G], l[G], o[G][8];
 #pragma unroll
@@ -340,6 +417,10 @@ __global__ __launch_bounds__(kBlockThreads) void AttnDecodeGroupKernel(
       key = key < hi ? key : hi - 1;  // clamped rows get probability 0
       kw[i] = *reinterpret_cast<const uint4*>(kb + key * kD);
       vw[i] = *reinterpret_cast<const uint4*>(vb + key * kD);
+      if (writer && key == pos) {  // the row this launch stores: from LDS, not the cache
+        kw[i] = knew;
+        vw[i] = vnew;
+      }
     }
     const int64_t skey = base + 4 * (rho >> 1) + r;  // the key whose score this lane ends with
     const bool valid = skey < hi;
@@ -741,7 +822,7 @@ size_t WarmupFloats(int64_t /*positions*/) { return static_cast<size_t>(64) * kM
 template <int G>
 void LaunchDecodeGroup(const ModelMeta& c, const Pos0Arg& p0, const float* q_dev, int64_t seq,
                        const uint16_t* k_layer, const uint16_t* v_layer, int64_t max_seq, float scale,
-                       int64_t positions, float* out_dev) {
+                       int64_t positions, float* out_dev, const DecodePrep* prep = nullptr) {
   int32_t n_chunks;
   int64_t chunk_len;
   PlanGroupChunks(seq * c.n_kv_heads, positions, &n_chunks, &chunk_len);
@@ -749,9 +830,15 @@ void LaunchDecodeGroup(const ModelMeta& c, const Pos0Arg& p0, const float* q_dev
   float* part = nullptr;
   if (n_chunks > 1) part = EnsurePartials(static_cast<size_t>(pairs) * n_chunks * kPartFloats);
   const int64_t units = seq * c.n_kv_heads * n_chunks;
-  Launch("AttnDecodeGroupKernel", AttnDecodeGroupKernel<G>, dim3(GridFor(units, kWaves)), dim3(kBlockThreads), q_dev,
-         k_layer, v_layer, max_seq, c.n_heads, c.n_kv_heads, scale, p0.value, p0.dev, seq, n_chunks, chunk_len,
-         out_dev, part);
+  if (prep != nullptr) {
+    Launch("AttnDecodePrepKernel", AttnDecodeGroupKernel<G, true>, dim3(GridFor(units, kWaves)),
+           dim3(kBlockThreads), q_dev, k_layer, v_layer, max_seq, c.n_heads, c.n_kv_heads, scale, p0.value, p0.dev,
+           seq, n_chunks, chunk_len, out_dev, part, *prep);
+  } else {
+    Launch("AttnDecodeGroupKernel", AttnDecodeGroupKernel<G>, dim3(GridFor(units, kWaves)), dim3(kBlockThreads),
+           q_dev, k_layer, v_layer, max_seq, c.n_heads, c.n_kv_heads, scale, p0.value, p0.dev, seq, n_chunks,
+           chunk_len, out_dev, part, DecodePrep{});
+  }
   if (n_chunks > 1) {
     Launch("AttnMergeKernel", AttnMergeKernel, dim3(GridFor(pairs, kWaves)), dim3(kBlockThreads), part, pairs,
            n_chunks, c.n_heads, chunk_len, p0.value, p0.dev, out_dev);
@@ -811,6 +898,37 @@ void GpuAttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev,
     Launch("AttnMergeKernel", AttnMergeKernel, dim3(GridFor(pairs, kWaves)), dim3(kBlockThreads), part, pairs,
            n_chunks, c.n_heads, chunk_len, p0.value, p0.dev, out_dev);
   }
+}
+
+bool GpuQkNormRopeKvAttention(const ModelMeta& c, int64_t pos0, const float* q_dev, const float* k_dev,
+                              const float* v_dev, const float* q_norm, const float* k_norm, const float* rope_tab,
+                              int64_t rope_rows, uint16_t* k_layer, uint16_t* v_layer, int64_t max_seq,
+                              float* out_dev, int64_t sh_positions) {
+  RPG_CHECK(pos0 >= 0, "pos0 must not be negative");
+  RPG_CHECK(c.n_heads > 0 && c.n_kv_heads > 0 && c.n_heads % c.n_kv_heads == 0,
+            "n_heads (%d) must be a positive multiple of n_kv_heads (%d)", c.n_heads, c.n_kv_heads);
+  RPG_CHECK(pos0 + 1 <= max_seq, "position %lld exceeds the cache capacity %lld", static_cast<long long>(pos0),
+            static_cast<long long>(max_seq));
+  RPG_CHECK(pos0 + 1 <= rope_rows, "position %lld exceeds the RoPE table (%lld rows)", static_cast<long long>(pos0),
+            static_cast<long long>(rope_rows));
+  const int64_t positions = sh_positions > 0 ? sh_positions : pos0 + 1;
+  RPG_CHECK(positions >= pos0 + 1, "position budget (%lld) is smaller than the positions this call needs (%lld)",
+            static_cast<long long>(positions), static_cast<long long>(pos0 + 1));
+  RPG_CHECK(q_dev && k_dev && v_dev && q_norm && k_norm && rope_tab && k_layer && v_layer && out_dev,
+            "QkNormRopeKvAttention got a null pointer");
+  const int group = c.n_heads / c.n_kv_heads;
+  auto a16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  if (c.head_dim != kD || !(group == 1 || group == 2 || group == 4) || !a16(q_dev) || !a16(k_dev) || !a16(v_dev) ||
+      !a16(q_norm) || !a16(k_norm) || !a16(rope_tab) || !a16(k_layer) || !a16(v_layer) || !a16(out_dev)) {
+    return false;
+  }
+  const float scale = 1.0f / sqrtf(static_cast<float>(c.head_dim));
+  const Pos0Arg p0 = Pos0ForLaunch(pos0);
+  const DecodePrep prep{k_dev, v_dev, q_norm, k_norm, rope_tab, rope_rows, c.rms_eps, k_layer, v_layer};
+  if (group == 1) LaunchDecodeGroup<1>(c, p0, q_dev, 1, k_layer, v_layer, max_seq, scale, positions, out_dev, &prep);
+  if (group == 2) LaunchDecodeGroup<2>(c, p0, q_dev, 1, k_layer, v_layer, max_seq, scale, positions, out_dev, &prep);
+  if (group == 4) LaunchDecodeGroup<4>(c, p0, q_dev, 1, k_layer, v_layer, max_seq, scale, positions, out_dev, &prep);
+  return true;
 }
 
 void GpuCausalAttention(const ModelMeta& c, const float* q_dev, const float* k_dev, const float* v_dev, int64_t seq,

@@ -192,6 +192,21 @@ void GpuEmbeddingLookupRaw(uint32_t type, const uint8_t* emb_dev, int64_t rows, 
 void GpuAttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev, int64_t seq, const uint16_t* k_layer,
                            const uint16_t* v_layer, int64_t max_seq, float* out_dev, int64_t sh_positions = -1);
 
+// One token at position pos0: GpuQkNormRopeKv (q / k per-head RMSNorm with
+// q_norm / k_norm and eps = c.rms_eps, RoPE at pos0, k and v rounded to fp16
+// into k_layer / v_layer at pos0) and GpuAttentionFromCache in one decode launch
+// (plus the chunk merge when the keys are split), bit-identical to the two
+// calls; q, k, v are the projections' raw [heads][128] rows and are not
+// modified. Returns false, having launched nothing, when the shape has no fused
+// kernel (head_dim != 128, a GQA group other than 1, 2, 4, pointers not 16-byte
+// aligned); the caller then makes the two calls. No counterpart in the
+// reference (src/qwen3_gpu.cu:77-96 runs norm, RoPE, KV write and attention as
+// separate launches).
+bool GpuQkNormRopeKvAttention(const ModelMeta& c, int64_t pos0, const float* q_dev, const float* k_dev,
+                              const float* v_dev, const float* q_norm, const float* k_norm, const float* rope_tab,
+                              int64_t rope_rows, uint16_t* k_layer, uint16_t* v_layer, int64_t max_seq,
+                              float* out_dev, int64_t sh_positions = -1);
+
 // Causal attention without a cache (src/kernels_gpu.h:82-84): the same maths
 // over the segment's own fp32 rows, k / v [seq][n_kv_heads][head_dim], token t
 // attending to tokens 0..t. The no-cache forward uses it; the difference from

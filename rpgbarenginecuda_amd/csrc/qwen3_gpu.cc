@@ -101,12 +101,19 @@ void ForwardLayer(const GpuModel& m, int32_t layer, int64_t pos0, GpuScratch* s,
   const float* qn = static_cast<const float*>(w.q_norm.buf.data());
   const float* kn = static_cast<const float*>(w.k_norm.buf.data());
   if (kv != nullptr) {
-    // the segment's K/V must be in the cache before attention reads it: token t
-    // attends to positions <= pos0 + t, including those written just now
-    GpuQkNormRopeKv(q, k, v, qn, kn, c.n_heads, c.n_kv_heads, hd, m.rope_dev(), m.rope_positions(), pos0, seq,
-                    c.rms_eps, kv->k_layer(layer), kv->v_layer(layer), kv->max_seq(), false);
-    GpuAttentionFromCache(c, pos0, q, seq, kv->k_layer(layer), kv->v_layer(layer), kv->max_seq(), attn,
-                          attn_sh_positions);
+    // One token: norm, RoPE, the K/V store and attention in one decode launch.
+    const bool fused = seq == 1 && GpuQkNormRopeKvAttention(c, pos0, q, k, v, qn, kn, m.rope_dev(),
+                                                            m.rope_positions(), kv->k_layer(layer),
+                                                            kv->v_layer(layer), kv->max_seq(), attn,
+                                                            attn_sh_positions);
+    if (!fused) {
+      // the segment's K/V must be in the cache before attention reads it: token t
+      // attends to positions <= pos0 + t, including those written just now
+      GpuQkNormRopeKv(q, k, v, qn, kn, c.n_heads, c.n_kv_heads, hd, m.rope_dev(), m.rope_positions(), pos0, seq,
+                      c.rms_eps, kv->k_layer(layer), kv->v_layer(layer), kv->max_seq(), false);
+      GpuAttentionFromCache(c, pos0, q, seq, kv->k_layer(layer), kv->v_layer(layer), kv->max_seq(), attn,
+                            attn_sh_positions);
+    }
   } else {
     GpuRmsNorm(q, qn, seq * c.n_heads, hd, hd, c.rms_eps, q);
     GpuRmsNorm(k, kn, seq * c.n_kv_heads, hd, hd, c.rms_eps, k);

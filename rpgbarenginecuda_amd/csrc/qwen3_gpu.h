@@ -19,7 +19,8 @@
 //     (GpuNormMatMulQuantGroup / GpuNormMatMulQuantSwiGLU), and the residual
 //     alternates between x and x_alt;
 //   * q / k RMSNorm, RoPE and the fp16 K/V store run as one pass
-//     (GpuQkNormRopeKv) on the cache path;
+//     (GpuQkNormRopeKv) on the cache path, and at one token inside the
+//     attention launch (GpuQkNormRopeKvAttention);
 //   * q / k / v go through GpuMatMulQuantGroup (at one token one launch per
 //     same-type run, bit-identical to separate calls), and gate / up with the
 //     SwiGLU through GpuMatMulQuantSwiGLU (at one token one launch that writes

@@ -89,6 +89,8 @@ SIGNATURES = {
     "rpg_op_embedding_lookup": (_i32, [_u32, _vp, _i64, _i64, _vp, _i64, _vp]),
     "rpg_op_matmul_quant": (_i32, [_u32, _vp, _i64, _i64, _vp, _i64, _vp]),
     "rpg_op_attention_from_cache": (_i32, [_vp, _i32, _i32, _i32, _i64, _i64, _vp, _vp, _i64, _vp, _i64]),
+    "rpg_op_qk_norm_rope_kv_attention": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _f32,
+                                                _vp, _vp, _i64, _vp, _i64, _vp]),
     "rpg_op_attention_warmup": (_i32, [_i64]),
     "rpg_op_add_rms_norm": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _vp]),
     "rpg_op_qk_norm_rope_kv": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _i64, _f32,
@@ -400,6 +402,25 @@ def GpuAttentionFromCache(n_heads: int, n_kv_heads: int, head_dim: int, pos0: in
         _addr(q, span, torch.float32, "q"), n_heads, n_kv_heads, head_dim, pos0, seq,
         _addr(k_layer, cache, name="k_layer"), _addr(v_layer, cache, name="v_layer"), max_seq,
         _addr(out, span, torch.float32, "out"), sh_positions))
+
+
+def GpuQkNormRopeKvAttention(n_heads: int, n_kv_heads: int, head_dim: int, pos0: int, q, k, v, q_norm, k_norm,
+                             rope_tab, rope_rows: int, eps: float, k_layer, v_layer, max_seq: int, out,
+                             sh_positions: int = -1) -> bool:
+    """One token: GpuQkNormRopeKv + GpuAttentionFromCache in one decode launch (no reference counterpart); q, k, v
+    are the raw projections and stay unchanged. Returns False, having launched nothing, when the shape has no
+    fused kernel."""
+    torch = _t()
+    cache = 2 * n_kv_heads * max_seq * head_dim
+    fused = ctypes.c_int32(0)
+    _check(load_library().rpg_op_qk_norm_rope_kv_attention(
+        _addr(q, 4 * n_heads * head_dim, torch.float32, "q"), _addr(k, 4 * n_kv_heads * head_dim, torch.float32, "k"),
+        _addr(v, 4 * n_kv_heads * head_dim, torch.float32, "v"), _addr(q_norm, 4 * head_dim, torch.float32, "q_norm"),
+        _addr(k_norm, 4 * head_dim, torch.float32, "k_norm"), n_heads, n_kv_heads, head_dim,
+        _addr(rope_tab, 4 * rope_rows * head_dim, torch.float32, "rope_tab"), rope_rows, pos0, eps,
+        _addr(k_layer, cache, name="k_layer"), _addr(v_layer, cache, name="v_layer"), max_seq,
+        _addr(out, 4 * n_heads * head_dim, torch.float32, "out"), sh_positions, ctypes.byref(fused)))
+    return bool(fused.value)
 
 
 def GpuAttentionWarmupShmem(sh_positions: int) -> None:

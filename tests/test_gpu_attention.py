@@ -183,3 +183,115 @@ def test_attention_rejects_bad_arguments(gpu):
         gpu.GpuAttentionFromCache(16, 6, 128, 0, q, 1, kc, kc, 64, out)
     with pytest.raises(gpu.RpgError, match="head_dim"):
         gpu.GpuAttentionFromCache(16, 8, 64, 0, q, 1, kc, kc, 64, out)
+
+
+# GpuQkNormRopeKvAttention: at one token the q/k norm, RoPE and the K/V store run
+# inside the decode attention launch with the same routines as GpuQkNormRopeKv,
+# so the output and the whole cache must be bit-identical to the two calls.
+FUSED = [
+    # (name, n_heads, n_kv_heads, max_seq, pos0)
+    ("1.7B at 0", 16, 8, 4096, 0),
+    ("1.7B at 21", 16, 8, 4096, 21),
+    ("1.7B at 127 (last single-chunk position)", 16, 8, 4096, 127),
+    ("1.7B at 128 (first split)", 16, 8, 4096, 128),
+    ("1.7B at 2731", 16, 8, 4096, 2731),
+    ("1.7B at 4095 (full cache)", 16, 8, 4096, 4095),
+    ("4B at 1000", 32, 8, 4096, 1000),
+    ("MHA at 1999", 8, 8, 2048, 1999),
+]
+
+
+def _fused_inputs(gpu, rng, nh, nkv, max_seq):
+    q = dev(rng.normal(0, 2, (1, nh, 128)).astype(np.float32))
+    k = dev(rng.normal(0, 2, (1, nkv, 128)).astype(np.float32))
+    v = dev(rng.normal(0, 1, (1, nkv, 128)).astype(np.float32))
+    qn = dev(rng.normal(1, 0.1, 128).astype(np.float32))
+    kn = dev(rng.normal(1, 0.1, 128).astype(np.float32))
+    tab = dev(gpu.build_rope_table(128, 1e6, max_seq))
+    _, kc, vc = make(rng, nh, nkv, max_seq, 1)
+    return q, k, v, qn, kn, tab, dev(kc), dev(vc)
+
+
+def _two_calls(gpu, nh, nkv, max_seq, pos0, q, k, v, qn, kn, tab, kc, vc, sh=-1):
+    import torch
+
+    qa, ka = q.clone(), k.clone()
+    out = torch.full((1, nh, 128), np.nan, dtype=torch.float32, device="cuda")
+    gpu.GpuQkNormRopeKv(qa, ka, v, qn, kn, nh, nkv, 128, tab, max_seq, pos0, 1, 1e-6, kc, vc, max_seq)
+    gpu.GpuAttentionFromCache(nh, nkv, 128, pos0, qa, 1, kc, vc, max_seq, out, sh)
+    return out
+
+
+@pytest.mark.parametrize("name,nh,nkv,max_seq,pos0", FUSED, ids=[f[0] for f in FUSED])
+def test_qk_norm_rope_kv_attention_equals_two_calls(gpu, ora, name, nh, nkv, max_seq, pos0):
+    import torch
+
+    case(f"fused q/k prep + attention {name}")
+    rng = np.random.default_rng(2100 + pos0 + nh)
+    q, k, v, qn, kn, tab, kc, vc = _fused_inputs(gpu, rng, nh, nkv, max_seq)
+    kc2, vc2 = kc.clone(), vc.clone()
+    want = _two_calls(gpu, nh, nkv, max_seq, pos0, q, k, v, qn, kn, tab, kc, vc)
+    q0, k0, v0 = q.clone(), k.clone(), v.clone()
+    out = torch.full((1, nh, 128), np.nan, dtype=torch.float32, device="cuda")
+    assert gpu.GpuQkNormRopeKvAttention(nh, nkv, 128, pos0, q, k, v, qn, kn, tab, max_seq, 1e-6, kc2, vc2, max_seq,
+                                        out)
+    torch.cuda.synchronize()
+    assert torch.equal(out, want)
+    assert torch.equal(kc2, kc) and torch.equal(vc2, vc)  # the new row at pos0, nothing else touched
+    assert torch.equal(q, q0) and torch.equal(k, k0) and torch.equal(v, v0)
+    # and the attention itself against the float64 oracle on the stored operands
+    qa = q.clone()
+    gpu.GpuQkNormRopeKv(qa, k.clone(), v, qn, kn, nh, nkv, 128, tab, max_seq, pos0, 1, 1e-6, kc.clone(), vc.clone(),
+                        max_seq)
+    ref, smag, vmax = ora.attention_f64(host(qa), host(kc), host(vc), max_seq, nh, nkv, 128, pos0, 1)
+    check(host(out), ref, smag, vmax, pos0)
+
+
+def test_qk_norm_rope_kv_attention_without_fused_form(gpu):
+    """A GQA group of 8 has no fused kernel: nothing runs and the caller is told."""
+    import torch
+
+    case("fused q/k prep + attention: group 8")
+    rng = np.random.default_rng(2200)
+    nh, nkv, max_seq = 64, 8, 512
+    q, k, v, qn, kn, tab, kc, vc = _fused_inputs(gpu, rng, nh, nkv, max_seq)
+    kc0 = kc.clone()
+    out = torch.full((1, nh, 128), np.nan, dtype=torch.float32, device="cuda")
+    assert not gpu.GpuQkNormRopeKvAttention(nh, nkv, 128, 7, q, k, v, qn, kn, tab, max_seq, 1e-6, kc, vc, max_seq,
+                                            out)
+    torch.cuda.synchronize()
+    assert torch.isnan(out).all() and torch.equal(kc, kc0)
+
+
+def test_qk_norm_rope_kv_attention_graph_replay(gpu):
+    """Captured once with the whole cache as the position budget; each replay
+    reads pos0 from the staging scalar, writes that row and attends up to it,
+    bit-identical to the two eager calls at the same position."""
+    import torch
+
+    case("fused q/k prep + attention graph replay")
+    nh, nkv, max_seq = 16, 8, 1024
+    rng = np.random.default_rng(2300)
+    q, k, v, qn, kn, tab, kc, vc = _fused_inputs(gpu, rng, nh, nkv, max_seq)
+    kc2, vc2 = kc.clone(), vc.clone()
+    out = torch.empty((1, nh, 128), dtype=torch.float32, device="cuda")
+    gpu.init()
+    gpu.GpuAttentionWarmupShmem(max_seq)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with gpu.ScopedEngineStream(s):
+            g.capture_begin()
+            assert gpu.GpuQkNormRopeKvAttention(nh, nkv, 128, 5, q, k, v, qn, kn, tab, max_seq, 1e-6, kc2, vc2,
+                                                max_seq, out, max_seq)
+            g.capture_end()
+    torch.cuda.synchronize()
+    for pos in (5, 17, 127, 128, 640, 1023, 64):
+        want = _two_calls(gpu, nh, nkv, max_seq, pos, q, k, v, qn, kn, tab, kc, vc, sh=max_seq)  # same chunk plan
+        gpu.stage_pos0(pos)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), pos
+        assert torch.equal(kc2, kc) and torch.equal(vc2, vc), pos
