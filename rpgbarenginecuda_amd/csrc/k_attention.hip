@@ -342,6 +342,24 @@ __global__ __launch_bounds__(kBlockThreads) void AttnDecodeGroupKernel(
   const int rho = lane & 15;
   const int r = lane >> 4;
   const bool writer = kPrep && c == live - 1;  // the chunk that holds key pos
+  const uint16_t* kb = kc + static_cast<int64_t>(kh) * max_seq * kD + 8 * rho;
+  const uint16_t* vb = vc + static_cast<int64_t>(kh) * max_seq * kD + 8 * rho;
+  // A slab of 32 keys; rows past hi are clamped to hi - 1 (always a valid
+  // address; their probability is 0). With kPipe the next slab's rows are
+  // loaded while this one is scored (G <= 2: the second set of 16 registers per
+  // row fits), and the first slab is requested before anything else.
+  constexpr bool kPipe = G <= 2;
+  auto load_slab = [&](int64_t base, uint4 (&kw)[8], uint4 (&vw)[8]) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      int64_t key = base + 4 * i + r;
+      key = key < hi ? key : hi - 1;
+      kw[i] = *reinterpret_cast<const uint4*>(kb + key * kD);
+      vw[i] = *reinterpret_cast<const uint4*>(vb + key * kD);
+    }
+  };
+  uint4 kw[8], vw[8];
+  if (kPipe) load_slab(lo, kw, vw);
 
   float qv[G][8];
   uint4 knew = make_uint4(0u, 0u, 0u, 0u), vnew = make_uint4(0u, 0u, 0u, 0u);
@@ -406,20 +424,24 @@ __global__ __launch_bounds__(kBlockThreads) void AttnDecodeGroupKernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[hh][j] = 0.0f;
   }
-  const uint16_t* kb = kc + static_cast<int64_t>(kh) * max_seq * kD + 8 * rho;
-  const uint16_t* vb = vc + static_cast<int64_t>(kh) * max_seq * kD + 8 * rho;
 
   for (int64_t base = lo; base < hi; base += 32) {
-    uint4 kw[8], vw[8];
+    uint4 kn[8], vn[8];
+    if (kPipe) {
+      load_slab(base + 32, kn, vn);  // past hi: clamped rows, not used
+      __builtin_amdgcn_sched_barrier(0);  // keep the next slab's loads ahead of this slab's scores
+    } else {
+      load_slab(base, kw, vw);
+    }
+    if (writer) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      int64_t key = base + 4 * i + r;
-      key = key < hi ? key : hi - 1;  // clamped rows get probability 0
-      kw[i] = *reinterpret_cast<const uint4*>(kb + key * kD);
-      vw[i] = *reinterpret_cast<const uint4*>(vb + key * kD);
-      if (writer && key == pos) {  // the row this launch stores: from LDS, not the cache
-        kw[i] = knew;
-        vw[i] = vnew;
+      for (int i = 0; i < 8; ++i) {
+        int64_t key = base + 4 * i + r;
+        key = key < hi ? key : hi - 1;
+        if (key == pos) {  // the row this launch stores: from LDS, not the cache
+          kw[i] = knew;
+          vw[i] = vnew;
+        }
       }
     }
     const int64_t skey = base + 4 * (rho >> 1) + r;  // the key whose score this lane ends with
@@ -487,6 +509,13 @@ __global__ __launch_bounds__(kBlockThreads) void AttnDecodeGroupKernel(
         const float pi = __shfl(p[hh], 16 * r + 2 * i, 64);  // probability of key base + 4 i + r
 #pragma unroll
         for (int j = 0; j < 8; ++j) o[hh][j] = __builtin_fmaf(pi, vf[j], o[hh][j]);
+      }
+    }
+    if (kPipe) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        kw[i] = kn[i];
+        vw[i] = vn[i];
       }
     }
   }

@@ -38,6 +38,8 @@ CONFIGS = {
     "h512_g4_tied": dict(n_layers=2, hidden=512, n_heads=4, n_kv_heads=1, inter=1024, vocab=3000, tied=True),
     "h256_g3": dict(n_layers=2, hidden=256, n_heads=6, n_kv_heads=2, inter=512, vocab=1000),
     "qwen3_1_7b_2layers": dict(n_layers=2, hidden=2048, n_heads=16, n_kv_heads=8, inter=6144, vocab=4096),
+    # rows of 10 blocks (the 4B hidden size): one-token steps take the unfused norm + matmul path
+    "h2560_g4_1layer": dict(n_layers=1, hidden=2560, n_heads=16, n_kv_heads=4, inter=1024, vocab=1500),
 }
 
 
@@ -148,7 +150,7 @@ def test_kv_self_check(gpu, models, name, seq):
     s.free()
 
 
-@pytest.mark.parametrize("name", ["h256_g2", "h512_g4_tied", "h256_g3"])
+@pytest.mark.parametrize("name", ["h256_g2", "h512_g4_tied", "h256_g3", "h2560_g4_1layer"])
 def test_prefill_pieces_and_decode_steps_match_oracle(gpu, models, name):
     """Segments at pos0 > 0 (one of them >= 64 tokens, the matrix-core attention)
     and single-token steps, each against the oracle's cached forward."""
