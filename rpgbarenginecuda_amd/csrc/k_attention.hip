@@ -555,7 +555,9 @@ __global__ __launch_bounds__(kBlockThreads) void AttnDecodeGroupKernel(
 //
 // Flash attention with v_mfma_f32_32x32x16_f16. One workgroup = one query head
 // and 128 consecutive tokens, 4 waves of 32 tokens; keys in blocks of 64 staged
-// in LDS (K as [key][dim], V transposed to [dim][key]) and shared by the waves.
+// in LDS as [key][dim] rows (16-byte writes) and shared by the waves; the V^T
+// fragments of the P.V step come out of the V rows through the transposing
+// LDS read (ds_read_b64_tr_b16).
 // Per wave and block:
 //   S^T (64 keys x 32 queries) = K . Q^T    2 key tiles x 8 dim steps x 2 terms
 //   O^T (128 dims x 32 queries) += V^T . P^T  4 dim tiles x 4 key steps x 2 terms
@@ -563,7 +565,7 @@ __global__ __launch_bounds__(kBlockThreads) void AttnDecodeGroupKernel(
 // l % 32 (its running max, sum and rescale are lane values; lanes l and l + 32
 // hold the two halves of the keys), and the S^T accumulator registers 0-7 / 8-15
 // are already the B operand of the P.V step for the keys they hold, provided
-// V^T is read in the same key order.
+// the V^T fragments follow the same key order.
 // Exact operands: K and V are fp16 cache values. q (fp32) is scaled per row by
 // 2^e (max |q| into [64, 128)) and split into two fp16 terms h + m that
 // reproduce it to ~2^-23 relative (a score error ~65x inside the fp32
@@ -578,7 +580,17 @@ typedef float F32x16 __attribute__((ext_vector_type(16)));
 constexpr int kFaTokens = 128;    // tokens (of one head) per workgroup
 constexpr int kFaKeys = 64;       // keys per LDS block
 constexpr int kFaKStride = 136;   // halves per K row in LDS (128 + 8: conflict-free 16-byte reads)
-constexpr int kFaVtStride = 68;   // halves per V^T row in LDS (64 + 4)
+constexpr int kFaVStride = 160;   // halves per V row in LDS (128 + 32: conflict-free transposing reads)
+
+// ds_read_b64_tr_b16: in each 16-lane group, lane j receives element j % 4 of
+// the 8 bytes addressed by lanes j / 4, 4 + j / 4, 8 + j / 4, 12 + j / 4.
+typedef short S16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ F16x4 VTr(const _Float16* lds_ptr) {
+  typedef __attribute__((address_space(3))) S16x4 LdsS16x4;
+  const S16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (LdsS16x4*)((__attribute__((address_space(3))) _Float16*)(lds_ptr)));
+  return __builtin_bit_cast(F16x4, v);
+}
 
 __device__ __forceinline__ F16x8 SplitTerm(float (&x)[8]) {
   // x <- x - fp16(x), returning fp16(x) (round to nearest even; the difference is exact in fp32)
@@ -596,7 +608,7 @@ __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
     int32_t n_heads, int32_t group, float scale, int64_t pos0_val, const int64_t* __restrict__ pos0_dev, int64_t seq,
     float* __restrict__ out) {
   __shared__ __attribute__((aligned(16))) _Float16 ks[kFaKeys * kFaKStride];
-  __shared__ __attribute__((aligned(16))) _Float16 vts[kD * kFaVtStride];
+  __shared__ __attribute__((aligned(16))) _Float16 vs[kFaKeys * kFaVStride];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int hf = lane >> 5;    // which half of the keys / dims this lane holds
@@ -674,15 +686,7 @@ __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&ks[key * kFaKStride + 32 * part + 8 * i]) = kw[i];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t w4[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          const int d = 32 * part + 8 * i + 2 * k;
-          vts[d * kFaVtStride + key] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(w4[k] & 0xFFFFu));
-          vts[(d + 1) * kFaVtStride + key] = __builtin_bit_cast(_Float16, static_cast<uint16_t>(w4[k] >> 16));
-        }
-      }
+      for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&vs[key * kFaVStride + 32 * part + 8 * i]) = vw[i];
     }
     __syncthreads();
     if (kb > wave_last) continue;  // every query of this wave is before the block (uniform per wave)
@@ -743,9 +747,14 @@ __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
       const int koff = 32 * mt + 16 * (ks2 & 1) + 4 * hf;  // keys koff + 0..3 and koff + 8..11
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const _Float16* vrow = &vts[(32 * dt + col) * kFaVtStride];
-        const F16x4 lo = *reinterpret_cast<const F16x4*>(vrow + koff);
-        const F16x4 hi = *reinterpret_cast<const F16x4*>(vrow + koff + 8);
+        // V^T fragment of dim 32 dt + col from V rows by transposing reads: in
+        // each 16-lane group, lane j points at key koff + j / 4 (resp. + 8),
+        // dims 32 dt + 16 (col / 16) + 4 (j % 4) .. + 3, and receives dim
+        // 32 dt + col of keys koff .. koff + 3 (resp. koff + 8 .. + 11)
+        const int gj = lane & 15;
+        const int vd = 32 * dt + (col & 16) + 4 * (gj & 3);
+        const F16x4 lo = VTr(&vs[(koff + (gj >> 2)) * kFaVStride + vd]);
+        const F16x4 hi = VTr(&vs[(koff + 8 + (gj >> 2)) * kFaVStride + vd]);
         const F16x8 a = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pl, o[dt], 0, 0, 0);
         o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, ph, o[dt], 0, 0, 0);
