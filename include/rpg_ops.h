@@ -160,7 +160,7 @@ RPG_OPS_API int32_t rpg_op_matmul_quant(uint32_t type, const uint8_t* w, int64_t
 /* rpg_op_matmul_quant over n matrices sharing x (a layer's q / k / v, or gate /
  * up): out[i] = x . w[i]^T, each w[i] [rows[i]][cols] of types[i]; all arrays
  * are host arrays of n entries (ws / outs hold device pointers). At n_tokens = 1
- * each run of consecutive same-type matrices (up to 4) is one launch, every
+ * up to 4 Q4_K / Q6_K matrices (either type or both) are one launch, every
  * output bit-identical to its own rpg_op_matmul_quant. No counterpart in the
  * reference (one launch per matrix, src/qwen3_gpu.cu:72-74, :104-105). */
 RPG_OPS_API int32_t rpg_op_matmul_quant_group(int32_t n, const uint32_t* types, const uint8_t* const* ws,
