@@ -653,7 +653,9 @@ void LaunchMatMulMfmaSplit(uint32_t type, const uint8_t* w, int64_t rows, int64_
   const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy), static_cast<unsigned>(splits));
   const _Float16* planes = static_cast<const _Float16*>(sa.planes);
   const _Float16* sums = static_cast<const _Float16*>(sa.sums);
-  const bool pp = tiles <= kPingPongTiles;
+  // wide matrices (more than 16 row tiles) only while the token tiles are
+  // mostly empty: ffn_gate measured 14% faster at 130 tokens, 9% slower at 256
+  const bool pp = tiles <= kPingPongTiles && (gx <= 16 || sa.n_tokens <= 160);
   const dim3 block(pp ? kGemmThreadsPP : kThreads);
   if (type == kGgmlQ4_K) {
     Launch(pp ? "MatMulMfmaQ4KPingPongKernel" : "MatMulMfmaQ4KKernel",
