@@ -742,6 +742,7 @@ def cpu_baseline():
         per_op[name] = {"ms": round(t * 1e3, 3), "GBps": round(nbytes / t / 1e9, 2)}
     t1 = pyoracle.bench_layer_chain(1, *args, 1)
     gq4 = pyoracle.bench_gather(threads, pyoracle.Q4_K, VOCAB, H, N_PREFILL, 3)
+    gref = pyoracle.ref_bench_gather(pyoracle.Q4_K, VOCAB, H, N_PREFILL, 3)  # the reference's own quant.cc
     mm = pyoracle.bench_matmul(pyoracle.Q6_K, 4096, 2048, 3)
     return {"value": round(b / sec / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"one layer of the n={N_PREFILL} chain (add+RMSNorm, qk-norm+RoPE+fp16 KV, SwiGLU; "
@@ -749,6 +750,11 @@ def cpu_baseline():
                       f"({sec * 1e3:.1f} ms each)",
             "per_op": per_op, "single_thread_GBps": round(b / t1 / 1e9, 2),
             "gather_q4k_GBps": round(bytes_gather(N_PREFILL, 144) / gq4 / 1e9, 2),
+            "gather_q4k_reference_1thread_GBps": (round(bytes_gather(N_PREFILL, 144) / gref / 1e9, 2)
+                                                  if gref else None),
+            "gather_reference_sample": "the reference's own src/quant.cc DequantizeRow per token row (the CPU "
+                                       "engine's gather), built into oracle/_ref, one thread, 2811 random rows of "
+                                       "the [151936, 2048] Q4_K table, best of 3",
             "matmul_q6k_n1_GBps": round((4096 * 8 * 210 + 4 * 2048 + 4 * 4096) / mm / 1e9, 3),
             "matmul_sample": "4096 x 2048 Q6_K rows times one fp32 vector by the oracle's float64 "
                              "restatement, one thread"}

@@ -93,6 +93,9 @@ def ref_lib():
         R.ref_f16_to_f32_array.argtypes = [_vp, _i64, _vp]
         R.ref_f32_to_f16_dtypes.restype = ctypes.c_uint16
         R.ref_f32_to_f16_dtypes.argtypes = [_f32]
+        if hasattr(R, "ref_bench_gather"):
+            R.ref_bench_gather.restype = ctypes.c_double
+            R.ref_bench_gather.argtypes = [_u32, _vp, _i64, _vp, _i64, _i64, _vp, ctypes.c_int]
         _ref = R
     return _ref
 
@@ -180,6 +183,28 @@ def attention_f64(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, max_seq: int, n
     assert lib().ora_attention_f64(_p(q), _p(kc), _p(vc), max_seq, n_heads, n_kv_heads, d, pos0, seq, _p(out),
                                    _p(smag), _p(vmax)) == 0
     return out, smag, vmax
+
+
+def ref_bench_gather(ggml_type: int, rows: int, cols: int, seq: int, reps: int):
+    """Seconds for the reference's own CPU gather (one DequantizeRow per token
+    row, one thread) of `seq` random rows of a [rows, cols] table with random
+    block bytes (finite fp16 scales), or None without oracle/_ref."""
+    R = ref_lib()
+    if R is None or not hasattr(R, "ref_bench_gather"):
+        return None
+    rb = int(R.ref_type_row_bytes(ggml_type, cols))
+    rng = np.random.default_rng(7)
+    table = rng.integers(0, 256, size=rows * rb, dtype=np.uint8)
+    blk = table.reshape(-1, 144 if ggml_type == Q4_K else 210)
+    if ggml_type == Q4_K:
+        blk[:, 1] &= 0x3B  # d, dmin: exponent below the Inf/NaN range
+        blk[:, 3] &= 0x3B
+    else:
+        blk[:, 209] &= 0x3B
+    ids = rng.integers(0, rows, size=seq).astype(np.int32)
+    out = np.empty(seq * cols, dtype=np.float32)
+    s = float(R.ref_bench_gather(ggml_type, _p(table), rb, _p(ids), seq, cols, _p(out), reps))
+    return s if s > 0 else None
 
 
 def ref_dequantize_row(ggml_type: int, raw: np.ndarray, n: int):

@@ -7,6 +7,7 @@
 // the reference is copied into this repository; this file only forwards.
 // Used to validate the oracle's restatement (tests/test_oracle.py) and to write
 // the golden vectors under tests/golden/.
+#include <chrono>
 #include <cstdint>
 
 #include "dtypes.h"
@@ -42,5 +43,27 @@ void ref_f16_to_f32_array(const uint16_t* src, int64_t n, float* dst) {
 // rpg::F32ToF16, src/dtypes.h:50-76 (ties away from zero; kept to show it is
 // not the KV write's rounding).
 uint16_t ref_f32_to_f16_dtypes(float f) { return rpg::F32ToF16(f); }
+
+// The CPU engine's embedding gather as the reference's CPU path runs it: one
+// rpg::DequantizeRow per token row (src/quant.cc:416-436), one thread, timed
+// here so no foreign-call overhead enters the figure. Returns the best of
+// `reps` wall-clock seconds, or -1 if a row threw.
+double ref_bench_gather(uint32_t type, const uint8_t* table, int64_t row_bytes, const int32_t* ids, int64_t seq,
+                        int64_t cols, float* out, int reps) {
+  double best = -1.0;
+  for (int r = 0; r < reps; ++r) {
+    const auto t0 = std::chrono::steady_clock::now();
+    try {
+      for (int64_t t = 0; t < seq; ++t) {
+        rpg::DequantizeRow(type, table + static_cast<int64_t>(ids[t]) * row_bytes, cols, out + t * cols);
+      }
+    } catch (...) {
+      return -1.0;
+    }
+    const double s = std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+    if (best < 0 || s < best) best = s;
+  }
+  return best;
+}
 
 }  // extern "C"
