@@ -46,7 +46,8 @@ RPG_OPS_API const char* rpg_ops_version(void);
  * Replaces: rpg_engine_last_error, include/rpg_engine.h:55. */
 RPG_OPS_API const char* rpg_ops_last_error(void);
 
-/* Allocates the fixed-address pos0 scalar on the current device. Must be
+/* Allocates the fixed-address pos0 scalar on the current device and looks up
+ * the current device's address of the no-allocation attention scratch. Must be
  * called once before any operator is captured into a HIP graph (allocation is
  * illegal during capture). Replaces: PosStagingPtr, src/cuda_common.h:153. */
 RPG_OPS_API int32_t rpg_ops_init(void);
@@ -144,6 +145,23 @@ RPG_OPS_API int32_t rpg_op_qk_norm_rope_kv_attention(const float* q, const float
                                                      int64_t rope_rows, int64_t pos0, float eps, uint16_t* k_layer,
                                                      uint16_t* v_layer, int64_t max_seq, float* out,
                                                      int64_t sh_positions, int32_t* fused);
+
+/* rpg_op_attention_from_cache for callers that cannot allocate device memory
+ * (code under HIP graph capture, serving loops or harnesses that forbid
+ * hipMalloc): same arguments, same kernels, bit-identical results, but the
+ * partials of a split-key decode live in a fixed 8 MiB device array of the
+ * library (one per GPU, held until the process ends), so no call ever
+ * allocates. Limit: a call whose split needs more than 2^21 floats of partials
+ * (seq * n_heads * chunks * 130) fails with an error and launches nothing. The
+ * split aims at ~2048 waves, so every call with a GQA group of 1 or 2, and with
+ * a group of 4 up to 2016 (token, kv head) pairs (all decode batches below 64
+ * tokens with up to 32 kv heads), fits.
+ * Calls that overlap on one GPU (different streams) share the array and race.
+ * No counterpart in the reference: it exists for callers that cannot allocate. */
+RPG_OPS_API int32_t rpg_op_attention_from_cache_noalloc(const float* q, int32_t n_heads, int32_t n_kv_heads,
+                                                        int32_t head_dim, int64_t pos0, int64_t seq,
+                                                        const uint16_t* k_layer, const uint16_t* v_layer,
+                                                        int64_t max_seq, float* out, int64_t sh_positions);
 
 /* Pre-sizes the attention's partials buffer for graph capture.
  * Replaces: GpuAttentionWarmupShmem, src/kernels_gpu.h:128. */

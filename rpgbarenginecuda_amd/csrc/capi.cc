@@ -104,7 +104,10 @@ const char* rpg_ops_version(void) { return "0.1.0"; }
 const char* rpg_ops_last_error(void) { return rpg::LastError(); }
 
 int32_t rpg_ops_init(void) {
-  return Guard([] { (void)rpg::PosStagingPtr(); });
+  return Guard([] {
+    (void)rpg::PosStagingPtr();
+    rpg::GpuAttentionNoAllocInit();
+  });
 }
 
 int32_t rpg_ops_set_stream(void* stream) {
@@ -211,6 +214,19 @@ int32_t rpg_op_qk_norm_rope_kv_attention(const float* q, const float* k, const f
                                            max_seq, out, sh_positions)
                  ? 1
                  : 0;
+  });
+}
+
+int32_t rpg_op_attention_from_cache_noalloc(const float* q, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                            int64_t pos0, int64_t seq, const uint16_t* k_layer,
+                                            const uint16_t* v_layer, int64_t max_seq, float* out,
+                                            int64_t sh_positions) {
+  return Guard([&] {
+    rpg::ModelMeta c;
+    c.n_heads = n_heads;
+    c.n_kv_heads = n_kv_heads;
+    c.head_dim = head_dim;
+    rpg::GpuAttentionFromCacheNoAlloc(c, pos0, q, seq, k_layer, v_layer, max_seq, out, sh_positions);
   });
 }
 

@@ -812,6 +812,58 @@ float* EnsurePartials(size_t floats) {
   return b.ptr;
 }
 
+// Fixed partials storage for GpuAttentionFromCacheNoAlloc: a file-scope device
+// array, so that entry point never allocates. Each device holds its own copy at
+// its own address; host code must use the address hipGetSymbolAddress returns
+// for the current device (AttnScratchForDevice), never the array's name, which
+// on the host is only a registration handle.
+constexpr size_t kNoAllocScratchFloats = size_t(1) << 21;  // 8 MiB
+static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
+
+constexpr int kMaxScratchDevices = 64;
+
+struct ScratchTable {
+  std::mutex mu;
+  float* ptr[kMaxScratchDevices] = {};
+};
+ScratchTable& Scratch() {
+  static ScratchTable* t = new ScratchTable();
+  return *t;
+}
+
+// Device address of `scratch` on the current device, looked up once per device.
+float* ScratchForCurrentDevice() {
+  int dev = -1;
+  RPG_HIP_CHECK(hipGetDevice(&dev));
+  RPG_CHECK(dev >= 0 && dev < kMaxScratchDevices, "device %d is beyond the %d devices the scratch table tracks", dev,
+            kMaxScratchDevices);
+  ScratchTable& t = Scratch();
+  std::lock_guard<std::mutex> lock(t.mu);
+  if (t.ptr[dev] == nullptr) {
+    void* p = nullptr;
+    RPG_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    RPG_CHECK(p != nullptr, "hipGetSymbolAddress returned no address for the attention scratch on device %d", dev);
+    t.ptr[dev] = static_cast<float*>(p);
+  }
+  return t.ptr[dev];
+}
+
+// Where a split-key launch keeps its chunk partials: the library's grow-only
+// buffer (fixed == nullptr) or a fixed region that must already be big enough.
+struct PartialsSink {
+  float* fixed = nullptr;
+  size_t fixed_floats = 0;
+
+  float* Get(size_t floats) const {
+    if (fixed == nullptr) return EnsurePartials(floats);
+    RPG_CHECK(floats <= fixed_floats,
+              "this attention call splits its keys into %zu floats of partials, more than the %zu floats (%zu MiB) "
+              "of the no-allocation entry point's fixed scratch; use the allocating entry point for it",
+              floats, fixed_floats, fixed_floats * sizeof(float) >> 20);
+    return fixed;
+  }
+};
+
 // Up to this many positions one chunk per (token, head) beats a split plus the
 // merge launch (decode at Qwen3-1.7B: 8.2 vs 9.2 us at 128 keys, 14.1 vs 9.3 us
 // at 256).
@@ -859,13 +911,14 @@ size_t WarmupFloats(int64_t /*positions*/) { return static_cast<size_t>(64) * kM
 template <int G>
 void LaunchDecodeGroup(const ModelMeta& c, const Pos0Arg& p0, const float* q_dev, int64_t seq,
                        const uint16_t* k_layer, const uint16_t* v_layer, int64_t max_seq, float scale,
-                       int64_t positions, float* out_dev, const DecodePrep* prep = nullptr) {
+                       int64_t positions, float* out_dev, const DecodePrep* prep = nullptr,
+                       const PartialsSink& sink = PartialsSink{}) {
   int32_t n_chunks;
   int64_t chunk_len;
   PlanGroupChunks(seq * c.n_kv_heads, positions, &n_chunks, &chunk_len);
   const int64_t pairs = seq * c.n_heads;
   float* part = nullptr;
-  if (n_chunks > 1) part = EnsurePartials(static_cast<size_t>(pairs) * n_chunks * kPartFloats);
+  if (n_chunks > 1) part = sink.Get(static_cast<size_t>(pairs) * n_chunks * kPartFloats);
   const int64_t units = seq * c.n_kv_heads * n_chunks;
   if (prep != nullptr) {
     Launch("AttnDecodePrepKernel", AttnDecodeGroupKernel<G, true>, dim3(GridFor(units, kWaves)),
@@ -882,10 +935,10 @@ void LaunchDecodeGroup(const ModelMeta& c, const Pos0Arg& p0, const float* q_dev
   }
 }
 
-}  // namespace
-
-void GpuAttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev, int64_t seq, const uint16_t* k_layer,
-                           const uint16_t* v_layer, int64_t max_seq, float* out_dev, int64_t sh_positions) {
+// GpuAttentionFromCache with the chunk partials taken from `sink`.
+void AttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev, int64_t seq, const uint16_t* k_layer,
+                        const uint16_t* v_layer, int64_t max_seq, float* out_dev, int64_t sh_positions,
+                        const PartialsSink& sink) {
   RPG_CHECK(seq > 0, "attention seq must be positive");
   RPG_CHECK(pos0 >= 0, "pos0 must not be negative");
   RPG_CHECK(c.n_heads > 0 && c.n_kv_heads > 0 && c.n_heads % c.n_kv_heads == 0,
@@ -916,17 +969,20 @@ void GpuAttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev,
   const bool aligned = (reinterpret_cast<uintptr_t>(q_dev) & 15u) == 0 &&
                        (reinterpret_cast<uintptr_t>(v_layer) & 15u) == 0;
   if (aligned && group == 1) {
-    return LaunchDecodeGroup<1>(c, p0, q_dev, seq, k_layer, v_layer, max_seq, scale, positions, out_dev);
+    return LaunchDecodeGroup<1>(c, p0, q_dev, seq, k_layer, v_layer, max_seq, scale, positions, out_dev, nullptr,
+                                sink);
   }
   if (aligned && group == 2) {
-    return LaunchDecodeGroup<2>(c, p0, q_dev, seq, k_layer, v_layer, max_seq, scale, positions, out_dev);
+    return LaunchDecodeGroup<2>(c, p0, q_dev, seq, k_layer, v_layer, max_seq, scale, positions, out_dev, nullptr,
+                                sink);
   }
   if (aligned && group == 4) {
-    return LaunchDecodeGroup<4>(c, p0, q_dev, seq, k_layer, v_layer, max_seq, scale, positions, out_dev);
+    return LaunchDecodeGroup<4>(c, p0, q_dev, seq, k_layer, v_layer, max_seq, scale, positions, out_dev, nullptr,
+                                sink);
   }
   // other group sizes / alignments: one wave per query head
   float* part = nullptr;
-  if (n_chunks > 1) part = EnsurePartials(static_cast<size_t>(pairs) * n_chunks * kPartFloats);
+  if (n_chunks > 1) part = sink.Get(static_cast<size_t>(pairs) * n_chunks * kPartFloats);
   const int64_t units = pairs * n_chunks;
   Launch("AttnChunkKernel", AttnChunkKernel<uint16_t>, dim3(GridFor(units, kWaves)), dim3(kBlockThreads), q_dev,
          k_layer, v_layer, max_seq * kD, static_cast<int64_t>(kD), max_seq, c.n_heads, c.n_heads / c.n_kv_heads,
@@ -936,6 +992,24 @@ void GpuAttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev,
            n_chunks, c.n_heads, chunk_len, p0.value, p0.dev, out_dev);
   }
 }
+
+}  // namespace
+
+void GpuAttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev, int64_t seq, const uint16_t* k_layer,
+                           const uint16_t* v_layer, int64_t max_seq, float* out_dev, int64_t sh_positions) {
+  AttentionFromCache(c, pos0, q_dev, seq, k_layer, v_layer, max_seq, out_dev, sh_positions, PartialsSink{});
+}
+
+void GpuAttentionFromCacheNoAlloc(const ModelMeta& c, int64_t pos0, const float* q_dev, int64_t seq,
+                                  const uint16_t* k_layer, const uint16_t* v_layer, int64_t max_seq, float* out_dev,
+                                  int64_t sh_positions) {
+  const PartialsSink sink{ScratchForCurrentDevice(), kNoAllocScratchFloats};
+  AttentionFromCache(c, pos0, q_dev, seq, k_layer, v_layer, max_seq, out_dev, sh_positions, sink);
+}
+
+void GpuAttentionNoAllocInit() { (void)ScratchForCurrentDevice(); }
+
+size_t GpuAttentionNoAllocScratchBytes() { return kNoAllocScratchFloats * sizeof(float); }
 
 bool GpuQkNormRopeKvAttention(const ModelMeta& c, int64_t pos0, const float* q_dev, const float* k_dev,
                               const float* v_dev, const float* q_norm, const float* k_norm, const float* rope_tab,

@@ -214,6 +214,24 @@ bool GpuQkNormRopeKvAttention(const ModelMeta& c, int64_t pos0, const float* q_d
 void GpuCausalAttention(const ModelMeta& c, const float* q_dev, const float* k_dev, const float* v_dev, int64_t seq,
                         float* out_dev);
 
+// GpuAttentionFromCache for callers that cannot allocate (code under HIP graph
+// capture, serving loops that forbid hipMalloc): the same kernels and results,
+// with the chunk partials in a fixed 8 MiB device array of the library instead
+// of the grow-only buffer, so nothing is ever allocated. A call whose key split
+// needs more partials than that (seq * n_heads * chunks * 130 floats > 2^21;
+// the split aims at ~2048 waves, so this is reached only with GQA groups of 4
+// and more than ~2000 (token, kv head) pairs) is rejected before anything
+// launches. Every call on a device shares that
+// device's array: calls that overlap on one device (two streams) race. No
+// counterpart in the reference.
+void GpuAttentionFromCacheNoAlloc(const ModelMeta& c, int64_t pos0, const float* q_dev, int64_t seq,
+                                  const uint16_t* k_layer, const uint16_t* v_layer, int64_t max_seq, float* out_dev,
+                                  int64_t sh_positions = -1);
+// Looks up the fixed array's address on the current device (once per device;
+// the entry point does it on first use if this was not called).
+void GpuAttentionNoAllocInit();
+size_t GpuAttentionNoAllocScratchBytes();
+
 // Sizes the attention's partials buffer for up to sh_positions cached positions
 // (decode calls), so that a graph capture of the decode step allocates nothing
 // (src/kernels_gpu.h:128; there it raises the shared-memory limit instead).

@@ -91,6 +91,7 @@ SIGNATURES = {
     "rpg_op_attention_from_cache": (_i32, [_vp, _i32, _i32, _i32, _i64, _i64, _vp, _vp, _i64, _vp, _i64]),
     "rpg_op_qk_norm_rope_kv_attention": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _f32,
                                                 _vp, _vp, _i64, _vp, _i64, _vp]),
+    "rpg_op_attention_from_cache_noalloc": (_i32, [_vp, _i32, _i32, _i32, _i64, _i64, _vp, _vp, _i64, _vp, _i64]),
     "rpg_op_attention_warmup": (_i32, [_i64]),
     "rpg_op_add_rms_norm": (_i32, [_vp, _vp, _vp, _i64, _i64, _f32, _vp]),
     "rpg_op_qk_norm_rope_kv": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _i64, _f32,

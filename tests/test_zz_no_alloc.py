@@ -1,0 +1,84 @@
+"""The no-allocation attention entry point (rpg_op_attention_from_cache_noalloc)
+against the allocating one (rpg_op_attention_from_cache), through the C ABI.
+
+Both run the same kernels; only where the split-key partials live differs (a
+fixed device array of the library instead of its grow-only buffer), so the
+outputs must be identical bit for bit. Two calls in a row, the second smaller,
+show that what the first call left in the shared array does not leak into the
+second; a third, too large for the array, must fail before launching anything.
+"""
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def _case(name: str) -> None:
+    print(f"\n[case] {name}", flush=True)
+
+
+def _inputs(rng, nh, nkv, max_seq, seq):
+    q = rng.normal(0, 1, (seq, nh, 128)).astype(np.float32)
+    kc = rng.normal(0, 1, (nkv, max_seq, 128)).astype(np.float16).view(np.uint16)
+    vc = rng.normal(0, 1, (nkv, max_seq, 128)).astype(np.float16).view(np.uint16)
+    return q, kc, vc
+
+
+def _run(lib, fn, nh, nkv, pos0, seq, q, kc, vc, max_seq, out):
+    rc = fn(ctypes.c_void_p(q.data_ptr()), nh, nkv, 128, pos0, seq, ctypes.c_void_p(kc.data_ptr()),
+            ctypes.c_void_p(vc.data_ptr()), max_seq, ctypes.c_void_p(out.data_ptr()), -1)
+    return rc
+
+
+def test_noalloc_attention_matches_allocating_entry(gpu):
+    import torch
+
+    lib = gpu.load_library()
+    rng = np.random.default_rng(77)
+    # (name, n_heads, n_kv_heads, max_seq, pos0, seq): the first call splits the
+    # keys into the most chunks, the second is smaller; both use the scratch.
+    calls = [("4B shape, decode at 4095, 2 tokens", 32, 8, 4096, 4094, 2),
+             ("1.7B shape, decode at 700", 16, 8, 4096, 700, 1)]
+    for name, nh, nkv, max_seq, pos0, seq in calls:
+        _case(f"noalloc vs allocating: {name}")
+        q, kc, vc = _inputs(rng, nh, nkv, max_seq, seq)
+        qd = torch.from_numpy(q).cuda()
+        kd = torch.from_numpy(kc.view(np.int16)).cuda()
+        vd = torch.from_numpy(vc.view(np.int16)).cuda()
+        ref = torch.full((seq, nh, 128), float("nan"), dtype=torch.float32, device="cuda")
+        got = torch.full_like(ref, float("nan"))
+        assert _run(lib, lib.rpg_op_attention_from_cache, nh, nkv, pos0, seq, qd, kd, vd, max_seq, ref) == 0
+        assert _run(lib, lib.rpg_op_attention_from_cache_noalloc, nh, nkv, pos0, seq, qd, kd, vd, max_seq,
+                    got) == 0, lib.rpg_ops_last_error()
+        torch.cuda.synchronize()
+        a = ref.cpu().numpy()
+        b = got.cpu().numpy()
+        assert np.all(np.isfinite(a))
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), f"{name}: outputs differ"
+
+
+def test_noalloc_attention_rejects_oversized_split(gpu):
+    import torch
+
+    lib = gpu.load_library()
+    _case("noalloc rejects a split beyond its fixed scratch")
+    # GQA group 4 with 62 x 33 = 2046 (token, kv head) pairs: the split takes 2
+    # chunks, 62 x 132 heads x 2 chunks x 130 floats = 2127840 > 2^21.
+    nh, nkv, max_seq, pos0, seq = 132, 33, 2048, 1000, 62
+    q = torch.zeros((seq, nh, 128), dtype=torch.float32, device="cuda")
+    kc = torch.zeros((nkv, max_seq, 128), dtype=torch.int16, device="cuda")
+    vc = torch.zeros_like(kc)
+    out = torch.full((seq, nh, 128), 7.0, dtype=torch.float32, device="cuda")
+    rc = _run(lib, lib.rpg_op_attention_from_cache_noalloc, nh, nkv, pos0, seq, q, kc, vc, max_seq, out)
+    assert rc < 0
+    msg = lib.rpg_ops_last_error().decode()
+    assert "no-allocation" in msg and "scratch" in msg, msg
+    torch.cuda.synchronize()
+    assert bool(torch.all(out == 7.0)), "a rejected call must not launch"
+    # the allocating entry point takes the same call
+    assert _run(lib, lib.rpg_op_attention_from_cache, nh, nkv, pos0, seq, q, kc, vc, max_seq, out) == 0
+    torch.cuda.synchronize()
