@@ -723,13 +723,38 @@ def measure_model_e2e(torch, ops, reps=3, decode_tokens=128):
         os.remove(path)
 
 
+def host_cpu():
+    """(threads this process may use, logical CPUs of the host, CPU model)."""
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return usable, os.cpu_count() or usable, model
+
+
+# CPU threads of the baseline: every thread the process may use, capped at the
+# 16-thread CPU share a one-GPU job gets on the GPU boxes (the host itself can
+# have many more logical CPUs; both counts are reported).
+CPU_SHARE = 16
+
+
 def cpu_baseline():
-    """The oracle's C restatement of one layer of the chain (n = 2811, 1.7B shape)
-    on the host cores, median of 5; plus per-op and single-thread figures. A
-    reported baseline only."""
+    """The oracle's C restatement of one layer of the chain (n = 2811, 1.7B shape,
+    the benchmark's input distributions) on the host cores, median of 5; plus
+    per-op and single-thread figures. A reported baseline only."""
     from oracle import pyoracle
 
-    threads = max(1, min(os.cpu_count() or 1, 16))
+    usable, host_cpus, model = host_cpu()
+    threads = max(1, min(usable, CPU_SHARE))
     args = (N_PREFILL, H, HQ, HKV, INTER)
     sec = pyoracle.bench_layer_chain(threads, *args, 5)
     if sec <= 0:
@@ -745,16 +770,17 @@ def cpu_baseline():
     gref = pyoracle.ref_bench_gather(pyoracle.Q4_K, VOCAB, H, N_PREFILL, 3)  # the reference's own quant.cc
     mm = pyoracle.bench_matmul(pyoracle.Q6_K, 4096, 2048, 3)
     return {"value": round(b / sec / 1e9, 2), "unit": "GB/s", "cores": threads, "kind": "port",
+            "host_logical_cpus": host_cpus, "usable_cpus": usable, "cpu_model": model,
             "sample": f"one layer of the n={N_PREFILL} chain (add+RMSNorm, qk-norm+RoPE+fp16 KV, SwiGLU; "
-                      f"{b} B) by the C oracle, rows split over {threads} threads, median of 5 runs "
-                      f"({sec * 1e3:.1f} ms each)",
+                      f"{b} B; activations N(0,1), norm weights N(1,0.1)) by the C oracle, rows split over "
+                      f"{threads} threads, median of 5 runs ({sec * 1e3:.1f} ms each)",
             "per_op": per_op, "single_thread_GBps": round(b / t1 / 1e9, 2),
             "gather_q4k_GBps": round(bytes_gather(N_PREFILL, 144) / gq4 / 1e9, 2),
             "gather_q4k_reference_1thread_GBps": (round(bytes_gather(N_PREFILL, 144) / gref / 1e9, 2)
                                                   if gref else None),
             "gather_reference_sample": "the reference's own src/quant.cc DequantizeRow per token row (the CPU "
                                        "engine's gather), built into oracle/_ref, one thread, 2811 random rows of "
-                                       "the [151936, 2048] Q4_K table, best of 3",
+                                       "the [151936, 2048] Q4_K table (fp16 d, dmin |N(0,0.01)|), best of 3",
             "matmul_q6k_n1_GBps": round((4096 * 8 * 210 + 4 * 2048 + 4 * 4096) / mm / 1e9, 3),
             "matmul_sample": "4096 x 2048 Q6_K rows times one fp32 vector by the oracle's float64 "
                              "restatement, one thread"}
@@ -767,6 +793,8 @@ SECTIONS = {
     "matmul_decode_n1": lambda torch, ops: measure_matmul_decode(torch, ops),
     "attention": lambda torch, ops: measure_attention(torch, ops),
     "sampler": lambda torch, ops: measure_sampler(torch, ops),
+    "gather": lambda torch, ops: {"q4k": measure_gather(torch, ops, ops.GGML_Q4_K, 144),
+                                  "q6k": measure_gather(torch, ops, ops.GGML_Q6_K, 210)},
 }
 
 

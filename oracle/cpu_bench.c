@@ -1,10 +1,14 @@
 /* cpu_bench.c -- CPU baseline timing for bench.py (TEST INFRASTRUCTURE ONLY).
  *
  * Times the oracle's restatement of the layer-op chain and of the embedding
- * gather on the host cores, rows partitioned over pthreads. Inputs are
- * synthetic (SplitMix64 -> uniform), allocated here, never read back.
+ * gather on the host cores, rows partitioned over pthreads. Inputs follow the
+ * benchmark configuration's distributions (activations N(0,1), norm weights
+ * N(1,0.1); Q4_K / Q6_K tables with fp16 d, dmin = |N(0,0.01)| and uniform
+ * scale / quant bytes), drawn from SplitMix64 through Box-Muller, allocated
+ * here and never read back.
  */
 #define _POSIX_C_SOURCE 200809L
+#include <math.h>
 #include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
@@ -19,11 +23,46 @@ static uint64_t splitmix64(uint64_t* s) {
   return z ^ (z >> 31);
 }
 
+/* Normal(mean, sd) floats: Box-Muller on two 53-bit uniforms in double. */
+static void fill_normal(float* p, int64_t n, uint64_t seed, float mean, float sd) {
+  uint64_t s = seed;
+  for (int64_t i = 0; i < n; i += 2) {
+    const double u1 = ((double)(splitmix64(&s) >> 11) + 1.0) * (1.0 / 9007199254740993.0);
+    const double u2 = (double)(splitmix64(&s) >> 11) * (1.0 / 9007199254740992.0);
+    const double r = sqrt(-2.0 * log(u1));
+    p[i] = (float)(mean + sd * r * cos(6.283185307179586 * u2));
+    if (i + 1 < n) p[i + 1] = (float)(mean + sd * r * sin(6.283185307179586 * u2));
+  }
+}
+
 static void fill_uniform(float* p, int64_t n, uint64_t seed, float lo, float hi) {
   uint64_t s = seed;
   for (int64_t i = 0; i < n; ++i) {
     const double u = (double)(splitmix64(&s) >> 11) * (1.0 / 9007199254740992.0);
     p[i] = (float)(lo + (hi - lo) * u);
+  }
+}
+
+/* A [rows, row_bytes] Q4_K / Q6_K table: uniform bytes, then every block's fp16
+ * scale fields set to fp16(|N(0, 0.01)|) (Q4_K d and dmin, Q6_K d). */
+static void fill_quant_table(uint8_t* emb, int64_t rows, int64_t rb, uint32_t type, uint64_t seed) {
+  uint64_t s = seed;
+  const int64_t total = rows * rb;
+  for (int64_t i = 0; i < total; i += 8) {
+    const uint64_t r = splitmix64(&s);
+    const int64_t m = total - i < 8 ? total - i : 8;
+    memcpy(emb + i, &r, (size_t)m);
+  }
+  const int64_t bb = type == ORA_GGML_Q4_K ? 144 : 210;
+  const int n_scales = type == ORA_GGML_Q4_K ? 2 : 1;
+  const int64_t first = type == ORA_GGML_Q4_K ? 0 : 208;
+  float sc[2];
+  for (int64_t b = 0; b < total / bb; ++b) {
+    fill_normal(sc, n_scales, seed + 0x9E37u * (uint64_t)(b + 1), 0.0f, 0.01f);
+    for (int j = 0; j < n_scales; ++j) {
+      const uint16_t h = ora_f32_to_f16_rne(fabsf(sc[j]));
+      memcpy(emb + b * bb + first + 2 * j, &h, 2);
+    }
   }
 }
 
@@ -96,17 +135,17 @@ double ora_bench_layer_op(int op, int threads, int64_t n, int64_t hidden, int32_
   if (!base.x || !base.d || !base.h || !base.wn || !base.q || !base.k || !base.v || !base.qn || !base.kn ||
       !base.tab || !base.gate || !base.up || !base.kc || !base.vc)
     goto done;
-  fill_uniform(base.x, n * hidden, 1, -2.f, 2.f);
-  fill_uniform(base.d, n * hidden, 2, -2.f, 2.f);
-  fill_uniform(base.wn, hidden, 3, 0.8f, 1.2f);
-  fill_uniform(base.q, n * n_heads * 128, 4, -2.f, 2.f);
-  fill_uniform(base.k, n * n_kv_heads * 128, 5, -2.f, 2.f);
-  fill_uniform(base.v, n * n_kv_heads * 128, 6, -2.f, 2.f);
-  fill_uniform(base.qn, 128, 7, 0.8f, 1.2f);
-  fill_uniform(base.kn, 128, 8, 0.8f, 1.2f);
+  fill_normal(base.x, n * hidden, 1, 0.f, 1.f);
+  fill_normal(base.d, n * hidden, 2, 0.f, 1.f);
+  fill_normal(base.wn, hidden, 3, 1.f, 0.1f);
+  fill_normal(base.q, n * n_heads * 128, 4, 0.f, 1.f);
+  fill_normal(base.k, n * n_kv_heads * 128, 5, 0.f, 1.f);
+  fill_normal(base.v, n * n_kv_heads * 128, 6, 0.f, 1.f);
+  fill_normal(base.qn, 128, 7, 1.f, 0.1f);
+  fill_normal(base.kn, 128, 8, 1.f, 0.1f);
   ora_build_rope_table(128, 1e6, n, base.tab);
-  fill_uniform(base.gate, n * inter, 9, -4.f, 4.f);
-  fill_uniform(base.up, n * inter, 10, -4.f, 4.f);
+  fill_normal(base.gate, n * inter, 9, 0.f, 1.f);
+  fill_normal(base.up, n * inter, 10, 0.f, 1.f);
 
   {
     pthread_t tid[256];
@@ -160,10 +199,10 @@ double ora_bench_gather(int threads, uint32_t type, int64_t rows, int64_t cols, 
   if (!emb || !toks || !x) goto done;
   {
     uint64_t s = 11;
-    for (int64_t i = 0; i < rows * rb; i += 8) {
-      const uint64_t r = splitmix64(&s);
-      const int64_t m = rows * rb - i < 8 ? rows * rb - i : 8;
-      memcpy(emb + i, &r, (size_t)m);
+    if (type == ORA_GGML_Q4_K || type == ORA_GGML_Q6_K) {
+      fill_quant_table(emb, rows, rb, type, 11);
+    } else {
+      fill_uniform((float*)emb, rows * rb / 4, 11, -1.f, 1.f);
     }
     for (int64_t t = 0; t < seq; ++t) toks[t] = (int32_t)(splitmix64(&s) % (uint64_t)rows);
     pthread_t tid[256];

@@ -187,8 +187,8 @@ def attention_f64(q: np.ndarray, kc: np.ndarray, vc: np.ndarray, max_seq: int, n
 
 def ref_bench_gather(ggml_type: int, rows: int, cols: int, seq: int, reps: int):
     """Seconds for the reference's own CPU gather (one DequantizeRow per token
-    row, one thread) of `seq` random rows of a [rows, cols] table with random
-    block bytes (finite fp16 scales), or None without oracle/_ref."""
+    row, one thread) of `seq` random rows of a [rows, cols] table with uniform
+    block bytes and fp16 scales |N(0, 0.01)|, or None without oracle/_ref."""
     R = ref_lib()
     if R is None or not hasattr(R, "ref_bench_gather"):
         return None
@@ -196,11 +196,11 @@ def ref_bench_gather(ggml_type: int, rows: int, cols: int, seq: int, reps: int):
     rng = np.random.default_rng(7)
     table = rng.integers(0, 256, size=rows * rb, dtype=np.uint8)
     blk = table.reshape(-1, 144 if ggml_type == Q4_K else 210)
-    if ggml_type == Q4_K:
-        blk[:, 1] &= 0x3B  # d, dmin: exponent below the Inf/NaN range
-        blk[:, 3] &= 0x3B
-    else:
-        blk[:, 209] &= 0x3B
+    # the benchmark configuration's fp16 scales: d (and dmin) = |N(0, 0.01)|
+    scales = [0, 2] if ggml_type == Q4_K else [208]
+    for off in scales:
+        half = np.abs(rng.normal(0.0, 0.01, blk.shape[0])).astype(np.float16)
+        blk[:, off:off + 2] = half.view(np.uint8).reshape(-1, 2)
     ids = rng.integers(0, rows, size=seq).astype(np.int32)
     out = np.empty(seq * cols, dtype=np.float32)
     s = float(R.ref_bench_gather(ggml_type, _p(table), rb, _p(ids), seq, cols, _p(out), reps))

@@ -133,6 +133,27 @@ __device__ __forceinline__ void StoreStreamHalf4(uint16_t* p, uint2 v) {
   __builtin_nontemporal_store(w, reinterpret_cast<U32x2*>(p));
 }
 
+// Write-through output stores for write-dominated kernels (the embedding
+// gather): a raw buffer store with the cache-policy bits sc0 | sc1 | nt, i.e.
+// system-scope write-through with the streaming hint, so the written lines are
+// not left dirty in the XCDs' L2s for the end-of-kernel release to flush.
+// Measured on MI355X: a 23 MB fill 4.45 us against 5.5-5.9 us with plain or
+// nontemporal global stores; the Q4_K gather at n = 2811 ~0.2 us faster. Every
+// store instruction of a wave must cover whole 128-byte lines: with partial
+// lines the write-through path is several times slower. The buffer resource
+// bounds every store to `bytes` from `base` (out-of-range stores are dropped).
+typedef unsigned int U32x4 __attribute__((ext_vector_type(4)));
+constexpr int kStoreThroughPolicy = 1 | 2 | 16;  // sc0 | nt | sc1
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t OutResource(void* base, uint32_t bytes) {
+  // 0x00020000: raw (untyped) buffer, 32-bit data format, as for gfx9 CDNA parts.
+  return __builtin_amdgcn_make_buffer_rsrc(base, static_cast<short>(0), static_cast<int>(bytes), 0x00020000);
+}
+__device__ __forceinline__ void StoreThrough4(__amdgpu_buffer_rsrc_t rs, uint32_t byte_off, float4 v) {
+  const U32x4 w = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
+  __builtin_amdgcn_raw_buffer_store_b128(w, rs, static_cast<int>(byte_off), 0, kStoreThroughPolicy);
+}
+
 // SwiGLU element (src/kernels_gpu.cu:868): silu(g) * u = (g / (1 + e^-g)) * u,
 // IEEE division. Shared by SiluMulKernel and the gate / up matvec that applies
 // it to its two row totals, so both produce the same bits.

@@ -32,25 +32,21 @@ unsigned GridFor(int64_t n, int threads) {
 
 DeviceInfo QueryDevice(int index) {
   DeviceInfo d;
+  auto fail = [&d](std::string why) {
+    d.reason = std::move(why);
+    return d;
+  };
   int count = 0;
-  const hipError_t e = hipGetDeviceCount(&count);
-  if (e != hipSuccess) {
-    d.reason = std::string("hipGetDeviceCount failed: ") + hipGetErrorString(e);
-    return d;
+  if (const hipError_t e = hipGetDeviceCount(&count); e != hipSuccess) {
+    return fail(std::string("the HIP runtime reports no usable GPU (") + hipGetErrorString(e) + ")");
   }
-  if (count <= 0) {
-    d.reason = "no HIP device found";
-    return d;
-  }
+  if (count <= 0) return fail("the HIP runtime sees no GPU");
   if (index < 0 || index >= count) {
-    d.reason = "device index out of range (there are " + std::to_string(count) + " devices)";
-    return d;
+    return fail("GPU " + std::to_string(index) + " requested, visible GPUs are 0.." + std::to_string(count - 1));
   }
   hipDeviceProp_t p{};
-  const hipError_t pe = hipGetDeviceProperties(&p, index);
-  if (pe != hipSuccess) {
-    d.reason = std::string("hipGetDeviceProperties failed: ") + hipGetErrorString(pe);
-    return d;
+  if (const hipError_t e = hipGetDeviceProperties(&p, index); e != hipSuccess) {
+    return fail("cannot read the properties of GPU " + std::to_string(index) + " (" + hipGetErrorString(e) + ")");
   }
   d.available = true;
   d.name = p.name;
@@ -180,41 +176,50 @@ ScopedEngineStream::ScopedEngineStream(hipStream_t s) : prev_(g_engine_stream) {
 ScopedEngineStream::~ScopedEngineStream() { g_engine_stream = prev_; }
 
 // ---------------------------------------------------------------- pos0 staging
+//
+// The staging scalar is one int64 of device memory at a fixed address. A
+// captured launch reads that address on every replay; the host writes the
+// position for the next replay through StagePos0. g_pos_last mirrors what the
+// last completed-or-queued write put there, so StagePos0Cached can skip a copy
+// of an unchanged value. Nothing is written while the engine stream captures:
+// a captured host-to-device copy would keep reading the caller's (dead) stack
+// slot on replay, and the address, not the value, is what the graph needs.
 
 int64_t* PosStagingPtr() {
-  if (g_pos_staging == nullptr) {
-    int64_t* p = nullptr;
-    RPG_HIP_CHECK(hipMalloc(&p, sizeof(int64_t)));
-    g_pos_staging = p;
-  }
+  if (g_pos_staging != nullptr) return g_pos_staging;
+  void* p = nullptr;
+  RPG_HIP_CHECK(hipMalloc(&p, sizeof(int64_t)));
+  g_pos_staging = static_cast<int64_t*>(p);
   return g_pos_staging;
 }
 
 bool StreamIsCapturing() {
   hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-  const hipError_t e = hipStreamIsCapturing(EngineStream(), &st);
-  if (e != hipSuccess) {
-    (void)hipGetLastError();  // the query failing means "not capturing"; do not leak the error
+  if (hipStreamIsCapturing(EngineStream(), &st) != hipSuccess) {
+    (void)hipGetLastError();  // a failed query counts as "not capturing"; the sticky error is cleared
     return false;
   }
   return st != hipStreamCaptureStatusNone;
 }
 
-void StagePos0(int64_t pos) {
-  int64_t* dev = PosStagingPtr();
-  if (StreamIsCapturing()) return;
-  // Pageable source: the runtime copies it out before this call returns, so the
-  // stack slot may die right after.
-  RPG_HIP_CHECK(hipMemcpyAsync(dev, &pos, sizeof(int64_t), hipMemcpyHostToDevice, EngineStream()));
-  g_pos_last = pos;
-}
+namespace {
 
-int64_t* StagePos0Cached(int64_t pos) {
+// Writes pos into the staging scalar unless capturing (or, with skip_same,
+// unless it already holds pos). The source is pageable host memory, which the
+// runtime copies out before the call returns.
+int64_t* StagePos(int64_t pos, bool skip_same) {
   int64_t* dev = PosStagingPtr();
-  if (StreamIsCapturing()) return dev;
-  if (g_pos_last != pos) StagePos0(pos);
+  if (StreamIsCapturing() || (skip_same && g_pos_last == pos)) return dev;
+  RPG_HIP_CHECK(hipMemcpyAsync(dev, &pos, sizeof(pos), hipMemcpyHostToDevice, EngineStream()));
+  g_pos_last = pos;
   return dev;
 }
+
+}  // namespace
+
+void StagePos0(int64_t pos) { (void)StagePos(pos, false); }
+
+int64_t* StagePos0Cached(int64_t pos) { return StagePos(pos, true); }
 
 // ---------------------------------------------------------------- launch profiling
 

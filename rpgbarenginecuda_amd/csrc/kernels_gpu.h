@@ -95,8 +95,11 @@ struct GpuTensor {
   int64_t row_bytes() const { return TypeRowBytes(type, cols); }
 };
 
-// Device-resident fp16 KV cache with the reference layout
-// [n_layers][n_kv_heads][max_seq][head_dim] (src/kv_cache_gpu.h:1-30, :50-100).
+// Device-resident fp16 KV cache with the reference's layout: K, and V, each
+// [n_layers][n_kv_heads][max_seq][head_dim] (src/kv_cache_gpu.h:1-30, :50-100),
+// reached through the per-layer bases. The interface is the reference's; the
+// storage is one device block per cache (all K layers, then all V layers), so
+// a session costs a single allocation.
 class GpuKvCache {
  public:
   GpuKvCache() = default;
@@ -110,26 +113,29 @@ class GpuKvCache {
   bool valid() const { return max_seq_ > 0; }
 
   // Base of layer `layer`: [n_kv_heads][max_seq][head_dim] fp16 bits.
-  uint16_t* k_layer(int32_t layer);
-  uint16_t* v_layer(int32_t layer);
-  const uint16_t* k_layer(int32_t layer) const;
+  uint16_t* k_layer(int32_t layer) { return Plane(layer, 0); }
+  uint16_t* v_layer(int32_t layer) { return Plane(layer, 1); }
+  const uint16_t* k_layer(int32_t layer) const { return Plane(layer, 0); }
+  const uint16_t* v_layer(int32_t layer) const { return Plane(layer, 1); }
 
+  // Positions [0, len()) hold valid K / V rows; nothing else is ever read.
   void Reset() { len_ = 0; }
   void SetLen(int64_t n);
   void AddLen(int64_t n) { SetLen(len_ + n); }
-  int64_t bytes() const { return static_cast<int64_t>(k_.size() + v_.size()); }
+  int64_t bytes() const { return static_cast<int64_t>(store_.size()); }
   std::string Describe() const;
 
  private:
-  int64_t LayerElems() const { return static_cast<int64_t>(n_kv_heads_) * max_seq_ * head_dim_; }
+  // Base of `layer` in plane 0 (K) or 1 (V).
+  uint16_t* Plane(int32_t layer, int plane) const;
 
   int32_t n_layers_ = 0;
   int32_t n_kv_heads_ = 0;
   int32_t head_dim_ = 0;
   int64_t max_seq_ = 0;
   int64_t len_ = 0;
-  DeviceBuffer k_;
-  DeviceBuffer v_;
+  int64_t plane_elems_ = 0;  // n_kv_heads * max_seq * head_dim
+  DeviceBuffer store_;
 };
 
 // Host-built RoPE table, [n_pos][head_dim] fp32, cos in the first half of a row and

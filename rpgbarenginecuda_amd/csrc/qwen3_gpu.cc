@@ -5,6 +5,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstring>
 #include <utility>
 
@@ -12,11 +13,6 @@ namespace rpg {
 namespace {
 
 float* F(DeviceBuffer& b) { return static_cast<float*>(b.data()); }
-
-void Need(DeviceBuffer& b, int64_t floats) {
-  const size_t bytes = static_cast<size_t>(floats) * sizeof(float);
-  if (b.size() < bytes) b.Alloc(bytes);
-}
 
 // Sub-layer input normalisation with the pending residual folded in: when the
 // previous sub-layer left its output in proj, x += proj happens inside the norm
@@ -182,62 +178,79 @@ void ForwardCore(const GpuModel& m, int64_t seq, GpuScratch* s, const int32_t* t
   s->logits.Download(logits->data(), logits->size() * sizeof(float));
 }
 
+// Host-side admission of a segment of `seq` tokens starting at position pos0:
+// it must fit the RoPE table and, on the cache path, the cache.
 void CheckPositions(const GpuModel& m, const GpuKvCache* kv, int64_t pos0, int64_t seq) {
-  RPG_CHECK(pos0 + seq <= m.rope_positions(),
-            "position %lld is beyond the %lld positions the RoPE table covers (load the model with a larger "
-            "max_pos, or reset the cache)",
-            static_cast<long long>(pos0 + seq), static_cast<long long>(m.rope_positions()));
-  if (kv != nullptr) {
-    RPG_CHECK(pos0 + seq <= kv->max_seq(), "position %lld exceeds the KV cache capacity %lld",
-              static_cast<long long>(pos0 + seq), static_cast<long long>(kv->max_seq()));
+  const long long end = static_cast<long long>(pos0 + seq);
+  if (pos0 + seq > m.rope_positions()) {
+    Throw("positions up to %lld requested, but the RoPE table was built for %lld (load the model with a larger "
+          "max_pos, or reset the cache)",
+          end, static_cast<long long>(m.rope_positions()));
+  }
+  if (kv != nullptr && pos0 + seq > kv->max_seq()) {
+    Throw("positions up to %lld do not fit the KV cache capacity of %lld", end, static_cast<long long>(kv->max_seq()));
   }
 }
 
 void CheckCache(const GpuModel& m, const GpuKvCache* kv) {
   const ModelMeta& c = m.config();
-  RPG_CHECK(kv->valid() && kv->n_layers() == c.n_layers && kv->n_kv_heads() == c.n_kv_heads &&
-                kv->head_dim() == c.head_dim,
-            "KV cache shape (%d layers x %d KV heads x %d) does not match the model (%d x %d x %d)", kv->n_layers(),
-            kv->n_kv_heads(), kv->head_dim(), c.n_layers, c.n_kv_heads, c.head_dim);
+  const bool same = kv->valid() && kv->n_layers() == c.n_layers && kv->n_kv_heads() == c.n_kv_heads &&
+                    kv->head_dim() == c.head_dim;
+  if (!same) {
+    Throw("the KV cache was built for %d layers / %d kv heads / head_dim %d, the model has %d / %d / %d",
+          kv->n_layers(), kv->n_kv_heads(), kv->head_dim(), c.n_layers, c.n_kv_heads, c.head_dim);
+  }
+}
+
+// Decode steps append: the step's position must be the cache's current length.
+void CheckAppend(const GpuKvCache* kv, int64_t pos) {
+  if (pos != kv->len()) {
+    Throw("a decode step writes at the end of the cache (length %lld); position %lld was given",
+          static_cast<long long>(kv->len()), static_cast<long long>(pos));
+  }
 }
 
 }  // namespace
 
 // ---------------------------------------------------------------- GpuScratch
 
+std::vector<const DeviceBuffer*> GpuScratch::buffers() const {
+  return {&x, &x_alt, &h, &q, &k, &v, &attn, &proj, &gate, &up, &toks, &logits, &probs, &argmax_idx};
+}
+
 void GpuScratch::Ensure(const ModelMeta& c, int64_t seq) {
-  RPG_CHECK(seq > 0, "scratch needs a positive segment length");
-  Need(x, seq * c.hidden);
-  Need(x_alt, c.hidden);
-  Need(h, seq * c.hidden);
-  Need(q, seq * c.q_dim());
-  Need(k, seq * c.kv_dim());
-  Need(v, seq * c.kv_dim());
-  Need(attn, seq * c.q_dim());
-  Need(proj, seq * c.hidden);
-  Need(gate, seq * c.intermediate);
-  Need(up, seq * c.intermediate);
-  Need(logits, seq * c.vocab);
-  Need(probs, c.vocab);
-  const size_t tok_bytes = static_cast<size_t>(seq) * sizeof(int32_t);
-  if (toks.size() < tok_bytes) toks.Alloc(tok_bytes);
-  if (argmax_idx.size() < sizeof(int32_t)) argmax_idx.Alloc(sizeof(int32_t));
+  if (seq <= 0) Throw("GpuScratch::Ensure: a segment of %lld tokens needs no buffers", static_cast<long long>(seq));
+  const int64_t fp = sizeof(float);
+  // Bytes each buffer must hold for a segment of `seq` tokens: per-token
+  // activations scale with seq; x_alt (the one-token residual twin), the
+  // sampling distribution and the sampled id do not.
+  const std::pair<DeviceBuffer*, int64_t> sizes[] = {
+      {&x, seq * c.hidden * fp},          {&x_alt, c.hidden * fp},
+      {&h, seq * c.hidden * fp},          {&q, seq * c.q_dim() * fp},
+      {&k, seq * c.kv_dim() * fp},        {&v, seq * c.kv_dim() * fp},
+      {&attn, seq * c.q_dim() * fp},      {&proj, seq * c.hidden * fp},
+      {&gate, seq * c.intermediate * fp}, {&up, seq * c.intermediate * fp},
+      {&toks, seq * 4},                   {&logits, seq * c.vocab * fp},
+      {&probs, c.vocab * fp},             {&argmax_idx, 4},
+  };
+  for (const auto& [buf, want] : sizes) {
+    if (static_cast<int64_t>(buf->size()) < want) buf->Alloc(static_cast<size_t>(want));
+  }
 }
 
 int64_t GpuScratch::bytes() const {
-  int64_t n = 0;
-  for (const DeviceBuffer* b : {&x, &x_alt, &h, &q, &k, &v, &attn, &proj, &gate, &up, &toks, &logits, &probs, &argmax_idx}) {
-    n += static_cast<int64_t>(b->size());
-  }
-  return n;
+  int64_t total = 0;
+  for (const DeviceBuffer* b : buffers()) total += static_cast<int64_t>(b->size());
+  return total;
 }
 
 GpuScratch::~GpuScratch() {
-  if (graph_exec != nullptr) {
-    const hipError_t e = hipGraphExecDestroy(graph_exec);
-    if (e != hipSuccess) RPG_LOG_WARN("hipGraphExecDestroy failed: %s", hipGetErrorString(e));
-    graph_exec = nullptr;
-  }
+  if (graph_exec == nullptr) return;
+  // A destructor cannot report failure; the only realistic one is a runtime
+  // already torn down at process exit, where the graph is gone anyway.
+  const hipError_t e = hipGraphExecDestroy(graph_exec);
+  if (e != hipSuccess) RPG_LOG_WARN("decode graph not released (%s)", hipGetErrorString(e));
+  graph_exec = nullptr;
 }
 
 // ---------------------------------------------------------------- forward
@@ -245,38 +258,39 @@ GpuScratch::~GpuScratch() {
 void GpuForwardFull(const GpuModel& m, const int32_t* tokens, int64_t seq, GpuScratch* s, std::vector<float>* logits,
                     const GpuForwardOptions& opt, GpuKvCache* kv) {
   const ModelMeta& c = m.config();
-  RPG_CHECK(s != nullptr, "GpuForwardFull needs a scratch");
-  RPG_CHECK(seq > 0, "prompt is empty");
-  RPG_CHECK(tokens != nullptr, "token array is null");
+  if (s == nullptr || tokens == nullptr) Throw("GpuForwardFull: %s is null", s == nullptr ? "scratch" : "tokens");
+  if (seq <= 0) Throw("GpuForwardFull: the token segment is empty");
   if (kv != nullptr) CheckCache(m, kv);
   const int64_t pos0 = kv != nullptr ? kv->len() : 0;
   CheckPositions(m, kv, pos0, seq);
-  for (int64_t t = 0; t < seq; ++t) {
-    RPG_CHECK(tokens[t] >= 0 && tokens[t] < c.vocab, "token #%lld has id %d, out of range (vocab %d)",
-              static_cast<long long>(t), tokens[t], c.vocab);
+  // Ids are checked here, on the host: the device gather turns a bad id into a
+  // zero row instead of failing, which would hide the caller's mistake.
+  const int32_t* bad = std::find_if(tokens, tokens + seq, [&c](int32_t id) { return id < 0 || id >= c.vocab; });
+  if (bad != tokens + seq) {
+    Throw("token %lld of the segment is %d, out of range for a vocabulary of %d",
+          static_cast<long long>(bad - tokens), *bad, c.vocab);
   }
   s->Ensure(c, seq);
   RPG_HIP_CHECK(hipMemcpyAsync(s->toks.data(), tokens, static_cast<size_t>(seq) * sizeof(int32_t),
                                hipMemcpyHostToDevice, EngineStream()));
   ForwardCore(m, seq, s, static_cast<const int32_t*>(s->toks.data()), logits, opt, kv, -1);
+  // The cache grows only once every layer has been written.
   if (kv != nullptr) kv->SetLen(pos0 + seq);
 }
 
 void GpuForwardStep(const GpuModel& m, int32_t token, int64_t pos, GpuKvCache* kv, GpuScratch* s,
                     std::vector<float>* logits) {
-  RPG_CHECK(kv != nullptr, "GpuForwardStep requires a KV cache");
-  RPG_CHECK(pos == kv->len(), "incremental decoding only appends in order: pos = %lld but the cache length is %lld",
-            static_cast<long long>(pos), static_cast<long long>(kv->len()));
+  if (kv == nullptr) Throw("GpuForwardStep: a decode step needs the KV cache");
+  CheckAppend(kv, pos);
   GpuForwardFull(m, &token, 1, s, logits, GpuForwardOptions(), kv);
 }
 
 void GpuForwardStepDev(const GpuModel& m, const int32_t* token_dev, int64_t pos, GpuKvCache* kv, GpuScratch* s) {
-  RPG_CHECK(kv != nullptr, "GpuForwardStepDev requires a KV cache");
-  RPG_CHECK(token_dev != nullptr, "GpuForwardStepDev requires a device-side token");
-  RPG_CHECK(s != nullptr, "GpuForwardStepDev needs a scratch");
+  if (kv == nullptr || s == nullptr || token_dev == nullptr) {
+    Throw("GpuForwardStepDev: the %s is null", kv == nullptr ? "KV cache" : s == nullptr ? "scratch" : "token pointer");
+  }
   CheckCache(m, kv);
-  RPG_CHECK(pos == kv->len(), "incremental decoding only appends in order: pos = %lld but the cache length is %lld",
-            static_cast<long long>(pos), static_cast<long long>(kv->len()));
+  CheckAppend(kv, pos);
   CheckPositions(m, kv, pos, 1);
   ForwardCore(m, 1, s, token_dev, nullptr, GpuForwardOptions(), kv, kv->max_seq());
   kv->SetLen(pos + 1);
@@ -286,39 +300,39 @@ void GpuForwardStepDev(const GpuModel& m, const int32_t* token_dev, int64_t pos,
 
 namespace {
 
-uint64_t MakeGraphKey(const GpuModel& m, GpuKvCache* kv, const GpuScratch* s, const GpuGenerateOptions& opt) {
+// Everything a captured decode step depends on, as plain words. Two
+// signatures compare equal only if a replay would touch exactly the same
+// memory with the same shapes and sampling parameters; no hashing, so no
+// collision can ever replay a stale graph.
+std::vector<uint64_t> DecodeStepSignature(const GpuModel& m, const GpuKvCache* kv, const GpuScratch* s,
+                                          const GpuGenerateOptions& opt) {
   const ModelMeta& c = m.config();
-  uint64_t h = 0x6A09E667F3BCC909ull;
-  auto mix = [&h](uint64_t v) { h = DevSplitMix64(h ^ v); };
-  auto mixf = [&mix](float f) {
+  auto bits = [](float f) {
     uint32_t u;
     std::memcpy(&u, &f, sizeof(u));
-    mix(u);
+    return static_cast<uint64_t>(u);
   };
-  // every device address the captured step holds: a buffer that was
-  // reallocated (a longer prefill grows the scratch) or a cache / model at a
-  // recycled host address must not replay a stale graph
-  mix(reinterpret_cast<uintptr_t>(&m));
-  mix(reinterpret_cast<uintptr_t>(m.token_embd().buf.data()));
-  mix(reinterpret_cast<uintptr_t>(kv));
-  mix(reinterpret_cast<uintptr_t>(kv->k_layer(0)));
-  mix(reinterpret_cast<uintptr_t>(kv->v_layer(0)));
-  for (const DeviceBuffer* b : {&s->x, &s->x_alt, &s->h, &s->q, &s->k, &s->v, &s->attn, &s->proj, &s->gate, &s->up, &s->logits,
-                                &s->probs, &s->argmax_idx}) {
-    mix(reinterpret_cast<uintptr_t>(b->data()));
-  }
-  mix(static_cast<uint64_t>(kv->max_seq()));
-  mix(static_cast<uint64_t>(c.n_layers));
-  mix(static_cast<uint64_t>(c.hidden));
-  mix(static_cast<uint64_t>(c.vocab));
-  mix(static_cast<uint64_t>(c.n_heads));
-  mix(static_cast<uint64_t>(c.n_kv_heads));
-  mix(static_cast<uint64_t>(c.head_dim));
-  mixf(opt.sample.temperature);
-  mix(static_cast<uint64_t>(static_cast<uint32_t>(opt.sample.top_k)));
-  mixf(opt.sample.top_p);
-  mix(opt.seed);
-  return h;
+  std::vector<uint64_t> sig = {
+      reinterpret_cast<uintptr_t>(&m),
+      reinterpret_cast<uintptr_t>(m.token_embd().buf.data()),
+      reinterpret_cast<uintptr_t>(m.lm_head().buf.data()),
+      reinterpret_cast<uintptr_t>(m.rope_dev()),
+      reinterpret_cast<uintptr_t>(kv),
+      reinterpret_cast<uintptr_t>(kv->k_layer(0)),
+      reinterpret_cast<uintptr_t>(kv->v_layer(0)),
+      static_cast<uint64_t>(kv->max_seq()),
+      static_cast<uint64_t>(c.n_layers),
+      static_cast<uint64_t>(c.hidden),
+      static_cast<uint64_t>(c.intermediate),
+      static_cast<uint64_t>(c.vocab),
+      static_cast<uint64_t>(c.n_heads) << 32 | static_cast<uint32_t>(c.n_kv_heads),
+      static_cast<uint64_t>(c.head_dim),
+      bits(opt.sample.temperature) << 32 | bits(opt.sample.top_p),
+      static_cast<uint64_t>(static_cast<uint32_t>(opt.sample.top_k)),
+      opt.seed,
+  };
+  for (const DeviceBuffer* b : s->buffers()) sig.push_back(reinterpret_cast<uintptr_t>(b->data()));
+  return sig;
 }
 
 // Captures one decode step on the capture stream: sample the next token from
@@ -392,15 +406,17 @@ bool GenerateGraph(const GpuModel& m, GpuKvCache* kv, GpuScratch* s, const GpuGe
                                  hipMemcpyDeviceToDevice, cap));
   }
   CheckRoom(m, kv, 1);  // the capture itself appends at kv->len()
-  const uint64_t key = MakeGraphKey(m, kv, s, opt);
-  if (s->graph_exec == nullptr || s->graph_key != key) {
-    if (s->graph_exec != nullptr) {
-      (void)hipGraphExecDestroy(s->graph_exec);
-      s->graph_exec = nullptr;
-      s->graph_key = 0;
-    }
+  std::vector<uint64_t> sig = DecodeStepSignature(m, kv, s, opt);
+  if (s->graph_exec != nullptr && s->graph_signature != sig) {
+    (void)hipGraphExecDestroy(s->graph_exec);
+    s->graph_exec = nullptr;
+    s->graph_signature.clear();
+  }
+  if (s->graph_exec == nullptr) {
     s->graph_exec = CaptureDecodeStep(m, kv, s, opt);
-    if (s->graph_exec != nullptr) s->graph_key = key;
+    // Capturing may have grown nothing (everything is allocated first), but the
+    // signature is taken again so it describes exactly what was captured.
+    if (s->graph_exec != nullptr) s->graph_signature = DecodeStepSignature(m, kv, s, opt);
   }
   if (s->graph_exec == nullptr) {
     RPG_LOG_WARN("HIP graph capture is unavailable; generating with per-step launches");

@@ -73,10 +73,15 @@ class GpuScratch {
   DeviceBuffer probs;   // [vocab] sampling distribution
   DeviceBuffer argmax_idx;  // [1] int32: the sampled / argmax token
 
-  // The captured decode step (sample -> forward) and the fingerprint of what it
-  // was captured for (model, cache, scratch, shapes, sampling options).
+  // The captured decode step (sample -> forward) and everything it baked in:
+  // the device addresses it reads and writes (model, cache layers, every
+  // scratch buffer), the shapes and the sampling options. The graph is
+  // replayed only while a fresh signature compares equal, element by element.
   hipGraphExec_t graph_exec = nullptr;
-  uint64_t graph_key = 0;
+  std::vector<uint64_t> graph_signature;
+
+  // Every device buffer above, in declaration order.
+  std::vector<const DeviceBuffer*> buffers() const;
 };
 
 struct GpuForwardOptions {

@@ -184,7 +184,7 @@ def test_prefill_pieces_and_decode_steps_match_oracle(gpu, models, name):
     print(f"  logits full-scale {fs:.3g}", flush=True)
     assert fs <= 1e-3
     assert_argmax_or_tie(lg_gpu, lg_ref)
-    with pytest.raises(gpu.RpgError, match="appends in order"):
+    with pytest.raises(gpu.RpgError, match="end of the cache"):
         gpu.GpuForwardStep(m, 1, 200, kv, s)
     kv.free()
     s.free()
