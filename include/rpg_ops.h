@@ -275,6 +275,9 @@ RPG_OPS_API int32_t rpg_model_describe(const rpg_model* m, char* buf, int32_t ca
 /* File bytes moved to the device, and the parse / upload wall times. */
 RPG_OPS_API int32_t rpg_model_upload_stats(const rpg_model* m, int64_t* bytes, double* parse_seconds,
                                            double* upload_seconds);
+/* Device bytes the model holds (weight arena and RoPE table).
+ * Replaces: GpuModel::device_bytes, src/gpu_model.h:101. */
+RPG_OPS_API int32_t rpg_model_device_bytes(const rpg_model* m, int64_t* out);
 
 /* ---------------------------------------------------------------- forward and generation
  * The Qwen3 layer chain over the operators above, for a loaded rpg_model.
@@ -287,6 +290,11 @@ typedef struct rpg_kv rpg_kv;
 typedef struct rpg_scratch rpg_scratch;
 
 RPG_OPS_API int32_t rpg_kv_create(const rpg_model* m, int64_t max_seq, rpg_kv** out);
+/* The same cache from the three shape numbers it depends on, with no loaded model
+ * at hand (the engine sizes its session caches from ModelMeta alone).
+ * Replaces: GpuKvCache::GpuKvCache(const ModelMeta&, int64_t), src/kv_cache_gpu.h:56. */
+RPG_OPS_API int32_t rpg_kv_create_shape(int32_t n_layers, int32_t n_kv_heads, int32_t head_dim, int64_t max_seq,
+                                        rpg_kv** out);
 RPG_OPS_API int32_t rpg_kv_free(rpg_kv* kv);
 /* Current length (positions filled), capacity and K + V bytes. */
 RPG_OPS_API int32_t rpg_kv_info(const rpg_kv* kv, int64_t* len, int64_t* max_seq, int64_t* bytes);

@@ -385,6 +385,13 @@ int32_t rpg_model_describe(const rpg_model* m, char* buf, int32_t cap) {
   return rc < 0 ? rc : len;
 }
 
+int32_t rpg_model_device_bytes(const rpg_model* m, int64_t* out) {
+  return Guard([&] {
+    RPG_CHECK(m != nullptr && out != nullptr, "null argument");
+    *out = m->model.device_bytes();
+  });
+}
+
 int32_t rpg_model_upload_stats(const rpg_model* m, int64_t* bytes, double* parse_seconds, double* upload_seconds) {
   return Guard([&] {
     RPG_CHECK(m != nullptr, "null model handle");
@@ -400,6 +407,18 @@ int32_t rpg_kv_create(const rpg_model* m, int64_t max_seq, rpg_kv** out) {
     RPG_CHECK(m != nullptr && out != nullptr, "null argument");
     *out = nullptr;
     *out = new rpg_kv{rpg::GpuKvCache(m->model.config(), max_seq)};
+  });
+}
+
+int32_t rpg_kv_create_shape(int32_t n_layers, int32_t n_kv_heads, int32_t head_dim, int64_t max_seq, rpg_kv** out) {
+  return Guard([&] {
+    RPG_CHECK(out != nullptr, "null argument");
+    *out = nullptr;
+    rpg::ModelMeta c;
+    c.n_layers = n_layers;
+    c.n_kv_heads = n_kv_heads;
+    c.head_dim = head_dim;
+    *out = new rpg_kv{rpg::GpuKvCache(c, max_seq)};
   });
 }
 

@@ -51,7 +51,9 @@ SIGNATURES = {
     "rpg_model_rope": (_i32, [_vp, _vp, _vp]),
     "rpg_model_describe": (_i32, [_vp, ctypes.c_char_p, _i32]),
     "rpg_model_upload_stats": (_i32, [_vp, _vp, _vp, _vp]),
+    "rpg_model_device_bytes": (_i32, [_vp, _vp]),
     "rpg_kv_create": (_i32, [_vp, _i64, _vp]),
+    "rpg_kv_create_shape": (_i32, [_i32, _i32, _i32, _i64, _vp]),
     "rpg_kv_free": (_i32, [_vp]),
     "rpg_kv_info": (_i32, [_vp, _vp, _vp, _vp]),
     "rpg_kv_set_len": (_i32, [_vp, _i64]),

@@ -97,12 +97,62 @@ def random_tensor(rng: np.random.Generator, ggml_type: int, dims, model_like: bo
     return rng.integers(0, 256, size=tensor_bytes(ggml_type, dims), dtype=np.uint8).tobytes()
 
 
+def byte_to_unicode() -> dict:
+    """The byte -> character map of byte-level BPE vocabularies (GPT-2's, used by
+    Qwen): printable Latin-1 bytes stand for themselves, every other byte b is
+    the character 256 + (its rank among those bytes)."""
+    keep = list(range(ord("!"), ord("~") + 1)) + list(range(0xA1, 0xAD)) + list(range(0xAE, 0x100))
+    out, extra = {}, 0
+    for b in range(256):
+        if b in keep:
+            out[b] = chr(b)
+        else:
+            out[b] = chr(256 + extra)
+            extra += 1
+    return out
+
+
+CHATML_SPECIALS = ("<|endoftext|>", "<|im_start|>", "<|im_end|>")
+
+
+def ascii_bpe_vocab(n_vocab: int):
+    """A byte-level BPE vocabulary whose every token decodes to ASCII: one token
+    per printable byte and newline, the ChatML control tokens (type 3), then
+    filler tokens "x<i>" up to n_vocab, and one merge ("z q") that no test text
+    contains. Returns (tokens, types, merges)."""
+    b2u = byte_to_unicode()
+    tokens = [b2u[b] for b in [10] + list(range(0x20, 0x7F))]
+    types = [1] * len(tokens)
+    tokens += list(CHATML_SPECIALS)
+    types += [3] * len(CHATML_SPECIALS)
+    tokens.append("zq")
+    types.append(1)
+    i = len(tokens)
+    while len(tokens) < n_vocab:
+        tokens.append(f"x{i}")
+        types.append(1)
+        i += 1
+    return tokens, types, ["z q"]
+
+
+def tokenizer_kv(n_vocab: int):
+    """GGUF tokenizer metadata for ascii_bpe_vocab: tokens, token types, merges,
+    eos = <|im_end|>, bos = <|endoftext|> (not prepended)."""
+    tokens, types, merges = ascii_bpe_vocab(n_vocab)
+    return [("tokenizer.ggml.model", STR, "gpt2"), ("tokenizer.ggml.tokens", ARR, (STR, tokens)),
+            ("tokenizer.ggml.token_type", ARR, (I32, types)), ("tokenizer.ggml.merges", ARR, (STR, merges)),
+            ("tokenizer.ggml.bos_token_id", U32, tokens.index("<|endoftext|>")),
+            ("tokenizer.ggml.eos_token_id", U32, tokens.index("<|im_end|>")),
+            ("tokenizer.ggml.padding_token_id", U32, tokens.index("<|endoftext|>"))]
+
+
 def qwen3_model(rng: np.random.Generator, n_layers=2, hidden=256, n_heads=2, n_kv_heads=1, head_dim=128,
                 inter=512, vocab=1000, tied=False, version=3, alignment=32, mat_type=None, norm_type=GGML_F32,
-                key_length=True, extra_kv=(), drop=(), override=None, model_like=False):
+                key_length=True, extra_kv=(), drop=(), override=None, model_like=False, tokenizer=False):
     """(bytes, tensors, kv) of a synthetic qwen3 GGUF with Q4_K / Q6_K matrices
     (Q4_K_M-like: attn_v, ffn_down and the embeddings Q6_K, the rest Q4_K).
-    model_like: zero-mean weights of trained-model size, for forward tests."""
+    model_like: zero-mean weights of trained-model size, for forward tests.
+    tokenizer: replace the placeholder token list with tokenizer_kv(vocab)."""
     kv = [("general.architecture", STR, "qwen3"), ("general.name", STR, "synthetic-qwen3"),
           ("qwen3.block_count", U32, n_layers), ("qwen3.embedding_length", U32, hidden),
           ("qwen3.attention.head_count", U32, n_heads), ("qwen3.attention.head_count_kv", U32, n_kv_heads),
@@ -111,6 +161,10 @@ def qwen3_model(rng: np.random.Generator, n_layers=2, hidden=256, n_heads=2, n_k
           ("tokenizer.ggml.bos_token_id", U32, 151643), ("tokenizer.ggml.eos_token_id", U32, 151645),
           ("tokenizer.ggml.padding_token_id", U32, 151643), ("tokenizer.ggml.add_bos_token", BOOL, False),
           ("tokenizer.ggml.tokens", ARR, (STR, [f"t{i}" for i in range(8)]))]
+    if tokenizer:
+        tok = tokenizer_kv(vocab)
+        names = {k for k, _, _ in tok}
+        kv = [e for e in kv if e[0] not in names] + tok
     if key_length:
         kv += [("qwen3.attention.key_length", U32, head_dim), ("qwen3.attention.value_length", U32, head_dim)]
     if alignment != 32:
