@@ -42,7 +42,10 @@ class _Reader:
         return self.take(n).decode("utf-8", "surrogateescape")
 
 
-def _value(r: _Reader, t: int):
+MAX_ARRAY_DEPTH = 64  # nesting bound of this build's reader (the reference recurses without one)
+
+
+def _value(r: _Reader, t: int, depth: int = 0):
     """Numbers become float (as the reference's JSON doubles), then bool, str, list."""
     fmts = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 10: "<Q", 11: "<q", 12: "<d"}
     if t in fmts:
@@ -55,11 +58,13 @@ def _value(r: _Reader, t: int):
     if t == 8:
         return r.string()
     if t == 9:
+        if depth >= MAX_ARRAY_DEPTH:
+            raise GgufError("arrays nested too deep")
         et = r.get("<I")
         n = r.get("<Q")
         if n >= 1 << 32:
             raise GgufError("array too long")
-        return [_value(r, et) for _ in range(n)]
+        return [_value(r, et, depth + 1) for _ in range(n)]
     raise GgufError(f"unknown metadata type {t}")
 
 

@@ -124,6 +124,7 @@ class Cursor {
  public:
   Cursor(const uint8_t* p, size_t n) : base_(p), size_(n) {}
   size_t pos() const { return pos_; }
+  size_t remaining() const { return size_ - pos_; }
 
   const uint8_t* Take(uint64_t n) {
     RPG_CHECK(n <= size_ - pos_, "GGUF truncated: need %llu bytes at offset %zu of %zu",
@@ -157,9 +158,26 @@ GgufValue Number(double v) {
   return x;
 }
 
+// Arrays of arrays deeper than this are rejected: the recursion below costs a
+// stack frame per level, and no real file nests metadata more than twice.
+constexpr int kMaxArrayDepth = 64;
+
+// Fewest bytes one encoded value of `type` can take (0 for an unknown type,
+// which ReadValue rejects): bounds what an array's item count may claim.
+uint64_t MinValueBytes(uint32_t type) {
+  switch (type) {
+    case 0: case 1: case 7: return 1;
+    case 2: case 3: return 2;
+    case 4: case 5: case 6: return 4;
+    case 10: case 11: case 12: case 8: return 8;  // a string is at least its u64 length
+    case 9: return 12;                             // u32 item type + u64 count
+    default: return 0;
+  }
+}
+
 // gguf_metadata_value_type: 0 u8, 1 i8, 2 u16, 3 i16, 4 u32, 5 i32, 6 f32, 7 bool,
 // 8 string, 9 array, 10 u64, 11 i64, 12 f64.
-GgufValue ReadValue(Cursor& c, uint32_t type) {
+GgufValue ReadValue(Cursor& c, uint32_t type, int depth = 0) {
   switch (type) {
     case 0: return Number(c.Get<uint8_t>());
     case 1: return Number(c.Get<int8_t>());
@@ -183,13 +201,22 @@ GgufValue ReadValue(Cursor& c, uint32_t type) {
       return x;
     }
     case 9: {
+      RPG_CHECK(depth < kMaxArrayDepth, "GGUF metadata nests arrays more than %d levels deep", kMaxArrayDepth);
       const uint32_t elem = c.Get<uint32_t>();
       const uint64_t n = c.Get<uint64_t>();
       RPG_CHECK(n < (uint64_t{1} << 32), "GGUF metadata array too long: %llu", static_cast<unsigned long long>(n));
+      // The count comes from the file: reserve only what the bytes left could hold,
+      // so a forged count fails as truncation instead of as a huge allocation.
+      const uint64_t min_bytes = MinValueBytes(elem);
+      if (min_bytes > 0 && n > c.remaining() / min_bytes) {
+        Throw("GGUF truncated: an array of %llu items of type %u needs at least %llu bytes, %zu remain",
+              static_cast<unsigned long long>(n), elem, static_cast<unsigned long long>(n * min_bytes),
+              c.remaining());
+      }
       GgufValue x;
       x.kind = GgufValue::Kind::kArray;
       x.items.reserve(static_cast<size_t>(n));
-      for (uint64_t i = 0; i < n; ++i) x.items.push_back(ReadValue(c, elem));
+      for (uint64_t i = 0; i < n; ++i) x.items.push_back(ReadValue(c, elem, depth + 1));
       return x;
     }
     case 10: return Number(static_cast<double>(c.Get<uint64_t>()));

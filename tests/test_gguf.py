@@ -4,6 +4,7 @@ runs without a GPU."""
 from __future__ import annotations
 
 import ctypes
+import struct
 
 import numpy as np
 import pytest
@@ -107,3 +108,44 @@ def test_open_errors(ops, tmp_path):
     with ops.GgufFile(write(tmp_path, "l.gguf", llama)) as g:
         with pytest.raises(ops.RpgError, match="qwen3"):
             g.model_meta()
+
+
+def _raw_kv_file(key: str, value_bytes: bytes) -> bytes:
+    """A v3 GGUF with general.architecture, one extra key whose type + value bytes
+    are given raw (so counts can lie), no tensors, and 64 bytes of padding."""
+    body = W.gstr("general.architecture") + struct.pack("<I", W.STR) + W.gstr("qwen3")
+    body += W.gstr(key) + value_bytes
+    return b"GGUF" + struct.pack("<IQQ", 3, 0, 2) + body + bytes(64)  # + room for the aligned data start
+
+
+def test_forged_array_count_fails_as_truncation(ops, tmp_path):
+    """An array claiming 2^32 - 1 u32 items with 72 bytes left: rejected as
+    truncated before anything is allocated for it (both readers)."""
+    blob = _raw_kv_file("big", struct.pack("<IIQ", W.ARR, W.U32, (1 << 32) - 1) + bytes(8))
+    with pytest.raises(ops.RpgError, match="truncated"):
+        ops.GgufFile(write(tmp_path, "big.gguf", blob))
+    with pytest.raises(R.GgufError):
+        R.read(blob)
+
+
+def _nested(depth: int) -> bytes:
+    """Type + value bytes of `depth` arrays nested one in another around one u8."""
+    inner = struct.pack("<IQ", W.U8, 1) + b"\x07"
+    for _ in range(depth - 1):
+        inner = struct.pack("<IQ", W.ARR, 1) + inner
+    return struct.pack("<I", W.ARR) + inner
+
+
+def test_array_nesting_is_bounded(ops, tmp_path):
+    ok = _raw_kv_file("deep", _nested(64))
+    g = ops.GgufFile(write(tmp_path, "ok.gguf", ok))
+    g.close()
+    assert R.read(ok)["meta"]["deep"] is not None
+    deep = _raw_kv_file("deep", _nested(65))
+    with pytest.raises(ops.RpgError, match="levels deep"):
+        ops.GgufFile(write(tmp_path, "deep.gguf", deep))
+    with pytest.raises(R.GgufError):
+        R.read(deep)
+    huge = _raw_kv_file("deep", _nested(100000))  # would exhaust the stack without the bound
+    with pytest.raises(ops.RpgError, match="levels deep"):
+        ops.GgufFile(write(tmp_path, "huge.gguf", huge))
