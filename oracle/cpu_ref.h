@@ -99,6 +99,13 @@ int32_t ora_argmax(const float* x, int64_t n, float init);
 int ora_filter_to_probs(const float* logits, int64_t n, float temperature, int32_t top_k, float top_p, float* probs,
                         double* margin);
 int32_t ora_inverse_sample(const float* probs, int64_t n, float u);
+/* The top_p cut's order key under three rules for comparing S(t) with 1 - top_p:
+ * the exact mass (the oracle's), the device's 2^-62 grid, the reference's double
+ * sums (see cpu_sample.c). */
+#define ORA_TOPP_EXACT 0
+#define ORA_TOPP_GRID62 1
+#define ORA_TOPP_DOUBLE 2
+uint32_t ora_top_p_cut_key(const float* probs, int64_t n, float top_p, int rule, double* margin);
 int32_t ora_sample_token(const float* logits, int64_t n, float temperature, int32_t top_k, float top_p, uint64_t seed,
                          uint64_t counter, float* probs);
 

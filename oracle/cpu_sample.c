@@ -92,6 +92,80 @@ static unsigned __int128 fix125(double p) {
 
 static double unfix125(unsigned __int128 v) { return (double)((long double)v * 0x1p-125L); }
 
+/* p * 2^62 truncated: the weight the device's top_p histograms sum (exact
+ * integers, so the sum does not depend on the order of the atomics). */
+static unsigned __int128 fix62(float p) {
+  if (!(p > 0.0f)) return 0;
+  return (unsigned __int128)(uint64_t)ldexp((double)p, 62);
+}
+
+/* The top_p cut (src/sampler_gpu.cu:243-270): with S(t) the mass of the
+ * probabilities whose order key is <= t, the cut is the largest t with
+ * S(t) <= 1 - top_p, and every p <= cut is dropped. Returns the cut's order
+ * key (0 on allocation failure: no real cut is 0). `rule` decides how S(t) is
+ * compared:
+ *   ORA_TOPP_EXACT   the real number (fixed point at 2^-125: exact for fp32
+ *                    probabilities); the oracle's semantics;
+ *   ORA_TOPP_GRID62  the device kernel's: every p truncated to the 2^-62 grid,
+ *                    summed as integers, against floor((1 - top_p) * 2^62);
+ *   ORA_TOPP_DOUBLE  the reference's: S(t) as a double sum (here in index
+ *                    order; the reference sums strided per thread, then over the
+ *                    block) against the double 1 - top_p.
+ * The three agree unless S(t) lies within rounding of 1 - top_p: about
+ * n * 2^-53 S for the double sums, n * 2^-62 for the grid.
+ * *margin (may be NULL; EXACT only) receives the distance between 1 - top_p
+ * and the nearest cumulative mass that decides the cut. */
+uint32_t ora_top_p_cut_key(const float* probs, int64_t n, float top_p, int rule, double* margin) {
+  const double threshold = 1.0 - (double)top_p;
+  const unsigned __int128 thr = rule == ORA_TOPP_GRID62 ? (unsigned __int128)(uint64_t)floor(ldexp(threshold, 62))
+                                                        : fix125(threshold);
+  KeyProb* kp = (KeyProb*)malloc((size_t)n * sizeof(KeyProb));
+  if (!kp) return 0u;
+  for (int64_t i = 0; i < n; ++i) {
+    kp[i].key = order_key(probs[i]);
+    kp[i].p = probs[i];
+  }
+  uint32_t cut_key = 0xFFFFFFFFu;
+  if (rule == ORA_TOPP_DOUBLE) {
+    /* the reference's binary search, literally: the largest key t whose double
+     * S(t) <= threshold (S is monotone in t) */
+    uint32_t lo = 0u, hi = 0xFFFFFFFFu;
+    while (lo < hi) {
+      const uint32_t mid = (uint32_t)(lo + (((uint64_t)hi - lo + 1) >> 1));
+      double sm = 0.0;
+      for (int64_t i = 0; i < n; ++i)
+        if (kp[i].key <= mid) sm += (double)kp[i].p;
+      if (sm <= threshold) {
+        lo = mid;
+      } else {
+        hi = mid - 1;
+      }
+    }
+    free(kp);
+    return lo;
+  }
+  qsort(kp, (size_t)n, sizeof(KeyProb), cmp_keyprob_asc);
+  /* one below the smallest key whose cumulative mass exceeds the threshold */
+  unsigned __int128 sum = 0;
+  double m = INFINITY;
+  int64_t i = 0;
+  while (i < n) {
+    const uint32_t key = kp[i].key;
+    unsigned __int128 s_next = sum;
+    for (; i < n && kp[i].key == key; ++i) s_next += rule == ORA_TOPP_GRID62 ? fix62(kp[i].p) : fix125(kp[i].p);
+    if (s_next > thr) {
+      cut_key = key - 1u;
+      m = fmin(unfix125(s_next - thr), unfix125(thr - sum));
+      break;
+    }
+    sum = s_next;
+  }
+  if (cut_key == 0xFFFFFFFFu) m = unfix125(thr - sum);
+  free(kp);
+  if (margin && rule == ORA_TOPP_EXACT) *margin = m;
+  return cut_key;
+}
+
 /* FilterProbsKernel semantics (src/sampler_gpu.cu:161-298). *margin (may be
  * NULL) receives, when top_p is active, the distance between 1 - top_p and the
  * nearest cumulative mass that decides the cut: agreement with any other
@@ -134,35 +208,8 @@ int ora_filter_to_probs(const float* logits, int64_t n, float temperature, int32
   for (int64_t i = 0; i < n; ++i) probs[i] *= inv;
 
   if (top_p > 0.0f && top_p < 1.0f) {
-    const double threshold = 1.0 - (double)top_p;
-    const unsigned __int128 thr = fix125(threshold);
-    KeyProb* kp = (KeyProb*)malloc((size_t)n * sizeof(KeyProb));
-    if (!kp) return -1;
-    for (int64_t i = 0; i < n; ++i) {
-      kp[i].key = order_key(probs[i]);
-      kp[i].p = probs[i];
-    }
-    qsort(kp, (size_t)n, sizeof(KeyProb), cmp_keyprob_asc);
-    /* S(t) = sum of p over keys <= t; the cut is the largest t with S(t) <= thr,
-     * i.e. one below the smallest key K* whose S exceeds thr. */
-    unsigned __int128 s = 0;
-    uint32_t cut_key = 0xFFFFFFFFu;
-    double m = INFINITY;
-    int64_t i = 0;
-    while (i < n) {
-      const uint32_t key = kp[i].key;
-      unsigned __int128 s_next = s;
-      while (i < n && kp[i].key == key) s_next += fix125(kp[i++].p);
-      if (s_next > thr) {
-        cut_key = key - 1u;
-        m = fmin(unfix125(s_next - thr), unfix125(thr - s));
-        break;
-      }
-      s = s_next;
-    }
-    if (cut_key == 0xFFFFFFFFu) m = unfix125(thr - s);
-    free(kp);
-    if (margin) *margin = m;
+    const uint32_t cut_key = ora_top_p_cut_key(probs, n, top_p, ORA_TOPP_EXACT, margin);
+    if (cut_key == 0u) return -1;
     const float cut = from_order_key(cut_key);
     for (int64_t j = 0; j < n; ++j)
       if (probs[j] <= cut) probs[j] = 0.0f;

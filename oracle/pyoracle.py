@@ -37,6 +37,7 @@ _SIGS = {
     "ora_argmax": (_i32, [_vp, _i64, _f32]),
     "ora_filter_to_probs": (ctypes.c_int, [_vp, _i64, _f32, _i32, _f32, _vp, _vp]),
     "ora_inverse_sample": (_i32, [_vp, _i64, _f32]),
+    "ora_top_p_cut_key": (ctypes.c_uint32, [_vp, _i64, _f32, ctypes.c_int, _vp]),
     "ora_sample_token": (_i32, [_vp, _i64, _f32, _i32, _f32, ctypes.c_uint64, ctypes.c_uint64, _vp]),
     "ora_rms_norm": (None, [_vp, _vp, _i64, _i64, _i64, _f32, _vp]),
     "ora_build_rope_table": (None, [_i32, _f64, _i64, _vp]),
@@ -247,6 +248,20 @@ def filter_to_probs(logits: np.ndarray, temperature: float, top_k: int, top_p: f
     if rc != 0:
         raise ValueError("ora_filter_to_probs failed")
     return probs, float(margin.value)
+
+
+TOPP_EXACT, TOPP_GRID62, TOPP_DOUBLE = 0, 1, 2
+
+
+def top_p_cut(probs: np.ndarray, top_p: float, rule: int) -> float:
+    """The top_p cut value (every p <= it is dropped) under `rule`: TOPP_EXACT (the
+    oracle's exact mass), TOPP_GRID62 (the device kernel's 2^-62 grid) or
+    TOPP_DOUBLE (the reference's double sums)."""
+    probs = _f(probs)
+    key = int(lib().ora_top_p_cut_key(_p(probs), probs.size, top_p, rule, None))
+    assert key != 0, "allocation failed"
+    u = key & 0x7FFFFFFF if key & 0x80000000 else ~key & 0xFFFFFFFF
+    return float(np.array([u], np.uint32).view(np.float32)[0])
 
 
 def inverse_sample(probs: np.ndarray, u: float) -> int:

@@ -161,3 +161,43 @@ def test_sample_token_greedy_draws_nothing(ora):
     logits = sample_logits(13, False, 4096)
     toks = {ora.sample_token(logits, 1.0, 0, 1.0, 13, c) for c in range(16)}
     assert len(toks) > 1
+
+
+def test_top_p_decision_rules_at_a_boundary(ora):
+    """Where the three ways of comparing the top_p mass S(t) with 1 - top_p part.
+
+    probs 2^-60, 0.25, 0.75 (exact in fp32) with top_p = 0.75, so 1 - top_p =
+    0.25 exactly. Dropping {2^-60, 0.25} removes a mass of
+    0.25 + 2^-60, just above 0.25: the exact rule (the oracle's) and the device
+    kernel's 2^-62 grid both refuse that cut and drop only 2^-60, while the
+    reference's double sums round 0.25 + 2^-60 to 0.25 (an ulp of 0.25 is 2^-54)
+    and drop 0.25 as well. This build decides on the exact mass (a recorded
+    deviation); the two differ only when S(t) lies within ~n * 2^-53 of
+    1 - top_p."""
+    tiny = 2.0 ** -60
+    probs = np.array([tiny, 0.25, 0.75], np.float32)
+    assert float(probs[0]) == tiny
+    assert float(probs[0]) + 0.25 == 0.25  # the double sum loses the tiny mass
+
+    def kept(top_p, rule):
+        return (probs > np.float32(ora.top_p_cut(probs, top_p, rule))).tolist()
+
+    assert kept(0.75, ora.TOPP_EXACT) == [False, True, True]
+    assert kept(0.75, ora.TOPP_GRID62) == [False, True, True]
+    assert kept(0.75, ora.TOPP_DOUBLE) == [False, False, True]
+    # away from the boundary the rules agree: with 1 - top_p = 0.5 the mass
+    # 2^-60 + 0.25 is well below it, and adding 0.75 well above
+    for rule in (ora.TOPP_EXACT, ora.TOPP_GRID62, ora.TOPP_DOUBLE):
+        assert kept(0.5, rule) == [False, False, True]
+
+
+def test_top_p_rules_agree_on_random_distributions(ora):
+    rng = np.random.default_rng(31)
+    for trial in range(40):
+        logits = rng.normal(0, 2, 4096).astype(np.float32)
+        e = np.exp(logits - logits.max())
+        probs = (e / e.sum()).astype(np.float32)
+        top_p = float(rng.uniform(0.5, 0.99))
+        kept = {tuple(np.flatnonzero(probs > np.float32(ora.top_p_cut(probs, top_p, r))))
+                for r in (ora.TOPP_EXACT, ora.TOPP_GRID62, ora.TOPP_DOUBLE)}
+        assert len(kept) == 1, trial
