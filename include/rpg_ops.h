@@ -175,6 +175,14 @@ RPG_OPS_API int32_t rpg_op_attention_warmup(int64_t sh_positions);
 RPG_OPS_API int32_t rpg_op_matmul_quant(uint32_t type, const uint8_t* w, int64_t rows, int64_t cols,
                                         const float* x, int64_t n_tokens, float* out);
 
+/* Path-equivalence switch: force != 0 makes every matmul entry point run the
+ * generic per-element kernel instead of the decode / tiled / matrix-core
+ * kernels (the norm-fused ones then report *fused = 0). For verification only;
+ * process-wide, off by default. rpg_op_force_generic_matmul returns 1 or 0.
+ * Replaces: GpuSetForceGenericMatMul / GpuForceGenericMatMul, src/kernels_gpu.h:57-58. */
+RPG_OPS_API int32_t rpg_op_set_force_generic_matmul(int32_t force);
+RPG_OPS_API int32_t rpg_op_force_generic_matmul(void);
+
 /* rpg_op_matmul_quant over n matrices sharing x (a layer's q / k / v, or gate /
  * up): out[i] = x . w[i]^T, each w[i] [rows[i]][cols] of types[i]; all arrays
  * are host arrays of n entries (ws / outs hold device pointers). At n_tokens = 1

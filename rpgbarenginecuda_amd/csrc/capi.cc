@@ -584,6 +584,12 @@ int32_t rpg_op_matmul_quant(uint32_t type, const uint8_t* w, int64_t rows, int64
   return Guard([&] { rpg::GpuMatMulQuantRaw(type, w, rows, cols, x, n_tokens, out); });
 }
 
+int32_t rpg_op_set_force_generic_matmul(int32_t force) {
+  return Guard([&] { rpg::GpuSetForceGenericMatMul(force != 0); });
+}
+
+int32_t rpg_op_force_generic_matmul(void) { return rpg::GpuForceGenericMatMul() ? 1 : 0; }
+
 int32_t rpg_op_matmul_quant_swiglu(uint32_t type, const uint8_t* w_gate, const uint8_t* w_up, int64_t rows,
                                    int64_t cols, const float* x, int64_t n_tokens, float* gate, float* up) {
   return Guard([&] {

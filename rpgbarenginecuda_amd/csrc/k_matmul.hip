@@ -28,6 +28,8 @@
 // matrices take a per-element generic kernel.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include <climits>
 
 #include "dev_util.h"
@@ -876,6 +878,19 @@ bool MfmaEligible(uint32_t type, const uint8_t* w_dev, const float* x_dev, int64
 
 }  // namespace
 
+namespace {
+
+// GpuSetForceGenericMatMul: while set, every matmul entry point runs
+// MatMulGenericKernel (per-element decode, one wave per output) so the
+// specialised kernels can be checked against it on the same inputs.
+std::atomic<bool> g_force_generic{false};
+
+}  // namespace
+
+void GpuSetForceGenericMatMul(bool force) { g_force_generic.store(force); }
+
+bool GpuForceGenericMatMul() { return g_force_generic.load(); }
+
 void GpuMatMulQuantRaw(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_t cols, const float* x_dev,
                        int64_t n_tokens, float* out_dev) {
   RPG_CHECK(rows > 0 && cols > 0, "invalid MatMulQuant shape [%lld, %lld]", static_cast<long long>(rows),
@@ -888,16 +903,17 @@ void GpuMatMulQuantRaw(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_
   const int64_t row_bytes = TypeRowBytes(type, cols);
   const bool x_ok = Aligned(x_dev, 16) && cols % 4 == 0;
   const int64_t nb = cols / kQK_K;
-  if (MfmaEligible(type, w_dev, x_dev, rows, cols, n_tokens)) {
+  const bool generic = g_force_generic.load();
+  if (!generic && MfmaEligible(type, w_dev, x_dev, rows, cols, n_tokens)) {
     LaunchMatMulMfma(type, w_dev, rows, row_bytes, static_cast<int32_t>(nb), x_dev, cols, n_tokens, out_dev);
     return;
   }
-  if (type == kGgmlQ4_K && x_ok && Aligned(w_dev, 16) && nb <= 0x7FFFFFFF) {
+  if (!generic && type == kGgmlQ4_K && x_ok && Aligned(w_dev, 16) && nb <= 0x7FFFFFFF) {
     LaunchByShape<kGgmlQ4_K>("MatMulQ4KKernel", w_dev, rows, row_bytes, static_cast<int32_t>(nb), x_dev, cols,
                              n_tokens, out_dev);
     return;
   }
-  if (type == kGgmlQ6_K && x_ok && Aligned(w_dev, 2) && nb <= 0x7FFFFFFF) {
+  if (!generic && type == kGgmlQ6_K && x_ok && Aligned(w_dev, 2) && nb <= 0x7FFFFFFF) {
     LaunchByShape<kGgmlQ6_K>("MatMulQ6KKernel", w_dev, rows, row_bytes, static_cast<int32_t>(nb), x_dev, cols,
                              n_tokens, out_dev);
     return;
@@ -1060,6 +1076,10 @@ void GpuMatMulQuantGroup(const GpuTensor* const* ws, int32_t n_mats, const float
                          float* const* outs) {
   CheckGroup(ws, n_mats, outs);
   const int64_t cols = ws[0]->cols;
+  if (g_force_generic.load()) {
+    for (int32_t i = 0; i < n_mats; ++i) GpuMatMulQuant(*ws[i], x_dev, n_tokens, outs[i]);
+    return;
+  }
   // Prefill: the activations are split once for all the matrices (each output
   // bit-identical to its own GpuMatMulQuant call, which splits the same way).
   bool mfma = true;
@@ -1091,7 +1111,7 @@ void GpuMatMulQuantSwiGLU(const GpuTensor& w_gate, const GpuTensor& w_up, const 
             static_cast<long long>(w_gate.cols), static_cast<long long>(w_up.rows), static_cast<long long>(w_up.cols));
   RPG_CHECK(n_tokens > 0, "n_tokens must be positive");
   RPG_CHECK(x_dev != nullptr && gate_dev != nullptr && up_dev != nullptr, "GpuMatMulQuantSwiGLU got a null pointer");
-  if (SwiGLUDecodeEligible(w_gate, w_up, x_dev, n_tokens)) {
+  if (!g_force_generic.load() && SwiGLUDecodeEligible(w_gate, w_up, x_dev, n_tokens)) {
     DecodeSwiGLU(w_gate, w_up, x_dev, gate_dev, nullptr);
     return;
   }
@@ -1104,7 +1124,9 @@ void GpuMatMulQuantSwiGLU(const GpuTensor& w_gate, const GpuTensor& w_up, const 
 bool GpuNormMatMulQuantGroup(const GpuNormIn& in, const GpuTensor* const* ws, int32_t n_mats, float* const* outs) {
   CheckGroup(ws, n_mats, outs);
   NormPrologue nrm;
-  if (!MakeNorm(in, ws[0]->cols, &nrm) || !DecodeEligible(ws, n_mats, in.x, 1)) return false;
+  if (g_force_generic.load() || !MakeNorm(in, ws[0]->cols, &nrm) || !DecodeEligible(ws, n_mats, in.x, 1)) {
+    return false;
+  }
   DecodeGroup(ws, n_mats, in.x, outs, &nrm);
   return true;
 }
@@ -1116,7 +1138,9 @@ bool GpuNormMatMulQuantSwiGLU(const GpuNormIn& in, const GpuTensor& w_gate, cons
   RPG_CHECK(w_gate.rows == w_up.rows && w_gate.cols == w_up.cols, "gate and up must have the same shape");
   RPG_CHECK(gate_dev != nullptr && up_dev != nullptr, "GpuNormMatMulQuantSwiGLU got a null output");
   NormPrologue nrm;
-  if (!MakeNorm(in, w_gate.cols, &nrm) || !SwiGLUDecodeEligible(w_gate, w_up, in.x, 1)) return false;
+  if (g_force_generic.load() || !MakeNorm(in, w_gate.cols, &nrm) || !SwiGLUDecodeEligible(w_gate, w_up, in.x, 1)) {
+    return false;
+  }
   DecodeSwiGLU(w_gate, w_up, in.x, gate_dev, &nrm);
   return true;
 }

@@ -252,6 +252,16 @@ void GpuAttentionWarmupShmem(int64_t sh_positions);
 // Weights are dequantised bit-exactly and accumulated in fp32 (fused multiply-add).
 void GpuMatMulQuant(const GpuTensor& w, const float* X_dev, int64_t n_tokens, float* OUT_dev);
 
+// Path-equivalence switch (src/kernels_gpu.h:51-58): while set, GpuMatMulQuant
+// and the grouped / fused matmul entry points run the generic kernel
+// (MatMulGenericKernel: per-element decode, one wave per output) instead of the
+// decode, tiled and matrix-core kernels; the norm-fused entry points then
+// return false. For verification only: the specialised kernels are checked bit
+// for bit against it on inputs where every summation order is exact. Off by
+// default; the flag is process-wide.
+void GpuSetForceGenericMatMul(bool force);
+bool GpuForceGenericMatMul();
+
 // GpuMatMulQuant over several matrices that read the same X (a layer's q / k / v,
 // or gate / up): OUT_i = X . W_i^T. At n_tokens = 1, up to 4 Q4_K / Q6_K
 // matrices (either type or both) are decoded in one launch, else each run of

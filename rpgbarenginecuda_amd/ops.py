@@ -90,6 +90,8 @@ SIGNATURES = {
     "rpg_op_vec_add_inplace": (_i32, [_vp, _vp, _i64]),
     "rpg_op_embedding_lookup": (_i32, [_u32, _vp, _i64, _i64, _vp, _i64, _vp]),
     "rpg_op_matmul_quant": (_i32, [_u32, _vp, _i64, _i64, _vp, _i64, _vp]),
+    "rpg_op_set_force_generic_matmul": (_i32, [_i32]),
+    "rpg_op_force_generic_matmul": (_i32, []),
     "rpg_op_attention_from_cache": (_i32, [_vp, _i32, _i32, _i32, _i64, _i64, _vp, _vp, _i64, _vp, _i64]),
     "rpg_op_qk_norm_rope_kv_attention": (_i32, [_vp, _vp, _vp, _vp, _vp, _i32, _i32, _i32, _vp, _i64, _i64, _f32,
                                                 _vp, _vp, _i64, _vp, _i64, _vp]),
@@ -309,6 +311,16 @@ def GpuEmbeddingLookup(emb: GpuTensor, toks, seq: int, x) -> None:
     _check(load_library().rpg_op_embedding_lookup(
         emb.type, _addr(emb.buf, emb.rows * emb.row_bytes(), name="emb"), emb.rows, emb.cols,
         _addr(toks, 4 * seq, torch.int32, "toks"), seq, _addr(x, 4 * seq * emb.cols, torch.float32, "x")))
+
+
+def GpuSetForceGenericMatMul(force: bool) -> None:
+    """Routes every matmul to the generic kernel (reference GpuSetForceGenericMatMul,
+    src/kernels_gpu.h:57); verification only."""
+    _check(load_library().rpg_op_set_force_generic_matmul(1 if force else 0))
+
+
+def GpuForceGenericMatMul() -> bool:
+    return load_library().rpg_op_force_generic_matmul() == 1
 
 
 def GpuMatMulQuant(w: GpuTensor, x, n_tokens: int, out) -> None:
