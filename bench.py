@@ -786,6 +786,19 @@ def cpu_baseline():
                              "restatement, one thread"}
 
 
+def calibration_copy(torch, ops):
+    """Calibration dispatch for the rocprofv3 counter runs: one StreamCopyKernel of
+    exactly CALIB_BYTES read + CALIB_BYTES written, whose FETCH_SIZE / WRITE_SIZE
+    give the counters' scale against known traffic."""
+    src = torch.empty(CALIB_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    ops.GpuStreamCopy(src, dst, CALIB_BYTES)
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
+
+
 # Secondary measurements that --only can run alone.
 SECTIONS = {
     "model_e2e": lambda torch, ops: measure_model_e2e(torch, ops),
@@ -826,7 +839,9 @@ def main():
     ok, desc = ops.device_info()
     log(desc)
     if args.only is not None:
-        print(json.dumps({args.only: SECTIONS[args.only](torch, ops)}), flush=True)
+        result = SECTIONS[args.only](torch, ops)
+        calibration_copy(torch, ops)
+        print(json.dumps({args.only: result}), flush=True)
         return
 
     tab = torch.from_numpy(ops.build_rope_table(D, THETA, MAX_SEQ)).cuda()
@@ -860,15 +875,7 @@ def main():
     del layers
     torch.cuda.empty_cache()
 
-    # Calibration dispatch for the rocprofv3 counter runs: one StreamCopyKernel of
-    # exactly CALIB_BYTES read + CALIB_BYTES written, whose FETCH_SIZE / WRITE_SIZE
-    # give the counters' scale against known traffic.
-    calib_src = torch.empty(CALIB_BYTES // 4, dtype=torch.float32, device="cuda").fill_(1.0)
-    calib_dst = torch.empty_like(calib_src)
-    torch.cuda.synchronize()
-    ops.GpuStreamCopy(calib_src, calib_dst, CALIB_BYTES)
-    torch.cuda.synchronize()
-    del calib_src, calib_dst
+    calibration_copy(torch, ops)
 
     extras = {}
     if not args.no_extras:
