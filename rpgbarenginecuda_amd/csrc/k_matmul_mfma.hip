@@ -542,6 +542,377 @@ __global__ __launch_bounds__(kThreads) void MatMulSplitReduceKernel(const float*
   out[e] = v;
 }
 
+// ---------------------------------------------------------------- large grids: pre-decoded weight planes
+//
+// For grids of many tiles the weights are decoded once per call instead of
+// once per token tile: DecodeWeightPlanesKernel writes the exact fp16 operands
+// StageChunk would build ([ops][rows][cols], K contiguous) and, per (row,
+// block), (d, dmin) and m_j 2^6. MatMulMfmaPlanesKernel then streams both
+// operands through LDS unchanged. Its workgroup is 8 waves (2 x 4) over 128
+// tokens x kPTileR rows, each wave 64 tokens x 32 kPNT rows; two LDS buffers
+// alternate every 64-column chunk, the next chunk's LDS writes and global loads
+// are issued after the first of its four K-steps, and the block-end values are
+// loaded a block ahead, so one barrier per chunk is the only synchronisation.
+// Per accumulator the MFMAs, block scales and min terms run in the order of
+// MatMulMfmaKernel, so the outputs are the same bits.
+typedef uint32_t U32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kPThreads = 512;
+constexpr int kPStage = 2 * kTileT * kRowStride;  // fp16 elements of one buffer's activation part
+
+template <uint32_t kType>
+struct PlanesCfg {
+  static constexpr bool kQ4 = kType == kGgmlQ4_K;
+  static constexpr int kOps = kQ4 ? 1 : 2;   // weight operands per column
+  static constexpr int kNT = kQ4 ? 2 : 1;    // 32-row MFMA tiles per wave
+  static constexpr int kTileR = 4 * 32 * kNT;
+  static constexpr int kBufHalfs = kPStage + kOps * kTileR * kRowStride;
+};
+
+// One thread per (row, block, 32-column run j = 2 kc + hf): the 32 operands
+// StageChunk<kQ4> builds for chunk kc, half hf, at the same chunk columns.
+template <uint32_t kType>
+__global__ __launch_bounds__(kThreads) void DecodeWeightPlanesKernel(const uint8_t* __restrict__ w, int64_t rows,
+                                                                      int64_t row_bytes, int32_t nb,
+                                                                      _Float16* __restrict__ planes,
+                                                                      float2* __restrict__ dd, U32x4* __restrict__ mm) {
+  constexpr bool kQ4 = kType == kGgmlQ4_K;
+  constexpr int64_t kBB = kQ4 ? kQ4KBlockBytes : kQ6KBlockBytes;
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (u >= rows * nb * 8) return;
+  const int j = static_cast<int>(u & 7);
+  const int64_t rb = u >> 3;  // row * nb + block
+  const int64_t r = rb / nb;
+  const int b = static_cast<int>(rb - r * nb);
+  const int kc = j >> 1, hf = j & 1;
+  const int64_t cols = static_cast<int64_t>(nb) * kQK_K;
+  const uint8_t* blk = w + r * row_bytes + b * kBB;
+  _Float16* dst = planes + r * cols + static_cast<int64_t>(kQK_K) * b + kChunk * kc;
+  const StageRaw raw = kQ4 ? FetchStageQ4K(blk, kc, hf) : FetchStageQ6K(blk, kc, hf);
+  if (kQ4) {
+    const uint32_t s0 = raw.hdr.y, s1 = raw.hdr.z, s2 = raw.hdr.w;
+    uint32_t scl, ml, sch, mh;
+    ScaleMinK4(2 * kc, s0, s1, s2, &scl, &ml);
+    ScaleMinK4(2 * kc + 1, s0, s1, s2, &sch, &mh);
+    const _Float16 fl = static_cast<_Float16>(static_cast<float>(scl));
+    const _Float16 fh = static_cast<_Float16>(static_cast<float>(sch));
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const uint32_t bx = raw.q[2 * g], by = raw.q[2 * g + 1];
+      *reinterpret_cast<F16x8*>(dst + 16 * hf + 8 * g) = ScaledQ4(make_uint2(bx & 0x0F0F0F0Fu, by & 0x0F0F0F0Fu), fl);
+      *reinterpret_cast<F16x8*>(dst + 32 + 16 * hf + 8 * g) =
+          ScaledQ4(make_uint2((bx >> 4) & 0x0F0F0F0Fu, (by >> 4) & 0x0F0F0F0Fu), fh);
+    }
+    if (j == 0) {
+      F16x8 mv;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        uint32_t sci, mi;
+        ScaleMinK4(i, s0, s1, s2, &sci, &mi);
+        mv[i] = static_cast<_Float16>(static_cast<float>(mi << kSumShift));
+      }
+      mm[rb] = __builtin_bit_cast(U32x4, mv);
+      dd[rb] = make_float2(HalfF(raw.hdr.x & 0xFFFFu), HalfF(raw.hdr.x >> 16));
+    }
+  } else {
+    const int64_t plane = rows * cols;
+    const int quarter = 2 * (kc & 1) + hf;
+    const int nshift = quarter < 2 ? 0 : 4;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t lx = raw.q[2 * g], ly = raw.q[2 * g + 1];
+      const uint32_t hx = raw.q[8 + 2 * g], hy = raw.q[8 + 2 * g + 1];
+      const uint2 q = make_uint2(((lx >> nshift) & 0x0F0F0F0Fu) | (((hx >> (2 * quarter)) & 0x03030303u) << 4),
+                                 ((ly >> nshift) & 0x0F0F0F0Fu) | (((hy >> (2 * quarter)) & 0x03030303u) << 4));
+      const F16x8 qc = CenteredQ6(q);
+      const int sc = static_cast<int8_t>(ByteOf(raw.hdr.y, g >> 1));
+      const _Float16 se = static_cast<_Float16>(static_cast<float>(sc & ~1));
+      const _Float16 so = static_cast<_Float16>(static_cast<float>(sc & 1));
+      *reinterpret_cast<F16x8*>(dst + 32 * hf + 8 * g) = qc * se;
+      *reinterpret_cast<F16x8*>(dst + plane + 32 * hf + 8 * g) = qc * so;
+    }
+    if (j == 0) dd[rb] = make_float2(HalfF(raw.hdr.x & 0xFFFFu), 0.0f);
+  }
+}
+
+// Tiles are numbered row tile fastest (tile = token tile * row_tiles + row
+// tile). Workgroup g < dp_tiles computes tile g over all of K, straight to
+// out. The others split the remaining tiles along K: g - dp_tiles =
+// (tile - dp_tiles) * splits + slice, slice covering blocks [slice bps,
+// min(nb, (slice + 1) bps)); each writes its 128 x kTileR partial tile (times
+// 1 / s_t, zero for tokens past n_tokens) to partial[g - dp_tiles], and
+// MatMulPlanesReduceKernel sums the slices in order. With a 1-D grid the
+// split workgroups are dispatched last, after the whole rounds.
+template <uint32_t kType>
+__global__ __launch_bounds__(kPThreads, 1) void MatMulMfmaPlanesKernel(
+    const _Float16* __restrict__ wplanes, const float2* __restrict__ dd, const U32x4* __restrict__ mm, int64_t rows,
+    int32_t nb, const _Float16* __restrict__ planes, const _Float16* __restrict__ sum_planes, int64_t sum_stride,
+    const float* __restrict__ inv_scale, int64_t n_tokens, int32_t row_tiles, int32_t dp_tiles, int32_t splits,
+    int32_t bps, float* __restrict__ out, float* __restrict__ partial) {
+  using C = PlanesCfg<kType>;
+  constexpr bool kQ4 = C::kQ4;
+  constexpr int kOps = C::kOps;
+  constexpr int kNT = C::kNT;
+  __shared__ __attribute__((aligned(16))) _Float16 lds[2 * C::kBufHalfs];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 2;  // 64-token half of the tile
+  const int wn = wave & 3;   // 32 kNT-row quarter of the tile
+  const int li = lane & 31;
+  const int h = lane >> 5;
+  const int g = static_cast<int>(blockIdx.x);
+  const bool split = g >= dp_tiles;
+  const int tile = split ? dp_tiles + (g - dp_tiles) / splits : g;
+  const int slice = split ? (g - dp_tiles) % splits : 0;
+  const int64_t t0 = static_cast<int64_t>(tile / row_tiles) * kTileT;
+  const int64_t r0 = static_cast<int64_t>(tile % row_tiles) * C::kTileR;
+  const int64_t cols = static_cast<int64_t>(nb) * kQK_K;
+  const int64_t runs = cols / 32;
+  const int64_t plane_elems = n_tokens * cols;
+  const int b0 = split ? slice * bps : 0;
+  const int n_blk = split ? (nb - b0 < bps ? nb - b0 : bps) : nb;
+  const int n_chunks = 4 * n_blk;
+
+  F32x16 acc[2][kNT], part[2][kNT];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        acc[mt][nt][i] = 0.0f;
+        part[mt][nt][i] = 0.0f;
+      }
+
+  // staging map: 16-byte piece j of thread tid is row (tid >> 3) + 64 j' of
+  // its operand, segment tid & 7 of the chunk. Activations: j = 0..3 ->
+  // plane j >> 1, token rows 64 (j & 1) + tid >> 3 (clamped; a token past
+  // n_tokens reads a valid row whose outputs are never stored). Weights:
+  // j = 0..3 -> operand j / (4 / kOps), rows 64 (j % (4 / kOps)) + tid >> 3
+  // (clamped to the last row likewise).
+  // element offsets are 32-bit: the launcher checks that both operand
+  // images hold fewer than 2^31 elements
+  const int seg = tid & 7;
+  const int row8 = tid >> 3;
+  const int icols = static_cast<int>(cols);
+  U32x4 ra[4], rb[4];
+  int aoff[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    int64_t t = t0 + 64 * k + row8;
+    t = t < n_tokens ? t : n_tokens - 1;
+    aoff[k] = static_cast<int>(t) * icols + kQK_K * b0 + 8 * seg;
+  }
+  constexpr int kRowsPerOp = 4 / kOps;  // 64-row groups per operand
+  int boff[kRowsPerOp];
+#pragma unroll
+  for (int k = 0; k < kRowsPerOp; ++k) {
+    int64_t r = r0 + 64 * k + row8;
+    r = r < rows ? r : rows - 1;
+    boff[k] = static_cast<int>(r) * icols + kQK_K * b0 + 8 * seg;
+  }
+  const int iplane = static_cast<int>(plane_elems);
+  const int wplane = static_cast<int>(rows * cols);
+  const int lds_a = row8 * kRowStride + 8 * seg;
+  const int lds_b = kPStage + row8 * kRowStride + 8 * seg;
+
+#define RPG_PLANES_LOAD(c)                                                                                  \
+  do {                                                                                                      \
+    const int off_ = (c) * kChunk;                                                                          \
+    _Pragma("unroll") for (int j = 0; j < 4; ++j) ra[j] =                                                   \
+        *reinterpret_cast<const U32x4*>(planes + (aoff[j & 1] + (j >> 1) * iplane + off_));                 \
+    _Pragma("unroll") for (int j = 0; j < 4; ++j) rb[j] =                                                   \
+        *reinterpret_cast<const U32x4*>(wplanes + (boff[j % kRowsPerOp] + (j / kRowsPerOp) * wplane + off_)); \
+  } while (0)
+#define RPG_PLANES_STAGE(buf)                                                                               \
+  do {                                                                                                      \
+    _Float16* base_ = lds + (buf) * C::kBufHalfs;                                                           \
+    _Pragma("unroll") for (int j = 0; j < 4; ++j)                                                           \
+        *reinterpret_cast<U32x4*>(base_ + lds_a + ((j >> 1) * kTileT + 64 * (j & 1)) * kRowStride) = ra[j]; \
+    _Pragma("unroll") for (int j = 0; j < 4; ++j)                                                           \
+        *reinterpret_cast<U32x4*>(base_ + lds_b +                                                           \
+                                  ((j / kRowsPerOp) * C::kTileR + 64 * (j % kRowsPerOp)) * kRowStride) = rb[j]; \
+  } while (0)
+
+  // Block-end values, loaded a block ahead: (d, dmin) and m of this lane's
+  // rows, the run sums of this lane's tokens (Q4_K).
+  int my_row[kNT];  // row * nb
+#pragma unroll
+  for (int nt = 0; nt < kNT; ++nt) {
+    const int64_t r = r0 + 32 * kNT * wn + 32 * nt + li;
+    my_row[nt] = static_cast<int>(r < rows ? r : rows - 1) * nb;
+  }
+  int my_tok[2];  // token * runs
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const int64_t t = t0 + 64 * wm + 32 * mt + li;
+    my_tok[mt] = static_cast<int>(t < n_tokens ? t : n_tokens - 1) * static_cast<int>(runs);
+  }
+  float2 bd[kNT];
+  U32x4 bm[kNT], bs[2][2];
+  auto load_block_end = [&](int blk) {
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      bd[nt] = dd[my_row[nt] + blk];
+      if (kQ4) bm[nt] = mm[my_row[nt] + blk];
+    }
+    if (kQ4) {
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int p = 0; p < kPlanes; ++p)
+          bs[mt][p] = *reinterpret_cast<const U32x4*>(sum_planes + p * sum_stride + (my_tok[mt] + 8 * blk));
+    }
+  };
+
+  auto k_step = [&](int buf, int ks) {
+    const _Float16* xs = lds + buf * C::kBufHalfs;
+    const _Float16* ws = xs + kPStage;
+    const int kcol = 16 * ks + 8 * h;
+    F16x8 af[2][kPlanes], bf[kNT][kOps];
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+      for (int o = 0; o < kOps; ++o)
+        bf[nt][o] = *reinterpret_cast<const F16x8*>(ws + (o * C::kTileR + 32 * kNT * wn + 32 * nt + li) * kRowStride + kcol);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int p = 0; p < kPlanes; ++p)
+        af[mt][p] = *reinterpret_cast<const F16x8*>(xs + (p * kTileT + 64 * wm + 32 * mt + li) * kRowStride + kcol);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int p = 0; p < kPlanes; ++p)
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+#pragma unroll
+          for (int o = 0; o < kOps; ++o)
+            part[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[mt][p], bf[nt][o], part[mt][nt], 0, 0, 0);
+  };
+
+  auto block_end = [&]() {
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      const float d = bd[nt].x;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          acc[mt][nt][i] = __builtin_fmaf(d, part[mt][nt][i], acc[mt][nt][i]);
+          part[mt][nt][i] = 0.0f;
+        }
+    }
+    if (!kQ4) return;
+    F16x8 bmf[kNT];
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      const F16x8 z = {};
+      bmf[nt] = h == 0 ? __builtin_bit_cast(F16x8, bm[nt]) : z;  // k 8..15 carry zero weights
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int p = 0; p < kPlanes; ++p) {
+        const F16x8 a = __builtin_bit_cast(F16x8, bs[mt][p]);
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt)
+          part[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bmf[nt], part[mt][nt], 0, 0, 0);
+      }
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) {
+      const float dmin = bd[nt].y;
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          acc[mt][nt][i] = __builtin_fmaf(-dmin, part[mt][nt][i], acc[mt][nt][i]);
+          part[mt][nt][i] = 0.0f;
+        }
+    }
+  };
+
+  // The loads and LDS writes are unconditional (the last chunks re-stage the
+  // final chunk into the idle buffer): registers filled under a condition that
+  // spans iterations end up in scratch memory.
+  const int last = n_chunks - 1;
+  load_block_end(b0);
+  RPG_PLANES_LOAD(0);
+  RPG_PLANES_STAGE(0);
+  RPG_PLANES_LOAD(last > 0 ? 1 : 0);
+  __syncthreads();
+  for (int c = 0; c < n_chunks; ++c) {
+    const int buf = c & 1;
+    // a block's end values are loaded at its first chunk, ahead of that
+    // chunk's staging loads: the wait for those (before the next LDS writes)
+    // then never waits for a load issued after them
+    if ((c & 3) == 0 && c > 0) load_block_end(b0 + (c >> 2));
+    k_step(buf, 0);
+    RPG_PLANES_STAGE(buf ^ 1);
+    RPG_PLANES_LOAD(c + 2 < last ? c + 2 : last);
+    k_step(buf, 1);
+    k_step(buf, 2);
+    k_step(buf, 3);
+    if ((c & 3) == 3) block_end();
+    __syncthreads();
+  }
+#undef RPG_PLANES_LOAD
+#undef RPG_PLANES_STAGE
+
+  if (split) {
+    float* dst = partial + static_cast<int64_t>(g - dp_tiles) * kTileT * C::kTileR;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int lt = 64 * wm + 32 * mt + (i & 3) + 8 * (i >> 2) + 4 * h;
+        const int64_t tok = t0 + lt;
+        const float inv = tok < n_tokens ? inv_scale[tok] : 0.0f;
+#pragma unroll
+        for (int nt = 0; nt < kNT; ++nt) dst[lt * C::kTileR + 32 * kNT * wn + 32 * nt + li] = acc[mt][nt][i] * inv;
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int64_t tok = t0 + 64 * wm + 32 * mt + (i & 3) + 8 * (i >> 2) + 4 * h;
+      if (tok >= n_tokens) continue;
+      const float inv = inv_scale[tok];
+#pragma unroll
+      for (int nt = 0; nt < kNT; ++nt) {
+        const int64_t row = r0 + 32 * kNT * wn + 32 * nt + li;
+        if (row < rows) out[tok * rows + row] = acc[mt][nt][i] * inv;
+      }
+    }
+  }
+}
+
+// out = the sum over slices, in order, of the split tiles' partial tiles.
+template <int kTileRows>
+__global__ __launch_bounds__(kThreads) void MatMulPlanesReduceKernel(const float* __restrict__ partial,
+                                                                      int64_t split_tiles, int32_t splits,
+                                                                      int32_t row_tiles, int32_t dp_tiles,
+                                                                      int64_t n_tokens, int64_t rows,
+                                                                      float* __restrict__ out) {
+  constexpr int64_t kTileElems = static_cast<int64_t>(kTileT) * kTileRows;
+  const int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (e >= split_tiles * kTileElems) return;
+  const int64_t st = e / kTileElems;
+  const int64_t le = e - st * kTileElems;
+  const int64_t tile = dp_tiles + st;
+  const int64_t tok = (tile / row_tiles) * kTileT + le / kTileRows;
+  const int64_t row = (tile % row_tiles) * kTileRows + le % kTileRows;
+  if (tok >= n_tokens || row >= rows) return;
+  const float* p = partial + st * splits * kTileElems + le;
+  float v = p[0];
+  for (int32_t z = 1; z < splits; ++z) v += p[z * kTileElems];
+  out[tok * rows + row] = v;
+}
+
 }  // namespace
 
 namespace {
@@ -602,6 +973,106 @@ void* EnsurePartialTiles(size_t bytes) {
   return b.ptr;
 }
 
+SplitBuffer& WeightPlanes() {
+  static SplitBuffer* b = new SplitBuffer();
+  return *b;
+}
+
+// Grow-only buffer of the decoded weight planes (same policy as the split buffer).
+void* EnsureWeightPlanes(size_t bytes) {
+  SplitBuffer& b = WeightPlanes();
+  std::lock_guard<std::mutex> lock(b.mu);
+  if (b.bytes < bytes) {
+    RPG_CHECK(!StreamIsCapturing(),
+              "the prefill matmul needs a %zu-byte weight-plane buffer (have %zu), which cannot be allocated during "
+              "graph capture; run the same shape once before capturing",
+              bytes, b.bytes);
+    void* p = nullptr;
+    RPG_HIP_CHECK(hipMalloc(&p, bytes));
+    b.ptr = p;  // the previous buffer stays allocated
+    b.bytes = bytes;
+  }
+  return b.ptr;
+}
+
+// Decoded planes are used for grids of many tiles (from kPlanesMinTokens
+// tokens) and matrices whose planes stay within kPlanesMaxBytes (the layer
+// matrices; a 151936-row output projection keeps decoding per tile).
+constexpr int64_t kPlanesMinTokens = 512;
+constexpr size_t kPlanesMaxBytes = size_t{64} << 20;
+
+template <uint32_t kType>
+void LaunchPlanes(const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb, const SplitActivations& sa,
+                  float* out) {
+  using C = PlanesCfg<kType>;
+  const int64_t cols = static_cast<int64_t>(nb) * kQK_K;
+  const size_t plane_bytes = static_cast<size_t>(C::kOps) * rows * cols * sizeof(_Float16);
+  const size_t dd_off = (plane_bytes + 255) / 256 * 256;
+  const size_t mm_off = dd_off + (static_cast<size_t>(rows) * nb * sizeof(float2) + 255) / 256 * 256;
+  const size_t bytes = mm_off + static_cast<size_t>(rows) * nb * sizeof(U32x4);
+  uint8_t* base = static_cast<uint8_t*>(EnsureWeightPlanes(bytes));
+  _Float16* wplanes = reinterpret_cast<_Float16*>(base);
+  float2* dd = reinterpret_cast<float2*>(base + dd_off);
+  U32x4* mm = reinterpret_cast<U32x4*>(base + mm_off);
+  const int64_t units = rows * nb * 8;
+  Launch(kType == kGgmlQ4_K ? "DecodeWeightPlanesQ4KKernel" : "DecodeWeightPlanesQ6KKernel",
+         DecodeWeightPlanesKernel<kType>, dim3(GridFor(units, kThreads)), dim3(kThreads), w, rows, row_bytes, nb,
+         wplanes, dd, mm);
+
+  const int64_t gy = (sa.n_tokens + kTileT - 1) / kTileT;
+  const int64_t gx = (rows + C::kTileR - 1) / C::kTileR;
+  const int64_t tiles = gx * gy;
+  RPG_CHECK(tiles * 8 <= 0x7FFFFFFF, "matmul grid too large: %lld tiles", static_cast<long long>(tiles));
+  // One workgroup per CU, so a grid runs in rounds of kCUs workgroups. Plans:
+  // whole rounds of tiles unsplit and the tiles left over split along K to
+  // fill the last round (dp = the whole rounds), or every tile split alike
+  // (dp = 0). Each is priced as rounds x blocks per workgroup x the time of
+  // one block of one tile, plus the reduce (slices + 1 passes over the split
+  // tiles at ~4 TB/s); the cheapest wins.
+  constexpr int64_t kCUs = 256;
+  constexpr double kBlockUs = C::kQ4 ? 10.0 : 6.6;  // measured, 2811 tokens
+  const double tile_bytes = 4.0 * kTileT * C::kTileR;
+  int64_t best_dp = tiles;
+  int32_t best_splits = 1, best_bps = nb;
+  double best = 0.0;
+  for (int plan = 0; plan < 2; ++plan) {
+    const int64_t dp = plan == 0 ? tiles / kCUs * kCUs : 0;
+    const int64_t rest = tiles - dp;
+    for (int32_t s = 1; s <= nb && s <= 16; ++s) {
+      const int32_t b = (nb + s - 1) / s;
+      const int32_t slices = (nb + b - 1) / b;
+      if (rest == 0 && slices > 1) break;
+      const int64_t rounds_rest = (rest * slices + kCUs - 1) / kCUs;
+      const double us = static_cast<double>(dp / kCUs) * nb * kBlockUs + static_cast<double>(rounds_rest) * b * kBlockUs +
+                        (slices > 1 ? (slices + 1) * static_cast<double>(rest) * tile_bytes / 4e6 : 0.0);
+      if (best == 0.0 || us < best) {
+        best = us;
+        best_dp = slices > 1 ? dp : tiles;
+        best_splits = slices;
+        best_bps = b;
+      }
+    }
+  }
+  const int64_t split_tiles = tiles - best_dp;
+  float* partial = nullptr;
+  if (split_tiles > 0) {
+    partial = static_cast<float*>(EnsurePartialTiles(static_cast<size_t>(split_tiles) * best_splits * kTileT *
+                                                     C::kTileR * sizeof(float)));
+  }
+  const int64_t wgs = best_dp + split_tiles * best_splits;
+  Launch(kType == kGgmlQ4_K ? "MatMulMfmaQ4KPlanesKernel" : "MatMulMfmaQ6KPlanesKernel", MatMulMfmaPlanesKernel<kType>,
+         dim3(static_cast<unsigned>(wgs)), dim3(kPThreads), static_cast<const _Float16*>(wplanes),
+         static_cast<const float2*>(dd), static_cast<const U32x4*>(mm), rows, nb,
+         static_cast<const _Float16*>(sa.planes), static_cast<const _Float16*>(sa.sums), sa.sum_stride, sa.inv_scale,
+         sa.n_tokens, static_cast<int32_t>(gx), static_cast<int32_t>(best_dp), best_splits, best_bps, out, partial);
+  if (split_tiles > 0) {
+    const int64_t elems = split_tiles * kTileT * C::kTileR;
+    Launch("MatMulPlanesReduceKernel", MatMulPlanesReduceKernel<C::kTileR>, dim3(GridFor(elems, kThreads)),
+           dim3(kThreads), static_cast<const float*>(partial), split_tiles, best_splits, static_cast<int32_t>(gx),
+           static_cast<int32_t>(best_dp), sa.n_tokens, rows, out);
+  }
+}
+
 }  // namespace
 
 SplitActivations SplitForMfma(const float* x, int64_t n_tokens, int64_t cols) {
@@ -641,6 +1112,17 @@ void LaunchMatMulMfmaSplit(uint32_t type, const uint8_t* w, int64_t rows, int64_
             static_cast<long long>(gy));
   RPG_CHECK(static_cast<int64_t>(nb) * kQK_K == sa.cols, "split activations have %lld columns, the matrix %lld",
             static_cast<long long>(sa.cols), static_cast<long long>(nb) * kQK_K);
+  const size_t plane_bytes = static_cast<size_t>(type == kGgmlQ4_K ? 1 : 2) * rows * sa.cols * sizeof(_Float16);
+  // (the planes kernel indexes both operand images with 32-bit offsets)
+  if (sa.n_tokens >= kPlanesMinTokens && plane_bytes <= kPlanesMaxBytes &&
+      kPlanes * sa.n_tokens * sa.cols < (int64_t{1} << 31)) {
+    if (type == kGgmlQ4_K) {
+      LaunchPlanes<kGgmlQ4_K>(w, rows, row_bytes, nb, sa, out);
+    } else {
+      LaunchPlanes<kGgmlQ6_K>(w, rows, row_bytes, nb, sa, out);
+    }
+    return;
+  }
   constexpr int64_t kFill = 256;
   const int64_t tiles = gx * gy;
   int64_t want = tiles >= kFill ? 1 : (kFill + tiles - 1) / tiles;

@@ -102,6 +102,13 @@ SHAPES = [
     (12, 6144, 2048, 17),    # wide matrix: matrix cores from 16 tokens, K split 8 ways
     (14, 4096, 2560, 16),    # ... Q6_K, 10 blocks per row split one each
     (12, 4095, 2048, 16),    # one row short of wide: the tiled kernel
+    (12, 2048, 2048, 600),   # decoded weight planes (from 512 tokens): 8 x 5 tiles, K split
+    (14, 1024, 2048, 700),   # ... Q6_K, ragged token tile, K split
+    (12, 1100, 2560, 513),   # ... ragged row tile (1100 = 4.3 x 256), 10 blocks per row
+    (14, 2048, 6144, 1030),  # ... ffn_down shape, 24 blocks per row
+    (12, 6144, 2048, 700),   # ... ffn_gate shape, 24 x 6 tiles: one slice, no split
+    (12, 4352, 512, 2048),   # ... 17 x 16 = 272 tiles: one whole round unsplit, the 16 left split along K
+    (14, 2176, 512, 2000),   # ... Q6_K likewise, ragged token tile
 ]
 
 
@@ -214,6 +221,7 @@ GROUPS = [
     ("odd rows (not fused)", [(12, 1001), (12, 7)], 256, 1),
     ("Q4_K of 32768+ rows (own shape)", [(12, 20000), (12, 16000)], 256, 1),
     ("prefill (one call per matrix)", [(12, 256), (14, 128)], 512, 40),
+    ("prefill, decoded planes", [(12, 2048), (12, 1024), (14, 1024)], 2048, 600),
     ("small batch", [(12, 256), (12, 256)], 512, 3),
 ]
 

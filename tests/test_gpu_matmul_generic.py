@@ -2,7 +2,8 @@
 src/kernels_gpu.h:51-58; the reference's bitwise generic-vs-specialised check,
 tools/matmul_bench.cu:149-219): every specialised kernel -- the one-token decode
 matvecs (2 and 4 rows per wave, and the split-columns form), the tiled
-small-batch kernel and the matrix-core prefill GEMM with and without split K --
+small-batch kernel and the matrix-core prefill GEMM with and without split K,
+decoding per tile or from decoded weight planes --
 against the generic per-element kernel on the same weights and inputs.
 
 The kernels sum in different orders (that is where their speed comes from), so
@@ -57,6 +58,11 @@ CASES = [
     ("matrix cores Q4_K", Q4_K, 6144, 2048, 300, "MatMulMfmaQ4K"),
     ("matrix cores Q6_K", Q6_K, 2048, 6144, 300, "MatMulMfmaQ6K"),
     ("matrix cores Q4_K, split K", Q4_K, 1024, 2048, 48, "MatMulSplitReduceKernel"),
+    ("decoded weight planes Q4_K", Q4_K, 6144, 2048, 700, "MatMulMfmaQ4KPlanes"),
+    ("decoded weight planes Q6_K", Q6_K, 2048, 2048, 600, "MatMulMfmaQ6KPlanes"),
+    ("decoded weight planes Q4_K, split K, ragged", Q4_K, 1152, 2048, 513, "MatMulMfmaQ4KPlanes"),
+    ("decoded weight planes Q4_K, whole rounds + split tail", Q4_K, 4352, 512, 2048, "MatMulPlanesReduceKernel"),
+    ("decoded weight planes Q6_K, whole rounds + split tail", Q6_K, 2176, 512, 2000, "MatMulPlanesReduceKernel"),
 ]
 
 
