@@ -153,7 +153,8 @@ __device__ __forceinline__ StageRaw FetchStageQ6K(const uint8_t* __restrict__ bl
   return r;
 }
 
-// Activation pre-pass: one workgroup per token row.
+// Activation pre-pass: one workgroup per token row, 8 consecutive columns
+// per thread (four threads per 32-column run).
 __global__ __launch_bounds__(kThreads) void SplitActivationsKernel(const float* __restrict__ x, int64_t cols,
                                                                    int64_t plane_elems, int64_t sum_elems,
                                                                    _Float16* __restrict__ planes,
@@ -165,12 +166,11 @@ __global__ __launch_bounds__(kThreads) void SplitActivationsKernel(const float* 
   const int64_t runs = cols / 32;
   const int tid = threadIdx.x;
   float mx = 0.0f;
-  for (int64_t r = tid; r < runs; r += kThreads) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float4 f = *reinterpret_cast<const float4*>(row + 32 * r + 4 * k);
-      mx = fmaxf(mx, fmaxf(fmaxf(fabsf(f.x), fabsf(f.y)), fmaxf(fabsf(f.z), fabsf(f.w))));
-    }
+  for (int64_t e = 8 * tid; e < cols; e += 8 * kThreads) {
+    const float4 f0 = *reinterpret_cast<const float4*>(row + e);
+    const float4 f1 = *reinterpret_cast<const float4*>(row + e + 4);
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(f0.x), fabsf(f0.y)), fmaxf(fabsf(f0.z), fabsf(f0.w))));
+    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(f1.x), fabsf(f1.y)), fmaxf(fabsf(f1.z), fabsf(f1.w))));
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
@@ -188,35 +188,34 @@ __global__ __launch_bounds__(kThreads) void SplitActivationsKernel(const float* 
   const float s = ldexpf(1.0f, e);
   const float ss = ldexpf(1.0f, e - kSumShift);
   if (tid == 0) inv_scale[t] = ldexpf(1.0f, -e);
-  for (int64_t r = tid; r < runs; r += kThreads) {
-    float v[32];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const float4 f = *reinterpret_cast<const float4*>(row + 32 * r + 4 * k);
-      v[4 * k] = f.x; v[4 * k + 1] = f.y; v[4 * k + 2] = f.z; v[4 * k + 3] = f.w;
-    }
+  // cols is a multiple of 32, so every group of four lanes walks whole runs
+  // together and the shuffles below stay inside a run
+  for (int64_t c = 8 * tid; c < cols; c += 8 * kThreads) {
+    const float4 f0 = *reinterpret_cast<const float4*>(row + c);
+    const float4 f1 = *reinterpret_cast<const float4*>(row + c + 4);
+    const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
+    F16x8 hi, lo;
     float sum = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 32; ++k) sum += v[k];
-    const int64_t e0 = t * cols + 32 * r;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      F16x8 hi, lo;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float y = v[8 * g + j] * s;
-        const _Float16 a = static_cast<_Float16>(y);
-        hi[j] = a;
-        lo[j] = static_cast<_Float16>(y - static_cast<float>(a));
-      }
-      *reinterpret_cast<F16x8*>(planes + e0 + 8 * g) = hi;
-      *reinterpret_cast<F16x8*>(planes + plane_elems + e0 + 8 * g) = lo;
+    for (int j = 0; j < 8; ++j) {
+      sum += v[j];
+      const float y = v[j] * s;
+      const _Float16 a = static_cast<_Float16>(y);
+      hi[j] = a;
+      lo[j] = static_cast<_Float16>(y - static_cast<float>(a));
     }
-    const float ys = sum * ss;
-    const _Float16 a = static_cast<_Float16>(ys);
-    const int64_t si = t * runs + r;
-    sum_planes[si] = a;
-    sum_planes[sum_elems + si] = static_cast<_Float16>(ys - static_cast<float>(a));
+    *reinterpret_cast<F16x8*>(planes + t * cols + c) = hi;
+    *reinterpret_cast<F16x8*>(planes + plane_elems + t * cols + c) = lo;
+    // run sum: the four 8-column partial sums, pairwise
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    if ((tid & 3) == 0) {
+      const float ys = sum * ss;
+      const _Float16 a = static_cast<_Float16>(ys);
+      const int64_t si = t * runs + c / 32;
+      sum_planes[si] = a;
+      sum_planes[sum_elems + si] = static_cast<_Float16>(ys - static_cast<float>(a));
+    }
   }
 }
 
@@ -545,16 +544,22 @@ __global__ __launch_bounds__(kThreads) void MatMulSplitReduceKernel(const float*
 // ---------------------------------------------------------------- large grids: pre-decoded weight planes
 //
 // For grids of many tiles the weights are decoded once per call instead of
-// once per token tile: DecodeWeightPlanesKernel writes the exact fp16 operands
-// StageChunk would build ([ops][rows][cols], K contiguous) and, per (row,
-// block), (d, dmin) and m_j 2^6. MatMulMfmaPlanesKernel then streams both
-// operands through LDS unchanged. Its workgroup is 8 waves (2 x 4) over 128
+// once per token tile: DecodeWeightPlanesKernel writes fp16 operand planes
+// ([ops][rows][cols], K contiguous) and, per (row, block), (d, dmin) and
+// m_j 2^6. Q4_K: the exact sc_j q of StageChunk. Q6_K: w = sc (q - 32) as
+// hi = w rounded to fp16 and lo = w - hi (exact; lo is nonzero only for
+// |w| > 2048, where it is +-1); the matrix cores form x_hi w_hi, x_lo w_hi and
+// x_hi w_lo and leave out x_lo w_lo, which is below 2^-22 |x w| (|x_lo| <=
+// 2^-11 |x|, |w_lo| <= 2^-11 |w|): three products instead of the four of the
+// even / odd scale split. MatMulMfmaPlanesKernel streams both operands
+// through LDS unchanged. Its workgroup is 8 waves (2 x 4) over 128
 // tokens x kPTileR rows, each wave 64 tokens x 32 kPNT rows; two LDS buffers
 // alternate every 64-column chunk, the next chunk's LDS writes and global loads
 // are issued after the first of its four K-steps, and the block-end values are
-// loaded a block ahead, so one barrier per chunk is the only synchronisation.
-// Per accumulator the MFMAs, block scales and min terms run in the order of
-// MatMulMfmaKernel, so the outputs are the same bits.
+// loaded at the block's first chunk, so one barrier per chunk is the only
+// synchronisation. For Q4_K the MFMAs, block scales and min terms of each
+// accumulator run in the order of MatMulMfmaKernel (the same bits for tiles
+// that are not split along K).
 typedef uint32_t U32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kPThreads = 512;
@@ -625,11 +630,19 @@ __global__ __launch_bounds__(kThreads) void DecodeWeightPlanesKernel(const uint8
       const uint2 q = make_uint2(((lx >> nshift) & 0x0F0F0F0Fu) | (((hx >> (2 * quarter)) & 0x03030303u) << 4),
                                  ((ly >> nshift) & 0x0F0F0F0Fu) | (((hy >> (2 * quarter)) & 0x03030303u) << 4));
       const F16x8 qc = CenteredQ6(q);
-      const int sc = static_cast<int8_t>(ByteOf(raw.hdr.y, g >> 1));
-      const _Float16 se = static_cast<_Float16>(static_cast<float>(sc & ~1));
-      const _Float16 so = static_cast<_Float16>(static_cast<float>(sc & 1));
-      *reinterpret_cast<F16x8*>(dst + 32 * hf + 8 * g) = qc * se;
-      *reinterpret_cast<F16x8*>(dst + plane + 32 * hf + 8 * g) = qc * so;
+      const float sc = static_cast<float>(static_cast<int8_t>(ByteOf(raw.hdr.y, g >> 1)));
+      // w = sc (q - 32), |w| <= 4096, exact in fp32; hi = w rounded to fp16
+      // (exact unless |w| > 2048 and odd), lo = w - hi in {-1, 0, 1}
+      F16x8 wh, wl;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const float wf = static_cast<float>(qc[i]) * sc;
+        const _Float16 a = static_cast<_Float16>(wf);
+        wh[i] = a;
+        wl[i] = static_cast<_Float16>(wf - static_cast<float>(a));
+      }
+      *reinterpret_cast<F16x8*>(dst + 32 * hf + 8 * g) = wh;
+      *reinterpret_cast<F16x8*>(dst + plane + 32 * hf + 8 * g) = wl;
     }
     if (j == 0) dd[rb] = make_float2(HalfF(raw.hdr.x & 0xFFFFu), 0.0f);
   }
@@ -788,8 +801,10 @@ __global__ __launch_bounds__(kPThreads, 1) void MatMulMfmaPlanesKernel(
 #pragma unroll
         for (int nt = 0; nt < kNT; ++nt)
 #pragma unroll
-          for (int o = 0; o < kOps; ++o)
+          for (int o = 0; o < kOps; ++o) {
+            if (p == 1 && o == 1) continue;  // Q6_K x_lo w_lo: below 2^-22 |x w|, not formed
             part[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[mt][p], bf[nt][o], part[mt][nt], 0, 0, 0);
+          }
   };
 
   auto block_end = [&]() {
