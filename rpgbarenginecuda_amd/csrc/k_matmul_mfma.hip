@@ -92,19 +92,6 @@ __device__ __forceinline__ F16x8 CenteredQ6(uint2 q) {
   return Join(MagicLo(q.x) + c2, MagicHi(q.x) + c2, MagicLo(q.y) + c2, MagicHi(q.y) + c2);
 }
 
-// 8 bytes starting `sh` (0 or 2) bytes into three aligned dwords.
-__device__ __forceinline__ uint2 Window8x(uint32_t w0, uint32_t w1, uint32_t w2, uint32_t sh) {
-  return make_uint2(__builtin_amdgcn_alignbyte(w1, w0, sh), __builtin_amdgcn_alignbyte(w2, w1, sh));
-}
-
-// 8 bytes at a 2-byte aligned address (see the Q6_K note in k_matmul.hip: the
-// aligned dwords around a field never leave the pages the tensor occupies).
-__device__ __forceinline__ uint2 Load8Aligned2(const uint8_t* p) {
-  const uint32_t sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p) & 3u);
-  const uint32_t* a = reinterpret_cast<const uint32_t*>(p - sh);
-  return Window8x(a[0], a[1], a[1 + (sh >> 1)], sh);
-}
-
 // 32 bytes at a 2-byte aligned address, from nine aligned dwords (Q6_K rows
 // are 210-byte blocks; the dwords around the field stay inside the tensor's pages).
 __device__ __forceinline__ void Load32Aligned2(const uint8_t* p, uint32_t out[8]) {
@@ -661,7 +648,7 @@ __global__ __launch_bounds__(kPThreads, 1) void MatMulMfmaPlanesKernel(
     const _Float16* __restrict__ wplanes, const float2* __restrict__ dd, const U32x4* __restrict__ mm, int64_t rows,
     int32_t nb, const _Float16* __restrict__ planes, const _Float16* __restrict__ sum_planes, int64_t sum_stride,
     const float* __restrict__ inv_scale, int64_t n_tokens, int32_t row_tiles, int32_t dp_tiles, int32_t splits,
-    int32_t bps, float* __restrict__ out, float* __restrict__ partial) {
+    int32_t bps, float* __restrict__ out, int64_t ldo, float* __restrict__ partial) {
   using C = PlanesCfg<kType>;
   constexpr bool kQ4 = C::kQ4;
   constexpr int kOps = C::kOps;
@@ -900,7 +887,7 @@ __global__ __launch_bounds__(kPThreads, 1) void MatMulMfmaPlanesKernel(
 #pragma unroll
       for (int nt = 0; nt < kNT; ++nt) {
         const int64_t row = r0 + 32 * kNT * wn + 32 * nt + li;
-        if (row < rows) out[tok * rows + row] = acc[mt][nt][i] * inv;
+        if (row < rows) out[tok * ldo + row] = acc[mt][nt][i] * inv;
       }
     }
   }
@@ -912,7 +899,7 @@ __global__ __launch_bounds__(kThreads) void MatMulPlanesReduceKernel(const float
                                                                       int64_t split_tiles, int32_t splits,
                                                                       int32_t row_tiles, int32_t dp_tiles,
                                                                       int64_t n_tokens, int64_t rows,
-                                                                      float* __restrict__ out) {
+                                                                      float* __restrict__ out, int64_t ldo) {
   constexpr int64_t kTileElems = static_cast<int64_t>(kTileT) * kTileRows;
   const int64_t e = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (e >= split_tiles * kTileElems) return;
@@ -925,7 +912,7 @@ __global__ __launch_bounds__(kThreads) void MatMulPlanesReduceKernel(const float
   const float* p = partial + st * splits * kTileElems + le;
   float v = p[0];
   for (int32_t z = 1; z < splits; ++z) v += p[z * kTileElems];
-  out[tok * rows + row] = v;
+  out[tok * ldo + row] = v;
 }
 
 }  // namespace
@@ -1011,14 +998,16 @@ void* EnsureWeightPlanes(size_t bytes) {
 }
 
 // Decoded planes are used for grids of many tiles (from kPlanesMinTokens
-// tokens) and matrices whose planes stay within kPlanesMaxBytes (the layer
-// matrices; a 151936-row output projection keeps decoding per tile).
+// tokens). A matrix whose planes exceed kPlanesMaxBytes (a 151936-row output
+// projection) is decoded and multiplied in row slices that fit, each writing
+// its columns of OUT.
 constexpr int64_t kPlanesMinTokens = 512;
 constexpr size_t kPlanesMaxBytes = size_t{64} << 20;
 
+// OUT[:, 0 : rows) with row stride ldo for the `rows` weight rows at w.
 template <uint32_t kType>
-void LaunchPlanes(const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb, const SplitActivations& sa,
-                  float* out) {
+void LaunchPlanesRows(const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb, const SplitActivations& sa,
+                      float* out, int64_t ldo) {
   using C = PlanesCfg<kType>;
   const int64_t cols = static_cast<int64_t>(nb) * kQK_K;
   const size_t plane_bytes = static_cast<size_t>(C::kOps) * rows * cols * sizeof(_Float16);
@@ -1079,12 +1068,25 @@ void LaunchPlanes(const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb,
          dim3(static_cast<unsigned>(wgs)), dim3(kPThreads), static_cast<const _Float16*>(wplanes),
          static_cast<const float2*>(dd), static_cast<const U32x4*>(mm), rows, nb,
          static_cast<const _Float16*>(sa.planes), static_cast<const _Float16*>(sa.sums), sa.sum_stride, sa.inv_scale,
-         sa.n_tokens, static_cast<int32_t>(gx), static_cast<int32_t>(best_dp), best_splits, best_bps, out, partial);
+         sa.n_tokens, static_cast<int32_t>(gx), static_cast<int32_t>(best_dp), best_splits, best_bps, out, ldo, partial);
   if (split_tiles > 0) {
     const int64_t elems = split_tiles * kTileT * C::kTileR;
     Launch("MatMulPlanesReduceKernel", MatMulPlanesReduceKernel<C::kTileR>, dim3(GridFor(elems, kThreads)),
            dim3(kThreads), static_cast<const float*>(partial), split_tiles, best_splits, static_cast<int32_t>(gx),
-           static_cast<int32_t>(best_dp), sa.n_tokens, rows, out);
+           static_cast<int32_t>(best_dp), sa.n_tokens, rows, out, ldo);
+  }
+}
+
+template <uint32_t kType>
+void LaunchPlanes(const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb, const SplitActivations& sa,
+                  float* out) {
+  using C = PlanesCfg<kType>;
+  const int64_t row_plane_bytes = static_cast<int64_t>(C::kOps) * nb * kQK_K * sizeof(_Float16);
+  int64_t slice = static_cast<int64_t>(kPlanesMaxBytes) / row_plane_bytes / C::kTileR * C::kTileR;
+  if (slice < C::kTileR) slice = C::kTileR;
+  for (int64_t r = 0; r < rows; r += slice) {
+    const int64_t n = rows - r < slice ? rows - r : slice;
+    LaunchPlanesRows<kType>(w + r * row_bytes, n, row_bytes, nb, sa, out + r, rows);
   }
 }
 
@@ -1127,10 +1129,9 @@ void LaunchMatMulMfmaSplit(uint32_t type, const uint8_t* w, int64_t rows, int64_
             static_cast<long long>(gy));
   RPG_CHECK(static_cast<int64_t>(nb) * kQK_K == sa.cols, "split activations have %lld columns, the matrix %lld",
             static_cast<long long>(sa.cols), static_cast<long long>(nb) * kQK_K);
-  const size_t plane_bytes = static_cast<size_t>(type == kGgmlQ4_K ? 1 : 2) * rows * sa.cols * sizeof(_Float16);
-  // (the planes kernel indexes both operand images with 32-bit offsets)
-  if (sa.n_tokens >= kPlanesMinTokens && plane_bytes <= kPlanesMaxBytes &&
-      kPlanes * sa.n_tokens * sa.cols < (int64_t{1} << 31)) {
+  // (the planes kernel indexes both operand images with 32-bit offsets;
+  // the weight slices stay within kPlanesMaxBytes)
+  if (sa.n_tokens >= kPlanesMinTokens && kPlanes * sa.n_tokens * sa.cols < (int64_t{1} << 31)) {
     if (type == kGgmlQ4_K) {
       LaunchPlanes<kGgmlQ4_K>(w, rows, row_bytes, nb, sa, out);
     } else {

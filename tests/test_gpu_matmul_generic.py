@@ -63,6 +63,8 @@ CASES = [
     ("decoded weight planes Q4_K, split K, ragged", Q4_K, 1152, 2048, 513, "MatMulMfmaQ4KPlanes"),
     ("decoded weight planes Q4_K, whole rounds + split tail", Q4_K, 4352, 512, 2048, "MatMulPlanesReduceKernel"),
     ("decoded weight planes Q6_K, whole rounds + split tail", Q6_K, 2176, 512, 2000, "MatMulPlanesReduceKernel"),
+    ("decoded weight planes Q6_K above 64 MB: two row slices, the last ragged", Q6_K, 8300, 2048, 512,
+     "MatMulMfmaQ6KPlanes"),
 ]
 
 
