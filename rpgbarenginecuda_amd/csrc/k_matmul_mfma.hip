@@ -654,6 +654,9 @@ __global__ __launch_bounds__(kPThreads, 1) void MatMulMfmaPlanesKernel(
   constexpr int kOps = C::kOps;
   constexpr int kNT = C::kNT;
   __shared__ __attribute__((aligned(16))) _Float16 lds[2 * C::kBufHalfs];
+  __shared__ float2 be_d[C::kTileR];                       // (d, dmin) of each row
+  __shared__ U32x4 be_m[kQ4 ? C::kTileR : 1];              // Q4_K: m_j 2^6 of each row
+  __shared__ U32x4 be_s[kQ4 ? kPlanes : 1][kQ4 ? kTileT : 1];  // Q4_K: run sums of each token
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -735,38 +738,46 @@ __global__ __launch_bounds__(kPThreads, 1) void MatMulMfmaPlanesKernel(
                                   ((j / kRowsPerOp) * C::kTileR + 64 * (j % kRowsPerOp)) * kRowStride) = rb[j]; \
   } while (0)
 
-  // Block-end values, loaded a block ahead: (d, dmin) and m of this lane's
-  // rows, the run sums of this lane's tokens (Q4_K).
-  int my_row[kNT];  // row * nb
-#pragma unroll
-  for (int nt = 0; nt < kNT; ++nt) {
-    const int64_t r = r0 + 32 * kNT * wn + 32 * nt + li;
-    my_row[nt] = static_cast<int>(r < rows ? r : rows - 1) * nb;
-  }
-  int my_tok[2];  // token * runs
-#pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    const int64_t t = t0 + 64 * wm + 32 * mt + li;
-    my_tok[mt] = static_cast<int>(t < n_tokens ? t : n_tokens - 1) * static_cast<int>(runs);
-  }
-  float2 bd[kNT];
-  U32x4 bm[kNT], bs[2][2];
-  auto load_block_end = [&](int blk) {
-#pragma unroll
-    for (int nt = 0; nt < kNT; ++nt) {
-      bd[nt] = dd[my_row[nt] + blk];
-      if (kQ4) bm[nt] = mm[my_row[nt] + blk];
-    }
+  // Block-end values of the tile, through LDS (registers are the scarce
+  // resource): per row (d, dmin) and m_j 2^6, per token and plane the
+  // block's 8 run sums (Q4_K). Thread tid fetches piece tid (and 512 + tid):
+  //   Q4_K: pieces 0..255 m of row tid; 256..511 run sums of plane (q - 256)
+  //         / 128, token (q - 256) % 128; 512..639 (d, dmin) of rows 2 (q -
+  //         512) and + 1.
+  //   Q6_K: pieces 0..63 (d, 0) of rows 2 q and + 1.
+  // Rows and tokens are clamped like the operand loads.
+  const int be_tok = static_cast<int>(t0 + (tid & 127) < n_tokens ? t0 + (tid & 127) : n_tokens - 1);
+  const int be_row = static_cast<int>(r0 + (tid & 255) < rows ? r0 + (tid & 255) : rows - 1);
+  const int be_row2a = static_cast<int>(r0 + 2 * tid < rows ? r0 + 2 * tid : rows - 1);
+  const int be_row2b = static_cast<int>(r0 + 2 * tid + 1 < rows ? r0 + 2 * tid + 1 : rows - 1);
+  constexpr int kDPairs = C::kTileR / 2;
+  U32x4 be_v;
+  float2 be_d0, be_d1;
+  auto fetch_block_end = [&](int blk) {
     if (kQ4) {
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-        for (int p = 0; p < kPlanes; ++p)
-          bs[mt][p] = *reinterpret_cast<const U32x4*>(sum_planes + p * sum_stride + (my_tok[mt] + 8 * blk));
+      if (tid < 256) be_v = mm[be_row * nb + blk];
+      else be_v = *reinterpret_cast<const U32x4*>(sum_planes + ((tid - 256) >> 7) * sum_stride +
+                                                  (be_tok * static_cast<int>(runs) + 8 * blk));
+    }
+    if (tid < kDPairs) {
+      be_d0 = dd[be_row2a * nb + blk];
+      be_d1 = dd[be_row2b * nb + blk];
+    }
+  };
+  auto store_block_end = [&]() {
+    if (kQ4) {
+      if (tid < 256) be_m[tid] = be_v;
+      else be_s[(tid - 256) >> 7][tid & 127] = be_v;
+    }
+    if (tid < kDPairs) {
+      be_d[2 * tid] = be_d0;
+      be_d[2 * tid + 1] = be_d1;
     }
   };
 
-  auto k_step = [&](int buf, int ks) {
+  // first: the block's first K-step, whose first product per accumulator
+  // starts from zero (an exact sum, so no zeroing pass at the block end)
+  auto k_step = [&](int buf, int ks, bool first) {
     const _Float16* xs = lds + buf * C::kBufHalfs;
     const _Float16* ws = xs + kPStage;
     const int kcol = 16 * ks + 8 * h;
@@ -790,37 +801,42 @@ __global__ __launch_bounds__(kPThreads, 1) void MatMulMfmaPlanesKernel(
 #pragma unroll
           for (int o = 0; o < kOps; ++o) {
             if (p == 1 && o == 1) continue;  // Q6_K x_lo w_lo: below 2^-22 |x w|, not formed
-            part[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[mt][p], bf[nt][o], part[mt][nt], 0, 0, 0);
+            const F32x16 zero = {};
+            part[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[mt][p], bf[nt][o],
+                                                                  first && p == 0 && o == 0 ? zero : part[mt][nt], 0, 0, 0);
           }
   };
 
+  // the next block's first K-step overwrites part (its products start from zero)
   auto block_end = [&]() {
+    float2 bd[kNT];
+#pragma unroll
+    for (int nt = 0; nt < kNT; ++nt) bd[nt] = be_d[32 * kNT * wn + 32 * nt + li];
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) {
       const float d = bd[nt].x;
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          acc[mt][nt][i] = __builtin_fmaf(d, part[mt][nt][i], acc[mt][nt][i]);
-          part[mt][nt][i] = 0.0f;
-        }
+        for (int i = 0; i < 16; ++i) acc[mt][nt][i] = __builtin_fmaf(d, part[mt][nt][i], acc[mt][nt][i]);
     }
     if (!kQ4) return;
     F16x8 bmf[kNT];
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) {
       const F16x8 z = {};
-      bmf[nt] = h == 0 ? __builtin_bit_cast(F16x8, bm[nt]) : z;  // k 8..15 carry zero weights
+      bmf[nt] = h == 0 ? __builtin_bit_cast(F16x8, be_m[32 * kNT * wn + 32 * nt + li]) : z;  // k 8..15: zero weights
     }
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
       for (int p = 0; p < kPlanes; ++p) {
-        const F16x8 a = __builtin_bit_cast(F16x8, bs[mt][p]);
+        const F16x8 a = __builtin_bit_cast(F16x8, be_s[p][64 * wm + 32 * mt + li]);
 #pragma unroll
-        for (int nt = 0; nt < kNT; ++nt)
-          part[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bmf[nt], part[mt][nt], 0, 0, 0);
+        for (int nt = 0; nt < kNT; ++nt) {
+          const F32x16 zero = {};
+          part[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, bmf[nt], p == 0 ? zero : part[mt][nt], 0, 0, 0);
+        }
       }
 #pragma unroll
     for (int nt = 0; nt < kNT; ++nt) {
@@ -828,10 +844,7 @@ __global__ __launch_bounds__(kPThreads, 1) void MatMulMfmaPlanesKernel(
 #pragma unroll
       for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          acc[mt][nt][i] = __builtin_fmaf(-dmin, part[mt][nt][i], acc[mt][nt][i]);
-          part[mt][nt][i] = 0.0f;
-        }
+        for (int i = 0; i < 16; ++i) acc[mt][nt][i] = __builtin_fmaf(-dmin, part[mt][nt][i], acc[mt][nt][i]);
     }
   };
 
@@ -839,25 +852,32 @@ __global__ __launch_bounds__(kPThreads, 1) void MatMulMfmaPlanesKernel(
   // final chunk into the idle buffer): registers filled under a condition that
   // spans iterations end up in scratch memory.
   const int last = n_chunks - 1;
-  load_block_end(b0);
+  fetch_block_end(b0);
   RPG_PLANES_LOAD(0);
   RPG_PLANES_STAGE(0);
   RPG_PLANES_LOAD(last > 0 ? 1 : 0);
+  store_block_end();
   __syncthreads();
-  for (int c = 0; c < n_chunks; ++c) {
-    const int buf = c & 1;
-    // a block's end values are loaded at its first chunk, ahead of that
-    // chunk's staging loads: the wait for those (before the next LDS writes)
-    // then never waits for a load issued after them
-    if ((c & 3) == 0 && c > 0) load_block_end(b0 + (c >> 2));
-    k_step(buf, 0);
-    RPG_PLANES_STAGE(buf ^ 1);
-    RPG_PLANES_LOAD(c + 2 < last ? c + 2 : last);
-    k_step(buf, 1);
-    k_step(buf, 2);
-    k_step(buf, 3);
-    if ((c & 3) == 3) block_end();
-    __syncthreads();
+  for (int blk = 0; blk < n_blk; ++blk) {
+    // A block's end values are fetched at its first chunk, ahead of that
+    // chunk's staging loads (so the wait before the next LDS writes never
+    // waits for a load issued after them), and stored to LDS before the
+    // chunk's barrier; the previous block's end read them three barriers
+    // earlier.
+    if (blk > 0) fetch_block_end(b0 + blk);
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {  // chunk 4 blk + kc, in LDS buffer kc & 1
+      const int c = 4 * blk + kc;
+      k_step(kc & 1, 0, kc == 0);
+      RPG_PLANES_STAGE((kc & 1) ^ 1);
+      RPG_PLANES_LOAD(c + 2 < last ? c + 2 : last);
+      k_step(kc & 1, 1, false);
+      k_step(kc & 1, 2, false);
+      k_step(kc & 1, 3, false);
+      if (kc == 0 && blk > 0) store_block_end();
+      if (kc == 3) block_end();
+      __syncthreads();
+    }
   }
 #undef RPG_PLANES_LOAD
 #undef RPG_PLANES_STAGE
