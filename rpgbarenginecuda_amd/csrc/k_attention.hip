@@ -47,6 +47,7 @@ constexpr int kWaves = kBlockThreads / 64;
 constexpr int kMaxChunks = 64;
 constexpr int kPartFloats = kD + 2;  // o[128], m, l
 constexpr int64_t kFaMinTokens = 64;  // prefill calls with at least this many tokens run on the matrix cores
+constexpr int64_t kFaMaxPartialFloats = int64_t{64} << 20;  // 256 MiB of prefill key-chunk partials at most
 
 __device__ __forceinline__ int64_t ReadPos0(int64_t value, const int64_t* dev) { return dev != nullptr ? *dev : value; }
 
@@ -276,6 +277,39 @@ __global__ __launch_bounds__(kBlockThreads) void AttnMergeKernel(const float* __
   const int32_t live = LiveChunks(ReadPos0(pos0_val, pos0_dev) + th / n_heads, chunk_len, n_chunks);
   if (live == 1) return;  // the chunk kernel wrote the output
   MergeChunks(part + th * n_chunks * kPartFloats, live, lane, out + th * kD);
+}
+
+// The same merge for many pairs with few chunks (prefill key chunks): 32
+// threads per (t, h), 4 dims each; the chunk weights exp(m_c - M) and the
+// normaliser are summed in chunk order.
+__global__ __launch_bounds__(kBlockThreads) void AttnMergeRowsKernel(const float* __restrict__ part, int64_t pairs,
+                                                                      int32_t n_chunks, int32_t n_heads,
+                                                                      int64_t chunk_len, int64_t pos0_val,
+                                                                      const int64_t* __restrict__ pos0_dev,
+                                                                      float* __restrict__ out) {
+  const int64_t u = static_cast<int64_t>(blockIdx.x) * kBlockThreads + threadIdx.x;
+  const int64_t th = u / (kD / 4);
+  if (th >= pairs) return;
+  const int dq = static_cast<int>(u - th * (kD / 4));
+  const int32_t live = LiveChunks(ReadPos0(pos0_val, pos0_dev) + th / n_heads, chunk_len, n_chunks);
+  if (live == 1) return;  // the prefill kernel wrote the output
+  const float* pp = part + th * n_chunks * kPartFloats;
+  float mx = -INFINITY;
+  for (int32_t c = 0; c < live; ++c) mx = fmaxf(mx, pp[c * kPartFloats + kD]);
+  float L = 0.0f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int32_t c = 0; c < live; ++c) {
+    const float mc = pp[c * kPartFloats + kD];
+    const float f = mc == -INFINITY ? 0.0f : expf(mc - mx);
+    L = __builtin_fmaf(pp[c * kPartFloats + kD + 1], f, L);
+    const float4 v = *reinterpret_cast<const float4*>(pp + c * kPartFloats + 4 * dq);
+    acc.x = __builtin_fmaf(v.x, f, acc.x);
+    acc.y = __builtin_fmaf(v.y, f, acc.y);
+    acc.z = __builtin_fmaf(v.z, f, acc.z);
+    acc.w = __builtin_fmaf(v.w, f, acc.w);
+  }
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  *reinterpret_cast<float4*>(out + th * kD + 4 * dq) = make_float4(acc.x * inv, acc.y * inv, acc.z * inv, acc.w * inv);
 }
 
 // ---------------------------------------------------------------- decode, one wave per kv head
@@ -603,19 +637,29 @@ __device__ __forceinline__ F16x8 SplitTerm(float (&x)[8]) {
   return h;
 }
 
+// Key chunks: workgroup (c, token tile, head) takes keys [c chunk_len, (c +
+// 1) chunk_len) of the tile's causal range, so the long tiles at the end of a
+// prompt spread over several workgroups. A token whose keys all lie in chunk
+// 0 (LiveChunks == 1) gets its normalised output from chunk 0; the others get
+// an unnormalised partial (o, m, l) per live chunk in `part`, laid out as the
+// decode partials ([token][head][chunk]), which AttnMergeKernel combines.
 __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
     const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t max_seq,
     int32_t n_heads, int32_t group, float scale, int64_t pos0_val, const int64_t* __restrict__ pos0_dev, int64_t seq,
-    float* __restrict__ out) {
+    int32_t n_chunks, int64_t chunk_len, float* __restrict__ out, float* __restrict__ part) {
   __shared__ __attribute__((aligned(16))) _Float16 ks[kFaKeys * kFaKStride];
   __shared__ __attribute__((aligned(16))) _Float16 vs[kFaKeys * kFaVStride];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int hf = lane >> 5;    // which half of the keys / dims this lane holds
   const int col = lane & 31;   // the lane's query within the wave
+  // grid (chunk, head, tile) with the last token tile first: workgroups are
+  // dispatched x fastest, so the longest key ranges start first and the short
+  // ones fill in at the end
+  const int32_t chunk = static_cast<int32_t>(blockIdx.x);
   const int h = blockIdx.y;
   const int kh = h / group;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kFaTokens;
+  const int64_t t0 = static_cast<int64_t>(gridDim.z - 1 - blockIdx.z) * kFaTokens;
   const int64_t pos0 = ReadPos0(pos0_val, pos0_dev);
   const int64_t tq = t0 + 32 * wv + col;
   const bool qvalid = tq < seq;
@@ -660,8 +704,11 @@ __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
   const int64_t wave_last = pos0 + (t0 + 32 * wv + 31 < seq ? t0 + 32 * wv + 31 : seq - 1);
   const uint16_t* kbase = kc + static_cast<int64_t>(kh) * max_seq * kD;
   const uint16_t* vbase = vc + static_cast<int64_t>(kh) * max_seq * kD;
+  const int64_t klo = static_cast<int64_t>(chunk) * chunk_len;
+  if (klo > last_key) return;  // no key of this chunk is visible to the tile (uniform: before any barrier)
+  const int64_t kend = klo + chunk_len;
 
-  for (int64_t kb = 0; kb <= last_key; kb += kFaKeys) {
+  for (int64_t kb = klo; kb <= last_key && kb < kend; kb += kFaKeys) {
     __syncthreads();  // the previous block is consumed
     {
       // thread t: key t / 4, dims 32 (t % 4) .. + 31 of K and V
@@ -764,6 +811,24 @@ __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
 
   // ---- out[tq][h][dim]: register r of tile dt is dim 32 dt + (r % 4) + 8 (r / 4) + 4 hf
   if (!qvalid) return;
+  const int32_t live = LiveChunks(qpos, chunk_len, n_chunks);
+  if (live > 1) {  // a partial of this chunk, if the query sees any of its keys
+    if (chunk >= live) return;
+    float* pp = part + ((tq * n_heads + h) * n_chunks + chunk) * kPartFloats;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 v = make_float4(o[dt][4 * g], o[dt][4 * g + 1], o[dt][4 * g + 2], o[dt][4 * g + 3]);
+        *reinterpret_cast<float4*>(pp + 32 * dt + 8 * g + 4 * hf) = v;
+      }
+    }
+    if (hf == 0) {
+      pp[kD] = m;
+      pp[kD + 1] = l;
+    }
+    return;
+  }
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   float* orow = out + (tq * n_heads + h) * kD;
 #pragma unroll
@@ -862,6 +927,9 @@ struct PartialsSink {
               floats, fixed_floats, fixed_floats * sizeof(float) >> 20);
     return fixed;
   }
+
+  // Floats a call may take (the library's buffer grows; a fixed region does not).
+  size_t Capacity() const { return fixed == nullptr ? SIZE_MAX : fixed_floats; }
 };
 
 // Up to this many positions one chunk per (token, head) beats a split plus the
@@ -959,10 +1027,41 @@ void AttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev, in
   PlanChunks(pairs, positions, &n_chunks, &chunk_len);
   const Pos0Arg p0 = Pos0ForLaunch(pos0);
   if (seq >= kFaMinTokens) {
+    // Key chunks of at most max(8, total / 512) key blocks per workgroup (two
+    // workgroups per CU), counted over the position budget; the partials stay
+    // within kFaMaxPartialFloats and within the sink (a fixed region that is
+    // too small keeps one chunk, with no partials at all).
+    const int64_t tiles = (seq + kFaTokens - 1) / kFaTokens;
+    const int64_t first = positions - seq;  // position of token 0 in the budget
+    int64_t total_blocks = 0;
+    for (int64_t tt = 0; tt < tiles; ++tt) {
+      const int64_t last = first + (tt + 1) * kFaTokens < positions ? first + (tt + 1) * kFaTokens : positions;
+      total_blocks += (last + kFaKeys - 1) / kFaKeys;
+    }
+    total_blocks *= c.n_heads;
+    const int64_t max_blocks = (positions + kFaKeys - 1) / kFaKeys;
+    int64_t per = (total_blocks + 511) / 512;
+    if (per < 8) per = 8;
+    int64_t fa_chunks = (max_blocks + per - 1) / per;
+    const int64_t room = static_cast<int64_t>(
+        sink.Capacity() < static_cast<size_t>(kFaMaxPartialFloats) ? sink.Capacity() : kFaMaxPartialFloats);
+    const int64_t cap = room / (seq * c.n_heads * kPartFloats);
+    if (fa_chunks > cap) fa_chunks = cap;
+    if (fa_chunks > kMaxChunks) fa_chunks = kMaxChunks;
+    if (fa_chunks < 1) fa_chunks = 1;
+    const int64_t fa_len = (max_blocks + fa_chunks - 1) / fa_chunks * kFaKeys;
+    fa_chunks = (positions + fa_len - 1) / fa_len;
+    float* part = fa_chunks > 1 ? sink.Get(static_cast<size_t>(pairs) * fa_chunks * kPartFloats) : nullptr;
+    RPG_CHECK(tiles <= 65535 && c.n_heads <= 65535, "prefill attention grid too large");
     Launch("AttnPrefillMfmaKernel", AttnPrefillMfmaKernel,
-           dim3(static_cast<unsigned>((seq + kFaTokens - 1) / kFaTokens), static_cast<unsigned>(c.n_heads)),
+           dim3(static_cast<unsigned>(fa_chunks), static_cast<unsigned>(c.n_heads), static_cast<unsigned>(tiles)),
            dim3(kBlockThreads), q_dev, k_layer, v_layer, max_seq, c.n_heads, c.n_heads / c.n_kv_heads, scale,
-           p0.value, p0.dev, seq, out_dev);
+           p0.value, p0.dev, seq, static_cast<int32_t>(fa_chunks), fa_len, out_dev, part);
+    if (fa_chunks > 1) {
+      Launch("AttnMergeRowsKernel", AttnMergeRowsKernel, dim3(GridFor(pairs * (kD / 4), kBlockThreads)),
+             dim3(kBlockThreads), static_cast<const float*>(part), pairs, static_cast<int32_t>(fa_chunks), c.n_heads,
+             fa_len, p0.value, p0.dev, out_dev);
+    }
     return;
   }
   const int group = c.n_heads / c.n_kv_heads;
