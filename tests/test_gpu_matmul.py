@@ -109,6 +109,7 @@ SHAPES = [
     (12, 6144, 2048, 700),   # ... ffn_gate shape, 24 x 6 tiles: one slice, no split
     (12, 4352, 512, 2048),   # ... 17 x 16 = 272 tiles: one whole round unsplit, the 16 left split along K
     (14, 2176, 512, 2000),   # ... Q6_K likewise, ragged token tile
+    (14, 2560, 9728, 520),   # ... 4B ffn_down: 38 blocks per row, K slices of unequal length
 ]
 
 

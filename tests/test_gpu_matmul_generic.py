@@ -65,6 +65,7 @@ CASES = [
     ("decoded weight planes Q6_K, whole rounds + split tail", Q6_K, 2176, 512, 2000, "MatMulPlanesReduceKernel"),
     ("decoded weight planes Q6_K above 64 MB: two row slices, the last ragged", Q6_K, 8300, 2048, 512,
      "MatMulMfmaQ6KPlanes"),
+    ("decoded weight planes Q4_K, 10 blocks per row (4B shape)", Q4_K, 1024, 2560, 520, "MatMulMfmaQ4KPlanes"),
 ]
 
 
