@@ -45,7 +45,7 @@ constexpr int kD = 128;          // head_dim of the fast path
 constexpr int kBlockThreads = 256;
 constexpr int kWaves = kBlockThreads / 64;
 constexpr int kMaxChunks = 64;
-constexpr int kPartFloats = kD + 2;  // o[128], m, l
+constexpr int kPartFloats = kD + 4;  // o[128], m, l, 2 unused: 16-byte aligned rows for the float4 accesses
 constexpr int64_t kFaMinTokens = 64;  // prefill calls with at least this many tokens run on the matrix cores
 constexpr int64_t kFaMaxPartialFloats = int64_t{64} << 20;  // 256 MiB of prefill key-chunk partials at most
 

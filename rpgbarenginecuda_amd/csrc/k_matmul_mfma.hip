@@ -1000,7 +1000,9 @@ SplitBuffer& WeightPlanes() {
   return *b;
 }
 
-// Grow-only buffer of the decoded weight planes (same policy as the split buffer).
+// Grow-only buffer of the decoded weight planes: an outgrown buffer is retired,
+// not freed, as for the split buffer; sized to the request (the largest is one
+// 64 MB slice of planes plus its block values).
 void* EnsureWeightPlanes(size_t bytes) {
   SplitBuffer& b = WeightPlanes();
   std::lock_guard<std::mutex> lock(b.mu);

@@ -224,7 +224,7 @@ void GpuCausalAttention(const ModelMeta& c, const float* q_dev, const float* k_d
 // capture, serving loops that forbid hipMalloc): the same kernels and results,
 // with the chunk partials in a fixed 8 MiB device array of the library instead
 // of the grow-only buffer, so nothing is ever allocated. A call whose key split
-// needs more partials than that (seq * n_heads * chunks * 130 floats > 2^21;
+// needs more partials than that (seq * n_heads * chunks * 132 floats > 2^21;
 // the split aims at ~2048 waves, so this is reached only with GQA groups of 4
 // and more than ~2000 (token, kv head) pairs) is rejected before anything
 // launches. Every call on a device shares that

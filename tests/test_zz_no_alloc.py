@@ -67,7 +67,7 @@ def test_noalloc_attention_rejects_oversized_split(gpu):
     lib = gpu.load_library()
     _case("noalloc rejects a split beyond its fixed scratch")
     # GQA group 4 with 62 x 33 = 2046 (token, kv head) pairs: the split takes 2
-    # chunks, 62 x 132 heads x 2 chunks x 130 floats = 2127840 > 2^21.
+    # chunks, 62 x 132 heads x 2 chunks x 132 floats = 2160576 > 2^21.
     nh, nkv, max_seq, pos0, seq = 132, 33, 2048, 1000, 62
     q = torch.zeros((seq, nh, 128), dtype=torch.float32, device="cuda")
     kc = torch.zeros((nkv, max_seq, 128), dtype=torch.int16, device="cuda")
