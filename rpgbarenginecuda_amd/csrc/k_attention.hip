@@ -279,9 +279,9 @@ __global__ __launch_bounds__(kBlockThreads) void AttnMergeKernel(const float* __
   MergeChunks(part + th * n_chunks * kPartFloats, live, lane, out + th * kD);
 }
 
-// The same merge for many pairs with few chunks (prefill key chunks): 32
-// threads per (t, h), 4 dims each; the chunk weights exp(m_c - M) and the
-// normaliser are summed in chunk order.
+// The merge of prefill key chunks (many pairs, few chunks): 32 threads per
+// (t, h), 4 dims each; the partials' maxima are in log2 units, so the chunk
+// weights are 2^(m_c - M); weights and normaliser are summed in chunk order.
 __global__ __launch_bounds__(kBlockThreads) void AttnMergeRowsKernel(const float* __restrict__ part, int64_t pairs,
                                                                       int32_t n_chunks, int32_t n_heads,
                                                                       int64_t chunk_len, int64_t pos0_val,
@@ -300,7 +300,7 @@ __global__ __launch_bounds__(kBlockThreads) void AttnMergeRowsKernel(const float
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int32_t c = 0; c < live; ++c) {
     const float mc = pp[c * kPartFloats + kD];
-    const float f = mc == -INFINITY ? 0.0f : expf(mc - mx);
+    const float f = mc == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc - mx);
     L = __builtin_fmaf(pp[c * kPartFloats + kD + 1], f, L);
     const float4 v = *reinterpret_cast<const float4*>(pp + c * kPartFloats + 4 * dq);
     acc.x = __builtin_fmaf(v.x, f, acc.x);
@@ -684,15 +684,22 @@ __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
   amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
   int e = 0;
   if (amax > 0.0f && amax <= 3.0e38f) e = 6 - ilogbf(amax);  // max |q| * 2^e in [64, 128)
+  // Scores are kept in log2 units, so each exponential is one v_exp_f32:
+  // p = 2^(s2 - m2) = e^(s - m). The score scale (1 / sqrt(d) times log2(e))
+  // is applied to q before the split (one fp32 rounding, ~2^-24, under the
+  // split's ~2^-23): q 2^e scale log2(e) lies in [8, 17), well inside fp16's
+  // range for both terms. The matrix cores return s2 2^e, and the exponent
+  // s2 - m2 is formed as fma(s2 2^e, 2^-e, -m2), exact scaling and one rounding.
+  const float qmul = ldexpf(scale * 1.44269504088896340736f, e);
+  const float sinv = ldexpf(1.0f, -e);
   F16x8 qb[2][8];
 #pragma unroll
   for (int s = 0; s < 8; ++s) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) qv[s][j] = ldexpf(qv[s][j], e);
+    for (int j = 0; j < 8; ++j) qv[s][j] *= qmul;
     qb[0][s] = SplitTerm(qv[s]);
     qb[1][s] = SplitTerm(qv[s]);
   }
-  const float sfac = scale * ldexpf(1.0f, -e);
 
   F32x16 o[4];
 #pragma unroll
@@ -702,6 +709,8 @@ __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
   const int64_t t_last = (t0 + kFaTokens < seq ? t0 + kFaTokens : seq) - 1;
   const int64_t last_key = pos0 + t_last;                                   // the workgroup's causal limit
   const int64_t wave_last = pos0 + (t0 + 32 * wv + 31 < seq ? t0 + 32 * wv + 31 : seq - 1);
+  const int64_t wave_first = pos0 + t0 + 32 * wv;   // the wave's first query position
+  const bool wave_full = t0 + 32 * wv + 31 < seq;   // all 32 queries of the wave are tokens
   const uint16_t* kbase = kc + static_cast<int64_t>(kh) * max_seq * kD;
   const uint16_t* vbase = vc + static_cast<int64_t>(kh) * max_seq * kD;
   const int64_t klo = static_cast<int64_t>(chunk) * chunk_len;
@@ -750,27 +759,41 @@ __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
       }
     }
 
-    // ---- online softmax: register r of tile mt is key kb + 32 mt + (r % 4) + 8 (r / 4) + 4 hf
+    // ---- online softmax: register r of tile mt is key kb + 32 mt + (r % 4) + 8 (r / 4) + 4 hf;
+    // the causal test on the key's offset in the block (32-bit)
+    // (a block wholly below every query of the wave, all of them valid, needs no mask)
     float bmax = -INFINITY;
+    if (kb + kFaKeys - 1 <= wave_first && wave_full) {
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
+      for (int mt = 0; mt < 2; ++mt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int64_t key = kb + 32 * mt + (r & 3) + 8 * (r >> 2) + 4 * hf;
-        const float sc = (qvalid && key <= qpos) ? st[mt][r] * sfac : -INFINITY;
-        st[mt][r] = sc;
-        bmax = fmaxf(bmax, sc);
+        for (int r = 0; r < 16; ++r) bmax = fmaxf(bmax, st[mt][r]);
+    } else {
+      const int64_t rel64 = qvalid ? qpos - kb : -1;
+      const int32_t rel = static_cast<int32_t>(rel64 < 64 ? rel64 : 64);  // offsets <= rel are visible
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int32_t off = 32 * mt + (r & 3) + 8 * (r >> 2) + 4 * hf;
+          const float sc = off <= rel ? st[mt][r] : -INFINITY;
+          st[mt][r] = sc;
+          bmax = fmaxf(bmax, sc);
+        }
       }
     }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64));
+    bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64)) * sinv;  // exact: a power of two
     const float mn = fmaxf(m, bmax);
-    const float corr = mn == -INFINITY ? 1.0f : expf(m - mn);  // exp(-inf) = 0 on the first live block
+    // 2^(-inf) = 0: masked scores give p = 0 once the row has a finite max;
+    // before that (mn = -inf) the block contributes nothing
+    const float base = mn == -INFINITY ? 0.0f : mn;
+    const float corr = __builtin_amdgcn_exp2f(m - base);  // m = -inf on the first live block: 0
     float psum = 0.0f;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = st[mt][r] == -INFINITY ? 0.0f : expf(st[mt][r] - mn);
+        const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(st[mt][r], sinv, -base));
         st[mt][r] = p;
         psum += p;
       }
@@ -812,8 +835,11 @@ __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
   // ---- out[tq][h][dim]: register r of tile dt is dim 32 dt + (r % 4) + 8 (r / 4) + 4 hf
   if (!qvalid) return;
   const int32_t live = LiveChunks(qpos, chunk_len, n_chunks);
-  if (live > 1) {  // a partial of this chunk, if the query sees any of its keys
-    if (chunk >= live) return;
+  // A chunk past the query's live chunks saw none of its keys and writes
+  // nothing: in particular, for a query whose keys all lie in chunk 0, only
+  // chunk 0 writes its output (another chunk would overwrite it with zeros).
+  if (chunk >= live) return;
+  if (live > 1) {  // a partial of this chunk
     float* pp = part + ((tq * n_heads + h) * n_chunks + chunk) * kPartFloats;
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
