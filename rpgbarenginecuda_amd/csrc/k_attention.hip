@@ -30,8 +30,11 @@
 // actual position inside the kernel.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <mutex>
+#include <utility>
+#include <vector>
 
 #include "dev_util.h"
 #include "head_row.h"
@@ -613,6 +616,8 @@ typedef float F32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kFaTokens = 128;    // tokens (of one head) per workgroup
 constexpr int kFaKeys = 64;       // keys per LDS block
+constexpr float kFaLazyLog2 = 8;  // the running max moves when a block's max exceeds it by more (log2 units)
+constexpr int kFaOrderMax = 1024; // (token tile, key chunk) pairs an ordered launch can list
 constexpr int kFaKStride = 136;   // halves per K row in LDS (128 + 8: conflict-free 16-byte reads)
 constexpr int kFaVStride = 160;   // halves per V row in LDS (128 + 32: conflict-free transposing reads)
 
@@ -637,29 +642,48 @@ __device__ __forceinline__ F16x8 SplitTerm(float (&x)[8]) {
   return h;
 }
 
-// Key chunks: workgroup (c, token tile, head) takes keys [c chunk_len, (c +
-// 1) chunk_len) of the tile's causal range, so the long tiles at the end of a
-// prompt spread over several workgroups. A token whose keys all lie in chunk
-// 0 (LiveChunks == 1) gets its normalised output from chunk 0; the others get
-// an unnormalised partial (o, m, l) per live chunk in `part`, laid out as the
-// decode partials ([token][head][chunk]), which AttnMergeKernel combines.
+// Dispatch order of the prefill workgroups. Workgroup g takes query head g %
+// n_heads of pair g / n_heads; with n > 0, pair i is (token tile e[i] >> 6, key
+// chunk e[i] & 63), the pairs sorted by their key blocks, most first, so the
+// longest workgroups start first and the short ones fill the gaps at the end
+// (longest-processing-time order). With n == 0 (more pairs than the table
+// holds) pair i is (tiles - 1 - i / n_chunks, i % n_chunks): last tile first.
+struct FaOrder {
+  int32_t n;
+  uint16_t e[kFaOrderMax];
+};
+
+// Key chunks: the workgroup of (token tile, key chunk c, head) takes keys
+// [c chunk_len, (c + 1) chunk_len) of the tile's causal range, so the long tiles
+// at the end of a prompt spread over several workgroups. A token whose keys all
+// lie in chunk 0 (LiveChunks == 1) gets its normalised output from chunk 0; the
+// others get an unnormalised partial (o, m, l) per live chunk in `part`, laid
+// out as the decode partials ([token][head][chunk]), which AttnMergeRowsKernel
+// combines.
 __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
     const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t max_seq,
     int32_t n_heads, int32_t group, float scale, int64_t pos0_val, const int64_t* __restrict__ pos0_dev, int64_t seq,
-    int32_t n_chunks, int64_t chunk_len, float* __restrict__ out, float* __restrict__ part) {
+    int32_t n_chunks, int64_t chunk_len, int32_t tiles, float* __restrict__ out, float* __restrict__ part,
+    FaOrder order) {
   __shared__ __attribute__((aligned(16))) _Float16 ks[kFaKeys * kFaKStride];
   __shared__ __attribute__((aligned(16))) _Float16 vs[kFaKeys * kFaVStride];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int hf = lane >> 5;    // which half of the keys / dims this lane holds
   const int col = lane & 31;   // the lane's query within the wave
-  // grid (chunk, head, tile) with the last token tile first: workgroups are
-  // dispatched x fastest, so the longest key ranges start first and the short
-  // ones fill in at the end
-  const int32_t chunk = static_cast<int32_t>(blockIdx.x);
-  const int h = blockIdx.y;
+  const int32_t pair = static_cast<int32_t>(blockIdx.x) / n_heads;
+  const int h = static_cast<int>(blockIdx.x) - pair * n_heads;
   const int kh = h / group;
-  const int64_t t0 = static_cast<int64_t>(gridDim.z - 1 - blockIdx.z) * kFaTokens;
+  int32_t chunk, tile;
+  if (order.n > 0) {
+    const uint32_t entry = order.e[pair];
+    chunk = static_cast<int32_t>(entry & 63u);
+    tile = static_cast<int32_t>(entry >> 6);
+  } else {
+    tile = tiles - 1 - pair / n_chunks;
+    chunk = pair - (tiles - 1 - tile) * n_chunks;
+  }
+  const int64_t t0 = static_cast<int64_t>(tile) * kFaTokens;
   const int64_t pos0 = ReadPos0(pos0_val, pos0_dev);
   const int64_t tq = t0 + 32 * wv + col;
   const bool qvalid = tq < seq;
@@ -723,21 +747,16 @@ __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
       // thread t: key t / 4, dims 32 (t % 4) .. + 31 of K and V
       const int key = threadIdx.x >> 2;
       const int part = threadIdx.x & 3;
-      const int64_t j = kb + key;
+      // rows past the causal limit repeat the last visible row: their scores are
+      // masked, so p = 0 meets finite values
+      const int64_t j = kb + key < last_key ? kb + key : last_key;
       uint4 kw[4], vw[4];
+      const uint4* kr = reinterpret_cast<const uint4*>(kbase + j * kD + 32 * part);
+      const uint4* vr = reinterpret_cast<const uint4*>(vbase + j * kD + 32 * part);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        kw[i] = make_uint4(0, 0, 0, 0);
-        vw[i] = kw[i];
-      }
-      if (j <= last_key) {  // keys past the causal limit stay zero: p = 0 must meet finite v
-        const uint4* kr = reinterpret_cast<const uint4*>(kbase + j * kD + 32 * part);
-        const uint4* vr = reinterpret_cast<const uint4*>(vbase + j * kD + 32 * part);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          kw[i] = kr[i];
-          vw[i] = vr[i];
-        }
+        kw[i] = kr[i];
+        vw[i] = vr[i];
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) *reinterpret_cast<uint4*>(&ks[key * kFaKStride + 32 * part + 8 * i]) = kw[i];
@@ -783,11 +802,19 @@ __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
       }
     }
     bmax = fmaxf(bmax, __shfl_xor(bmax, 32, 64)) * sinv;  // exact: a power of two
-    const float mn = fmaxf(m, bmax);
+    // The running max m moves only when a block's max exceeds it by more than
+    // kFaLazyLog2, so p <= 2^kFaLazyLog2 and most blocks rescale nothing (o and
+    // l are relative to whatever m is; the final o / l does not depend on it).
+    const float mn = bmax > m + kFaLazyLog2 ? bmax : m;
     // 2^(-inf) = 0: masked scores give p = 0 once the row has a finite max;
     // before that (mn = -inf) the block contributes nothing
     const float base = mn == -INFINITY ? 0.0f : mn;
-    const float corr = __builtin_amdgcn_exp2f(m - base);  // m = -inf on the first live block: 0
+    if (__builtin_amdgcn_ballot_w64(mn != m) != 0) {  // some row of the wave moved
+      const float corr = __builtin_amdgcn_exp2f(m - base);  // 1 where m stays; 0 on a row's first live block
+      l *= corr;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) o[dt] *= corr;
+    }
     float psum = 0.0f;
 #pragma unroll
     for (int mt = 0; mt < 2; ++mt) {
@@ -799,10 +826,8 @@ __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
       }
     }
     psum += __shfl_xor(psum, 32, 64);
-    l = l * corr + psum;
+    l += psum;
     m = mn;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt) o[dt] *= corr;
 
     // ---- O^T += V^T . P^T: key step ks takes registers 8 (ks % 2) .. + 7 of tile ks / 2
 #pragma unroll
@@ -1078,11 +1103,32 @@ void AttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev, in
     const int64_t fa_len = (max_blocks + fa_chunks - 1) / fa_chunks * kFaKeys;
     fa_chunks = (positions + fa_len - 1) / fa_len;
     float* part = fa_chunks > 1 ? sink.Get(static_cast<size_t>(pairs) * fa_chunks * kPartFloats) : nullptr;
-    RPG_CHECK(tiles <= 65535 && c.n_heads <= 65535, "prefill attention grid too large");
-    Launch("AttnPrefillMfmaKernel", AttnPrefillMfmaKernel,
-           dim3(static_cast<unsigned>(fa_chunks), static_cast<unsigned>(c.n_heads), static_cast<unsigned>(tiles)),
+    const int64_t n_pairs = tiles * fa_chunks;
+    RPG_CHECK(n_pairs * c.n_heads < (int64_t{1} << 31), "prefill attention grid too large");
+    // (tile, chunk) pairs sorted by their key blocks over the position budget,
+    // most first (ties: later tile first)
+    FaOrder order;
+    order.n = 0;
+    if (n_pairs <= kFaOrderMax && tiles <= 1024) {
+      std::vector<std::pair<int64_t, int32_t>> by_size;
+      by_size.reserve(static_cast<size_t>(n_pairs));
+      const int64_t len_blocks = fa_len / kFaKeys;
+      for (int64_t tt = 0; tt < tiles; ++tt) {
+        const int64_t last = first + (tt + 1) * kFaTokens < positions ? first + (tt + 1) * kFaTokens : positions;
+        const int64_t n_blocks = (last + kFaKeys - 1) / kFaKeys;
+        for (int64_t ch = 0; ch < fa_chunks; ++ch) {
+          const int64_t size = std::min(std::max<int64_t>(n_blocks - ch * len_blocks, 0), len_blocks);
+          by_size.emplace_back(-(size * 1024 + tt), static_cast<int32_t>((tt << 6) | ch));
+        }
+      }
+      std::sort(by_size.begin(), by_size.end());
+      for (int64_t i = 0; i < n_pairs; ++i) order.e[i] = static_cast<uint16_t>(by_size[i].second);
+      order.n = static_cast<int32_t>(n_pairs);
+    }
+    Launch("AttnPrefillMfmaKernel", AttnPrefillMfmaKernel, dim3(static_cast<unsigned>(n_pairs * c.n_heads)),
            dim3(kBlockThreads), q_dev, k_layer, v_layer, max_seq, c.n_heads, c.n_heads / c.n_kv_heads, scale,
-           p0.value, p0.dev, seq, static_cast<int32_t>(fa_chunks), fa_len, out_dev, part);
+           p0.value, p0.dev, seq, static_cast<int32_t>(fa_chunks), fa_len, static_cast<int32_t>(tiles), out_dev,
+           part, order);
     if (fa_chunks > 1) {
       Launch("AttnMergeRowsKernel", AttnMergeRowsKernel, dim3(GridFor(pairs * (kD / 4), kBlockThreads)),
              dim3(kBlockThreads), static_cast<const float*>(part), pairs, static_cast<int32_t>(fa_chunks), c.n_heads,

@@ -112,6 +112,26 @@ def test_attention_prefill_ignores_rows_past_the_limit(gpu, ora):
     check(host(out1), ref, smag, vmax, pos0)
 
 
+def test_attention_prefill_long_one_head(gpu, ora):
+    """Matrix-core prefill of 16512 tokens on one head: 129 token tiles x 8 key
+    chunks, more (tile, chunk) pairs than the launch's ordered list holds, so the
+    workgroups run last tile first. Rows from the first tile, a chunk boundary
+    and the last tile are held to the bound (token t's result depends only on
+    q_t and keys <= pos0 + t, so a slice of the oracle covers them)."""
+    import torch
+
+    case("attention prefill n=16512, one head")
+    nh, nkv, max_seq, pos0, seq = 1, 1, 16512, 0, 16512
+    rng = np.random.default_rng(1460)
+    q, kc, vc = make(rng, nh, nkv, max_seq, seq, qscale=0.5)
+    out = torch.full((seq, nh, 128), np.nan, dtype=torch.float32, device="cuda")
+    gpu.GpuAttentionFromCache(nh, nkv, 128, pos0, dev(q), seq, dev(kc), dev(vc), max_seq, out)
+    got = host(out)
+    for t0, n in ((0, 64), (2080, 64), (seq - 48, 48)):
+        ref, smag, vmax = ora.attention_f64(q[t0:t0 + n], kc, vc, max_seq, nh, nkv, 128, pos0 + t0, n)
+        check(got[t0:t0 + n], ref, smag, vmax, pos0 + t0)
+
+
 def test_attention_causal_limit_and_budget(gpu, ora):
     """Cache rows past pos0 + t are never read into the result (garbage there
     changes nothing, bit for bit); a larger position budget (the graph-capture
