@@ -141,23 +141,57 @@ __device__ __forceinline__ StageRaw FetchStageQ6K(const uint8_t* __restrict__ bl
 }
 
 // Activation pre-pass: one workgroup per token row, 8 consecutive columns
-// per thread (four threads per 32-column run).
-__global__ __launch_bounds__(kThreads) void SplitActivationsKernel(const float* __restrict__ x, int64_t cols,
-                                                                   int64_t plane_elems, int64_t sum_elems,
-                                                                   _Float16* __restrict__ planes,
-                                                                   _Float16* __restrict__ sum_planes,
-                                                                   float* __restrict__ inv_scale) {
+// per thread and step (four threads per 32-column run). kU > 0: the row has at
+// most kU * 8 * kThreads columns and each thread keeps its kU steps in
+// registers between the max pass and the split pass; kU == 0 reads the row
+// twice (any width). Both give the same bits.
+struct SplitArgs {
+  const float* x;
+  int64_t cols;
+  int64_t plane_elems;
+  int64_t sum_elems;
+  _Float16* planes;
+  _Float16* sum_planes;
+  float* inv_scale;
+};
+
+template <int kU>
+__device__ __forceinline__ void SplitRow(const SplitArgs& a, int64_t t) {
+  const float* __restrict__ x = a.x;
+  const int64_t cols = a.cols;
+  const int64_t plane_elems = a.plane_elems;
+  const int64_t sum_elems = a.sum_elems;
+  _Float16* __restrict__ planes = a.planes;
+  _Float16* __restrict__ sum_planes = a.sum_planes;
+  constexpr int kSteps = kU > 0 ? kU : 1;
+  constexpr int64_t kStride = 8 * kThreads;
   __shared__ float red[kThreads / 64];
-  const int64_t t = blockIdx.x;
   const float* row = x + t * cols;
   const int64_t runs = cols / 32;
   const int tid = threadIdx.x;
+  float4 held[kSteps][2];
   float mx = 0.0f;
-  for (int64_t e = 8 * tid; e < cols; e += 8 * kThreads) {
-    const float4 f0 = *reinterpret_cast<const float4*>(row + e);
-    const float4 f1 = *reinterpret_cast<const float4*>(row + e + 4);
-    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(f0.x), fabsf(f0.y)), fmaxf(fabsf(f0.z), fabsf(f0.w))));
-    mx = fmaxf(mx, fmaxf(fmaxf(fabsf(f1.x), fabsf(f1.y)), fmaxf(fabsf(f1.z), fabsf(f1.w))));
+  auto absmax8 = [](float m, const float4& f0, const float4& f1) {
+    m = fmaxf(m, fmaxf(fmaxf(fabsf(f0.x), fabsf(f0.y)), fmaxf(fabsf(f0.z), fabsf(f0.w))));
+    return fmaxf(m, fmaxf(fmaxf(fabsf(f1.x), fabsf(f1.y)), fmaxf(fabsf(f1.z), fabsf(f1.w))));
+  };
+  if (kU > 0) {
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) {
+      const int64_t e = 8 * tid + kStride * u;
+      held[u][0] = make_float4(0.f, 0.f, 0.f, 0.f);
+      held[u][1] = held[u][0];
+      if (e < cols) {
+        held[u][0] = *reinterpret_cast<const float4*>(row + e);
+        held[u][1] = *reinterpret_cast<const float4*>(row + e + 4);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) mx = absmax8(mx, held[u][0], held[u][1]);
+  } else {
+    for (int64_t e = 8 * tid; e < cols; e += kStride) {
+      mx = absmax8(mx, *reinterpret_cast<const float4*>(row + e), *reinterpret_cast<const float4*>(row + e + 4));
+    }
   }
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
@@ -174,12 +208,10 @@ __global__ __launch_bounds__(kThreads) void SplitActivationsKernel(const float* 
   }
   const float s = ldexpf(1.0f, e);
   const float ss = ldexpf(1.0f, e - kSumShift);
-  if (tid == 0) inv_scale[t] = ldexpf(1.0f, -e);
+  if (tid == 0) a.inv_scale[t] = ldexpf(1.0f, -e);
   // cols is a multiple of 32, so every group of four lanes walks whole runs
   // together and the shuffles below stay inside a run
-  for (int64_t c = 8 * tid; c < cols; c += 8 * kThreads) {
-    const float4 f0 = *reinterpret_cast<const float4*>(row + c);
-    const float4 f1 = *reinterpret_cast<const float4*>(row + c + 4);
+  auto split8 = [&](int64_t c, const float4& f0, const float4& f1) {
     const float v[8] = {f0.x, f0.y, f0.z, f0.w, f1.x, f1.y, f1.z, f1.w};
     F16x8 hi, lo;
     float sum = 0.0f;
@@ -203,7 +235,23 @@ __global__ __launch_bounds__(kThreads) void SplitActivationsKernel(const float* 
       sum_planes[si] = a;
       sum_planes[sum_elems + si] = static_cast<_Float16>(ys - static_cast<float>(a));
     }
+  };
+  if (kU > 0) {
+#pragma unroll
+    for (int u = 0; u < kSteps; ++u) {
+      const int64_t c = 8 * tid + kStride * u;
+      if (c < cols) split8(c, held[u][0], held[u][1]);
+    }
+  } else {
+    for (int64_t c = 8 * tid; c < cols; c += kStride) {
+      split8(c, *reinterpret_cast<const float4*>(row + c), *reinterpret_cast<const float4*>(row + c + 4));
+    }
   }
+}
+
+template <int kU>
+__global__ __launch_bounds__(kThreads) void SplitActivationsKernel(SplitArgs a) {
+  SplitRow<kU>(a, blockIdx.x);
 }
 
 // LDS image of the workgroup's operands: two buffers of activation planes
@@ -563,14 +611,27 @@ struct PlanesCfg {
 
 // One thread per (row, block, 32-column run j = 2 kc + hf): the 32 operands
 // StageChunk<kQ4> builds for chunk kc, half hf, at the same chunk columns.
+struct PlanesArgs {
+  const uint8_t* w;
+  int64_t rows;
+  int64_t row_bytes;
+  int32_t nb;
+  _Float16* planes;
+  float2* dd;
+  U32x4* mm;
+};
+
 template <uint32_t kType>
-__global__ __launch_bounds__(kThreads) void DecodeWeightPlanesKernel(const uint8_t* __restrict__ w, int64_t rows,
-                                                                      int64_t row_bytes, int32_t nb,
-                                                                      _Float16* __restrict__ planes,
-                                                                      float2* __restrict__ dd, U32x4* __restrict__ mm) {
+__device__ __forceinline__ void DecodeWeightUnit(const PlanesArgs& a, int64_t u) {
+  const uint8_t* __restrict__ w = a.w;
+  const int64_t rows = a.rows;
+  const int64_t row_bytes = a.row_bytes;
+  const int32_t nb = a.nb;
+  _Float16* __restrict__ planes = a.planes;
+  float2* __restrict__ dd = a.dd;
+  U32x4* __restrict__ mm = a.mm;
   constexpr bool kQ4 = kType == kGgmlQ4_K;
   constexpr int64_t kBB = kQ4 ? kQ4KBlockBytes : kQ6KBlockBytes;
-  const int64_t u = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
   if (u >= rows * nb * 8) return;
   const int j = static_cast<int>(u & 7);
   const int64_t rb = u >> 3;  // row * nb + block
@@ -633,6 +694,23 @@ __global__ __launch_bounds__(kThreads) void DecodeWeightPlanesKernel(const uint8
     }
     if (j == 0) dd[rb] = make_float2(HalfF(raw.hdr.x & 0xFFFFu), 0.0f);
   }
+}
+
+template <uint32_t kType>
+__global__ __launch_bounds__(kThreads) void DecodeWeightPlanesKernel(PlanesArgs a) {
+  DecodeWeightUnit<kType>(a, static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x);
+}
+
+// The activation split and a matrix's weight decode in one launch: workgroups
+// below n_split split token row blockIdx.x, the others decode weights, so the
+// two independent passes share the chip instead of following each other.
+template <uint32_t kType, int kU>
+__global__ __launch_bounds__(kThreads) void PrepareKernel(SplitArgs sa, int32_t n_split, PlanesArgs pa) {
+  if (static_cast<int32_t>(blockIdx.x) < n_split) {
+    SplitRow<kU>(sa, blockIdx.x);
+    return;
+  }
+  DecodeWeightUnit<kType>(pa, (static_cast<int64_t>(blockIdx.x) - n_split) * kThreads + threadIdx.x);
 }
 
 // Tiles are numbered row tile fastest (tile = token tile * row_tiles + row
@@ -1027,6 +1105,60 @@ constexpr int64_t kPlanesMinTokens = 512;
 constexpr size_t kPlanesMaxBytes = size_t{64} << 20;
 
 // OUT[:, 0 : rows) with row stride ldo for the `rows` weight rows at w.
+SplitArgs SplitArgsOf(const SplitActivations& sa) {
+  return SplitArgs{sa.x, sa.cols, sa.n_tokens * sa.cols, sa.sum_stride, static_cast<_Float16*>(sa.planes),
+                   static_cast<_Float16*>(sa.sums), sa.inv_scale};
+}
+
+// Register steps per thread of the split (a row of up to 5 steps, 10240
+// columns, stays in registers between its two passes; 0: wider rows).
+int SplitSteps(int64_t cols) {
+  const int64_t steps = (cols + 8 * kThreads - 1) / (8 * kThreads);
+  return steps <= 5 ? static_cast<int>(steps) : 0;
+}
+
+// Launches a pending split on its own.
+void LaunchPendingSplit(const SplitActivations& sa) {
+  if (!sa.pending) return;
+  sa.pending = false;
+  const SplitArgs a = SplitArgsOf(sa);
+  const dim3 grid(static_cast<unsigned>(sa.n_tokens)), block(kThreads);
+  switch (SplitSteps(sa.cols)) {
+    case 1: Launch("SplitActivationsKernel", SplitActivationsKernel<1>, grid, block, a); break;
+    case 2: Launch("SplitActivationsKernel", SplitActivationsKernel<2>, grid, block, a); break;
+    case 3: Launch("SplitActivationsKernel", SplitActivationsKernel<3>, grid, block, a); break;
+    case 4: Launch("SplitActivationsKernel", SplitActivationsKernel<4>, grid, block, a); break;
+    case 5: Launch("SplitActivationsKernel", SplitActivationsKernel<5>, grid, block, a); break;
+    default: Launch("SplitActivationsKernel", SplitActivationsKernel<0>, grid, block, a); break;
+  }
+}
+
+// The weight decode of one row slice, with a pending split in the same launch.
+template <uint32_t kType>
+void LaunchDecode(const PlanesArgs& pa, const SplitActivations& sa) {
+  const int64_t units = pa.rows * pa.nb * 8;
+  const unsigned decode_wgs = GridFor(units, kThreads);
+  if (!sa.pending) {
+    Launch(kType == kGgmlQ4_K ? "DecodeWeightPlanesQ4KKernel" : "DecodeWeightPlanesQ6KKernel",
+           DecodeWeightPlanesKernel<kType>, dim3(decode_wgs), dim3(kThreads), pa);
+    return;
+  }
+  sa.pending = false;
+  const SplitArgs a = SplitArgsOf(sa);
+  RPG_CHECK(sa.n_tokens + static_cast<int64_t>(decode_wgs) <= 0x7FFFFFFF, "split + decode grid too large");
+  const int32_t n_split = static_cast<int32_t>(sa.n_tokens);
+  const dim3 grid(static_cast<unsigned>(sa.n_tokens + decode_wgs)), block(kThreads);
+  const char* name = kType == kGgmlQ4_K ? "PrepareQ4KKernel" : "PrepareQ6KKernel";
+  switch (SplitSteps(sa.cols)) {
+    case 1: Launch(name, PrepareKernel<kType, 1>, grid, block, a, n_split, pa); break;
+    case 2: Launch(name, PrepareKernel<kType, 2>, grid, block, a, n_split, pa); break;
+    case 3: Launch(name, PrepareKernel<kType, 3>, grid, block, a, n_split, pa); break;
+    case 4: Launch(name, PrepareKernel<kType, 4>, grid, block, a, n_split, pa); break;
+    case 5: Launch(name, PrepareKernel<kType, 5>, grid, block, a, n_split, pa); break;
+    default: Launch(name, PrepareKernel<kType, 0>, grid, block, a, n_split, pa); break;
+  }
+}
+
 template <uint32_t kType>
 void LaunchPlanesRows(const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb, const SplitActivations& sa,
                       float* out, int64_t ldo) {
@@ -1040,10 +1172,7 @@ void LaunchPlanesRows(const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t
   _Float16* wplanes = reinterpret_cast<_Float16*>(base);
   float2* dd = reinterpret_cast<float2*>(base + dd_off);
   U32x4* mm = reinterpret_cast<U32x4*>(base + mm_off);
-  const int64_t units = rows * nb * 8;
-  Launch(kType == kGgmlQ4_K ? "DecodeWeightPlanesQ4KKernel" : "DecodeWeightPlanesQ6KKernel",
-         DecodeWeightPlanesKernel<kType>, dim3(GridFor(units, kThreads)), dim3(kThreads), w, rows, row_bytes, nb,
-         wplanes, dd, mm);
+  LaunchDecode<kType>(PlanesArgs{w, rows, row_bytes, nb, wplanes, dd, mm}, sa);
 
   const int64_t gy = (sa.n_tokens + kTileT - 1) / kTileT;
   const int64_t gx = (rows + C::kTileR - 1) / C::kTileR;
@@ -1131,8 +1260,8 @@ SplitActivations SplitForMfma(const float* x, int64_t n_tokens, int64_t cols) {
   sa.sum_stride = static_cast<int64_t>(sum_bytes / sizeof(_Float16));
   sa.n_tokens = n_tokens;
   sa.cols = cols;
-  Launch("SplitActivationsKernel", SplitActivationsKernel, dim3(static_cast<unsigned>(n_tokens)), dim3(kThreads), x,
-         cols, elems, sa.sum_stride, static_cast<_Float16*>(sa.planes), static_cast<_Float16*>(sa.sums), sa.inv_scale);
+  sa.x = x;
+  sa.pending = true;
   return sa;
 }
 
@@ -1161,6 +1290,7 @@ void LaunchMatMulMfmaSplit(uint32_t type, const uint8_t* w, int64_t rows, int64_
     }
     return;
   }
+  LaunchPendingSplit(sa);
   constexpr int64_t kFill = 256;
   const int64_t tiles = gx * gy;
   int64_t want = tiles >= kFill ? 1 : (kFill + tiles - 1) / tiles;

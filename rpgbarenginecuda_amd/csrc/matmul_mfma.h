@@ -17,9 +17,15 @@ struct SplitActivations {
   int64_t sum_stride = 0;       // fp16 elements between the two sum planes
   int64_t n_tokens = 0;
   int64_t cols = 0;
+  // The split is launched by the first GEMM launch that reads it (beside that
+  // matrix's weight decode when it takes the decoded-planes path); until then
+  // x must stay unchanged.
+  const float* x = nullptr;
+  mutable bool pending = false;
 };
 
-// Splits x [n_tokens][cols] fp32 (16-byte aligned, cols % 32 == 0).
+// Prepares the split of x [n_tokens][cols] fp32 (16-byte aligned, cols % 32 ==
+// 0) into the split buffer; the first LaunchMatMulMfmaSplit on it launches it.
 SplitActivations SplitForMfma(const float* x, int64_t n_tokens, int64_t cols);
 
 // OUT = X . W^T for one Q4_K / Q6_K matrix from split activations (cols =
