@@ -134,11 +134,12 @@ __device__ __forceinline__ void StoreStreamHalf4(uint16_t* p, uint2 v) {
 }
 
 // Write-through output stores for write-dominated kernels (the embedding
-// gather): a raw buffer store with the cache-policy bits sc0 | sc1 | nt, i.e.
+// gathers): a raw buffer store with the cache-policy bits sc0 | sc1 | nt, i.e.
 // system-scope write-through with the streaming hint, so the written lines are
 // not left dirty in the XCDs' L2s for the end-of-kernel release to flush.
 // Measured on MI355X: a 23 MB fill 4.45 us against 5.5-5.9 us with plain or
-// nontemporal global stores; the Q4_K gather at n = 2811 ~0.2 us faster. Every
+// nontemporal global stores; the Q4_K and Q6_K gathers at n = 2811 0.2-0.4 us
+// faster. Every
 // store instruction of a wave must cover whole 128-byte lines: with partial
 // lines the write-through path is several times slower. The buffer resource
 // bounds every store to `bytes` from `base` (out-of-range stores are dropped).
@@ -152,6 +153,19 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t OutResource(void* base, uint32
 __device__ __forceinline__ void StoreThrough4(__amdgpu_buffer_rsrc_t rs, uint32_t byte_off, float4 v) {
   const U32x4 w = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
   __builtin_amdgcn_raw_buffer_store_b128(w, rs, static_cast<int>(byte_off), 0, kStoreThroughPolicy);
+}
+
+// The device-scope form (sc1 | nt): the store is made coherent across the XCDs, so
+// it also writes through the XCD's L2, with the streaming hint. Used by SwiGLU's
+// output (207 MB at n = 2811): measured on MI355X in the layer's kernel order
+// (add + RMSNorm, q/k, SwiGLU over 28 rotated layers) 32.3-32.5 us against
+// 33.0-33.2 us with nontemporal global stores, and the add + RMSNorm launched after
+// it 0.05-0.1 us faster. Same whole-line rule as StoreThrough4.
+constexpr int kStoreDeviceThroughPolicy = 2 | 16;  // nt | sc1
+
+__device__ __forceinline__ void StoreDeviceThrough4(__amdgpu_buffer_rsrc_t rs, uint32_t byte_off, float4 v) {
+  const U32x4 w = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
+  __builtin_amdgcn_raw_buffer_store_b128(w, rs, static_cast<int>(byte_off), 0, kStoreDeviceThroughPolicy);
 }
 
 // SwiGLU element (src/kernels_gpu.cu:868): silu(g) * u = (g / (1 + e^-g)) * u,

@@ -19,10 +19,10 @@
 //     half*128 + 32*quarter + 4kq. Q6_K blocks are 210 bytes, so a block start is
 //     only 2-byte aligned; loads are 16-bit.
 // Every lane ends with float4 stores, so a wave writes 2 KiB (Q4_K) or 4 KiB (Q6_K)
-// of fp32 as full 128-byte lines. The one-workgroup-per-token Q4_K gather stores
-// them write-through (dev::StoreThrough4, measured faster for this
-// write-dominated kernel); Q6_K and the flat block kernel keep nontemporal
-// global stores (write-through measured slower for the Q6_K lane layout).
+// of fp32 as full 128-byte lines. The one-workgroup-per-token gathers store them
+// write-through (dev::StoreThrough4, measured faster for these write-dominated
+// kernels: Q4_K 4.5-4.8 vs 4.9-5.7 us, Q6_K 4.75-5.0 vs 4.95-5.25 us at n = 2811);
+// the flat block kernel keeps nontemporal global stores.
 #include <hip/hip_runtime.h>
 
 #include "dev_util.h"
@@ -122,7 +122,7 @@ struct QuantTraits;
 template <>
 struct QuantTraits<kGgmlQ4_K> {
   static constexpr int kLanes = 32;
-  static constexpr bool kStoreThrough = true;  // measured faster at n = 2811 (~5.0 vs ~5.3 us)
+  static constexpr bool kStoreThrough = true;  // measured faster at n = 2811 (~4.6 vs ~5.0 us)
   static constexpr int64_t kBytes = kQ4KBlockBytes;
   template <typename Put>
   __device__ static void Decode(const uint8_t* blk, int j, const Put& put) { DecodeQ4KLane(blk, j, put); }
@@ -138,7 +138,7 @@ struct QuantTraits<kGgmlQ4_K> {
 template <>
 struct QuantTraits<kGgmlQ6_K> {
   static constexpr int kLanes = 16;
-  static constexpr bool kStoreThrough = false;  // write-through measured slower here (5.7-6.3 vs ~5.4 us)
+  static constexpr bool kStoreThrough = true;  // ~0.2 us faster at n = 2811 with launches queued back to back
   static constexpr int64_t kBytes = kQ6KBlockBytes;
   template <typename Put>
   __device__ static void Decode(const uint8_t* blk, int j, const Put& put) { DecodeQ6KLane(blk, j, put); }

