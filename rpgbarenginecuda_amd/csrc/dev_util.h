@@ -163,10 +163,26 @@ __device__ __forceinline__ void StoreThrough4(__amdgpu_buffer_rsrc_t rs, uint32_
 // it 0.05-0.1 us faster. Same whole-line rule as StoreThrough4.
 constexpr int kStoreDeviceThroughPolicy = 2 | 16;  // nt | sc1
 
-__device__ __forceinline__ void StoreDeviceThrough4(__amdgpu_buffer_rsrc_t rs, uint32_t byte_off, float4 v) {
+// 16-byte buffer stores with an explicit cache policy (sc0 = 1, nt = 2, sc1 = 16).
+template <int kPolicy>
+__device__ __forceinline__ void StoreBuf4(__amdgpu_buffer_rsrc_t rs, uint32_t byte_off, float4 v) {
   const U32x4 w = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z), __float_as_uint(v.w)};
-  __builtin_amdgcn_raw_buffer_store_b128(w, rs, static_cast<int>(byte_off), 0, kStoreDeviceThroughPolicy);
+  __builtin_amdgcn_raw_buffer_store_b128(w, rs, static_cast<int>(byte_off), 0, kPolicy);
 }
+template <int kPolicy>
+__device__ __forceinline__ void StoreBufU4(__amdgpu_buffer_rsrc_t rs, uint32_t byte_off, uint4 v) {
+  const U32x4 w = {v.x, v.y, v.z, v.w};
+  __builtin_amdgcn_raw_buffer_store_b128(w, rs, static_cast<int>(byte_off), 0, kPolicy);
+}
+
+__device__ __forceinline__ void StoreDeviceThrough4(__amdgpu_buffer_rsrc_t rs, uint32_t byte_off, float4 v) {
+  StoreBuf4<kStoreDeviceThroughPolicy>(rs, byte_off, v);
+}
+
+// No cache-policy bits: an ordinary write-back store, for buffer stores that want
+// the default policy (the fp16 KV-cache rows of the fused q/k kernel; the
+// streaming hint on those scattered 256-byte rows made the kernel ~5% slower).
+constexpr int kStorePlainPolicy = 0;
 
 // SwiGLU element (src/kernels_gpu.cu:868): silu(g) * u = (g / (1 + e^-g)) * u,
 // IEEE division. Shared by SiluMulKernel and the gate / up matvec that applies

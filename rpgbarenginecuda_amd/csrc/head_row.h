@@ -45,6 +45,17 @@ __device__ __forceinline__ void StoreHeadRowStream(float* p, int l, const HeadRo
   }
 }
 
+// The same fp32 row through a buffer resource: `off` is the byte offset of the
+// row's first element in rs, and every store carries the cache policy kPolicy.
+template <int kPolicy>
+__device__ __forceinline__ void StoreHeadRowBuf(__amdgpu_buffer_rsrc_t rs, uint32_t off, int l, const HeadRow& r) {
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    StoreBuf4<kPolicy>(rs, off + 4u * HeadOffset(l, c), r.a[c]);
+    StoreBuf4<kPolicy>(rs, off + 4u * (64 + HeadOffset(l, c)), r.b[c]);
+  }
+}
+
 // Swap one dword between the lanes of each even/odd pair (DPP quad_perm [1,0,3,2]).
 __device__ __forceinline__ uint32_t SwapLanePair(uint32_t x) {
   return static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(x), 0xB1, 0xF, 0xF, false));
@@ -57,18 +68,29 @@ __device__ __forceinline__ uint32_t SwapLanePair(uint32_t x) {
 // then covers whole 128-byte lines. Both lanes of a pair must be active (the
 // callers' conditions are uniform over the 8 lanes of a row). Plain stores:
 // nontemporal ones measured no faster for these scattered 256-byte cache rows.
-__device__ __forceinline__ void StoreHeadRowHalf(uint16_t* p, int l, const HeadRow& r) {
+template <typename Put>
+__device__ __forceinline__ void HeadRowHalfChunks(int l, const HeadRow& r, const Put& put) {
   const bool odd = (l & 1) != 0;
-  uint16_t* dst = p + (odd ? 32 + 8 * (l >> 1) : 8 * (l >> 1));
+  const int e0 = odd ? 32 + 8 * (l >> 1) : 8 * (l >> 1);
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     const uint2 c0 = PackHalf4(s == 0 ? r.a[0] : r.b[0]);
     const uint2 c1 = PackHalf4(s == 0 ? r.a[1] : r.b[1]);
     const uint2 send = odd ? c0 : c1;
     const uint2 recv = make_uint2(SwapLanePair(send.x), SwapLanePair(send.y));
-    *reinterpret_cast<uint4*>(dst + 64 * s) =
-        odd ? make_uint4(recv.x, recv.y, c1.x, c1.y) : make_uint4(c0.x, c0.y, recv.x, recv.y);
+    put(e0 + 64 * s, odd ? make_uint4(recv.x, recv.y, c1.x, c1.y) : make_uint4(c0.x, c0.y, recv.x, recv.y));
   }
+}
+
+__device__ __forceinline__ void StoreHeadRowHalf(uint16_t* p, int l, const HeadRow& r) {
+  HeadRowHalfChunks(l, r, [p](int e, uint4 v) { *reinterpret_cast<uint4*>(p + e) = v; });
+}
+
+// The same fp16 row through a buffer resource (`off` = byte offset of the row in rs),
+// every store with the cache policy kPolicy.
+template <int kPolicy>
+__device__ __forceinline__ void StoreHeadRowHalfBuf(__amdgpu_buffer_rsrc_t rs, uint32_t off, int l, const HeadRow& r) {
+  HeadRowHalfChunks(l, r, [rs, off](int e, uint4 v) { StoreBufU4<kPolicy>(rs, off + 2u * e, v); });
 }
 
 // Per-lane share of a 128-element vector read from cache (weights, RoPE rows).

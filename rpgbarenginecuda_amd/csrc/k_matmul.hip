@@ -470,6 +470,21 @@ __device__ __forceinline__ int SegOf(const MatSegs& sg, int64_t r) {
   return (r >= sg.end[0]) + (r >= sg.end[1]) + (r >= sg.end[2]);
 }
 
+// a[i] through selects over constant indices. Indexing the kernel-argument
+// arrays with a runtime i makes the compiler issue one more scalar load that
+// waits for i; with constant indices every field is fetched in the kernel's first
+// batch of argument loads, so the first weight load waits on one round trip
+// instead of a chain of four or five.
+template <typename T>
+__device__ __forceinline__ T PickSeg(const T (&a)[kMaxSegs], int i) {
+  static_assert(kMaxSegs == 4, "PickSeg selects among four segments");
+  return i == 0 ? a[0] : i == 1 ? a[1] : i == 2 ? a[2] : a[3];
+}
+// First global row of segment i (0 for the first segment).
+__device__ __forceinline__ int64_t SegFirst(const MatSegs& sg, int i) {
+  return i == 0 ? 0 : i == 1 ? sg.end[0] : i == 2 ? sg.end[1] : sg.end[2];
+}
+
 // Each lane keeps the activations of its NX block groups in registers (rows of
 // up to 8 * NX blocks; used for NX == 1). Rows run over all segments; a row
 // group of RI rows never straddles two (segment sizes are multiples of RI).
@@ -489,7 +504,7 @@ __device__ __forceinline__ int SegOf(const MatSegs& sg, int64_t r) {
 // another order than GpuAddRmsNorm's, so the scale can differ from it in the
 // last bit of the double sum.
 template <uint32_t kType, int NX, int RI, bool kPaired = false, uint32_t kTypeB = kType, bool kNorm = false>
-__global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int32_t n_seg, int64_t row_bytes, int32_t nb,
+__global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_t rows, int64_t row_bytes, int32_t nb,
                                                               const float* __restrict__ x, NormPrologue nrm) {
   static_assert(!kNorm || NX == 1, "the norm prologue needs the whole row in one wave");
   constexpr int64_t kBB = BlockBytesOf<kType>::value;
@@ -498,13 +513,21 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int32_
   const int lane = threadIdx.x & 63;
   const int c = lane / kGroupLanes;
   const int s = lane % kGroupLanes;
-  const int64_t rows = sg.end[n_seg - 1];
+  // Every kernel argument the first activation and weight loads depend on, fetched
+  // in one batch: the empty asm takes them as scalar inputs (it emits nothing), so
+  // the compiler issues their loads together at entry instead of one at a time
+  // next to each use, where each waited for the one before (4-5 serial scalar
+  // round trips before the first weight load).
+  asm volatile("" ::"s"(sg.w[0]), "s"(sg.w[1]), "s"(sg.w[2]), "s"(sg.w[3]), "s"(sg.end[0]), "s"(sg.end[1]),
+               "s"(sg.end[2]), "s"(rows), "s"(row_bytes), "s"(nb), "s"(x));
 
   // Row bookkeeping is uniform over the wave: keep it in scalar registers.
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kWavesPerBlock * RI;
   int64_t r0 = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(
                    static_cast<int>(blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6)))) * RI;
-  if (!kNorm && r0 >= rows) return;
+  // No early exit for waves past the last row: a branch here would keep the
+  // compiler from fetching the remaining kernel arguments in the first batch. Such
+  // waves load in-bounds (clamped) bytes below and skip the row loop.
 
   float xv[NX][32];
   float sx[NX][2];
@@ -605,8 +628,8 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int32_
       return;
     }
     const int sgi = SegOf(sg, base_row);
-    const uint8_t* wseg = sg.w[sgi];
-    const int64_t first = sgi == 0 ? 0 : sg.end[sgi - 1];
+    const uint8_t* wseg = PickSeg(sg.w, sgi);
+    const int64_t first = SegFirst(sg, sgi);
     if (kMixed && ((sg.b_mask >> sgi) & 1u)) {
 #pragma unroll
       for (int r = 0; r < RI; ++r) {
@@ -656,8 +679,8 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int32_
     } else {
       const int rr = ReducedRow<RI>(lane);
       const int sgi = SegOf(sg, r0);
-      const int64_t first = sgi == 0 ? 0 : sg.end[sgi - 1];
-      if ((lane & 15) == 0 && lane < 16 * RI && r0 + rr < rows) sg.out[sgi][r0 - first + rr] = total;
+      const int64_t first = SegFirst(sg, sgi);
+      if ((lane & 15) == 0 && lane < 16 * RI && r0 + rr < rows) PickSeg(sg.out, sgi)[r0 - first + rr] = total;
     }
 #pragma unroll
     for (int r = 0; r < RI; ++r)
@@ -682,6 +705,8 @@ __global__ __launch_bounds__(64 * WS) void MatVecSplitKernel(const uint8_t* __re
   const int q = threadIdx.x >> 6;
   const int c = lane / kGroupLanes;
   const int s = lane % kGroupLanes;
+  // The kernel arguments in one batch at entry (see MatVecQuantKernel).
+  asm volatile("" ::"s"(w), "s"(rows), "s"(row_bytes), "s"(nb), "s"(x), "s"(out));
   const int64_t stride = static_cast<int64_t>(gridDim.x) * RI;
   int64_t r0 = static_cast<int64_t>(blockIdx.x) * RI;  // uniform over the workgroup
 
@@ -795,12 +820,12 @@ void LaunchDecodeSegs(const char* name, const MatSegs& sg, int32_t n_seg, int64_
   const int64_t need = (rows + kWavesPerBlock * RI - 1) / (kWavesPerBlock * RI);
   const unsigned grid = static_cast<unsigned>(need < kDecodeGrid ? need : kDecodeGrid);
   if (nrm != nullptr) {
-    Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB, true>, dim3(grid), dim3(kMmBlock), sg, n_seg,
+    Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB, true>, dim3(grid), dim3(kMmBlock), sg, rows,
            row_bytes, nb, x, *nrm);
     nrm->x_out = nullptr;
     return;
   }
-  Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB>, dim3(grid), dim3(kMmBlock), sg, n_seg, row_bytes, nb,
+  Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB>, dim3(grid), dim3(kMmBlock), sg, rows, row_bytes, nb,
          x, NormPrologue{});
 }
 
