@@ -34,8 +34,12 @@ bool Aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 using dev::SiluMul;
 
-// The output goes out through a buffer resource bounded to the block's own span of
-// gate (kBlock float4 at most), with device-scope write-through stores.
+// kThrough: the output goes out through a buffer resource bounded to the block's
+// own span of gate (kBlock float4 at most), with device-scope write-through stores;
+// otherwise with nontemporal global stores. Write-through pays off on prefill-sized
+// launches and costs latency on a few blocks (decode at n = 1: 2.2 against 1.9 us),
+// so the launcher picks it by size.
+template <bool kThrough>
 __global__ __launch_bounds__(kBlock) void SiluMulKernel(float* gate, const float* __restrict__ up, int64_t n4,
                                                         int64_t n) {
   const int64_t first = static_cast<int64_t>(blockIdx.x) * kBlock;
@@ -43,10 +47,13 @@ __global__ __launch_bounds__(kBlock) void SiluMulKernel(float* gate, const float
   if (i < n4) {
     const float4 g = LoadStream4(gate + 4 * i);
     const float4 u = LoadStream4(up + 4 * i);
-    const int64_t span = n4 - first < kBlock ? n4 - first : kBlock;
-    const auto rs = dev::OutResource(gate + 4 * first, static_cast<uint32_t>(16 * span));
-    dev::StoreDeviceThrough4(rs, 16u * threadIdx.x,
-                             make_float4(SiluMul(g.x, u.x), SiluMul(g.y, u.y), SiluMul(g.z, u.z), SiluMul(g.w, u.w)));
+    const float4 y = make_float4(SiluMul(g.x, u.x), SiluMul(g.y, u.y), SiluMul(g.z, u.z), SiluMul(g.w, u.w));
+    if constexpr (kThrough) {
+      const int64_t span = n4 - first < kBlock ? n4 - first : kBlock;
+      dev::StoreDeviceThrough4(dev::OutResource(gate + 4 * first, static_cast<uint32_t>(16 * span)), 16u * threadIdx.x, y);
+    } else {
+      StoreStream4(gate + 4 * i, y);
+    }
   }
   if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
     const int64_t j = 4 * n4 + threadIdx.x;
@@ -94,6 +101,11 @@ __global__ __launch_bounds__(kFillBlock) void StreamFillKernel(float* __restrict
   if (i < n16) StoreStream4(dst + 4 * i, make_float4(value, value, value, value));
 }
 
+// Write-through output stores from this many elements up (64 blocks of kBlock
+// float4): below it the launch is latency-bound and the write-through
+// acknowledgement only lengthens it.
+constexpr int64_t kThroughMinElems = int64_t{64} * kBlock * 4;
+
 // Blocks for the vector kernels: at least one, so block 0 exists for the tail.
 unsigned VecGrid(int64_t n4) { return n4 > 0 ? GridFor(n4, kBlock) : 1u; }
 
@@ -108,7 +120,8 @@ void GpuSiluMulInPlace(float* gate_dev, const float* up_dev, int64_t n) {
   if (n <= 0) return;
   RPG_CHECK(gate_dev != nullptr && up_dev != nullptr, "SiluMul got a null pointer");
   if (Aligned16(gate_dev) && Aligned16(up_dev)) {
-    Launch("SiluMulKernel", SiluMulKernel, dim3(VecGrid(n / 4)), dim3(kBlock), gate_dev, up_dev, n / 4, n);
+    Launch("SiluMulKernel", n >= kThroughMinElems ? SiluMulKernel<true> : SiluMulKernel<false>, dim3(VecGrid(n / 4)),
+           dim3(kBlock), gate_dev, up_dev, n / 4, n);
   } else {
     Launch("SiluMulScalarKernel", SiluMulScalarKernel, dim3(ScalarGrid(n)), dim3(kBlock), gate_dev, up_dev, n);
   }
