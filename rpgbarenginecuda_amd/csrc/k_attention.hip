@@ -20,7 +20,8 @@
 //     shapes one wave per query head (AttnChunkKernel);
 //   * prefill (many (t, h) pairs) uses a single chunk per pair and writes the
 //     normalised output directly; decode (few pairs) splits the keys into up to
-//     kMaxChunks chunks so the whole chip streams the cache, each chunk storing
+//     kMaxChunks (kMaxGroupChunks for the grouped decode kernel) chunks so the
+//     whole chip streams the cache, each chunk storing
 //     (m, l, o) to a partials buffer that a second kernel merges;
 //   * the partials buffer is library-owned and grows on demand;
 //     GpuAttentionWarmupShmem(max positions) sizes it before a graph capture,
@@ -48,6 +49,9 @@ constexpr int kD = 128;          // head_dim of the fast path
 constexpr int kBlockThreads = 256;
 constexpr int kWaves = kBlockThreads / 64;
 constexpr int kMaxChunks = 64;
+// The grouped decode kernel splits the keys finer: up to 128 chunks of 32 keys,
+// one 32-key slab per wave at the decode positions that fill the chip.
+constexpr int kMaxGroupChunks = 128;
 constexpr int kPartFloats = kD + 4;  // o[128], m, l, 2 unused: 16-byte aligned rows for the float4 accesses
 constexpr int64_t kFaMinTokens = 64;  // prefill calls with at least this many tokens run on the matrix cores
 constexpr int64_t kFaMaxPartialFloats = int64_t{64} << 20;  // 256 MiB of prefill key-chunk partials at most
@@ -91,39 +95,6 @@ __device__ __forceinline__ float WaveSumF(float v) {
 
 __device__ __forceinline__ float HalfToF(uint32_t bits) {
   return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(bits)));
-}
-
-// Merges the chunks of one (t, h): M = max m_c, L = sum l_c e^(m_c - M),
-// out = sum o_c e^(m_c - M) / L. Lane c holds chunk c's (m, l) and weight; the
-// partial outputs are read 16 chunks at a time (lane l owns dims 2l, 2l + 1).
-// n_chunks <= 64.
-__device__ __forceinline__ void MergeChunks(const float* pp, int32_t n_chunks, int lane, float* ot) {
-  const bool has = lane < n_chunks;
-  const float mc = has ? pp[lane * kPartFloats + kD] : -INFINITY;
-  const float lc = has ? pp[lane * kPartFloats + kD + 1] : 0.0f;
-  const float mx = WaveMax(mc);
-  const float f = mc == -INFINITY ? 0.0f : expf(mc - mx);
-  const float L = WaveSumF(lc * f);
-  float o0 = 0.0f, o1 = 0.0f;
-  for (int c0 = 0; c0 < n_chunks; c0 += 16) {
-    float2 v[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int c = c0 + i < n_chunks ? c0 + i : n_chunks - 1;  // clamped: its weight is used only if c0 + i < n
-      v[i] = *reinterpret_cast<const float2*>(pp + c * kPartFloats + 2 * lane);
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float fc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), c0 + i));
-      if (c0 + i < n_chunks) {
-        o0 = __builtin_fmaf(v[i].x, fc, o0);
-        o1 = __builtin_fmaf(v[i].y, fc, o1);
-      }
-    }
-  }
-  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-  ot[2 * lane] = o0 * inv;
-  ot[2 * lane + 1] = o1 * inv;
 }
 
 // Key / value rows: the fp16 cache ([kv head][position][d], 16-bit bits) or
@@ -267,19 +238,67 @@ __global__ __launch_bounds__(kBlockThreads) void AttnChunkKernel(
   }
 }
 
-// One wave per (t, h): merges its n_chunks partials into out. (A merge by the
-// last chunk to arrive would save this launch, but its device-scope release
-// fence writes the whole L2 back once per chunk, which costs more.)
+// One workgroup per (t, h) merges its n_chunks partials (n_chunks <= 128) into
+// out: M = max m_c, L = sum l_c e^(m_c - M), out = sum o_c e^(m_c - M) / L. Every
+// wave forms M and L itself (lane c holds chunks c and c + 64, summed in the same
+// order in each wave); the chunks' outputs are split over the waves in groups of
+// 16 (wave w takes groups w, w + 4, ...; lane l owns dims 2l, 2l + 1), so the
+// workgroup's loads are in flight together, and the waves' sums meet in LDS,
+// added in wave order. (A merge by the last chunk to arrive would save this
+// launch, but its device-scope release fence writes the whole L2 back once per
+// chunk, which costs more.)
 __global__ __launch_bounds__(kBlockThreads) void AttnMergeKernel(const float* __restrict__ part, int64_t pairs,
                                                                   int32_t n_chunks, int32_t n_heads, int64_t chunk_len,
                                                                   int64_t pos0_val, const int64_t* __restrict__ pos0_dev,
                                                                   float* __restrict__ out) {
+  __shared__ float2 osum[kWaves][64];
   const int lane = threadIdx.x & 63;
-  const int64_t th = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
-  if (th >= pairs) return;
+  const int w = threadIdx.x >> 6;
+  const int64_t th = blockIdx.x;
+  if (th >= pairs) return;  // uniform over the workgroup
   const int32_t live = LiveChunks(ReadPos0(pos0_val, pos0_dev) + th / n_heads, chunk_len, n_chunks);
-  if (live == 1) return;  // the chunk kernel wrote the output
-  MergeChunks(part + th * n_chunks * kPartFloats, live, lane, out + th * kD);
+  if (live == 1) return;  // the chunk kernel wrote the output (uniform over the workgroup)
+  const float* pp = part + th * n_chunks * kPartFloats;
+  const bool has0 = lane < live;
+  const bool has1 = lane + 64 < live;
+  const float m0 = has0 ? pp[lane * kPartFloats + kD] : -INFINITY;
+  const float l0 = has0 ? pp[lane * kPartFloats + kD + 1] : 0.0f;
+  const float m1 = has1 ? pp[(lane + 64) * kPartFloats + kD] : -INFINITY;
+  const float l1 = has1 ? pp[(lane + 64) * kPartFloats + kD + 1] : 0.0f;
+  const float mx = WaveMax(fmaxf(m0, m1));
+  const float f0 = m0 == -INFINITY ? 0.0f : expf(m0 - mx);
+  const float f1 = m1 == -INFINITY ? 0.0f : expf(m1 - mx);
+  const float L = WaveSumF(l0 * f0 + l1 * f1);
+  float o0 = 0.0f, o1 = 0.0f;
+  for (int c0 = 16 * w; c0 < live; c0 += 16 * kWaves) {
+    float2 v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int c = c0 + i < live ? c0 + i : live - 1;  // clamped: its weight is used only if c0 + i < live
+      v[i] = *reinterpret_cast<const float2*>(pp + c * kPartFloats + 2 * lane);
+    }
+    const float fset = c0 < 64 ? f0 : f1;  // a group of 16 lies in one set
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float fc = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(fset), (c0 + i) & 63));
+      if (c0 + i < live) {
+        o0 = __builtin_fmaf(v[i].x, fc, o0);
+        o1 = __builtin_fmaf(v[i].y, fc, o1);
+      }
+    }
+  }
+  osum[w][lane] = make_float2(o0, o1);
+  __syncthreads();
+  if (w != 0) return;
+  float2 acc = osum[0][lane];
+#pragma unroll
+  for (int q = 1; q < kWaves; ++q) {
+    acc.x += osum[q][lane].x;
+    acc.y += osum[q][lane].y;
+  }
+  const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+  out[th * kD + 2 * lane] = acc.x * inv;
+  out[th * kD + 2 * lane + 1] = acc.y * inv;
 }
 
 // The merge of prefill key chunks (many pairs, few chunks): 32 threads per
@@ -465,7 +484,7 @@ __global__ __launch_bounds__(kBlockThreads) void AttnDecodeGroupKernel(
   for (int64_t base = lo; base < hi; base += 32) {
     uint4 kn[8], vn[8];
     if (kPipe) {
-      load_slab(base + 32, kn, vn);  // past hi: clamped rows, not used
+      if (base + 32 < hi) load_slab(base + 32, kn, vn);  // uniform: the chunk's last slab prefetches nothing
       __builtin_amdgcn_sched_barrier(0);  // keep the next slab's loads ahead of this slab's scores
     } else {
       load_slab(base, kw, vw);
@@ -1016,7 +1035,7 @@ void PlanGroupChunks(int64_t units, int64_t positions, int32_t* n_chunks, int64_
     return;
   }
   int64_t want = (2048 + units - 1) / units;
-  if (want > kMaxChunks) want = kMaxChunks;
+  if (want > kMaxGroupChunks) want = kMaxGroupChunks;
   int64_t len = (positions + want - 1) / want;
   len = (len + 31) / 32 * 32;
   *chunk_len = len;
@@ -1024,8 +1043,8 @@ void PlanGroupChunks(int64_t units, int64_t positions, int32_t* n_chunks, int64_
 }
 
 // Partials needed by any decode-sized call (seq 1, up to 64 heads, at most
-// kMaxChunks chunks): what a captured decode graph may replay.
-size_t WarmupFloats(int64_t /*positions*/) { return static_cast<size_t>(64) * kMaxChunks * kPartFloats; }
+// kMaxGroupChunks chunks): what a captured decode graph may replay.
+size_t WarmupFloats(int64_t /*positions*/) { return static_cast<size_t>(64) * kMaxGroupChunks * kPartFloats; }
 
 template <int G>
 void LaunchDecodeGroup(const ModelMeta& c, const Pos0Arg& p0, const float* q_dev, int64_t seq,
@@ -1049,7 +1068,7 @@ void LaunchDecodeGroup(const ModelMeta& c, const Pos0Arg& p0, const float* q_dev
            chunk_len, out_dev, part, DecodePrep{});
   }
   if (n_chunks > 1) {
-    Launch("AttnMergeKernel", AttnMergeKernel, dim3(GridFor(pairs, kWaves)), dim3(kBlockThreads), part, pairs,
+    Launch("AttnMergeKernel", AttnMergeKernel, dim3(static_cast<unsigned>(pairs)), dim3(kBlockThreads), part, pairs,
            n_chunks, c.n_heads, chunk_len, p0.value, p0.dev, out_dev);
   }
 }
@@ -1159,7 +1178,7 @@ void AttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev, in
          k_layer, v_layer, max_seq * kD, static_cast<int64_t>(kD), max_seq, c.n_heads, c.n_heads / c.n_kv_heads,
          scale, p0.value, p0.dev, seq, n_chunks, chunk_len, out_dev, part);
   if (n_chunks > 1) {
-    Launch("AttnMergeKernel", AttnMergeKernel, dim3(GridFor(pairs, kWaves)), dim3(kBlockThreads), part, pairs,
+    Launch("AttnMergeKernel", AttnMergeKernel, dim3(static_cast<unsigned>(pairs)), dim3(kBlockThreads), part, pairs,
            n_chunks, c.n_heads, chunk_len, p0.value, p0.dev, out_dev);
   }
 }
@@ -1235,7 +1254,7 @@ void GpuCausalAttention(const ModelMeta& c, const float* q_dev, const float* k_d
          k_dev, v_dev, static_cast<int64_t>(kD), row, seq, c.n_heads, c.n_heads / c.n_kv_heads, scale,
          static_cast<int64_t>(0), static_cast<const int64_t*>(nullptr), seq, n_chunks, chunk_len, out_dev, part);
   if (n_chunks > 1) {
-    Launch("AttnMergeKernel", AttnMergeKernel, dim3(GridFor(pairs, kWaves)), dim3(kBlockThreads), part, pairs,
+    Launch("AttnMergeKernel", AttnMergeKernel, dim3(static_cast<unsigned>(pairs)), dim3(kBlockThreads), part, pairs,
            n_chunks, c.n_heads, chunk_len, static_cast<int64_t>(0), static_cast<const int64_t*>(nullptr), out_dev);
   }
 }

@@ -284,6 +284,9 @@ QK_CASES = [
     ("1.7B prefill n=2811", 16, 8, 2811, 0),
     ("4B prefill n=4096 (fills cache)", 32, 8, 4096, 0),
     ("1.7B continuation", 16, 8, 300, 3796),
+    # the launcher switches to buffer stores from 64 tokens on: both sides of that line
+    ("1.7B n=63 (global stores)", 16, 8, 63, 17),
+    ("1.7B n=64 (buffer stores)", 16, 8, 64, 4032),
 ]
 
 
@@ -399,7 +402,9 @@ def test_qk_norm_rope_kv_unaligned_cache_base(gpu, ora, cache_off):
 
 
 @pytest.mark.parametrize("n,off", [(21 * 6144, 0), (2811 * 6144, 0), (6144, 0), (1, 0), (1001, 0), (1003, 1),
-                                   (4096 * 9728, 0)])
+                                   (4096 * 9728, 0),
+                                   # write-through stores from 131072 elements on; the last block partial
+                                   (131071, 0), (131072, 0), (131072 + 2050, 0), (262147, 1)])
 def test_silu_mul(gpu, ora, n, off):
     import torch
 
