@@ -527,7 +527,8 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_
                    static_cast<int>(blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6)))) * RI;
   // No early exit for waves past the last row: a branch here would keep the
   // compiler from fetching the remaining kernel arguments in the first batch. Such
-  // waves load in-bounds (clamped) bytes below and skip the row loop.
+  // waves load the last row's bytes (the load below clamps the row) and skip the
+  // row loop.
 
   float xv[NX][32];
   float sx[NX][2];
@@ -627,13 +628,17 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_
       }
       return;
     }
-    const int sgi = SegOf(sg, base_row);
+    // base_row is clamped before the segment lookup: past the last row the lookup
+    // would name an unused (null) segment, and the row offset from its first row
+    // would be negative.
+    const int64_t br = base_row < rows ? base_row : rows - 1;
+    const int sgi = SegOf(sg, br);
     const uint8_t* wseg = PickSeg(sg.w, sgi);
     const int64_t first = SegFirst(sg, sgi);
     if (kMixed && ((sg.b_mask >> sgi) & 1u)) {
 #pragma unroll
       for (int r = 0; r < RI; ++r) {
-        const int64_t row = base_row + r < rows ? base_row + r : rows - 1;
+        const int64_t row = br + r < rows ? br + r : rows - 1;
         const uint8_t* rp = wseg + (row - first) * sg.row_bytes_b;
 #pragma unroll
         for (int it = 0; it < NX; ++it) lb[r][it] = LoadLaneBytes<kTypeB>(rp + lane_off_b[it], s);
@@ -642,7 +647,7 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_
     }
 #pragma unroll
     for (int r = 0; r < RI; ++r) {
-      const int64_t row = base_row + r < rows ? base_row + r : rows - 1;
+      const int64_t row = br + r < rows ? br + r : rows - 1;
       const uint8_t* rp = wseg + (row - first) * row_bytes;
 #pragma unroll
       for (int it = 0; it < NX; ++it) lb[r][it] = LoadLaneBytes<kType>(rp + lane_off[it], s);
