@@ -87,6 +87,48 @@ def hold_launches(torch, n_launches, host_us_per_launch=40.0):
     torch.cuda._sleep(int((100.0 + host_us_per_launch * n_launches) * _SPIN["cycles_per_us"]))
 
 
+def back_to_back_us(torch, ops, launch, n=100, trials=3):
+    """Per-launch GPU time of `launch(i)` run n times back to back: the n launches are
+    captured into one HIP graph (on the library's stream), and the graph's replays
+    are timed with stream events (best of `trials`). This is the cost of one more
+    launch in a graph-replayed decode loop. Dispatch-attached events put a floor of
+    ~4 us under any kernel, and launches issued one by one from Python are bound by
+    the host (~3.3 us each), so neither shows the difference between two short
+    kernels. `launch` must not allocate or stage anything (it is captured)."""
+    for i in range(8):
+        launch(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        with ops.ScopedEngineStream(st):
+            g.capture_begin()
+            for i in range(n):
+                launch(i)
+            g.capture_end()
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    best = float("inf")
+    for _ in range(trials):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        best = min(best, a.elapsed_time(b) * 1e3 / n)
+    del g
+    return best
+
+
+def launch_floor_us(torch, ops):
+    """The same for a one-workgroup kernel (a 4 KiB fill): what any launch in a graph costs."""
+    buf = torch.empty(1024, dtype=torch.float32, device="cuda")
+    return back_to_back_us(torch, ops, lambda i: ops.GpuStreamFill(buf, 4096, 0), n=200)
+
+
 class Layer:
     """One layer's device buffers (all distinct per layer)."""
 
@@ -401,21 +443,28 @@ def measure_matmul_decode(torch, ops, reps=20, span=768 << 20):
         kname, k = next(iter(rep.items()))
         nbytes = wbytes + 4 * cols + 4 * rows
         us = k["avg_us"]
+        b2b = back_to_back_us(torch, ops, lambda i: ops.GpuMatMulQuant(mats[i % copies], x, 1, out))
         res[name] = {"type": "Q4_K" if t == 12 else "Q6_K", "rows": rows, "cols": cols, "us": round(us, 2),
                      "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
                      "pct_peak": round(nbytes / (us * 1e-6) / 1e9 / PEAK_GBPS * 100, 1), "kernel": kname,
-                     "bytes": nbytes}
+                     "bytes": nbytes, "us_back_to_back": round(b2b, 2),
+                     "GBps_back_to_back": round(nbytes / (b2b * 1e-6) / 1e9, 1)}
         if name != OUTPUT_MATRIX[0]:
             layer_us += us
         del blob, blocks, mats, x, out
         torch.cuda.empty_cache()
     token_us = LAYERS * layer_us + res[OUTPUT_MATRIX[0]]["us"]
     grouped = measure_matmul_decode_grouped(torch, ops, reps, span)
-    return {"matrices": res, "layer_us": round(layer_us, 2), "token_matmul_us": round(token_us, 1),
+    return {"matrices": res, "launch_floor_us_back_to_back": round(launch_floor_us(torch, ops), 2),
+            "layer_us": round(layer_us, 2), "token_matmul_us": round(token_us, 1),
             "grouped": grouped,
             "token_matmul_us_grouped": round(LAYERS * grouped["layer_us"] + res[OUTPUT_MATRIX[0]]["us"], 1),
             "note": "n = 1, Qwen3-1.7B Q4_K_M layout; token_matmul_us = 28 layers + output projection, "
-                    "matmuls only; _grouped = with q/k and gate/up fused per layer (GpuMatMulQuantGroup)"}
+                    "matmuls only; _grouped = with q/k and gate/up fused per layer (GpuMatMulQuantGroup); "
+                    "us: dispatch-attached events (a ~4 us floor under any kernel); us_back_to_back: 100 "
+                    "launches captured in one HIP graph, replays timed with stream events (the per-launch "
+                    "cost in a graph-replayed decode loop), beside launch_floor_us_back_to_back for a "
+                    "one-workgroup kernel"}
 
 
 def measure_matmul_decode_grouped(torch, ops, reps, span):
