@@ -144,6 +144,25 @@ __device__ __forceinline__ LaneBytes LoadLaneBytes(const uint8_t* __restrict__ b
 // Byte k of a word as an exact float (v_cvt_f32_ubyte{0..3}).
 __device__ __forceinline__ float UByteF(uint32_t w, int k) { return static_cast<float>((w >> (8 * k)) & 0xFFu); }
 
+// The four bytes of a word whose bytes are all below 16 (4-bit quants), as the
+// exact floats q * 2^-9, two per instruction (v_cvt_pk_f32_fp8): gfx950 reads a
+// byte as an OCP FP8 E4M3 value, whose subnormals are m * 2^-9 (m = 0..7) and
+// whose smallest binade is (8 + m) * 2^-9, so every byte 0..15 is q * 2^-9
+// (checked on the device for all sixteen). The caller scales the block factor by
+// 2^9 instead, which is exact, so each product and sum is the unscaled one times
+// 2^-9: the same roundings, hence the same bits, as with q itself, except where
+// a partial sum would fall below 2^-126 (activations of magnitude < ~2^-117).
+typedef float F32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ void NibblesF(uint32_t w, float (&f)[4]) {
+  const F32x2 a = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), false);
+  const F32x2 b = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(w), true);
+  f[0] = a.x;
+  f[1] = a.y;
+  f[2] = b.x;
+  f[3] = b.y;
+}
+constexpr float kNibbleScale = 512.0f;  // 2^9: undoes NibblesF's factor
+
 // Hides a packed-quant word's known-zero bits from the optimiser, which would
 // otherwise extract each field with a bit-field extract and then convert it (two
 // instructions per weight) instead of converting the byte directly (one). Emits
@@ -173,19 +192,21 @@ __device__ __forceinline__ void DecodeLane(const LaneBytes& r, int s, float (&wv
     uint32_t sc0, m0, sc1, m1;
     ScaleMinK4(2 * g, r.a.y, r.a.z, r.a.w, &sc0, &m0);
     ScaleMinK4(2 * g + 1, r.a.y, r.a.z, r.a.w, &sc1, &m1);
-    const float d1 = d * static_cast<float>(sc0);
+    // (d * sc * 2^9) * (q * 2^-9) is the exact d * sc * q inside the fma
+    const float d1 = (d * static_cast<float>(sc0)) * kNibbleScale;
     const float n1 = -(dmin * static_cast<float>(m0));
-    const float d2 = d * static_cast<float>(sc1);
+    const float d2 = (d * static_cast<float>(sc1)) * kNibbleScale;
     const float n2 = -(dmin * static_cast<float>(m1));
     const uint32_t qw[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const uint32_t lo = Opaque(qw[k] & 0x0F0F0F0Fu);
-      const uint32_t hi = Opaque((qw[k] >> 4) & 0x0F0F0F0Fu);
+      float lo[4], hi[4];
+      NibblesF(qw[k] & 0x0F0F0F0Fu, lo);
+      NibblesF((qw[k] >> 4) & 0x0F0F0F0Fu, hi);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        wv[4 * k + j] = __builtin_fmaf(d1, UByteF(lo, j), n1);
-        wv[16 + 4 * k + j] = __builtin_fmaf(d2, UByteF(hi, j), n2);
+        wv[4 * k + j] = __builtin_fmaf(d1, lo[j], n1);
+        wv[16 + 4 * k + j] = __builtin_fmaf(d2, hi[j], n2);
       }
     }
   } else {
@@ -388,20 +409,22 @@ __device__ __forceinline__ float BlockDot(const LaneBytes& r, int s, const float
     ScaleMinK4(2 * g, r.a.y, r.a.z, r.a.w, &sc0, &m0);
     ScaleMinK4(2 * g + 1, r.a.y, r.a.z, r.a.w, &sc1, &m1);
     const uint32_t qw[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
-    float slo = 0.0f, shi = 0.0f;
+    float slo = 0.0f, shi = 0.0f;  // 2^-9 sum(q x) of the two runs
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const uint32_t lo = Opaque(qw[k] & 0x0F0F0F0Fu);
-      const uint32_t hi = Opaque((qw[k] >> 4) & 0x0F0F0F0Fu);
+      float lo[4], hi[4];
+      NibblesF(qw[k] & 0x0F0F0F0Fu, lo);
+      NibblesF((qw[k] >> 4) & 0x0F0F0F0Fu, hi);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        slo = __builtin_fmaf(UByteF(lo, j), xv[4 * k + j], slo);
-        shi = __builtin_fmaf(UByteF(hi, j), xv[16 + 4 * k + j], shi);
+        slo = __builtin_fmaf(lo[j], xv[4 * k + j], slo);
+        shi = __builtin_fmaf(hi[j], xv[16 + 4 * k + j], shi);
       }
     }
-    float acc = (d * static_cast<float>(sc0)) * slo;
+    const float d9 = d * kNibbleScale;
+    float acc = (d9 * static_cast<float>(sc0)) * slo;
     acc = __builtin_fmaf(-(dmin * static_cast<float>(m0)), sx[0], acc);
-    acc = __builtin_fmaf(d * static_cast<float>(sc1), shi, acc);
+    acc = __builtin_fmaf(d9 * static_cast<float>(sc1), shi, acc);
     return __builtin_fmaf(-(dmin * static_cast<float>(m1)), sx[1], acc);
   } else {
     const int is = (s & 3) >> 1;
