@@ -163,7 +163,8 @@ def layer_bytes(n, shape):
 
 
 OP_NAMES = ("add_rms_norm", "qk_norm_rope_kv", "swiglu")
-KERNEL_NAMES = {"add_rms_norm": "AddRmsNormRowBlockKernel", "qk_norm_rope_kv": "QkNormRopeKvKernel",
+# the kernels the n = 2811 prefill launches (add + RMSNorm: the persistent form, two or more rows per workgroup)
+KERNEL_NAMES = {"add_rms_norm": "AddRmsNormRowsKernel", "qk_norm_rope_kv": "QkNormRopeKvKernel",
                 "swiglu": "SiluMulKernel"}
 
 

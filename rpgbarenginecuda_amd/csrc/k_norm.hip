@@ -13,13 +13,17 @@
 //     them), so each load instruction of a wave covers 1 KiB of the row; the
 //     activations stream with nontemporal hints, the weight row stays cached.
 //     Measured at n = 2811 x 2048 over 28 rotated layers: 5.5 TB/s for the fused
-//     add+norm vs 4.1 TB/s for a wave-per-row layout with plain accesses.
+//     add+norm vs 4.1 TB/s for a wave-per-row layout with plain accesses. The
+//     fused add+norm with at least two rows per workgroup of a four-per-CU grid
+//     runs persistent (AddRmsNormRowsKernel), the next row's loads in flight.
 //   * rows with n % 256 == 0 otherwise: one wave64 per row, V = n/256 float4 per lane.
 //   * head rows (n = 128): 8 lanes per row with the layout of head_row.h (the
 //     one the RoPE fusion needs), 3-step butterfly, shared with the fused kernel.
 //   * anything else (odd n, unaligned rows): a 256-thread block per row, two
 //     passes, the second re-reading the row from cache.
 #include <hip/hip_runtime.h>
+
+#include <atomic>
 
 #include "dev_util.h"
 #include "head_row.h"
@@ -94,6 +98,62 @@ __global__ __launch_bounds__(kRowBlock) void AddRmsNormRowBlockKernel(float* x, 
 #pragma unroll
   for (int c = 0; c < U; ++c) {
     StoreStream4(out + base + 4 * kRowBlock * c, ScaleMul(v[c], scale, Load4(wr + 4 * kRowBlock * c)));
+  }
+}
+
+// The same rows with a persistent grid of four workgroups per CU for prefill-sized
+// launches: workgroup b takes rows b, b + G, ... (G = gridDim.x) and requests the
+// next row's x and d before it stores and reduces the current one, so each
+// workgroup's writes overlap its next reads; the weight row stays in registers.
+// Every row goes through the same operations in the same order as in
+// AddRmsNormRowBlockKernel (bit-identical). Measured in the prefill chain at
+// n = 2811 (28 rotated layers): 16.03-16.05 against 16.26-16.27 us; grids that
+// give the CUs unequal workgroup counts (896, 1152, 1408) took 17.3-17.7 us.
+template <int U>
+__global__ __launch_bounds__(kRowBlock) void AddRmsNormRowsKernel(float* x, const float* __restrict__ d,
+                                                                  const float* __restrict__ w, int64_t n_rows,
+                                                                  float eps, float* __restrict__ out) {
+  constexpr int kN = 4 * kRowBlock * U;
+  // wave partials, alternating between two slots: a wave writes slot p of row i + 2
+  // only after the barrier of row i + 1, which the other wave reaches after it has
+  // read slot p of row i
+  __shared__ double part[2][kRowBlock / 64];
+  const int tid = threadIdx.x;
+  float4 wv[U], a[U], b[U];
+#pragma unroll
+  for (int c = 0; c < U; ++c) wv[c] = Load4(w + 4 * tid + 4 * kRowBlock * c);
+  int64_t row = blockIdx.x;  // < n_rows: the grid never exceeds the rows
+#pragma unroll
+  for (int c = 0; c < U; ++c) {
+    a[c] = LoadStream4(x + row * kN + 4 * tid + 4 * kRowBlock * c);
+    b[c] = LoadStream4(d + row * kN + 4 * tid + 4 * kRowBlock * c);
+  }
+  int slot = 0;
+  for (; row < n_rows; row += gridDim.x) {
+    float4 v[U];
+#pragma unroll
+    for (int c = 0; c < U; ++c) v[c] = make_float4(a[c].x + b[c].x, a[c].y + b[c].y, a[c].z + b[c].z, a[c].w + b[c].w);
+    const int64_t next = row + gridDim.x;
+    if (next < n_rows) {  // uniform over the workgroup
+#pragma unroll
+      for (int c = 0; c < U; ++c) {
+        a[c] = LoadStream4(x + next * kN + 4 * tid + 4 * kRowBlock * c);
+        b[c] = LoadStream4(d + next * kN + 4 * tid + 4 * kRowBlock * c);
+      }
+    }
+    const int64_t base = row * kN + 4 * tid;
+#pragma unroll
+    for (int c = 0; c < U; ++c) StoreStream4(x + base + 4 * kRowBlock * c, v[c]);
+    double ss = 0.0;
+#pragma unroll
+    for (int c = 0; c < U; ++c) ss = AddSquares(ss, v[c]);
+    ss = dev::WaveSum(ss);
+    if ((tid & 63) == 0) part[slot][tid >> 6] = ss;
+    __syncthreads();
+    const float scale = RmsScale(part[slot][0] + part[slot][1], kN, eps);
+    slot ^= 1;
+#pragma unroll
+    for (int c = 0; c < U; ++c) StoreStream4(out + base + 4 * kRowBlock * c, ScaleMul(v[c], scale, wv[c]));
   }
 }
 
@@ -235,10 +295,38 @@ struct RmsNormRowBlockLauncher {
   }
 };
 
+// Compute units of the current device, queried once per device.
+int CurrentDeviceCUs() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cached[kMaxDevices];  // 0: not queried yet
+  int dev = 0;
+  RPG_HIP_CHECK(hipGetDevice(&dev));
+  int cus = dev >= 0 && dev < kMaxDevices ? cached[dev].load(std::memory_order_relaxed) : 0;
+  if (cus == 0) {
+    RPG_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    RPG_CHECK(cus > 0, "device %d reports %d compute units", dev, cus);
+    if (dev >= 0 && dev < kMaxDevices) cached[dev].store(cus, std::memory_order_relaxed);
+  }
+  return cus;
+}
+
+// AddRmsNormRowsKernel takes launches with at least two rows per workgroup of its
+// grid (four workgroups per CU); smaller ones run one workgroup per row.
+constexpr int kRowsBlocksPerCu = 4;
+constexpr int64_t kRowsMinRows = 2048;  // below this no device needs the CU count
+
 template <int U>
 struct AddRmsNormRowBlockLauncher {
   static void Run(float* x, const float* d, const float* w, int64_t n_rows, float eps, float* out) {
     RPG_CHECK(n_rows <= 0x7FFFFFFF, "too many rows: %lld", static_cast<long long>(n_rows));
+    if (n_rows >= kRowsMinRows) {
+      const int64_t grid = int64_t{kRowsBlocksPerCu} * CurrentDeviceCUs();
+      if (n_rows >= 2 * grid) {
+        Launch("AddRmsNormRowsKernel", AddRmsNormRowsKernel<U>, dim3(static_cast<unsigned>(grid)), dim3(kRowBlock), x,
+               d, w, n_rows, eps, out);
+        return;
+      }
+    }
     Launch("AddRmsNormRowBlockKernel", AddRmsNormRowBlockKernel<U>, dim3(static_cast<unsigned>(n_rows)),
            dim3(kRowBlock), x, d, w, eps, out);
   }
