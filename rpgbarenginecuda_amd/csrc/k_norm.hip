@@ -313,7 +313,7 @@ int CurrentDeviceCUs() {
 // AddRmsNormRowsKernel takes launches with at least two rows per workgroup of its
 // grid (four workgroups per CU); smaller ones run one workgroup per row.
 constexpr int kRowsBlocksPerCu = 4;
-constexpr int64_t kRowsMinRows = 2048;  // below this no device needs the CU count
+constexpr int64_t kRowsMinRows = 2048;  // smaller launches skip the CU query (MI355X: 2 x 4 x 256 = 2048)
 
 template <int U>
 struct AddRmsNormRowBlockLauncher {
