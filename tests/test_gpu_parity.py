@@ -257,9 +257,9 @@ def test_add_rms_norm(gpu, ora, rows, n):
 def test_add_rms_norm_persistent_equals_row_blocks(gpu, ora, rows, n):
     """Launches of at least two rows per workgroup of a four-per-CU grid run the
     persistent kernel (the next row's loads in flight); smaller launches run one
-    workgroup per row. The same rows in one launch and in slices of 1000 rows must
-    give the same bits (2049 rows: one workgroup of a 1024 grid takes three rows,
-    the others two)."""
+    workgroup per row. The same rows in one launch and in slices of 1000 and of 50
+    rows must give the same bits (2049 rows: one workgroup of a 1024 grid takes three
+    rows, the others two)."""
     import torch
 
     case(f"add_rms_norm persistent rows={rows} n={n}")
@@ -276,14 +276,15 @@ def test_add_rms_norm_persistent_equals_row_blocks(gpu, ora, rows, n):
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     if rows >= 2 * 4 * cus:
         assert "AddRmsNormRowsKernel" in gpu.profile_report()
-    xb = dev(x)
-    hb = torch.empty_like(xb)
-    for r0 in range(0, rows, 1000):
-        r1 = min(rows, r0 + 1000)
-        gpu.GpuAddRmsNorm(xb[r0:r1], dd[r0:r1], wd, r1 - r0, n, EPS, hb[r0:r1])
     assert np.array_equal(bits(host(xa)), bits(x + d))
-    assert np.array_equal(bits(host(xa)), bits(host(xb)))
-    assert np.array_equal(bits(host(ha)), bits(host(hb)))
+    for step in (1000, 50):  # one workgroup per row
+        xb = dev(x)
+        hb = torch.empty_like(xb)
+        for r0 in range(0, rows, step):
+            r1 = min(rows, r0 + step)
+            gpu.GpuAddRmsNorm(xb[r0:r1], dd[r0:r1], wd, r1 - r0, n, EPS, hb[r0:r1])
+        assert np.array_equal(bits(host(xa)), bits(host(xb))), step
+        assert np.array_equal(bits(host(ha)), bits(host(hb))), step
     ok, err = within(host(ha), ora.rms_norm_f64(x + d, w, rows, n, n, EPS))
     assert ok, err
 
