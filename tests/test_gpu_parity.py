@@ -253,7 +253,7 @@ def test_add_rms_norm(gpu, ora, rows, n):
     assert ok, err
 
 
-@pytest.mark.parametrize("rows,n", [(2811, 2048), (4096, 2560), (2049, 4096)])
+@pytest.mark.parametrize("rows,n", [(2811, 2048), (4096, 2560), (2049, 4096), (2048, 2048), (2100, 512), (2300, 3072)])
 def test_add_rms_norm_persistent_equals_row_blocks(gpu, ora, rows, n):
     """Launches of at least two rows per workgroup of a four-per-CU grid run the
     persistent kernel (the next row's loads in flight); smaller launches run one
