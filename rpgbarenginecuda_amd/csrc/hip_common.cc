@@ -13,18 +13,18 @@
 namespace rpg {
 
 void ThrowHipError(hipError_t err, const char* expr, const char* file, int line) {
-  Throw("HIP call failed: %s (%d)\n  expression: %s\n  at: %s:%d", hipGetErrorString(err),
-        static_cast<int>(err), expr, file, line);
+  Throw("%s:%d: %s returned %s (HIP error %d)", file, line, expr, hipGetErrorString(err), static_cast<int>(err));
 }
 
 void CheckLaunch(const char* what) {
   const hipError_t e = hipGetLastError();
-  if (e != hipSuccess) Throw("kernel launch failed (%s): %s", what, hipGetErrorString(e));
+  if (e != hipSuccess) Throw("%s: the kernel launch reported %s", what, hipGetErrorString(e));
 }
 
 unsigned GridFor(int64_t n, int threads) {
   const int64_t g = (n + threads - 1) / threads;
-  RPG_CHECK(g > 0 && g <= 0x7FFFFFFF, "grid dimension out of range: %lld", static_cast<long long>(g));
+  RPG_CHECK(g > 0 && g <= 0x7FFFFFFF, "launch grid of %lld workgroups does not fit a grid dimension",
+            static_cast<long long>(g));
   return static_cast<unsigned>(g);
 }
 
@@ -104,7 +104,7 @@ DeviceBuffer DeviceBuffer::View(void* p, size_t bytes) {
 }
 
 void DeviceBuffer::Alloc(size_t bytes) {
-  RPG_CHECK(bytes > 0, "DeviceBuffer::Alloc got 0 bytes");
+  RPG_CHECK(bytes > 0, "DeviceBuffer: refusing a zero-byte allocation");
   Free();
   RPG_HIP_CHECK(hipMalloc(&ptr_, bytes));
   bytes_ = bytes;

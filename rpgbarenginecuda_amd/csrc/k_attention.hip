@@ -1077,8 +1077,8 @@ void LaunchDecodeGroup(const ModelMeta& c, const Pos0Arg& p0, const float* q_dev
 void AttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev, int64_t seq, const uint16_t* k_layer,
                         const uint16_t* v_layer, int64_t max_seq, float* out_dev, int64_t sh_positions,
                         const PartialsSink& sink) {
-  RPG_CHECK(seq > 0, "attention seq must be positive");
-  RPG_CHECK(pos0 >= 0, "pos0 must not be negative");
+  RPG_CHECK(seq > 0, "attention: the query batch is empty (seq <= 0)");
+  RPG_CHECK(pos0 >= 0, "attention: a negative start position");
   RPG_CHECK(c.n_heads > 0 && c.n_kv_heads > 0 && c.n_heads % c.n_kv_heads == 0,
             "n_heads (%d) must be a positive multiple of n_kv_heads (%d)", c.n_heads, c.n_kv_heads);
   RPG_CHECK(c.head_dim == kD, "attention supports head_dim %d (got %d)", kD, c.head_dim);
@@ -1205,10 +1205,10 @@ bool GpuQkNormRopeKvAttention(const ModelMeta& c, int64_t pos0, const float* q_d
                               const float* v_dev, const float* q_norm, const float* k_norm, const float* rope_tab,
                               int64_t rope_rows, uint16_t* k_layer, uint16_t* v_layer, int64_t max_seq,
                               float* out_dev, int64_t sh_positions) {
-  RPG_CHECK(pos0 >= 0, "pos0 must not be negative");
+  RPG_CHECK(pos0 >= 0, "attention: a negative start position");
   RPG_CHECK(c.n_heads > 0 && c.n_kv_heads > 0 && c.n_heads % c.n_kv_heads == 0,
             "n_heads (%d) must be a positive multiple of n_kv_heads (%d)", c.n_heads, c.n_kv_heads);
-  RPG_CHECK(pos0 + 1 <= max_seq, "position %lld exceeds the cache capacity %lld", static_cast<long long>(pos0),
+  RPG_CHECK(pos0 + 1 <= max_seq, "attention: position %lld has no slot in a cache of %lld positions", static_cast<long long>(pos0),
             static_cast<long long>(max_seq));
   RPG_CHECK(pos0 + 1 <= rope_rows, "position %lld exceeds the RoPE table (%lld rows)", static_cast<long long>(pos0),
             static_cast<long long>(rope_rows));
@@ -1234,7 +1234,7 @@ bool GpuQkNormRopeKvAttention(const ModelMeta& c, int64_t pos0, const float* q_d
 
 void GpuCausalAttention(const ModelMeta& c, const float* q_dev, const float* k_dev, const float* v_dev, int64_t seq,
                         float* out_dev) {
-  RPG_CHECK(seq > 0, "attention seq must be positive");
+  RPG_CHECK(seq > 0, "attention: the query batch is empty (seq <= 0)");
   RPG_CHECK(c.n_heads > 0 && c.n_kv_heads > 0 && c.n_heads % c.n_kv_heads == 0,
             "n_heads (%d) must be a positive multiple of n_kv_heads (%d)", c.n_heads, c.n_kv_heads);
   RPG_CHECK(c.head_dim == kD, "attention supports head_dim %d (got %d)", kD, c.head_dim);
@@ -1260,7 +1260,7 @@ void GpuCausalAttention(const ModelMeta& c, const float* q_dev, const float* k_d
 }
 
 void GpuAttentionWarmupShmem(int64_t sh_positions) {
-  RPG_CHECK(sh_positions > 0, "sh_positions must be positive (got %lld)", static_cast<long long>(sh_positions));
+  RPG_CHECK(sh_positions > 0, "attention warmup: the position budget has to be at least 1 (got %lld)", static_cast<long long>(sh_positions));
   EnsurePartials(WarmupFloats(sh_positions));
 }
 

@@ -310,7 +310,7 @@ void LaunchGather(uint32_t type, const uint8_t* emb, int64_t rows, int64_t cols,
 
 void GpuDequantRow(uint32_t type, const uint8_t* src_dev, int64_t n_elems, float* dst_dev) {
   const BlockShape bs = DeviceBlockShape(type);
-  RPG_CHECK(n_elems > 0 && n_elems % bs.elems == 0, "dequant length %lld is not a multiple of the block size %d",
+  RPG_CHECK(n_elems > 0 && n_elems % bs.elems == 0, "dequant: %lld elements do not fill whole blocks of %d",
             static_cast<long long>(n_elems), bs.elems);
   RPG_CHECK(src_dev != nullptr && dst_dev != nullptr, "DequantRow got a null pointer");
   LaunchGather(type, src_dev, 1, n_elems, nullptr, 1, dst_dev);

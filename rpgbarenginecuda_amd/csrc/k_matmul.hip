@@ -948,9 +948,9 @@ void GpuMatMulQuantRaw(uint32_t type, const uint8_t* w_dev, int64_t rows, int64_
                        int64_t n_tokens, float* out_dev) {
   RPG_CHECK(rows > 0 && cols > 0, "invalid MatMulQuant shape [%lld, %lld]", static_cast<long long>(rows),
             static_cast<long long>(cols));
-  RPG_CHECK(n_tokens > 0, "n_tokens must be positive");
+  RPG_CHECK(n_tokens > 0, "matmul: no tokens (n_tokens <= 0)");
   const BlockShape bs = DeviceBlockShape(type);
-  RPG_CHECK(cols % bs.elems == 0, "dot length %lld is not a multiple of the block size %d",
+  RPG_CHECK(cols % bs.elems == 0, "matmul: %lld columns do not fill whole blocks of %d",
             static_cast<long long>(cols), bs.elems);
   RPG_CHECK(w_dev != nullptr && x_dev != nullptr && out_dev != nullptr, "MatMulQuant got a null pointer");
   const int64_t row_bytes = TypeRowBytes(type, cols);
@@ -1162,7 +1162,7 @@ void GpuMatMulQuantSwiGLU(const GpuTensor& w_gate, const GpuTensor& w_up, const 
   RPG_CHECK(w_gate.rows == w_up.rows && w_gate.cols == w_up.cols,
             "gate [%lld, %lld] and up [%lld, %lld] must have the same shape", static_cast<long long>(w_gate.rows),
             static_cast<long long>(w_gate.cols), static_cast<long long>(w_up.rows), static_cast<long long>(w_up.cols));
-  RPG_CHECK(n_tokens > 0, "n_tokens must be positive");
+  RPG_CHECK(n_tokens > 0, "matmul: no tokens (n_tokens <= 0)");
   RPG_CHECK(x_dev != nullptr && gate_dev != nullptr && up_dev != nullptr, "GpuMatMulQuantSwiGLU got a null pointer");
   if (!g_force_generic.load() && SwiGLUDecodeEligible(w_gate, w_up, x_dev, n_tokens)) {
     DecodeSwiGLU(w_gate, w_up, x_dev, gate_dev, nullptr);
@@ -1199,7 +1199,7 @@ bool GpuNormMatMulQuantSwiGLU(const GpuNormIn& in, const GpuTensor& w_gate, cons
 }
 
 void GpuMatMulQuant(const GpuTensor& w, const float* X_dev, int64_t n_tokens, float* OUT_dev) {
-  RPG_CHECK(w.matrix, "GpuMatMulQuant got a non-matrix tensor (%s)", w.type_name());
+  RPG_CHECK(w.matrix, "GpuMatMulQuant: the %s weight tensor is not a 2-D matrix", w.type_name());
   RPG_CHECK(w.valid(), "GpuMatMulQuant got an empty tensor");
   RPG_CHECK(w.buf.size() == static_cast<size_t>(w.rows * w.row_bytes()),
             "tensor byte count does not match the [%lld, %lld] shape", static_cast<long long>(w.rows),

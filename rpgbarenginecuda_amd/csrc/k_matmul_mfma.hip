@@ -1079,7 +1079,8 @@ SplitBuffer& WeightPlanes() {
 }
 
 // Grow-only buffer of the decoded weight planes: an outgrown buffer is retired,
-// not freed, as for the split buffer; sized to the request (the largest is one
+// not freed, as for the split buffer, and it grows at least twofold, so a
+// forward's growing matrix shapes retire few buffers (the largest request is one
 // 64 MB slice of planes plus its block values).
 void* EnsureWeightPlanes(size_t bytes) {
   SplitBuffer& b = WeightPlanes();
@@ -1089,10 +1090,11 @@ void* EnsureWeightPlanes(size_t bytes) {
               "the prefill matmul needs a %zu-byte weight-plane buffer (have %zu), which cannot be allocated during "
               "graph capture; run the same shape once before capturing",
               bytes, b.bytes);
+    const size_t grow = bytes > 2 * b.bytes ? bytes : 2 * b.bytes;
     void* p = nullptr;
-    RPG_HIP_CHECK(hipMalloc(&p, bytes));
+    RPG_HIP_CHECK(hipMalloc(&p, grow));
     b.ptr = p;  // the previous buffer stays allocated
-    b.bytes = bytes;
+    b.bytes = grow;
   }
   return b.ptr;
 }

@@ -352,7 +352,7 @@ struct AddRmsNormWaveLauncher {
 
 void GpuRmsNorm(const float* x, const float* w, int64_t n_rows, int64_t n, int64_t stride, float eps,
                 float* out) {
-  RPG_CHECK(n > 0 && n_rows > 0 && stride >= n, "invalid RmsNorm arguments");
+  RPG_CHECK(n > 0 && n_rows > 0 && stride >= n, "RMSNorm: n and n_rows have to be positive and stride at least n");
   RPG_CHECK(x != nullptr && w != nullptr && out != nullptr, "RmsNorm got a null pointer");
   const bool vec_ok = Aligned16(x) && Aligned16(w) && Aligned16(out) && stride % 4 == 0;
   if (vec_ok && n == 128) {

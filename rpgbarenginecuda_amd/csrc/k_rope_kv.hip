@@ -212,7 +212,7 @@ __global__ __launch_bounds__(kBlock) void QkNormRopeKvKernel(
 }  // namespace
 
 void GpuRope(float* x, int32_t n_heads, int32_t head_dim, const float* rope_tab, int64_t pos0, int64_t n_rows) {
-  RPG_CHECK(head_dim > 0 && head_dim % 2 == 0, "head_dim %d must be even (RoPE pairs half-dimensions)", head_dim);
+  RPG_CHECK(head_dim > 0 && head_dim % 2 == 0, "RoPE rotates pairs (i, i + head_dim/2), so head_dim has to be even and positive (got %d)", head_dim);
   RPG_CHECK(n_heads > 0 && n_rows >= 0, "invalid Rope arguments");
   RPG_CHECK(pos0 >= 0, "RoPE position %lld must not be negative", static_cast<long long>(pos0));
   if (n_rows == 0) return;
@@ -231,9 +231,9 @@ void GpuRope(float* x, int32_t n_heads, int32_t head_dim, const float* rope_tab,
 
 void GpuKvWrite(const float* k_dev, const float* v_dev, int32_t n_kv_heads, int32_t head_dim, int64_t pos0,
                 int64_t seq, uint16_t* k_cache_layer, uint16_t* v_cache_layer, int64_t max_seq) {
-  RPG_CHECK(seq > 0 && n_kv_heads > 0 && head_dim > 0, "invalid KvWrite arguments");
-  RPG_CHECK(pos0 >= 0, "write position %lld must not be negative", static_cast<long long>(pos0));
-  RPG_CHECK(pos0 + seq <= max_seq, "write range [%lld, %lld) exceeds the cache capacity %lld",
+  RPG_CHECK(seq > 0 && n_kv_heads > 0 && head_dim > 0, "KV write: seq, n_kv_heads and head_dim have to be positive");
+  RPG_CHECK(pos0 >= 0, "KV write: start position %lld is negative", static_cast<long long>(pos0));
+  RPG_CHECK(pos0 + seq <= max_seq, "KV write: positions [%lld, %lld) run past the %lld cache slots",
             static_cast<long long>(pos0), static_cast<long long>(pos0 + seq), static_cast<long long>(max_seq));
   RPG_CHECK(k_dev != nullptr && v_dev != nullptr && k_cache_layer != nullptr && v_cache_layer != nullptr,
             "KvWrite got a null pointer");
@@ -256,8 +256,8 @@ void GpuQkNormRopeKv(float* q, float* k, const float* v, const float* q_norm, co
                      bool write_k_f32) {
   RPG_CHECK(seq > 0 && n_heads > 0 && n_kv_heads > 0 && head_dim > 0, "invalid QkNormRopeKv arguments");
   RPG_CHECK(head_dim % 2 == 0, "head_dim %d must be even", head_dim);
-  RPG_CHECK(pos0 >= 0, "write position %lld must not be negative", static_cast<long long>(pos0));
-  RPG_CHECK(pos0 + seq <= max_seq, "write range [%lld, %lld) exceeds the cache capacity %lld",
+  RPG_CHECK(pos0 >= 0, "KV write: start position %lld is negative", static_cast<long long>(pos0));
+  RPG_CHECK(pos0 + seq <= max_seq, "KV write: positions [%lld, %lld) run past the %lld cache slots",
             static_cast<long long>(pos0), static_cast<long long>(pos0 + seq), static_cast<long long>(max_seq));
   RPG_CHECK(pos0 + seq <= rope_rows, "positions [%lld, %lld) exceed the RoPE table (%lld rows)",
             static_cast<long long>(pos0), static_cast<long long>(pos0 + seq), static_cast<long long>(rope_rows));

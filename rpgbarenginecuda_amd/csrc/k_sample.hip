@@ -809,7 +809,7 @@ SampleScratch* Scratch() {
 }
 
 void CheckVocab(int64_t n) {
-  RPG_CHECK(n > 0, "the sampling vocab size must be positive (got %lld)", static_cast<long long>(n));
+  RPG_CHECK(n > 0, "sampler: empty vocabulary (n = %lld)", static_cast<long long>(n));
   RPG_CHECK(n <= kSamplerMaxVocab, "vocab size %lld exceeds the device sampler's limit %lld",
             static_cast<long long>(n), static_cast<long long>(kSamplerMaxVocab));
 }
@@ -844,7 +844,7 @@ void LaunchFilter(const float* logits, int64_t n, const SampleOptions& opt, floa
 }
 
 void CheckBuffers(const void* a, const void* b) {
-  RPG_CHECK(a != nullptr && b != nullptr, "the sampling buffer must not be null");
+  RPG_CHECK(a != nullptr && b != nullptr, "sampler: a probability buffer is null");
 }
 
 }  // namespace
@@ -874,7 +874,7 @@ void GpuFilterToProbs(const float* logits_dev, int64_t n, const SampleOptions& o
 void GpuInverseSample(const float* probs_dev, int64_t n, float u, int32_t* out_idx_dev) {
   CheckBuffers(probs_dev, out_idx_dev);
   CheckVocab(n);
-  RPG_CHECK(u >= 0.0f && u < 1.0f, "u must be in [0,1), got %g", static_cast<double>(u));
+  RPG_CHECK(u >= 0.0f && u < 1.0f, "inverse sampling needs a uniform draw in [0, 1), got %g", static_cast<double>(u));
   RPG_CHECK(!StreamIsCapturing(),
             "GpuInverseSample takes u from the host and is therefore not capturable; use GpuSampleTokenDev inside a "
             "graph");
@@ -891,7 +891,7 @@ void GpuSampleToken(const float* logits_dev, int64_t n, const SampleOptions& opt
     return;
   }
   CheckBuffers(logits_dev, out_idx_dev);
-  RPG_CHECK(probs_dev != nullptr, "the sampling buffer must not be null");
+  RPG_CHECK(probs_dev != nullptr, "sampler: a probability buffer is null");
   CheckVocab(n);
   RPG_CHECK(!StreamIsCapturing(),
             "GpuSampleToken takes the counter from the host and is therefore not capturable; use GpuSampleTokenDev "
@@ -908,9 +908,9 @@ void GpuSampleTokenDev(const float* logits_dev, int64_t n, const SampleOptions& 
     GpuArgMax(logits_dev, n, out_idx_dev);
     return;
   }
-  RPG_CHECK(counter_dev != nullptr, "the device-side counter must not be null");
+  RPG_CHECK(counter_dev != nullptr, "sampler: counter_dev is null");
   CheckBuffers(logits_dev, out_idx_dev);
-  RPG_CHECK(probs_dev != nullptr, "the sampling buffer must not be null");
+  RPG_CHECK(probs_dev != nullptr, "sampler: a probability buffer is null");
   CheckVocab(n);
   SampleScratch* s = Scratch();
   LaunchFilter(logits_dev, n, opt, probs_dev, s);

@@ -58,15 +58,20 @@ std::string GpuKvCache::Describe() const {
 }
 
 // tab[p][i] = cos(p * w_i), tab[p][head_dim/2 + i] = sin(p * w_i) with
-// w_i = theta^(-2i / head_dim), every angle in double and rounded to fp32 once
-// (the table src/gpu_model.cu:90-120 uploads).
+// w_i = 1 / theta^(2i / head_dim), every angle in double and rounded to fp32 once
+// (the table src/gpu_model.cu:90-120 uploads). The inverse frequency is formed as a
+// reciprocal of the power, as the reference forms it: pow(theta, -2i/d) differs from
+// it in the last double bit for about a third of the i, which moves some fp32 table
+// entries at positions past ~6500.
 std::vector<float> BuildRopeTable(int32_t head_dim, double theta, int64_t n_pos) {
   RPG_CHECK(head_dim > 0 && head_dim % 2 == 0, "RoPE needs an even head size, got %d", head_dim);
   RPG_CHECK(theta > 0.0, "RoPE base theta must be positive, got %g", theta);
   const int64_t rows = n_pos > 0 ? n_pos : 1;
   const int32_t pairs = head_dim / 2;
   std::vector<double> freq(static_cast<size_t>(pairs));
-  for (int32_t i = 0; i < pairs; ++i) freq[static_cast<size_t>(i)] = std::pow(theta, -2.0 * i / head_dim);
+  for (int32_t i = 0; i < pairs; ++i) {
+    freq[static_cast<size_t>(i)] = 1.0 / std::pow(theta, static_cast<double>(2 * i) / static_cast<double>(head_dim));
+  }
   std::vector<float> tab(static_cast<size_t>(rows * head_dim));
   float* out = tab.data();
   for (int64_t p = 0; p < rows; ++p, out += head_dim) {

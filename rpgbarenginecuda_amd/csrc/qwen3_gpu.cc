@@ -389,7 +389,7 @@ bool IsStop(const GpuGenerateOptions& opt, int32_t id) {
 
 void CheckRoom(const GpuModel& m, const GpuKvCache* kv, int32_t generated) {
   RPG_CHECK(kv->len() < kv->max_seq(),
-            "context is full (%lld positions, %d tokens generated); a larger max_seq is needed, or reset the cache",
+            "KV cache has no free slot: all %lld positions are taken after %d generated tokens (reset it, or size it for more positions)",
             static_cast<long long>(kv->max_seq()), generated);
   RPG_CHECK(kv->len() + 1 <= m.rope_positions(), "position %lld is beyond the %lld positions the RoPE table covers",
             static_cast<long long>(kv->len() + 1), static_cast<long long>(m.rope_positions()));
@@ -470,15 +470,15 @@ void GenerateNoGraph(const GpuModel& m, GpuKvCache* kv, GpuScratch* s, const Gpu
 void GpuGenerate(const GpuModel& m, GpuKvCache* kv, GpuScratch* s, const float* first_logits_dev,
                  const GpuGenerateOptions& opt, std::vector<int32_t>* out_ids) {
   const ModelMeta& c = m.config();
-  RPG_CHECK(kv != nullptr, "GpuGenerate requires a KV cache");
+  RPG_CHECK(kv != nullptr, "GpuGenerate: no KV cache was given");
   RPG_CHECK(s != nullptr && out_ids != nullptr, "GpuGenerate got a null scratch or output");
-  RPG_CHECK(first_logits_dev != nullptr, "first_logits is null (it exists only after a prefill)");
-  RPG_CHECK(opt.max_tokens > 0, "max_tokens must be positive, got %d", opt.max_tokens);
+  RPG_CHECK(first_logits_dev != nullptr, "GpuGenerate: first_logits_dev is null; the first token is sampled from the last prefill row's logits");
+  RPG_CHECK(opt.max_tokens > 0, "GpuGenerate: max_tokens has to be at least 1 (got %d)", opt.max_tokens);
   RPG_CHECK(!s->argmax_idx.empty() && s->probs.size() >= static_cast<size_t>(c.vocab) * sizeof(float),
             "the scratch has not been sized yet (run a prefill first)");
   CheckCache(m, kv);
   if (opt.use_graph && opt.step_logits != nullptr) {
-    RPG_LOG_WARN("use_graph is ignored: step_logits needs a per-step download, which a graph cannot do");
+    RPG_LOG_WARN("GpuGenerate: step_logits are requested, so the decode loop runs without a HIP graph");
   }
   const bool use_graph = opt.use_graph && opt.step_logits == nullptr;
   if (use_graph && GenerateGraph(m, kv, s, opt, first_logits_dev, out_ids)) return;

@@ -241,8 +241,8 @@ void GpuGenerate(const GpuModel& m, GpuKvCache* kv, GpuScratch* s, const float* 
                  const GpuGenerateOptions& opt, std::vector<int32_t>* out_ids) {
   RPG_CHECK(kv != nullptr && s != nullptr && out_ids != nullptr, "GpuGenerate needs a KV cache, a scratch and an "
                                                                  "output vector");
+  RPG_CHECK(opt.max_tokens > 0, "GpuGenerate: max_tokens has to be at least 1 (got %d)", opt.max_tokens);
   out_ids->clear();
-  if (opt.max_tokens <= 0) return;
   const int64_t vocab = m.config().vocab;
   rpg_generate_opts_t o{};
   o.max_tokens = opt.max_tokens;
@@ -252,18 +252,29 @@ void GpuGenerate(const GpuModel& m, GpuKvCache* kv, GpuScratch* s, const float* 
   o.top_k = opt.sample.top_k;
   o.top_p = opt.sample.top_p;
   o.seed = opt.seed;
-  o.use_graph = opt.use_graph ? 1 : 0;
+  // Per-step logits are downloaded after every step, which a replayed graph
+  // cannot do: such a call runs the per-step loop, and says so.
+  if (opt.use_graph && opt.step_logits != nullptr) {
+    RPG_LOG_WARN("GpuGenerate: step_logits are requested, so the decode loop runs without a HIP graph");
+  }
+  o.use_graph = (opt.use_graph && opt.step_logits == nullptr) ? 1 : 0;
+  // One row of `vocab` floats per generated token, appended after whatever the
+  // caller's vector already holds.
+  std::vector<float> rows;
   if (opt.step_logits != nullptr) {
-    opt.step_logits->assign(static_cast<size_t>(opt.max_tokens) * static_cast<size_t>(vocab), 0.0f);
-    o.step_logits = opt.step_logits->data();
-    o.step_logits_cap = static_cast<int64_t>(opt.step_logits->size());
+    rows.assign(static_cast<size_t>(opt.max_tokens) * static_cast<size_t>(vocab), 0.0f);
+    o.step_logits = rows.data();
+    o.step_logits_cap = static_cast<int64_t>(rows.size());
   }
   std::vector<int32_t> ids(static_cast<size_t>(opt.max_tokens));
   int32_t n = 0;
   Check(rpg_generate(m.handle(), kv->handle(), s->handle(), first_logits_dev, &o, ids.data(), opt.max_tokens, &n),
         "rpg_generate");
   out_ids->assign(ids.begin(), ids.begin() + n);
-  if (opt.step_logits != nullptr) opt.step_logits->resize(static_cast<size_t>(n) * static_cast<size_t>(vocab));
+  if (opt.step_logits != nullptr) {
+    opt.step_logits->insert(opt.step_logits->end(), rows.begin(),
+                            rows.begin() + static_cast<std::ptrdiff_t>(n) * static_cast<std::ptrdiff_t>(vocab));
+  }
 }
 
 void GpuGenerateGreedy(const GpuModel& m, GpuKvCache* kv, GpuScratch* s, const float* first_logits_dev,

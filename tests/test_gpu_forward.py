@@ -281,7 +281,7 @@ def test_stop_ids_and_full_context(gpu, models):
         kv.free()
         s.free()
         s, kv, first = prefill(gpu, m, prompt, 13)
-        with pytest.raises(gpu.RpgError, match="context is full"):
+        with pytest.raises(gpu.RpgError, match="KV cache has no free slot"):
             gpu.GpuGenerate(m, kv, s, first, gpu.GpuGenerateOptions(max_tokens=8, use_graph=use_graph))
         assert kv.len() == 13
         kv.free()

@@ -82,3 +82,60 @@ def test_noalloc_attention_rejects_oversized_split(gpu):
     # the allocating entry point takes the same call
     assert _run(lib, lib.rpg_op_attention_from_cache, nh, nkv, pos0, seq, q, kc, vc, max_seq, out) == 0
     torch.cuda.synchronize()
+
+
+def _group_partials_floats(units, group, positions):
+    """Partials floats of a grouped decode call: chunks of a multiple of 32 keys,
+    enough for ~2048 waves over `units` (token, kv head) pairs, 132 floats per
+    (token, query head, chunk); no split at >= 2048 units or <= 128 positions."""
+    if units >= 2048 or positions <= 128:
+        return 0
+    want = min((2048 + units - 1) // units, 128)
+    length = ((positions + want - 1) // want + 31) // 32 * 32
+    chunks = (positions + length - 1) // length
+    return units * group * chunks * 132 if chunks > 1 else 0
+
+
+def test_noalloc_attention_group4_boundary(gpu):
+    """GQA group 4 at 1985 (token, kv head) pairs fits the 2^21-float scratch and
+    matches the allocating entry bit for bit; 1986 pairs is rejected unlaunched."""
+    import torch
+
+    lib = gpu.load_library()
+    rng = np.random.default_rng(78)
+    max_seq, pos0 = 256, 200
+    # (seq, n_kv_heads): 5 x 397 = 1985 pairs, 6 x 331 = 1986 pairs
+    fits, over = (5, 397), (6, 331)
+    assert _group_partials_floats(fits[0] * fits[1], 4, pos0 + fits[0]) == 1985 * 1056 <= 1 << 21
+    assert _group_partials_floats(over[0] * over[1], 4, pos0 + over[0]) == 1986 * 1056 > 1 << 21
+
+    seq, nkv = fits
+    nh = 4 * nkv
+    _case(f"noalloc group-4 boundary: seq {seq}, {nh}/{nkv} heads, 1985 pairs (fits)")
+    q, kc, vc = _inputs(rng, nh, nkv, max_seq, seq)
+    qd = torch.from_numpy(q).cuda()
+    kd = torch.from_numpy(kc.view(np.int16)).cuda()
+    vd = torch.from_numpy(vc.view(np.int16)).cuda()
+    ref = torch.full((seq, nh, 128), float("nan"), dtype=torch.float32, device="cuda")
+    got = torch.full_like(ref, float("nan"))
+    assert _run(lib, lib.rpg_op_attention_from_cache, nh, nkv, pos0, seq, qd, kd, vd, max_seq, ref) == 0
+    assert _run(lib, lib.rpg_op_attention_from_cache_noalloc, nh, nkv, pos0, seq, qd, kd, vd, max_seq,
+                got) == 0, lib.rpg_ops_last_error()
+    torch.cuda.synchronize()
+    a = ref.cpu().numpy()
+    b = got.cpu().numpy()
+    assert np.all(np.isfinite(a))
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+
+    seq, nkv = over
+    nh = 4 * nkv
+    _case(f"noalloc group-4 boundary: seq {seq}, {nh}/{nkv} heads, 1986 pairs (rejected)")
+    q = torch.zeros((seq, nh, 128), dtype=torch.float32, device="cuda")
+    kc = torch.zeros((nkv, max_seq, 128), dtype=torch.int16, device="cuda")
+    vc = torch.zeros_like(kc)
+    out = torch.full((seq, nh, 128), 7.0, dtype=torch.float32, device="cuda")
+    rc = _run(lib, lib.rpg_op_attention_from_cache_noalloc, nh, nkv, pos0, seq, q, kc, vc, max_seq, out)
+    assert rc < 0
+    assert "no-allocation" in lib.rpg_ops_last_error().decode()
+    torch.cuda.synchronize()
+    assert bool(torch.all(out == 7.0)), "a rejected call must not launch"
