@@ -129,6 +129,35 @@ def launch_floor_us(torch, ops):
     return back_to_back_us(torch, ops, lambda i: ops.GpuStreamFill(buf, 4096, 0), n=200)
 
 
+def batch_us(torch, launch, count, trials=5, start=0):
+    """Per-launch GPU time of `count` launches run back to back, median over
+    `trials` batches: the reference's BenchItem method (tools/matmul_bench.cu:114-132:
+    launches issued back to back, one clock read around the batch), with stream
+    events in place of the host clock. Each batch queues behind a bounded spin
+    kernel (hold_launches) and the start event follows it, so the kernels run
+    with no idle gap and no per-dispatch event packets between them, as the
+    product runs them. launch(i) receives a running index (continued across
+    batches from `start`) so callers can rotate through distinct buffers.
+    Returns (median us per launch, [us per launch of each batch])."""
+    import statistics
+
+    samples = []
+    i = start
+    for _ in range(trials):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        hold_launches(torch, count)
+        e0.record()
+        for _ in range(count):
+            launch(i)
+            i += 1
+        e1.record()
+        torch.cuda.synchronize()
+        samples.append(e0.elapsed_time(e1) * 1e3 / count)
+    return statistics.median(samples), samples
+
+
 class Layer:
     """One layer's device buffers (all distinct per layer)."""
 
@@ -155,6 +184,28 @@ def run_layer(ops, L, n, tab, pos0):
     ops.GpuAddRmsNorm(L.x, L.d, L.w, n, L.hid, EPS, L.h)
     ops.GpuQkNormRopeKv(L.q, L.k, L.v, L.qn, L.kn, L.hq, L.hkv, D, tab, MAX_SEQ, pos0, n, EPS, L.kc, L.vc, MAX_SEQ)
     ops.GpuSiluMulInPlace(L.gate, L.up, n * L.inter)
+
+
+def op_launchers(ops, n, tab, pos0=0):
+    """One launch of each layer op on a layer's buffers, keyed by op name."""
+    return {
+        "add_rms_norm": lambda L: ops.GpuAddRmsNorm(L.x, L.d, L.w, n, L.hid, EPS, L.h),
+        "qk_norm_rope_kv": lambda L: ops.GpuQkNormRopeKv(L.q, L.k, L.v, L.qn, L.kn, L.hq, L.hkv, D, tab, MAX_SEQ,
+                                                         pos0, n, EPS, L.kc, L.vc, MAX_SEQ),
+        "swiglu": lambda L: ops.GpuSiluMulInPlace(L.gate, L.up, n * L.inter),
+    }
+
+
+def op_batches(torch, ops, layers, tab, n, trials=5):
+    """Each op timed alone the way the product runs it: one launch per layer's
+    buffers (28 or 36 distinct buffer sets, far beyond the Infinity Cache), all
+    back to back, one event pair around the batch, median of `trials` batches."""
+    out = {}
+    for name, fn in op_launchers(ops, n, tab).items():
+        fn(layers[0])
+        med, samples = batch_us(torch, lambda i, fn=fn: fn(layers[i % len(layers)]), len(layers), trials)
+        out[name] = (med, samples)
+    return out
 
 
 def layer_bytes(n, shape):
@@ -271,7 +322,9 @@ def measure_decode(torch, ops, tab, steps):
 
 
 def measure_prefill_4b(torch, ops, tab, steps=5, warmup=2):
-    """Prefill n = 4096 at Qwen3-4B shape, 36 layers (the 4096-slot caches are filled)."""
+    """Prefill n = 4096 at Qwen3-4B shape, 36 layers (the 4096-slot caches are filled):
+    the chain's step time, then each op's 36 launches back to back (median of 5
+    batches) and, secondary, each op's average under dispatch-attached events."""
     n, shape = 4096, QWEN3_4B
     gen = torch.Generator(device="cuda")
     gen.manual_seed(4)
@@ -290,92 +343,174 @@ def measure_prefill_4b(torch, ops, tab, steps=5, warmup=2):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     b = shape["layers"] * layer_bytes(n, shape)
+    hid, hq, hkv, inter = shape["hidden"], shape["n_heads"], shape["n_kv_heads"], shape["inter"]
+    op_bytes = {"add_rms_norm": bytes_add_rms(n, hid), "qk_norm_rope_kv": bytes_qk(n, hq, hkv),
+                "swiglu": bytes_swiglu(n, inter)}
+    batches = op_batches(torch, ops, layers, tab, n)
+    ops.profile_start(3 * len(layers))
+    hold_launches(torch, 3 * len(layers))
+    for L in layers:
+        run_layer(ops, L, n, tab, 0)
+    ops.profile_stop()
+    report = ops.profile_report()
+    per_op = {}
+    for name in OP_NAMES:
+        us, samples = batches[name]
+        kname = launched_kernel(report, name)
+        ev = report[kname]["avg_us"]
+        per_op[name] = {"us": round(us, 2), "pct_peak": round(op_bytes[name] / us / 1e3 / PEAK_GBPS * 100, 1),
+                        "GBps": round(op_bytes[name] / us / 1e3, 1), "batch_us": [round(x, 2) for x in samples],
+                        "us_event": round(ev, 2),
+                        "pct_peak_event": round(op_bytes[name] / ev / 1e3 / PEAK_GBPS * 100, 1),
+                        "bytes": op_bytes[name], "kernel": kname}
     del layers
     torch.cuda.empty_cache()
     return {"ms_per_step": round(ms, 4), "GBps": round(b / (ms * 1e-3) / 1e9, 1),
             "pct_of_peak": round(b / (ms * 1e-3) / 1e9 / PEAK_GBPS * 100, 2), "bytes_per_step": b,
-            "us_per_layer": round(ms * 1e3 / shape["layers"], 2), "layers": shape["layers"], "n_tokens": n}
+            "us_per_layer": round(ms * 1e3 / shape["layers"], 2), "layers": shape["layers"], "n_tokens": n,
+            "ops": per_op}
 
 
-def measure_gather(torch, ops, ggml_type, bb, copies=4, reps=20):
-    """n = 2811 ids gathered from a [151936, 2048] table, rotating over `copies` table copies."""
+def gather_table(torch, ops, ggml_type, gen):
+    """A [151936, 2048] token_embd of configs[1]'s distributions on the device:
+    Q4_K: fp16 d, dmin = |N(0, 0.01)|, the 12 scale bytes and the 4-bit quants
+    uniform random bytes; Q6_K: fp16 d = |N(0, 0.01)|, int8 scales uniform over
+    -32..31, the 6-bit quants (ql, qh) uniform random bytes."""
+    bb = 144 if ggml_type == ops.GGML_Q4_K else 210
+    blocks_n = VOCAB * (H // 256)
+    blob = torch.randint(0, 256, (blocks_n * bb,), dtype=torch.uint8, device="cuda", generator=gen)
+    blocks = blob.view(blocks_n, bb)
+
+    def f16_bytes():
+        d = (torch.randn(blocks_n, generator=gen, device="cuda") * 0.01).abs().half()
+        return d.view(torch.uint8).view(blocks_n, 2)
+
+    if ggml_type == ops.GGML_Q4_K:
+        blocks[:, 0:2] = f16_bytes()
+        blocks[:, 2:4] = f16_bytes()
+    else:
+        sc = torch.randint(-32, 32, (blocks_n, 16), dtype=torch.int8, device="cuda", generator=gen)
+        blocks[:, 192:208] = sc.view(torch.uint8)
+        blocks[:, 208:210] = f16_bytes()
+    return blob
+
+
+def measure_gather(torch, ops, ggml_type, bb, copies=4, id_sets=64, reps=20):
+    """n = 2811 ids gathered from a [151936, 2048] table. Launch i reads table copy
+    i % copies with id set i % id_sets (each set uniform over the vocabulary, so
+    each launch's rows are cold) and writes output window i % windows of a 1 GiB
+    span, so no launch finds its rows or its output in the 256 MB Infinity Cache.
+    `us`: median of 5 batches of `reps` launches back to back (batch_us);
+    `us_event`: the same launches under dispatch-attached events;
+    `us_idle_start`: each launch issued from Python after the previous one ended."""
     gen = torch.Generator(device="cuda")
     gen.manual_seed(10 + ggml_type)
-    row_bytes = (H // 256) * bb
-    tables = [torch.randint(0, 256, (VOCAB * row_bytes,), dtype=torch.uint8, device="cuda", generator=gen)
-              for _ in range(copies)]
-    toks = torch.randint(0, VOCAB, (N_PREFILL,), dtype=torch.int32, device="cuda", generator=gen)
-    outs = [torch.empty((N_PREFILL, H), dtype=torch.float32, device="cuda") for _ in range(copies)]
+    tables = [gather_table(torch, ops, ggml_type, gen) for _ in range(copies)]
+    ids = [torch.randint(0, VOCAB, (N_PREFILL,), dtype=torch.int32, device="cuda", generator=gen)
+           for _ in range(id_sets)]
+    out_floats = N_PREFILL * H
+    windows = max(2, -(-(1 << 30) // (4 * out_floats)))
+    span = torch.empty(windows * out_floats, dtype=torch.float32, device="cuda")
+    outs = [span[w * out_floats:(w + 1) * out_floats] for w in range(windows)]
     embs = [ops.GpuTensor(t, ggml_type, VOCAB, H) for t in tables]
+
+    def launch(i):
+        ops.GpuEmbeddingLookup(embs[i % copies], ids[i % id_sets], N_PREFILL, outs[i % windows])
+
     for i in range(copies):
-        ops.GpuEmbeddingLookup(embs[i], toks, N_PREFILL, outs[i])
+        launch(i)
     torch.cuda.synchronize()
     name = "GatherQ4KKernel" if ggml_type == ops.GGML_Q4_K else "GatherQ6KKernel"
-    def timed(queued):
+    us, samples = batch_us(torch, launch, reps, trials=5, start=copies)
+    nxt = copies + 5 * reps
+
+    def evented(queued, start):
         ops.profile_start(reps)
         if queued:
             hold_launches(torch, reps)
         for r in range(reps):
-            ops.GpuEmbeddingLookup(embs[r % copies], toks, N_PREFILL, outs[r % copies])
+            launch(start + r)
         ops.profile_stop()
         return ops.profile_report()[name]
 
-    idle = timed(False)
-    rep = timed(True)
-    avg_ms = rep["avg_us"] * 1e-3
+    ev = evented(True, nxt)
+    idle = evented(False, nxt + reps)
     nbytes = bytes_gather(N_PREFILL, bb)
-    del tables, outs
-    return {"us": round(avg_ms * 1e3, 2), "GBps": round(nbytes / (avg_ms * 1e-3) / 1e9, 1), "bytes": nbytes,
-            "kernel": name, "launches": rep["count"],
-            "us_idle_start": round(idle["avg_us"], 2),
-            "timing": "us: launches queued back to back; us_idle_start: each launch issued from Python "
-                      "after the previous kernel ended"}
+    del tables, outs, span
+    torch.cuda.empty_cache()
+    return {"us": round(us, 2), "GBps": round(nbytes / us / 1e3, 1),
+            "pct_peak": round(nbytes / us / 1e3 / PEAK_GBPS * 100, 1), "batch_us": [round(x, 2) for x in samples],
+            "bytes": nbytes, "kernel": name, "us_event": round(ev["avg_us"], 2),
+            "us_idle_start": round(idle["avg_us"], 2), "table_copies": copies, "id_sets": id_sets,
+            "output_windows": windows,
+            "timing": "us: median of 5 batches of 20 launches back to back, one event pair per batch; "
+                      "us_event: dispatch-attached events, launches queued; us_idle_start: each launch issued "
+                      "from Python after the previous kernel ended"}
 
 
 def measure_ceilings(torch, ops, sizes, reps=20):
-    """Same-size streaming ceilings, timed like the ops (dispatch-attached events):
-    for each (label, total_bytes, write_bytes), a StreamCopyKernel moving total_bytes
-    (half read, half written) and a StreamFillKernel writing write_bytes. Launches
-    walk through 1 GiB source / destination buffers so no launch reuses a window
-    while it could still sit in the 256 MB Infinity Cache."""
+    """Same-size streaming ceilings, timed like the ops (batch_us: `reps` launches
+    back to back, one event pair per batch, median of 5). For each (label,
+    total_bytes, write_bytes, read_bytes): a StreamCopyKernel moving total_bytes
+    (half read, half written), a StreamFillKernel writing write_bytes and a
+    StreamReadKernel reading read_bytes (a 0 skips that probe). Launches walk
+    through 1 GiB source / destination spans, so no launch finds its window in
+    the 256 MB Infinity Cache."""
     span = 1 << 30
     src = torch.empty(span // 4, dtype=torch.float32, device="cuda").fill_(1.0)
     dst = torch.empty_like(src)
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
     torch.cuda.synchronize()
     out = {}
 
-    def timed(kernel, per_launch, launch):
-        windows = max(1, span // per_launch)
-        for r in range(2):
-            launch(r % windows)
-        torch.cuda.synchronize()
-        ops.profile_start(reps)
-        hold_launches(torch, reps)
-        for r in range(reps):
-            launch(r % windows)
-        ops.profile_stop()
-        return ops.profile_report()[kernel]["avg_us"]
+    def timed(per_launch, launch):
+        windows = max(2, span // per_launch)
+        launch(0)
+        us, _ = batch_us(torch, lambda i: launch(i % windows), reps, trials=5, start=1)
+        return us
 
-    for label, total, written in sizes:
+    for label, total, written, read in sizes:
+        res = {}
         half = (total // 2) // 16 * 16
+        if half > 0:
+            def copy(i, half=half):
+                off = i * half // 4
+                ops.GpuStreamCopy(src[off:off + half // 4], dst[off:off + half // 4], half)
+
+            res["copy_us"] = round(timed(half, copy), 2)
+            res["copy_GBps"] = round(2 * half / res["copy_us"] / 1e3, 1)
         w = written // 16 * 16
+        if w > 0:
+            def fill(i, w=w):
+                off = i * w // 4
+                ops.GpuStreamFill(dst[off:off + w // 4], w, 0x3F800000)
 
-        def copy(i, half=half):
-            off = i * half // 4
-            ops.GpuStreamCopy(src[off:off + half // 4], dst[off:off + half // 4], half)
+            res["fill_us"] = round(timed(w, fill), 2)
+            res["fill_GBps"] = round(w / res["fill_us"] / 1e3, 1)
+        rd = read // 16 * 16
+        if rd > 0:
+            def rdl(i, rd=rd):
+                off = i * rd // 4
+                ops.GpuStreamRead(src[off:off + rd // 4], rd, sink)
 
-        def fill(i, w=w):
-            off = i * w // 4
-            ops.GpuStreamFill(dst[off:off + w // 4], w, 0x3F800000)
-
-        copy_us = timed("StreamCopyKernel", half, copy)
-        fill_us = timed("StreamFillKernel", w, fill)
-        out[label] = {"copy_us": round(copy_us, 2), "fill_us": round(fill_us, 2),
-                      "copy_GBps": round(2 * half / (copy_us * 1e-6) / 1e9, 1),
-                      "fill_GBps": round(w / (fill_us * 1e-6) / 1e9, 1)}
+            res["read_us"] = round(timed(rd, rdl), 2)
+            res["read_GBps"] = round(rd / res["read_us"] / 1e3, 1)
+        out[label] = res
+    assert int(sink.item()) == 0, "the read probe's key was hit"
     del src, dst
     torch.cuda.empty_cache()
     return out
+
+
+def measure_stream_read(torch, ops, nbytes=1 << 30, reps=10):
+    """Read-only streaming ceiling over 1 GiB (StreamReadKernel, the reference's BwReadKernel probe)."""
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    ops.GpuStreamRead(src, nbytes, sink)
+    torch.cuda.synchronize()
+    us, _ = batch_us(torch, lambda i: ops.GpuStreamRead(src, nbytes, sink), reps, trials=3)
+    del src
+    return round(nbytes / us / 1e3, 1)
 
 
 def measure_copy(torch, ops, nbytes=1 << 30, reps=10):
@@ -482,7 +617,7 @@ def measure_matmul_decode_grouped(torch, ops, reps, span):
     [v] (Q6_K), [o], [gate, up], [down]; copies rotated past the Infinity Cache."""
     mats = {name: (t, rows, cols) for name, t, rows, cols in DECODE_MATRICES}
     groups = [["attn_q", "attn_k"], ["attn_v"], ["attn_output"], ["ffn_gate", "ffn_up"], ["ffn_down"]]
-    res, layer_us = {}, 0.0
+    res, layer_us, layer_b2b = {}, 0.0, 0.0
     for grp in groups:
         specs = [mats[n] for n in grp]
         sizes = [rows * (cols // 256) * (144 if t == 12 else 210) for t, rows, cols in specs]
@@ -515,12 +650,16 @@ def measure_matmul_decode_grouped(torch, ops, reps, span):
         ops.profile_stop()
         rep = ops.profile_report()
         us = sum(k["total_us"] for k in rep.values()) / reps
+        nbytes = sum(sizes) + 4 * cols + 4 * sum(r for _, r, _ in specs)
+        b2b = back_to_back_us(torch, ops, lambda i: ops.GpuMatMulQuantGroup(sets[i % copies], x, 1, outs))
         res["+".join(grp)] = {"us": round(us, 2), "launches": int(sum(k["count"] for k in rep.values()) // reps),
-                              "GBps": round((sum(sizes) + 4 * cols + 4 * sum(r for _, r, _ in specs)) / us / 1e3, 1)}
+                              "GBps": round(nbytes / us / 1e3, 1), "bytes": nbytes,
+                              "us_back_to_back": round(b2b, 2), "GBps_back_to_back": round(nbytes / b2b / 1e3, 1)}
         layer_us += us
+        layer_b2b += b2b
         del sets, x, outs
         torch.cuda.empty_cache()
-    return {"groups": res, "layer_us": round(layer_us, 2)}
+    return {"groups": res, "layer_us": round(layer_us, 2), "layer_us_back_to_back": round(layer_b2b, 2)}
 
 
 def measure_matmul_prefill(torch, ops, n=N_PREFILL, reps=3):
@@ -915,6 +1054,8 @@ SECTIONS = {
     "sampler": lambda torch, ops: measure_sampler(torch, ops),
     "gather": lambda torch, ops: {"q4k": measure_gather(torch, ops, ops.GGML_Q4_K, 144),
                                   "q6k": measure_gather(torch, ops, ops.GGML_Q6_K, 210)},
+    "prefill_4b_n4096": lambda torch, ops: measure_prefill_4b(
+        torch, ops, torch.from_numpy(ops.build_rope_table(D, THETA, MAX_SEQ)).cuda()),
 }
 
 
@@ -965,21 +1106,28 @@ def main():
     value = step_bytes / (ms_step * 1e-3) / 1e9
     op_bytes = {"add_rms_norm": bytes_add_rms(N_PREFILL), "qk_norm_rope_kv": bytes_qk(N_PREFILL),
                 "swiglu": bytes_swiglu(N_PREFILL)}
+    log("per-op batches: each op's 28 launches back to back, median of 5")
+    batches = op_batches(torch, ops, layers, tab, N_PREFILL)
     op_stats = {}
     for name in OP_NAMES:
         kname = launched_kernel(report, name)
         k = report[kname]
         assert k["count"] == args.steps * LAYERS, (name, k)
-        avg_s = k["avg_us"] * 1e-6
-        op_stats[name] = {"us": round(k["avg_us"], 2), "GBps": round(op_bytes[name] / avg_s / 1e9, 1),
-                          "pct_peak": round(op_bytes[name] / avg_s / 1e9 / PEAK_GBPS * 100, 1),
-                          "bytes": op_bytes[name], "kernel": kname, "launches": k["count"]}
+        us, samples = batches[name]
+        op_stats[name] = {"us": round(us, 2), "GBps": round(op_bytes[name] / us / 1e3, 1),
+                          "pct_peak": round(op_bytes[name] / us / 1e3 / PEAK_GBPS * 100, 1),
+                          "batch_us": [round(x, 2) for x in samples],
+                          "us_event": round(k["avg_us"], 2),
+                          "pct_peak_event": round(op_bytes[name] / k["avg_us"] / 1e3 / PEAK_GBPS * 100, 1),
+                          "bytes": op_bytes[name], "kernel": kname, "launches_event_pass": k["count"]}
     dominant = max(OP_NAMES, key=lambda k: op_stats[k]["us"])
-    d_avg_s = op_stats[dominant]["us"] * 1e-6
-    achieved = op_bytes[dominant] / d_avg_s / 1e9
+    achieved = op_bytes[dominant] / op_stats[dominant]["us"] / 1e3
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / PEAK_GBPS, 4), "traffic": profile_traffic(op_stats[dominant]["kernel"]),
-                "kernel": op_stats[dominant]["kernel"], "algorithmic_bytes_per_launch": op_bytes[dominant]}
+                "kernel": op_stats[dominant]["kernel"], "algorithmic_bytes_per_launch": op_bytes[dominant],
+                "timing": "median of 5 batches of the kernel's 28 launches (one per layer's buffers) back to back, "
+                          "one stream-event pair around each batch",
+                "achieved_event_pass": round(op_bytes[dominant] / op_stats[dominant]["us_event"] / 1e3, 1)}
     del layers
     torch.cuda.empty_cache()
 
@@ -1007,22 +1155,40 @@ def main():
         log("gather Q4_K / Q6_K")
         extras["gather_q4k_n2811"] = measure_gather(torch, ops, ops.GGML_Q4_K, 144)
         extras["gather_q6k_n2811"] = measure_gather(torch, ops, ops.GGML_Q6_K, 210)
-        log("stream copy ceiling")
+        log("stream copy / read ceilings (1 GiB)")
         extras["stream_copy_GBps"] = measure_copy(torch, ops)
-        log("same-size copy / fill ceilings")
-        ceil = measure_ceilings(torch, ops, [
-            ("add_rms_norm", op_bytes["add_rms_norm"], 8 * N_PREFILL * H),
-            ("qk_norm_rope_kv", op_bytes["qk_norm_rope_kv"], N_PREFILL * (4 * HQ * D + 4 * HKV * D)),
-            ("swiglu", op_bytes["swiglu"], 4 * N_PREFILL * INTER),
-            ("gather", bytes_gather(N_PREFILL, 144), 4 * N_PREFILL * H)])
+        extras["stream_read_GBps"] = measure_stream_read(torch, ops)
+        log("same-size copy / fill / read ceilings")
+        out_bytes = 4 * N_PREFILL * H
+        ceil_sizes = [
+            ("add_rms_norm", op_bytes["add_rms_norm"], 8 * N_PREFILL * H, 0),
+            ("qk_norm_rope_kv", op_bytes["qk_norm_rope_kv"], N_PREFILL * (4 * HQ * D + 4 * HKV * D), 0),
+            ("swiglu", op_bytes["swiglu"], 4 * N_PREFILL * INTER, 0),
+            ("gather_q4k", bytes_gather(N_PREFILL, 144), out_bytes, bytes_gather(N_PREFILL, 144) - out_bytes),
+            ("gather_q6k", 0, 0, bytes_gather(N_PREFILL, 210) - out_bytes)]
+        mm = extras.get("matmul_decode_n1")
+        if mm:
+            for name, m in mm["matrices"].items():
+                ceil_sizes.append((f"matvec_{name}", 0, 0, m["bytes"]))
+            for name, g in mm["grouped"]["groups"].items():
+                ceil_sizes.append((f"matvec_group_{name}", 0, 0, g["bytes"]))
+        ceil = measure_ceilings(torch, ops, ceil_sizes)
         for name in OP_NAMES:
             c = ceil[name]
             op_stats[name]["copy_ceiling_us"] = c["copy_us"]
             op_stats[name]["pct_of_copy_ceiling"] = round(c["copy_us"] / op_stats[name]["us"] * 100, 1)
-        for key, bb in (("gather_q4k_n2811", 144), ("gather_q6k_n2811", 210)):
+        for key, label in (("gather_q4k_n2811", "gather_q4k"), ("gather_q6k_n2811", "gather_q6k")):
             g = extras[key]
-            g["write_ceiling_us"] = ceil["gather"]["fill_us"]
-            g["pct_of_write_ceiling"] = round(ceil["gather"]["fill_us"] / g["us"] * 100, 1)
+            g["write_ceiling_us"] = ceil["gather_q4k"]["fill_us"]
+            g["pct_of_write_ceiling"] = round(ceil["gather_q4k"]["fill_us"] / g["us"] * 100, 1)
+            g["table_read_ceiling_us"] = ceil[label]["read_us"]
+        if mm:
+            for name, m in mm["matrices"].items():
+                m["read_ceiling_us"] = ceil[f"matvec_{name}"]["read_us"]
+                m["pct_of_read_ceiling"] = round(m["read_ceiling_us"] / m["us_back_to_back"] * 100, 1)
+            for name, g in mm["grouped"]["groups"].items():
+                g["read_ceiling_us"] = ceil[f"matvec_group_{name}"]["read_us"]
+                g["pct_of_read_ceiling"] = round(g["read_ceiling_us"] / g["us_back_to_back"] * 100, 1)
         extras["ceilings"] = ceil
     cpu = None if args.no_cpu else cpu_baseline()
 

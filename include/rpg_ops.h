@@ -439,6 +439,14 @@ RPG_OPS_API int32_t rpg_op_stream_copy(const void* src, void* dst, int64_t bytes
  * probes copies only (tools/matmul_bench.cu:230-289). */
 RPG_OPS_API int32_t rpg_op_stream_fill(void* dst, int64_t bytes, uint32_t pattern);
 
+/* Reads `bytes` (a positive multiple of 16) of src (16-byte aligned) and writes
+ * nothing, unless the XOR fold of one thread's 16 words equals `key`; then that
+ * fold is stored to *sink (device memory, one word). The read-only bandwidth
+ * probe (the ceiling of read-dominated kernels: decode matvecs, the output
+ * projection, decode attention). Replaces: BwReadKernel,
+ * tools/matmul_bench.cu:239-250,269-286. */
+RPG_OPS_API int32_t rpg_op_stream_read(const void* src, int64_t bytes, uint32_t key, uint32_t* sink);
+
 /* out_dev[i] = fp32 value of the binary16 bit pattern i, i in [0, 65536).
  * Replaces: F16SweepKernel, tools/dequant_check.cu:44-48. */
 RPG_OPS_API int32_t rpg_op_f16_sweep(float* out_dev);

@@ -696,6 +696,10 @@ int32_t rpg_op_stream_copy(const void* src, void* dst, int64_t bytes) {
   return Guard([&] { rpg::GpuStreamCopy(src, dst, bytes); });
 }
 
+int32_t rpg_op_stream_read(const void* src, int64_t bytes, uint32_t key, uint32_t* sink) {
+  return Guard([&] { rpg::GpuStreamRead(src, bytes, key, sink); });
+}
+
 int32_t rpg_op_stream_fill(void* dst, int64_t bytes, uint32_t pattern) {
   return Guard([&] { rpg::GpuStreamFill(dst, bytes, pattern); });
 }

@@ -1,5 +1,6 @@
 // Element-wise operators: SwiGLU gate (silu(gate) * up), the residual add, and
-// the streaming copy / fill probes used to calibrate bandwidth and HBM counters.
+// the streaming copy / read / fill probes used to calibrate bandwidth and HBM
+// counters.
 //
 // Reference semantics:
 //   SiluMul (src/kernels_gpu.cu:863-869): gate[i] = (v / (1.0f + expf(-v))) * up[i]
@@ -101,6 +102,29 @@ __global__ __launch_bounds__(kFillBlock) void StreamFillKernel(float* __restrict
   if (i < n16) StoreStream4(dst + 4 * i, make_float4(value, value, value, value));
 }
 
+// Read-only probe: each thread reads kReadUnroll float4 (the workgroup's span is
+// contiguous, lane-strided by the block so every load instruction covers whole
+// lines) and folds their bits with XOR. The fold is stored only when it equals
+// `key`, which the caller chooses so that it does not occur: the loads stay live
+// and the kernel writes nothing (the sink is at most one word).
+constexpr int kReadBlock = 256;
+constexpr int kReadUnroll = 4;
+
+__global__ __launch_bounds__(kReadBlock) void StreamReadKernel(const float* __restrict__ src, int64_t n16,
+                                                               uint32_t key, uint32_t* __restrict__ sink) {
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kReadBlock * kReadUnroll) + threadIdx.x;
+  uint32_t fold = 0;
+#pragma unroll
+  for (int u = 0; u < kReadUnroll; ++u) {
+    const int64_t i = base + static_cast<int64_t>(u) * kReadBlock;
+    if (i < n16) {
+      const float4 v = LoadStream4(src + 4 * i);
+      fold ^= __float_as_uint(v.x) ^ __float_as_uint(v.y) ^ __float_as_uint(v.z) ^ __float_as_uint(v.w);
+    }
+  }
+  if (fold == key) sink[0] = fold;
+}
+
 // Write-through output stores from this many elements up (64 blocks of kBlock
 // float4): below it the launch is latency-bound and the write-through
 // acknowledgement only lengthens it.
@@ -144,6 +168,15 @@ void GpuStreamCopy(const void* src, void* dst, int64_t bytes) {
   const int64_t n16 = bytes / 16;
   Launch("StreamCopyKernel", StreamCopyKernel, dim3(GridFor(n16, kBlock)), dim3(kBlock),
          static_cast<const float*>(src), static_cast<float*>(dst), n16);
+}
+
+void GpuStreamRead(const void* src, int64_t bytes, uint32_t key, uint32_t* sink) {
+  RPG_CHECK(bytes > 0 && bytes % 16 == 0, "stream read size %lld must be a positive multiple of 16",
+            static_cast<long long>(bytes));
+  RPG_CHECK(Aligned16(src) && sink != nullptr, "stream read needs a 16-byte aligned source and a sink word");
+  const int64_t n16 = bytes / 16;
+  Launch("StreamReadKernel", StreamReadKernel, dim3(GridFor(n16, kReadBlock * kReadUnroll)), dim3(kReadBlock),
+         static_cast<const float*>(src), n16, key, sink);
 }
 
 void GpuStreamFill(void* dst, int64_t bytes, uint32_t pattern) {

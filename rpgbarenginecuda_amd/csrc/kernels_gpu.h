@@ -329,6 +329,11 @@ void GpuStreamCopy(const void* src, void* dst, int64_t bytes);
 // Write-only probe: every 32-bit word of dst <- pattern (`bytes` a multiple of 16).
 void GpuStreamFill(void* dst, int64_t bytes, uint32_t pattern);
 
+// Read-only probe: reads `bytes` (a multiple of 16) of src and writes nothing
+// unless the XOR fold of some thread's words equals `key` (then that fold goes to
+// *sink). The reference's read probe (BwReadKernel, tools/matmul_bench.cu:239-250).
+void GpuStreamRead(const void* src, int64_t bytes, uint32_t key, uint32_t* sink);
+
 // out[i] = binary16 bits i converted to fp32, i in [0, 65536): exhaustive check
 // of the device f16 -> f32 conversion (tools/dequant_check.cu:44-48).
 void GpuF16Sweep(float* out_dev);

@@ -102,6 +102,7 @@ SIGNATURES = {
                                       _vp, _vp, _i64, _i32]),
     "rpg_op_stream_copy": (_i32, [_vp, _vp, _i64]),
     "rpg_op_stream_fill": (_i32, [_vp, _i64, _u32]),
+    "rpg_op_stream_read": (_i32, [_vp, _i64, _u32, _vp]),
     "rpg_op_f16_sweep": (_i32, [_vp]),
     "rpg_ops_profile_start": (_i32, [_i32]),
     "rpg_ops_profile_stop": (_i32, []),
@@ -852,6 +853,14 @@ def GpuStreamCopy(src, dst, nbytes: int) -> None:
 
 def GpuStreamFill(dst, nbytes: int, pattern: int) -> None:
     _check(load_library().rpg_op_stream_fill(_addr(dst, nbytes, name="dst"), nbytes, pattern & 0xFFFFFFFF))
+
+
+def GpuStreamRead(src, nbytes: int, sink, key: int = 0x9E3779B9) -> None:
+    """Reads nbytes of src and writes nothing (unless a thread's XOR fold equals key;
+    then one word goes to sink, an int32 device tensor)."""
+    torch = _t()
+    _check(load_library().rpg_op_stream_read(_addr(src, nbytes, name="src"), nbytes, key & 0xFFFFFFFF,
+                                             _addr(sink, 4, torch.int32, "sink")))
 
 
 def profile_start(max_launches: int) -> None:

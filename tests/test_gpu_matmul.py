@@ -206,7 +206,7 @@ def test_matmul_quant_rejects_bad_shapes(gpu):
     out = torch.zeros(8, dtype=torch.float32, device="cuda")
     L = gpu.load_library()
     assert L.rpg_op_matmul_quant(12, w.data_ptr(), 2, 300, x.data_ptr(), 1, out.data_ptr()) != 0
-    assert "multiple of the block size" in last_error(gpu)
+    assert "do not fill whole blocks of 256" in last_error(gpu)
     assert L.rpg_op_matmul_quant(12, w.data_ptr(), 2, 512, x.data_ptr(), 0, out.data_ptr()) != 0
     assert L.rpg_op_matmul_quant(99, w.data_ptr(), 2, 512, x.data_ptr(), 1, out.data_ptr()) != 0
 

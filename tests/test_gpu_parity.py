@@ -492,6 +492,36 @@ def test_stream_fill(gpu):
     assert not got[:4].any() and not got[4 + n:].any()
 
 
+def test_stream_read(gpu):
+    import torch
+
+    case("stream read 64 MiB + 48 B: writes only when a thread's fold equals the key")
+    rng = np.random.default_rng(31)
+    n16 = (4 << 20) + 3                                    # a ragged last workgroup
+    words = rng.integers(0, 1 << 32, 4 * n16, dtype=np.uint64).astype(np.uint32)
+    src = torch.from_numpy(words.view(np.int32)).cuda()
+    sink = torch.full((1,), 7, dtype=torch.int32, device="cuda")
+    gpu.GpuStreamRead(src, 4 * words.size, sink, key=0x9E3779B9)
+    torch.cuda.synchronize()
+    assert int(sink.item()) == 7                           # no thread folds to the key: nothing written
+    # thread 0 of workgroup 0 reads float4 0, 256, 512, 768 (256 threads, 4 per thread)
+    f4 = words.reshape(-1, 4)
+    fold = np.bitwise_xor.reduce(f4[[0, 256, 512, 768]].ravel())
+    gpu.GpuStreamRead(src, 4 * words.size, sink, key=int(fold))
+    torch.cuda.synchronize()
+    assert int(sink.cpu().numpy().view(np.uint32)[0]) == int(fold)
+    # the last thread of the ragged tail: float4 n16 - 1 alone (its other three are past the end)
+    last = n16 - 1
+    blk, t = divmod(last, 1024)
+    idx = [blk * 1024 + t % 256 + u * 256 for u in range(4)]
+    idx = [i for i in idx if i < n16]
+    tail_fold = np.bitwise_xor.reduce(f4[idx].ravel())
+    sink.fill_(7)
+    gpu.GpuStreamRead(src, 4 * words.size, sink, key=int(tail_fold))
+    torch.cuda.synchronize()
+    assert int(sink.cpu().numpy().view(np.uint32)[0]) == int(tail_fold)
+
+
 # ----------------------------------------------------------------------------- graph capture
 
 
