@@ -81,9 +81,17 @@ __device__ __forceinline__ void DecodeQ4KLane(const uint8_t* blk, int j, const P
   put(64 * g + 32 + 4 * kq, make_float4(hi[0], hi[1], hi[2], hi[3]));
 }
 
+// 4 (8) bytes at a 2-byte aligned address as one dword (dwordx2) load: the
+// device runs in unaligned-access mode, which the compiler assumes for amdhsa.
 __device__ __forceinline__ uint32_t Load4Bytes2Aligned(const uint8_t* p) {
-  const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
-  return static_cast<uint32_t>(h[0]) | (static_cast<uint32_t>(h[1]) << 16);
+  uint32_t w;
+  __builtin_memcpy(&w, __builtin_assume_aligned(p, 2), 4);
+  return w;
+}
+__device__ __forceinline__ uint2 Load8Bytes2Aligned(const uint8_t* p) {
+  uint2 w;
+  __builtin_memcpy(&w, __builtin_assume_aligned(p, 2), 8);
+  return w;
 }
 
 // One lane's share (16 elements) of a Q6_K block; blk must be 2-byte aligned.
@@ -94,8 +102,9 @@ __device__ __forceinline__ void DecodeQ6KLane(const uint8_t* blk, int j, const P
   const uint32_t ql0 = Load4Bytes2Aligned(blk + 64 * half + 4 * kq);
   const uint32_t ql1 = Load4Bytes2Aligned(blk + 64 * half + 32 + 4 * kq);
   const uint32_t qh = Load4Bytes2Aligned(blk + 128 + 32 * half + 4 * kq);
-  const uint32_t sc_lo = Load4Bytes2Aligned(blk + 192 + 8 * half);      // scales 0..3 of this half
-  const uint32_t sc_hi = Load4Bytes2Aligned(blk + 192 + 8 * half + 4);  // scales 4..7 of this half
+  const uint2 scw = Load8Bytes2Aligned(blk + 192 + 8 * half);  // scales 0..3 / 4..7 of this half
+  const uint32_t sc_lo = scw.x;
+  const uint32_t sc_hi = scw.y;
   const float d = HalfBitsToFloat(*reinterpret_cast<const uint16_t*>(blk + 208));
   const int is = kq >> 2;  // (l >> 4) for l = 4kq..4kq+3
 #pragma unroll
@@ -122,6 +131,7 @@ struct QuantTraits;
 template <>
 struct QuantTraits<kGgmlQ4_K> {
   static constexpr int kLanes = 32;
+  static constexpr int kWaveTok = 2;           // token gathers: GatherWaveKernel, 2 tokens per workgroup
   static constexpr bool kStoreThrough = true;  // measured faster at n = 2811 (~4.6 vs ~5.0 us)
   static constexpr bool kVectorId = false;     // token id through a scalar load (GatherRowsKernel)
   static constexpr int64_t kBytes = kQ4KBlockBytes;
@@ -139,6 +149,7 @@ struct QuantTraits<kGgmlQ4_K> {
 template <>
 struct QuantTraits<kGgmlQ6_K> {
   static constexpr int kLanes = 16;
+  static constexpr int kWaveTok = 0;           // token gathers: GatherRowsKernel
   static constexpr bool kStoreThrough = true;  // ~0.2 us faster at n = 2811 with launches queued back to back
   static constexpr bool kVectorId = true;      // token id through a vector load (GatherRowsKernel)
   static constexpr int64_t kBytes = kQ6KBlockBytes;
@@ -221,6 +232,103 @@ __global__ __launch_bounds__(1024) void GatherRowsKernel(const uint8_t* __restri
   }
 }
 
+// Gather with one wave per token (kTok tokens per workgroup): 8 lanes per
+// super-block, lane kq covering the elements 4kq..4kq+3 of every 32-element
+// sub-block, so each store instruction of the block's 8 lanes writes one whole
+// 128-byte line. A lane issues all of its block's loads before it decodes and
+// stores. Rows wider than 8 blocks loop (lane block b, b + 8, ...). Workgroups
+// hold kTok waves, so 2811 tokens are 2811 waves: every token's id load and row
+// loads are in flight at once on 256 CUs, where one workgroup of 8 x 32 lanes
+// per token leaves a second round of workgroups waiting for a slot.
+__device__ __forceinline__ void DecodeQ4KLane8(const uint8_t* blk, int kq, const ThroughOut& put) {
+  const uint4 hdr = *reinterpret_cast<const uint4*>(blk);
+  uint32_t qw[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) qw[g] = *reinterpret_cast<const uint32_t*>(blk + 16 + 32 * g + 4 * kq);
+  const float d = HalfBitsToFloat(hdr.x & 0xFFFFu);
+  const float dmin = HalfBitsToFloat(hdr.x >> 16);
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    uint32_t sc0, m0, sc1, m1;
+    ScaleMinK4(2 * g, hdr.y, hdr.z, hdr.w, &sc0, &m0);
+    ScaleMinK4(2 * g + 1, hdr.y, hdr.z, hdr.w, &sc1, &m1);
+    const float d1 = d * static_cast<float>(sc0);
+    const float n1 = dmin * static_cast<float>(m0);
+    const float d2 = d * static_cast<float>(sc1);
+    const float n2 = dmin * static_cast<float>(m1);
+    float lo[4], hi[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      lo[b] = d1 * static_cast<float>((qw[g] >> (8 * b)) & 0xFu) - n1;
+      hi[b] = d2 * static_cast<float>((qw[g] >> (8 * b + 4)) & 0xFu) - n2;
+    }
+    put(64 * g + 4 * kq, make_float4(lo[0], lo[1], lo[2], lo[3]));
+    put(64 * g + 32 + 4 * kq, make_float4(hi[0], hi[1], hi[2], hi[3]));
+  }
+}
+
+__device__ __forceinline__ void DecodeQ6KLane8(const uint8_t* blk, int kq, const ThroughOut& put) {
+  uint32_t ql0[2], ql1[2], qh[2], sc_lo[2], sc_hi[2];
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+    ql0[half] = Load4Bytes2Aligned(blk + 64 * half + 4 * kq);
+    ql1[half] = Load4Bytes2Aligned(blk + 64 * half + 32 + 4 * kq);
+    qh[half] = Load4Bytes2Aligned(blk + 128 + 32 * half + 4 * kq);
+    const uint2 scw = Load8Bytes2Aligned(blk + 192 + 8 * half);
+    sc_lo[half] = scw.x;
+    sc_hi[half] = scw.y;
+  }
+  const float d = HalfBitsToFloat(*reinterpret_cast<const uint16_t*>(blk + 208));
+  const int is = kq >> 2;
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int quarter = 0; quarter < 4; ++quarter) {
+      const int si = is + 2 * quarter;
+      const int8_t sc = static_cast<int8_t>(ByteOf(si < 4 ? sc_lo[half] : sc_hi[half], si & 3));
+      const float ds = d * static_cast<float>(sc);
+      const uint32_t qlw = (quarter & 1) ? ql1[half] : ql0[half];
+      const int nib_shift = quarter < 2 ? 0 : 4;
+      float y[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const uint32_t nib = (qlw >> (8 * b + nib_shift)) & 0xFu;
+        const uint32_t hi2 = (ByteOf(qh[half], b) >> (2 * quarter)) & 3u;
+        const int q = static_cast<int>(nib | (hi2 << 4)) - 32;
+        y[b] = ds * static_cast<float>(q);
+      }
+      put(128 * half + 32 * quarter + 4 * kq, make_float4(y[0], y[1], y[2], y[3]));
+    }
+  }
+}
+
+template <uint32_t kType, int kTok>
+__global__ __launch_bounds__(64 * kTok) void GatherWaveKernel(const uint8_t* __restrict__ emb, int64_t rows,
+                                                              int64_t row_bytes, int32_t nb,
+                                                              const int32_t* __restrict__ toks, int64_t seq,
+                                                              float* __restrict__ x) {
+  const int lane = threadIdx.x & 63;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kTok + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (t >= seq) return;  // no barriers below
+  const int64_t tok = static_cast<int64_t>(toks[t]);
+  const bool valid = tok >= 0 && tok < rows;
+  const uint8_t* row = emb + (valid ? tok : 0) * row_bytes;
+  const uint32_t row_out_bytes = static_cast<uint32_t>(nb) * static_cast<uint32_t>(kQK_K * sizeof(float));
+  const __amdgpu_buffer_rsrc_t rs = dev::OutResource(x + t * nb * kQK_K, row_out_bytes);
+  const int kq = lane & 7;
+  for (int32_t b = lane >> 3; b < nb; b += 8) {
+    const ThroughOut put{rs, static_cast<uint32_t>(b) * static_cast<uint32_t>(kQK_K * sizeof(float))};
+    if (!valid) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) put(32 * i + 4 * kq, make_float4(0.f, 0.f, 0.f, 0.f));
+    } else if constexpr (kType == kGgmlQ4_K) {
+      DecodeQ4KLane8(row + b * kQ4KBlockBytes, kq, put);
+    } else {
+      DecodeQ6KLane8(row + b * kQ6KBlockBytes, kq, put);
+    }
+  }
+}
+
 // F32 tables: rows are plain floats; one float4 per thread.
 __global__ __launch_bounds__(kBlock) void GatherF32Kernel(const float* __restrict__ emb, int64_t rows, int64_t cols,
                                                           const int32_t* __restrict__ toks, int64_t total4,
@@ -259,6 +367,23 @@ __global__ __launch_bounds__(kBlock) void F16SweepKernel(float* out) {
   if (i < 65536) out[i] = HalfBitsToFloat(static_cast<uint32_t>(i));
 }
 
+// GatherWaveKernel for the token gathers of type kType when its traits ask for it.
+template <uint32_t kType>
+bool LaunchGatherWave(const uint8_t* emb, int64_t rows, int64_t row_bytes, int64_t nb, const int32_t* toks,
+                      int64_t seq, float* x, const char* name) {
+  constexpr int kTok = QuantTraits<kType>::kWaveTok;
+  if constexpr (kTok == 0) {
+    return false;
+  } else {
+    RPG_CHECK(seq <= 0x7FFFFFFFLL * kTok, "too many tokens: %lld", static_cast<long long>(seq));
+    RPG_CHECK(nb <= 0xFFFFFFFFLL / (kQK_K * sizeof(float)), "row of %lld blocks is too wide for one output resource",
+              static_cast<long long>(nb));
+    Launch(name, GatherWaveKernel<kType, kTok>, dim3(static_cast<unsigned>((seq + kTok - 1) / kTok)), dim3(64 * kTok),
+           emb, rows, row_bytes, static_cast<int32_t>(nb), toks, seq, x);
+    return true;
+  }
+}
+
 // Shared launcher for the gather and the single-row dequant (toks == nullptr,
 // rows == 1, seq == 1, cols == n_elems).
 void LaunchGather(uint32_t type, const uint8_t* emb, int64_t rows, int64_t cols, const int32_t* toks, int64_t seq,
@@ -270,6 +395,14 @@ void LaunchGather(uint32_t type, const uint8_t* emb, int64_t rows, int64_t cols,
   if (seq <= 0) return;
   const int64_t total = seq * cols;
   const int64_t nb64 = cols / kQK_K;
+  if (toks != nullptr && type == kGgmlQ4_K && Aligned(emb, 16) && Aligned(x, 16) &&
+      LaunchGatherWave<kGgmlQ4_K>(emb, rows, row_bytes, nb64, toks, seq, x, "GatherQ4KKernel")) {
+    return;
+  }
+  if (toks != nullptr && type == kGgmlQ6_K && Aligned(emb, 2) && Aligned(x, 16) &&
+      LaunchGatherWave<kGgmlQ6_K>(emb, rows, row_bytes, nb64, toks, seq, x, "GatherQ6KKernel")) {
+    return;
+  }
   if (toks != nullptr && type == kGgmlQ4_K && nb64 * 32 <= 1024 && Aligned(emb, 16) && Aligned(x, 16)) {
     RPG_CHECK(seq <= 0x7FFFFFFF, "too many tokens: %lld", static_cast<long long>(seq));
     Launch("GatherQ4KKernel", GatherRowsKernel<kGgmlQ4_K>, dim3(static_cast<unsigned>(seq)),
