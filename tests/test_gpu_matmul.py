@@ -85,7 +85,9 @@ SHAPES = [
     (12, 300, 16384, 1),     # 64 blocks per row: the widest LDS-staged decode
     (14, 100, 20480, 1),     # 80 blocks per row: the tiled kernel
     (12, 40000, 2048, 1),    # 4 rows per wave
-    (14, 40001, 2048, 1),    # 4 rows per wave, ragged last wave
+    (14, 40001, 2048, 1),    # Q6_K on the matrix cores, ragged last tile of 16 rows
+    (14, 16384, 2048, 1),    # ... the smallest such matrix, whole tiles
+    (14, 16393, 2560, 1),    # ... 10 blocks per row (4B width), ragged tile
     (12, 2048, 2048, 2),
     (14, 2048, 2048, 3),
     (12, 1000, 2048, 4),
@@ -146,6 +148,34 @@ def test_matmul_quant_lm_head_shape(gpu, ora):
     out2 = torch.empty_like(out)
     gpu.GpuMatMulQuant(gpu.GpuTensor(wd, t, rows, cols), dev(x), 1, out2)
     assert np.array_equal(host(out2).view(np.uint32), got.view(np.uint32))
+
+
+@pytest.mark.parametrize("scale", [0.0, 1e-30, 1e30, "outlier"])
+def test_matmul_q6k_matrix_core_decode_activation_range(gpu, ora, scale):
+    """The matrix-core Q6_K decode splits x 2^k into two fp16 terms with 2^k chosen
+    from max |x|: all-zero rows, tiny and huge activations and one outlier 2^20
+    times the rest all stay within the summation bound."""
+    import torch
+
+    t, rows, cols = 14, 16400, 2048
+    case(f"matmul Q6_K matrix-core decode, activations x {scale}")
+    rng = np.random.default_rng(791)
+    w = synth.quant_table(rng, t, rows, cols)
+    x = rng.normal(0, 1, (1, cols)).astype(np.float32)
+    if scale == "outlier":
+        x[0, 77] = 2.0 ** 20
+    else:
+        x = (x * np.float32(scale)).astype(np.float32)
+    out = torch.full((1, rows), np.nan, dtype=torch.float32, device="cuda")
+    gpu.profile_start(4)
+    gpu.GpuMatMulQuant(gpu.GpuTensor(dev(w), t, rows, cols), dev(x), 1, out)
+    gpu.profile_stop()
+    assert "MatVecMfmaQ6KKernel" in gpu.profile_report()
+    exact, absdot = ora.matmul_quant_f64(t, w, rows, cols, x)
+    got = host(out)
+    if scale == 0.0:
+        assert np.all(got == 0.0)
+    check(got, exact, absdot, cols)
 
 
 @pytest.mark.parametrize("t,w_off,x_off", [(12, 4, 0), (14, 1, 0), (14, 2, 0), (12, 0, 1), (0, 0, 0), (0, 4, 3)])

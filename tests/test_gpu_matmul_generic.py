@@ -52,6 +52,8 @@ CASES = [
     ("decode Q4_K, 4 rows per wave", Q4_K, 32768, 2048, 1, "MatVecQ4KKernel"),
     ("decode Q6_K", Q6_K, 1024, 2048, 1, "MatVecQ6KKernel"),
     ("decode Q6_K, split columns", Q6_K, 2048, 6144, 1, "MatVecSplitQ6KKernel"),
+    ("decode Q6_K on the matrix cores, ragged tile", Q6_K, 16400, 2048, 1, "MatVecMfmaQ6KKernel"),
+    ("decode Q6_K on the matrix cores, 10 blocks per row", Q6_K, 16384, 2560, 1, "MatVecMfmaQ6KKernel"),
     ("decode Q4_K, split columns", Q4_K, 1024, 4096, 1, "MatVecSplitQ4KKernel"),
     ("small batch Q4_K", Q4_K, 2048, 2048, 8, "MatMulQ4KKernel"),
     ("small batch Q6_K", Q6_K, 1024, 2048, 5, "MatMulQ6KKernel"),
