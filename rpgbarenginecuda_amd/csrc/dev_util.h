@@ -175,6 +175,22 @@ __device__ __forceinline__ void StoreBufU4(__amdgpu_buffer_rsrc_t rs, uint32_t b
   __builtin_amdgcn_raw_buffer_store_b128(w, rs, static_cast<int>(byte_off), 0, kPolicy);
 }
 
+template <int kPolicy>
+__device__ __forceinline__ void StoreBufU2(__amdgpu_buffer_rsrc_t rs, uint32_t byte_off, uint2 v) {
+  const U32x2 w = {v.x, v.y};
+  __builtin_amdgcn_raw_buffer_store_b64(w, rs, static_cast<int>(byte_off), 0, kPolicy);
+}
+
+// 8-byte buffer load with an explicit cache policy; with sc1 (16) the load is
+// device-coherent: it returns what a device-scope store from another XCD left,
+// not a stale line of this XCD's L2.
+template <int kPolicy>
+__device__ __forceinline__ uint2 LoadBufU2(__amdgpu_buffer_rsrc_t rs, uint32_t byte_off) {
+  const U32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs, static_cast<int>(byte_off), 0, kPolicy);
+  return make_uint2(v.x, v.y);
+}
+constexpr int kLoadDevicePolicy = 16;  // sc1
+
 __device__ __forceinline__ void StoreDeviceThrough4(__amdgpu_buffer_rsrc_t rs, uint32_t byte_off, float4 v) {
   StoreBuf4<kStoreDeviceThroughPolicy>(rs, byte_off, v);
 }

@@ -355,6 +355,118 @@ __global__ __launch_bounds__(kBlockThreads) void AttnMergeRowsKernel(const float
 // rounded to fp16. The wave of the chunk that holds pos stores the new K / V
 // rows into the cache and uses them for that key straight from LDS (the store
 // need not be visible to its own loads); the other chunks never read key pos.
+constexpr int kMaxFusedGroups = 32;
+// uint32 slots between two (token, kv head) pairs' arrival counters: one counter
+// per 256 bytes. Packed counters (8 pairs in one 32-byte line) serialized the
+// pairs' atomics on one line: 13.8 against 11.7 us at 4096 positions.
+constexpr int kCounterStride = 64;  // workgroups per pair in the one-launch decode: kMaxGroupChunks / kWaves
+
+// The merge of the fused grouped decode (AttnDecodeGroupKernel<G, kPrep, true>),
+// reached by every wave of a workgroup with at least two live chunks per pair.
+// Partials are rows of kPartFloats: o[128], m, l.
+template <int G>
+__device__ __forceinline__ void FusedMerge(float (*wpart)[G][kPartFloats], int* last_flag, const float (&m)[G],
+                                           const float (&l)[G], const float (&o)[G][8], int lane, int wave, int r,
+                                           int rho, int64_t t, int32_t kh, int32_t n_heads, int32_t n_kv_heads,
+                                           int32_t n_groups, int32_t live_groups, int32_t grp,
+                                           float* __restrict__ out, float* __restrict__ part,
+                                           uint32_t* __restrict__ cnt) {
+  // 1. the workgroup's chunks, in chunk order: wave w's (m, l, o) to LDS, then wave hh < G merges head hh
+  if (r == 0) {
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) {
+      *reinterpret_cast<float4*>(&wpart[wave][hh][8 * rho]) = make_float4(o[hh][0], o[hh][1], o[hh][2], o[hh][3]);
+      *reinterpret_cast<float4*>(&wpart[wave][hh][8 * rho + 4]) = make_float4(o[hh][4], o[hh][5], o[hh][6], o[hh][7]);
+      if (rho == 0) {
+        wpart[wave][hh][kD] = m[hh];
+        wpart[wave][hh][kD + 1] = l[hh];
+      }
+    }
+  }
+  __syncthreads();
+  const int hh = wave;
+  const int64_t th = t * n_heads + static_cast<int64_t>(kh) * G + hh;
+  if (hh < G) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, wpart[w][hh][kD]);
+    float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float mw = wpart[w][hh][kD];
+      const float f = mw == -INFINITY ? 0.0f : expf(mw - mx);
+      L = __builtin_fmaf(wpart[w][hh][kD + 1], f, L);
+      const float2 v = *reinterpret_cast<const float2*>(&wpart[w][hh][2 * lane]);
+      o0 = __builtin_fmaf(v.x, f, o0);
+      o1 = __builtin_fmaf(v.y, f, o1);
+    }
+    if (live_groups == 1) {  // one workgroup holds every live chunk: the output directly
+      const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+      *reinterpret_cast<float2*>(out + th * kD + 2 * lane) = make_float2(o0 * inv, o1 * inv);
+      return;
+    }
+    const __amdgpu_buffer_rsrc_t rs =
+        dev::OutResource(part + (th * n_groups + grp) * kPartFloats, kPartFloats * sizeof(float));
+    dev::StoreBufU2<dev::kStoreDeviceThroughPolicy>(rs, 8u * lane, make_uint2(__float_as_uint(o0), __float_as_uint(o1)));
+    if (lane == 0) {
+      dev::StoreBufU2<dev::kStoreDeviceThroughPolicy>(rs, 4u * kD, make_uint2(__float_as_uint(mx), __float_as_uint(L)));
+    }
+    // The stores are device-scope write-through: once they are acknowledged they
+    // are visible to every XCD, so waiting for them stands in for an agent-scope
+    // release fence (whose L2 write-back, one per workgroup, cost more than the
+    // separate merge launch). The clobber keeps the compiler from moving memory
+    // accesses across the wait.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+  if (live_groups == 1) return;  // uniform over the workgroup
+  // 2. count the workgroup in; the last of the pair's live workgroups merges them all
+  __syncthreads();
+  uint32_t* counter = cnt + (t * n_kv_heads + kh) * kCounterStride;
+  if (threadIdx.x == 0) {
+    const uint32_t before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *last_flag = before == static_cast<uint32_t>(live_groups - 1);
+  }
+  __syncthreads();
+  if (!*last_flag) return;  // uniform over the workgroup
+  if (hh < G) {
+    // Device-coherent (sc1) loads of the partials, issued after the barrier that
+    // follows the counter's atomic: every other workgroup's stores were
+    // acknowledged before its atomic. Lane i < live_groups holds group i's (m, l);
+    // every lane then walks the groups for its two dims.
+    const __amdgpu_buffer_rsrc_t rs = dev::OutResource(part + th * n_groups * kPartFloats,
+                                                       static_cast<uint32_t>(live_groups) * kPartFloats * sizeof(float));
+    auto load2 = [&](int g, int off) {
+      const uint2 u = dev::LoadBufU2<dev::kLoadDevicePolicy>(rs, 4u * static_cast<uint32_t>(g * kPartFloats + off));
+      return make_float2(__uint_as_float(u.x), __uint_as_float(u.y));
+    };
+    const bool has = lane < live_groups;
+    const float2 ml = has ? load2(lane, kD) : make_float2(-INFINITY, 0.0f);
+    const float mx = WaveMax(ml.x);
+    const float f = ml.x == -INFINITY ? 0.0f : expf(ml.x - mx);
+    const float L = WaveSumF(ml.y * f);
+    // every group's rows requested at once (one memory round trip), then summed in group order
+    static_assert(kMaxGroupChunks / kWaves <= kMaxFusedGroups, "a pair has at most kMaxFusedGroups workgroups");
+    float2 v[kMaxFusedGroups];
+#pragma unroll
+    for (int g = 0; g < kMaxFusedGroups; ++g) {
+      if (g < live_groups) v[g] = load2(g, 2 * lane);  // uniform
+    }
+    float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+    for (int g = 0; g < kMaxFusedGroups; ++g) {
+      if (g < live_groups) {
+        const float fg = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(f), g));
+        o0 = __builtin_fmaf(v[g].x, fg, o0);
+        o1 = __builtin_fmaf(v[g].y, fg, o1);
+      }
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    *reinterpret_cast<float2*>(out + th * kD + 2 * lane) = make_float2(o0 * inv, o1 * inv);
+  }
+  // every workgroup of the pair has counted in: ready for the next call
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 struct DecodePrep {
   const float* k;
   const float* v;
@@ -367,32 +479,59 @@ struct DecodePrep {
   uint16_t* v_store;
 };
 
-template <int G, bool kPrep = false>
+// kFused: one launch also merges. A workgroup takes kWaves consecutive chunks of
+// one (token, kv head); its waves' (m, l, o) meet in LDS and the workgroup stores
+// one partial per query head; the workgroup whose vector atomic on the pair's
+// counter (cnt[(t * n_kv_heads + kh) * kCounterStride]) arrives last merges the
+// partials of all the pair's workgroups into out and puts the counter back to
+// zero for the next call. With one live workgroup per pair there are no partials
+// (part may be null) and that workgroup writes out directly.
+// The partials go out device-scope write-through and are acknowledged before the
+// atomic; the merging workgroup reads them with device-coherent loads. No wave
+// waits on another workgroup: the first workgroups to finish just leave.
+template <int G, bool kPrep = false, bool kFused = false>
 __global__ __launch_bounds__(kBlockThreads) void AttnDecodeGroupKernel(
     const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t max_seq,
     int32_t n_heads, int32_t n_kv_heads, float scale, int64_t pos0_val, const int64_t* __restrict__ pos0_dev,
     int64_t seq, int32_t n_chunks, int64_t chunk_len, float* __restrict__ out, float* __restrict__ part,
-    DecodePrep prep) {
+    DecodePrep prep, uint32_t* __restrict__ cnt) {
   static_assert(!kPrep || G + 2 <= 8, "q heads, k and v: one 8-lane group each");
+  static_assert(!kFused || G <= kWaves, "the fused merge gives each query head of the group one wave");
   struct PrepLds {
     float q[G][kD];
     uint16_t k[kD];
     uint16_t v[kD];
   };
   __shared__ __attribute__((aligned(16))) PrepLds prep_lds[kPrep ? kWaves : 1];
+  __shared__ __attribute__((aligned(16))) float wpart[kFused ? kWaves : 1][kFused ? G : 1][kPartFloats];
+  __shared__ int last_flag;
   const int lane = threadIdx.x & 63;
-  const int64_t unit = static_cast<int64_t>(blockIdx.x) * kWaves + (threadIdx.x >> 6);
-  if (unit >= seq * n_kv_heads * n_chunks) return;  // no barriers below
-  const int64_t tk = unit / n_chunks;
-  const int32_t c = static_cast<int32_t>(unit - tk * n_chunks);
+  const int wave = threadIdx.x >> 6;
+  const int32_t n_groups = kFused ? (n_chunks + kWaves - 1) / kWaves : 1;
+  int64_t tk;
+  int32_t c;
+  if constexpr (kFused) {
+    tk = static_cast<int64_t>(blockIdx.x) / n_groups;
+    if (tk >= seq * n_kv_heads) return;  // uniform over the workgroup
+    c = (static_cast<int32_t>(blockIdx.x - tk * n_groups)) * kWaves + wave;
+  } else {
+    const int64_t unit = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
+    if (unit >= seq * n_kv_heads * n_chunks) return;  // no barriers below
+    tk = unit / n_chunks;
+    c = static_cast<int32_t>(unit - tk * n_chunks);
+  }
   const int64_t t = tk / n_kv_heads;
   const int32_t kh = static_cast<int32_t>(tk - t * n_kv_heads);
   const int64_t pos = ReadPos0(pos0_val, pos0_dev) + t;
   const int32_t live = LiveChunks(pos, chunk_len, n_chunks);
-  if (c >= live) return;  // no key of this chunk is visible at this position
+  const int32_t live_groups = kFused ? (live + kWaves - 1) / kWaves : 0;
+  if (kFused && c / kWaves >= live_groups) return;  // the whole workgroup: no visible key (uniform)
+  // kFused: a wave past the live chunks keeps m = -inf, l = 0, o = 0 and joins the barriers
+  const bool dead = c >= live;
+  if (!kFused && dead) return;  // no key of this chunk is visible at this position
   if (live == 1) part = nullptr;
-  const int64_t lo = static_cast<int64_t>(c) * chunk_len;
-  int64_t hi = lo + chunk_len;
+  const int64_t lo = dead ? 0 : static_cast<int64_t>(c) * chunk_len;
+  int64_t hi = dead ? 0 : lo + chunk_len;
   if (hi > pos + 1) hi = pos + 1;
   if (hi > max_seq) hi = max_seq;  // only reachable through a replayed graph with a bad staged pos0
   const int rho = lane & 15;
@@ -415,11 +554,11 @@ __global__ __launch_bounds__(kBlockThreads) void AttnDecodeGroupKernel(
     }
   };
   uint4 kw[8], vw[8];
-  if (kPipe) load_slab(lo, kw, vw);
+  if (kPipe && !dead) load_slab(lo, kw, vw);
 
   float qv[G][8];
   uint4 knew = make_uint4(0u, 0u, 0u, 0u), vnew = make_uint4(0u, 0u, 0u, 0u);
-  if (kPrep) {
+  if (kPrep) {  // a dead wave (kFused) runs it too and stores nothing: writer is false there
     PrepLds& P = prep_lds[threadIdx.x >> 6];
     const int g = lane >> 3;
     const int hl = lane & 7;
@@ -584,6 +723,12 @@ __global__ __launch_bounds__(kBlockThreads) void AttnDecodeGroupKernel(
       o[hh][j] += __shfl_xor(o[hh][j], 16, 64);
       o[hh][j] += __shfl_xor(o[hh][j], 32, 64);
     }
+  }
+  if constexpr (kFused) {
+    if (live > 1) return FusedMerge<G>(wpart, &last_flag, m, l, o, lane, wave, r, rho, t, kh, n_heads, n_kv_heads,
+                                        n_groups, live_groups, c / kWaves, out, part, cnt);
+    // one live chunk: its wave writes the output (the other waves are dead)
+    if (dead) return;
   }
   if (r != 0) return;
 #pragma unroll
@@ -983,11 +1128,51 @@ float* ScratchForCurrentDevice() {
   return t.ptr[dev];
 }
 
+// Arrival counters of the one-launch split decode (AttnDecodeGroupKernel<G, kPrep,
+// true>), one per (token, kv head) pair: zero at load, counted up by the pair's
+// workgroups and put back to zero by the last of them, so they are zero between
+// launches and a captured graph replays them as they are. The first half serves
+// the allocating entry points, the second the no-allocation one. A split needs
+// fewer than 2048 pairs (PlanGroupChunks gives one chunk from 2048 on).
+constexpr int64_t kFusedCounterPairs = 2048;
+static __device__ __align__(256) uint32_t pair_counters[2 * kFusedCounterPairs * kCounterStride];
+
+struct CounterTable {
+  std::mutex mu;
+  uint32_t* ptr[kMaxScratchDevices] = {};
+};
+CounterTable& CounterTableInstance() {
+  static CounterTable* t = new CounterTable();
+  return *t;
+}
+
+// Device address of `pair_counters` on the current device, looked up once per device.
+uint32_t* CountersForCurrentDevice() {
+  int dev = -1;
+  RPG_HIP_CHECK(hipGetDevice(&dev));
+  RPG_CHECK(dev >= 0 && dev < kMaxScratchDevices, "device %d is beyond the %d devices the counter table tracks", dev,
+            kMaxScratchDevices);
+  CounterTable& t = CounterTableInstance();
+  std::lock_guard<std::mutex> lock(t.mu);
+  if (t.ptr[dev] == nullptr) {
+    void* p = nullptr;
+    RPG_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(pair_counters)));
+    RPG_CHECK(p != nullptr, "hipGetSymbolAddress returned no address for the attention counters on device %d", dev);
+    t.ptr[dev] = static_cast<uint32_t*>(p);
+  }
+  return t.ptr[dev];
+}
+
 // Where a split-key launch keeps its chunk partials: the library's grow-only
 // buffer (fixed == nullptr) or a fixed region that must already be big enough.
+// The one-launch decode also takes its arrival counters from here.
 struct PartialsSink {
   float* fixed = nullptr;
   size_t fixed_floats = 0;
+
+  uint32_t* Counters() const {
+    return CountersForCurrentDevice() + (fixed == nullptr ? 0 : kFusedCounterPairs * kCounterStride);
+  }
 
   float* Get(size_t floats) const {
     if (fixed == nullptr) return EnsurePartials(floats);
@@ -1046,6 +1231,15 @@ void PlanGroupChunks(int64_t units, int64_t positions, int32_t* n_chunks, int64_
 // kMaxGroupChunks chunks): what a captured decode graph may replay.
 size_t WarmupFloats(int64_t /*positions*/) { return static_cast<size_t>(64) * kMaxGroupChunks * kPartFloats; }
 
+// Split grouped decode in one launch (merge by the last workgroup of each pair)
+// up to this position budget, the chunk kernel plus AttnMergeKernel above it.
+// Measured on MI355X, Qwen3-1.7B decode (8 kv heads), kernel time per call: one
+// launch 9.0 / 9.7 / 11.7 us at positions 512 / 2048 / 4096, two launches 9.6 /
+// 9.9 / 11.0 us. Past ~3000 positions a pair has over 24 workgroups, and the
+// serialized atomics on its counter and the last workgroup's longer merge cost
+// more than the second launch.
+constexpr int64_t kFusedMaxPositions = 3072;
+
 template <int G>
 void LaunchDecodeGroup(const ModelMeta& c, const Pos0Arg& p0, const float* q_dev, int64_t seq,
                        const uint16_t* k_layer, const uint16_t* v_layer, int64_t max_seq, float scale,
@@ -1055,17 +1249,38 @@ void LaunchDecodeGroup(const ModelMeta& c, const Pos0Arg& p0, const float* q_dev
   int64_t chunk_len;
   PlanGroupChunks(seq * c.n_kv_heads, positions, &n_chunks, &chunk_len);
   const int64_t pairs = seq * c.n_heads;
+  if (n_chunks > 1 && positions <= kFusedMaxPositions) {
+    // one launch: workgroups of kWaves chunks, merged by the pair's last workgroup
+    const int64_t kv_pairs = seq * c.n_kv_heads;
+    RPG_CHECK(kv_pairs <= kFusedCounterPairs, "a split decode over %lld (token, kv head) pairs exceeds the %lld "
+              "arrival counters", static_cast<long long>(kv_pairs), static_cast<long long>(kFusedCounterPairs));
+    const int32_t n_groups = (n_chunks + kWaves - 1) / kWaves;
+    // one workgroup per pair holds every chunk: it merges in LDS and needs no partials
+    float* part = n_groups > 1 ? sink.Get(static_cast<size_t>(pairs) * n_groups * kPartFloats) : nullptr;
+    uint32_t* cnt = sink.Counters();
+    const dim3 grid(static_cast<unsigned>(kv_pairs * n_groups));
+    if (prep != nullptr) {
+      Launch("AttnDecodePrepFusedKernel", AttnDecodeGroupKernel<G, true, true>, grid, dim3(kBlockThreads), q_dev,
+             k_layer, v_layer, max_seq, c.n_heads, c.n_kv_heads, scale, p0.value, p0.dev, seq, n_chunks, chunk_len,
+             out_dev, part, *prep, cnt);
+    } else {
+      Launch("AttnDecodeFusedKernel", AttnDecodeGroupKernel<G, false, true>, grid, dim3(kBlockThreads), q_dev,
+             k_layer, v_layer, max_seq, c.n_heads, c.n_kv_heads, scale, p0.value, p0.dev, seq, n_chunks, chunk_len,
+             out_dev, part, DecodePrep{}, cnt);
+    }
+    return;
+  }
   float* part = nullptr;
   if (n_chunks > 1) part = sink.Get(static_cast<size_t>(pairs) * n_chunks * kPartFloats);
   const int64_t units = seq * c.n_kv_heads * n_chunks;
   if (prep != nullptr) {
     Launch("AttnDecodePrepKernel", AttnDecodeGroupKernel<G, true>, dim3(GridFor(units, kWaves)),
            dim3(kBlockThreads), q_dev, k_layer, v_layer, max_seq, c.n_heads, c.n_kv_heads, scale, p0.value, p0.dev,
-           seq, n_chunks, chunk_len, out_dev, part, *prep);
+           seq, n_chunks, chunk_len, out_dev, part, *prep, static_cast<uint32_t*>(nullptr));
   } else {
     Launch("AttnDecodeGroupKernel", AttnDecodeGroupKernel<G>, dim3(GridFor(units, kWaves)), dim3(kBlockThreads),
            q_dev, k_layer, v_layer, max_seq, c.n_heads, c.n_kv_heads, scale, p0.value, p0.dev, seq, n_chunks,
-           chunk_len, out_dev, part, DecodePrep{});
+           chunk_len, out_dev, part, DecodePrep{}, static_cast<uint32_t*>(nullptr));
   }
   if (n_chunks > 1) {
     Launch("AttnMergeKernel", AttnMergeKernel, dim3(static_cast<unsigned>(pairs)), dim3(kBlockThreads), part, pairs,
@@ -1197,7 +1412,10 @@ void GpuAttentionFromCacheNoAlloc(const ModelMeta& c, int64_t pos0, const float*
   AttentionFromCache(c, pos0, q_dev, seq, k_layer, v_layer, max_seq, out_dev, sh_positions, sink);
 }
 
-void GpuAttentionNoAllocInit() { (void)ScratchForCurrentDevice(); }
+void GpuAttentionNoAllocInit() {
+  (void)ScratchForCurrentDevice();
+  (void)CountersForCurrentDevice();
+}
 
 size_t GpuAttentionNoAllocScratchBytes() { return kNoAllocScratchFloats * sizeof(float); }
 
@@ -1262,6 +1480,7 @@ void GpuCausalAttention(const ModelMeta& c, const float* q_dev, const float* k_d
 void GpuAttentionWarmupShmem(int64_t sh_positions) {
   RPG_CHECK(sh_positions > 0, "attention warmup: the position budget has to be at least 1 (got %lld)", static_cast<long long>(sh_positions));
   EnsurePartials(WarmupFloats(sh_positions));
+  (void)CountersForCurrentDevice();
 }
 
 }  // namespace rpg

@@ -41,8 +41,11 @@ def test_noalloc_attention_matches_allocating_entry(gpu):
     rng = np.random.default_rng(77)
     # (name, n_heads, n_kv_heads, max_seq, pos0, seq): the first call splits the
     # keys into the most chunks, the second is smaller; both use the scratch.
-    calls = [("4B shape, decode at 4095, 2 tokens", 32, 8, 4096, 4094, 2),
-             ("1.7B shape, decode at 700", 16, 8, 4096, 700, 1)]
+    # Up to 3072 positions a split decode is one launch whose last workgroup per
+    # (token, kv head) merges; past that, the chunk kernel and a merge launch.
+    calls = [("4B shape, decode at 4095, 2 tokens (two launches)", 32, 8, 4096, 4094, 2),
+             ("1.7B shape, decode at 3000 (one launch, 24 workgroups per pair)", 16, 8, 3072, 3000, 1),
+             ("1.7B shape, decode at 700 (one launch)", 16, 8, 4096, 700, 1)]
     for name, nh, nkv, max_seq, pos0, seq in calls:
         _case(f"noalloc vs allocating: {name}")
         q, kc, vc = _inputs(rng, nh, nkv, max_seq, seq)
@@ -66,9 +69,10 @@ def test_noalloc_attention_rejects_oversized_split(gpu):
 
     lib = gpu.load_library()
     _case("noalloc rejects a split beyond its fixed scratch")
-    # GQA group 4 with 62 x 33 = 2046 (token, kv head) pairs: the split takes 2
-    # chunks, 62 x 132 heads x 2 chunks x 132 floats = 2160576 > 2^21.
-    nh, nkv, max_seq, pos0, seq = 132, 33, 2048, 1000, 62
+    # GQA group 4 with 62 x 33 = 2046 (token, kv head) pairs past 3072 positions
+    # (chunk kernel + merge launch): the split takes 2 chunks, 62 x 132 heads x 2
+    # chunks x 132 floats = 2160576 > 2^21.
+    nh, nkv, max_seq, pos0, seq = 132, 33, 3200, 3100, 62
     q = torch.zeros((seq, nh, 128), dtype=torch.float32, device="cuda")
     kc = torch.zeros((nkv, max_seq, 128), dtype=torch.int16, device="cuda")
     vc = torch.zeros_like(kc)
@@ -86,32 +90,42 @@ def test_noalloc_attention_rejects_oversized_split(gpu):
 
 def _group_partials_floats(units, group, positions):
     """Partials floats of a grouped decode call: chunks of a multiple of 32 keys,
-    enough for ~2048 waves over `units` (token, kv head) pairs, 132 floats per
-    (token, query head, chunk); no split at >= 2048 units or <= 128 positions."""
+    enough for ~2048 waves over `units` (token, kv head) pairs; no split at >= 2048
+    units or <= 128 positions. Up to 3072 positions (one launch) 132 floats per
+    (token, query head, workgroup of 4 chunks), none when one workgroup takes every
+    chunk; past that 132 floats per (token, query head, chunk)."""
     if units >= 2048 or positions <= 128:
         return 0
     want = min((2048 + units - 1) // units, 128)
     length = ((positions + want - 1) // want + 31) // 32 * 32
     chunks = (positions + length - 1) // length
-    return units * group * chunks * 132 if chunks > 1 else 0
+    if chunks <= 1:
+        return 0
+    if positions <= 3072:
+        groups = (chunks + 3) // 4
+        return units * group * groups * 132 if groups > 1 else 0
+    return units * group * chunks * 132
 
 
 def test_noalloc_attention_group4_boundary(gpu):
-    """GQA group 4 at 1985 (token, kv head) pairs fits the 2^21-float scratch and
-    matches the allocating entry bit for bit; 1986 pairs is rejected unlaunched."""
+    """GQA group 4 past 3072 positions (chunk kernel + merge launch): 45 x 44 =
+    1980 (token, kv head) pairs fit the 2^21-float scratch and match the allocating
+    entry bit for bit; 39 x 51 = 1989 pairs are rejected unlaunched. Below 3072
+    positions (one launch) the same 1989 pairs need no partials at all."""
     import torch
 
     lib = gpu.load_library()
     rng = np.random.default_rng(78)
-    max_seq, pos0 = 256, 200
-    # (seq, n_kv_heads): 5 x 397 = 1985 pairs, 6 x 331 = 1986 pairs
-    fits, over = (5, 397), (6, 331)
-    assert _group_partials_floats(fits[0] * fits[1], 4, pos0 + fits[0]) == 1985 * 1056 <= 1 << 21
-    assert _group_partials_floats(over[0] * over[1], 4, pos0 + over[0]) == 1986 * 1056 > 1 << 21
+    max_seq, pos0 = 3200, 3100
+    # (seq, n_kv_heads)
+    fits, over = (45, 44), (39, 51)
+    assert _group_partials_floats(fits[0] * fits[1], 4, pos0 + fits[0]) == 1980 * 1056 <= 1 << 21
+    assert _group_partials_floats(over[0] * over[1], 4, pos0 + over[0]) == 1989 * 1056 > 1 << 21
+    assert _group_partials_floats(over[0] * over[1], 4, 1000 + over[0]) == 0
 
     seq, nkv = fits
     nh = 4 * nkv
-    _case(f"noalloc group-4 boundary: seq {seq}, {nh}/{nkv} heads, 1985 pairs (fits)")
+    _case(f"noalloc group-4 boundary: seq {seq}, {nh}/{nkv} heads, 1980 pairs (fits)")
     q, kc, vc = _inputs(rng, nh, nkv, max_seq, seq)
     qd = torch.from_numpy(q).cuda()
     kd = torch.from_numpy(kc.view(np.int16)).cuda()
@@ -129,7 +143,7 @@ def test_noalloc_attention_group4_boundary(gpu):
 
     seq, nkv = over
     nh = 4 * nkv
-    _case(f"noalloc group-4 boundary: seq {seq}, {nh}/{nkv} heads, 1986 pairs (rejected)")
+    _case(f"noalloc group-4 boundary: seq {seq}, {nh}/{nkv} heads, 1989 pairs (rejected)")
     q = torch.zeros((seq, nh, 128), dtype=torch.float32, device="cuda")
     kc = torch.zeros((nkv, max_seq, 128), dtype=torch.int16, device="cuda")
     vc = torch.zeros_like(kc)
@@ -139,3 +153,19 @@ def test_noalloc_attention_group4_boundary(gpu):
     assert "no-allocation" in lib.rpg_ops_last_error().decode()
     torch.cuda.synchronize()
     assert bool(torch.all(out == 7.0)), "a rejected call must not launch"
+
+    # the same pairs at 1039 positions: one launch, no partials; the call goes through
+    pos0 = 1000
+    _case(f"noalloc group-4: seq {seq}, {nh}/{nkv} heads, 1989 pairs at {pos0} (one launch, accepted)")
+    gen = torch.Generator(device="cuda").manual_seed(79)
+    q = torch.randn((seq, nh, 128), generator=gen, device="cuda")
+    kc = torch.randn((nkv, max_seq, 128), generator=gen, device="cuda").half().view(torch.int16)
+    vc = torch.randn((nkv, max_seq, 128), generator=gen, device="cuda").half().view(torch.int16)
+    ref = torch.full((seq, nh, 128), float("nan"), dtype=torch.float32, device="cuda")
+    got = torch.full_like(ref, float("nan"))
+    assert _run(lib, lib.rpg_op_attention_from_cache, nh, nkv, pos0, seq, q, kc, vc, max_seq, ref) == 0
+    assert _run(lib, lib.rpg_op_attention_from_cache_noalloc, nh, nkv, pos0, seq, q, kc, vc, max_seq,
+                got) == 0, lib.rpg_ops_last_error()
+    torch.cuda.synchronize()
+    assert bool(torch.all(torch.isfinite(ref)))
+    assert torch.equal(ref.view(torch.int32), got.view(torch.int32))
