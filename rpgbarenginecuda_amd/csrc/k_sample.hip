@@ -8,26 +8,36 @@
 // 151936 floats and ~20 us for a pass that evaluates expf, so here every pass
 // is a grid of 1024-element slices (149 workgroups for Qwen3's vocabulary):
 //   * top_k's threshold and top_p's cut are radix selects over the 32-bit order
-//     keys with 12/12/8-bit digits: 3 passes instead of 32. Each workgroup
+//     keys with 12/12/8-bit digits. Level 1 is a histogram pass (each workgroup
 //     histograms its slice in LDS and adds the non-zero bins to a global
-//     histogram; every workgroup of the next kernel picks the digit from it
-//     (same data, same order, same answer) and workgroup 0 records the state;
+//     histogram). In the next pass every workgroup picks level 1's digit from it
+//     (same data, same order, same answer) and appends its keys with that digit
+//     to a candidate list; the workgroup that arrives last selects the other 20
+//     bits among the candidates in LDS. Two passes instead of 32;
 //   * top_p's S(t) is summed as integers, p * 2^62 truncated, so the histogram
 //     sums do not depend on the order of the atomics (they differ from the real
-//     sums by less than n * 2^-62);
+//     sums by less than n * 2^-62); the kept mass for the second normalisation
+//     comes from the same integers;
 //   * values that couple slices (max, sums, argmax) travel as per-slice
 //     partials that every workgroup of the next kernel reduces in one fixed
 //     order, so every result is the same from run to run;
+//   * "the last workgroup to arrive" is one vector atomic per workgroup on a
+//     counter that the last one puts back to zero; what it reads from the other
+//     workgroups was stored device-scope write-through and is loaded
+//     device-coherent. No workgroup ever waits for another (a grid barrier was
+//     measured at ~3 us per barrier over 149 workgroups, no cheaper than a launch);
 //   * the inverse transform keeps the serial double semantics exactly: a
 //     fixed-point prefix (p * 2^52 truncated) over slices and then within one
 //     slice finds the first index whose prefix exceeds u. The serial double sum
 //     differs from the exact prefix by at most n * 2^-53 * max(prefix), so when
 //     u is further than that (plus the truncation) from both neighbouring
 //     prefixes the serial loop picks the same index. Otherwise (u within
-//     ~1e-10 of a boundary) one thread runs the serial loop.
+//     ~1e-10 of a boundary) one thread runs the serial loop. The last workgroup
+//     of the normalising pass runs it.
 // Kernels, for T > 0 with top_p (the engine's default, top_k off):
-//   Prep -> Sum -> TopP x3 -> Cut -> Norm -> Inverse (8 launches);
-// top_k adds TopK x3 after Prep; without top_p the TopP and Cut kernels drop out.
+//   Prep -> Sum -> TopP -> TopPCand -> Norm (+ inverse transform): 5 launches;
+// top_k adds TopKCand after Prep (its level-1 histogram is built in Prep);
+// without top_p the TopP kernels drop out. GpuArgMax is one launch.
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
@@ -50,36 +60,39 @@ constexpr int kPerThread = kSlice / kThreads;
 constexpr int kMaxSlices = static_cast<int>(kSamplerMaxVocab / kSlice);
 constexpr int kPartsPerThread = kMaxSlices / kThreads;  // partials one thread reduces
 constexpr int kBins = 4096;                              // widest radix digit (12 bits)
+enum ArriveCounter { kArriveArgMax, kArriveTopK, kArriveTopP, kArriveFinal, kArriveCounters };
 
 // Radix levels: digit = (key >> shift) & (2^bits - 1); level L keeps only keys
 // whose bits above its digit equal the prefix chosen by the levels before it.
 __host__ __device__ constexpr int LevelShift(int level) { return level == 1 ? 20 : (level == 2 ? 8 : 0); }
 __host__ __device__ constexpr int LevelBits(int level) { return level == 3 ? 8 : 12; }
 
-struct KState {  // top_k select after a level: key prefix, rank still to find
-  uint32_t prefix;
-  uint32_t rem;
-};
-struct PState {  // top_p select after a level: key prefix, S below the prefix range, no-cut flag
-  uint64_t prefix;
-  uint64_t base;
-  uint64_t none;
-};
-
 struct SampleScratch {
   float max_part[kMaxSlices];
   double sum_part[kMaxSlices];
-  double sum2_part[kMaxSlices];
   float best_val[kMaxSlices];
   int32_t best_idx[kMaxSlices];
   uint64_t fix_part[kMaxSlices];
   double tot_part[kMaxSlices];
-  uint32_t khist[3][kBins];
-  uint64_t phist[3][kBins];
-  KState kstate[4];  // index = level
-  PState pstate[4];
-  uint32_t kth_key;
-  uint32_t cut_key;
+  uint32_t khist[kBins];  // top_k level-1 counts; zero between calls
+  uint64_t phist[kBins];  // top_p level-1 weights; zero between calls
+  uint32_t kth_key;       // top_k threshold key
+  uint32_t cut_key;       // top_p: keys <= cut_key are cut (0xFFFFFFFF: no cut)
+  uint64_t kept_w;        // top_p: Fix62 weight of the keys above the cut
+  // Counters of the passes whose last workgroup finishes the step (zero between
+  // calls: the last workgroup puts its counter back), one per 256 bytes.
+  uint32_t arrive[kArriveCounters][64];
+  uint32_t cand_count[kMaxSlices];  // candidates of each slice (at key[slice * kSlice ...])
+};
+
+// Candidate lists of the radix selects: the keys (and top_p weights) whose
+// level-1 digit equals the selected one, each slice's in its own region (slice
+// g at [g * kSlice, g * kSlice + cand_count[g])), resolved by the last
+// workgroup. Sized for the whole vocabulary (ties can make every value a
+// candidate).
+struct SampleCandidates {
+  uint32_t key[kSamplerMaxVocab];
+  uint64_t w[kSamplerMaxVocab];
 };
 
 // ---------------------------------------------------------------- random source
@@ -205,6 +218,46 @@ __device__ __forceinline__ uint64_t BlockExclScan(uint64_t v, uint64_t* sh, uint
   return before + incl - v;
 }
 
+// ---------------------------------------------------------------- hand-off to the last workgroup
+
+// Data that the last workgroup of the same launch reads crosses the XCDs'
+// separate L2s: it is stored device-scope write-through (a relaxed agent-scope
+// atomic store: a vector store with the sc1 policy), and the last workgroup
+// takes an agent-scope acquire fence (invalidating its stale L1 / L2 lines)
+// before its plain loads. kDev = false is the plain store, for data that a later
+// launch reads (a kernel boundary orders it).
+template <bool kDev, typename T>
+__device__ __forceinline__ void St(T* p, T v) {
+  if constexpr (kDev) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    *p = v;
+  }
+}
+
+// Called by every thread after its hand-off stores; returns true (uniformly) in
+// the workgroup whose count arrives last, which puts the counter back to zero.
+// Each wave waits for its stores to be acknowledged (device scope, so visible to
+// every XCD) before the barrier ahead of the count, with no release fence (its
+// L2 write-back costs more than the whole hand-off); the last workgroup takes an
+// acquire fence after the barrier behind it. No workgroup waits for another.
+// Measured against device-coherent (sc1) loads in the last workgroup instead of
+// the fence: 1-1.6 us faster per hand-off.
+__device__ bool ArriveLast(uint32_t* counter, int* flag) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = before == gridDim.x - 1;
+    if (last) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *flag = last;
+  }
+  __syncthreads();
+  if (*flag == 0) return false;
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  return true;
+}
+
 // Partials of all slices, reduced in one fixed order (identical in every workgroup).
 __device__ float MaxOfParts(const float* parts, int n_slices, float* sh) {
   float m = -INFINITY;
@@ -264,8 +317,10 @@ __device__ Pick PickDescending(const uint32_t* hist, uint32_t rem, uint64_t* sh,
 }
 
 // top_p: the smallest digit d with base + sum(digit <= d) > thr; carry = base + sum(digit < d).
+// *total_out (optional) gets the histogram's total.
 template <int kNumBins>
-__device__ Pick PickAscending(const uint64_t* hist, uint64_t base, uint64_t thr, uint64_t* sh, Pick* pick) {
+__device__ Pick PickAscending(const uint64_t* hist, uint64_t base, uint64_t thr, uint64_t* sh, Pick* pick,
+                              uint64_t* total_out = nullptr) {
   constexpr int kPer = kNumBins / kThreads;
   uint64_t h[kPer];
   uint64_t s = 0;
@@ -276,6 +331,7 @@ __device__ Pick PickAscending(const uint64_t* hist, uint64_t base, uint64_t thr,
   }
   uint64_t total;
   const uint64_t below = BlockExclScan(s, sh, &total);
+  if (total_out != nullptr) *total_out = total;
   if (threadIdx.x == 0) *pick = Pick{0, 0, 0};
   __syncthreads();
   if (base + below <= thr && base + below + s > thr) {
@@ -294,10 +350,7 @@ __device__ Pick PickAscending(const uint64_t* hist, uint64_t base, uint64_t thr,
   return r;
 }
 
-template <typename F>
-__device__ __forceinline__ auto PickLevel(int level, F&& f) {
-  return level == 3 ? f(std::integral_constant<int, 256>{}) : f(std::integral_constant<int, kBins>{});
-}
+
 
 // ---------------------------------------------------------------- value pipeline
 
@@ -308,10 +361,8 @@ struct Logits {
   int scale;    // temperature != 1
 };
 
-__device__ __forceinline__ float LoadV(const Logits& lg, int64_t i) {
-  const float v = lg.x[i];
-  return lg.scale ? v * lg.inv_t : v;
-}
+__device__ __forceinline__ float ScaleV(const Logits& lg, float raw) { return lg.scale ? raw * lg.inv_t : raw; }
+__device__ __forceinline__ float LoadV(const Logits& lg, int64_t i) { return ScaleV(lg, lg.x[i]); }
 
 struct ProbCtx {
   float mx;
@@ -320,17 +371,216 @@ struct ProbCtx {
   int topk;
 };
 
+__device__ __forceinline__ float MaskV(const ProbCtx& c, float v) { return (c.topk && v < c.kth) ? -INFINITY : v; }
 __device__ __forceinline__ float MaskedV(const Logits& lg, const ProbCtx& c, int64_t i) {
-  const float v = LoadV(lg, i);
-  return (c.topk && v < c.kth) ? -INFINITY : v;
+  return MaskV(c, LoadV(lg, i));
+}
+// p of a raw logit (the one formula every pass uses)
+__device__ __forceinline__ float ProbOfRaw(const Logits& lg, const ProbCtx& c, float raw) {
+  return expf(MaskV(c, ScaleV(lg, raw)) - c.mx) * c.inv;
 }
 __device__ __forceinline__ float ProbAt(const Logits& lg, const ProbCtx& c, int64_t i) {
-  return expf(MaskedV(lg, c, i) - c.mx) * c.inv;
+  return ProbOfRaw(lg, c, lg.x[i]);
 }
 
 __device__ __forceinline__ int NumSlices(int64_t n) { return static_cast<int>((n + kSlice - 1) / kSlice); }
 __device__ __forceinline__ int64_t ElemIndex(int j) {
   return static_cast<int64_t>(blockIdx.x) * kSlice + threadIdx.x + j * kThreads;
+}
+
+
+// ---------------------------------------------------------------- kernels
+
+// Per-slice max and first argmax of the (scaled) logits; with top_k also the
+// level-1 count histogram of their keys (bits 31..20), added to khist.
+__global__ __launch_bounds__(kThreads) void SamplePrepKernel(Logits lg, int32_t topk, SampleScratch* __restrict__ s) {
+  __shared__ uint32_t hist[kBins];
+  __shared__ Best shb[kWaves];
+  if (topk) {
+    for (int b = threadIdx.x; b < kBins; b += kThreads) hist[b] = 0;
+    __syncthreads();
+  }
+  Best b{-INFINITY, 0x7FFFFFFF};
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j) {
+    const int64_t i = ElemIndex(j);
+    if (i < lg.n) {
+      const float v = LoadV(lg, i);
+      if (v > b.v || (v == b.v && b.i == 0x7FFFFFFF)) b = Best{v, static_cast<int32_t>(i)};
+      if (topk) atomicAdd(&hist[OrderKey(v) >> LevelShift(1)], 1u);
+    }
+  }
+  b = BlockBest(b, shb);
+  if (threadIdx.x == 0) {
+    s->max_part[blockIdx.x] = b.v;
+    s->best_val[blockIdx.x] = b.v;
+    s->best_idx[blockIdx.x] = b.i;
+  }
+  if (topk) {
+    __syncthreads();
+    for (int k = threadIdx.x; k < kBins; k += kThreads) {
+      if (hist[k] != 0) atomicAdd(&s->khist[k], hist[k]);
+    }
+  }
+}
+
+// Stores this workgroup's elements that pass `match` in its slice's region of
+// the candidate list, and their number in cand_count (both device-coherent, for
+// the last workgroup).
+template <typename F>
+__device__ void StoreCandidates(const uint32_t (&key)[kPerThread], const uint64_t (&w)[kPerThread], F match,
+                                bool with_w, SampleScratch* s, SampleCandidates* cand, uint64_t* sh) {
+  uint64_t cnt = 0;
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j) cnt += match(j) ? 1 : 0;
+  uint64_t total;
+  uint32_t at = static_cast<uint32_t>(blockIdx.x) * kSlice + static_cast<uint32_t>(BlockExclScan(cnt, sh, &total));
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j) {
+    if (match(j)) {
+      St<true>(&cand->key[at], key[j]);
+      if (with_w) St<true>(&cand->w[at], w[j]);
+      ++at;
+    }
+  }
+  if (threadIdx.x == 0) St<true>(&s->cand_count[blockIdx.x], static_cast<uint32_t>(total));
+}
+
+// In the last workgroup: where each slice's candidates start in the compacted
+// (slice-order) list, into lstart; returns the number of candidates. When they
+// fit in LDS (kCap) they are copied there, keys to lkey and (kWithW) weights to
+// lw; otherwise every level reads them from their slices' regions.
+constexpr int kTopKCandLds = 8192;  // keys: 32 KB of LDS
+constexpr int kTopPCandLds = 4096;  // keys and weights: 48 KB
+__device__ __forceinline__ int SliceOf(const uint32_t* lstart, int n_slices, uint32_t i) {
+  int lo = 0, hi = n_slices - 1;  // the largest g with lstart[g] <= i
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (lstart[mid] <= i) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+template <bool kWithW, int kCap>
+__device__ uint32_t GatherCandidates(const SampleScratch* s, const SampleCandidates* cand, int n_slices,
+                                     uint32_t* lkey, uint64_t* lw, uint32_t* lstart, uint64_t* sh) {
+  // thread t owns slices [t * kPartsPerThread, ...)
+  uint32_t cnt[kPartsPerThread];
+  uint64_t mine = 0;
+#pragma unroll
+  for (int k = 0; k < kPartsPerThread; ++k) {
+    const int g = threadIdx.x * kPartsPerThread + k;
+    cnt[k] = g < n_slices ? s->cand_count[g] : 0u;
+    mine += cnt[k];
+  }
+  uint64_t total;
+  uint64_t at = BlockExclScan(mine, sh, &total);
+#pragma unroll
+  for (int k = 0; k < kPartsPerThread; ++k) {
+    const int g = threadIdx.x * kPartsPerThread + k;
+    if (g < n_slices) lstart[g] = static_cast<uint32_t>(at);
+    at += cnt[k];
+  }
+  __syncthreads();
+  const uint32_t n_c = static_cast<uint32_t>(total);
+  if (n_c <= kCap) {
+    // every address first, then every load in flight at once, then the LDS copies
+    constexpr int kItems = kCap / kThreads;
+    uint32_t at_g[kItems];
+#pragma unroll
+    for (int r = 0; r < kItems; ++r) {
+      const uint32_t i = threadIdx.x + static_cast<uint32_t>(r) * kThreads;
+      if (i < n_c) {
+        const int g = SliceOf(lstart, n_slices, i);
+        at_g[r] = static_cast<uint32_t>(g) * kSlice + (i - lstart[g]);
+      }
+    }
+    uint32_t kv[kItems];
+    uint64_t wv[kWithW ? kItems : 1];
+#pragma unroll
+    for (int r = 0; r < kItems; ++r) {
+      if (threadIdx.x + static_cast<uint32_t>(r) * kThreads < n_c) {
+        kv[r] = cand->key[at_g[r]];
+        if constexpr (kWithW) wv[r] = cand->w[at_g[r]];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kItems; ++r) {
+      const uint32_t i = threadIdx.x + static_cast<uint32_t>(r) * kThreads;
+      if (i < n_c) {
+        lkey[i] = kv[r];
+        if constexpr (kWithW) lw[i] = wv[r];
+      }
+    }
+    __syncthreads();
+  }
+  return n_c;
+}
+// Candidate i of the compacted list: from LDS when it was copied there, else
+// from its slice's region.
+template <bool kWithW, int kCap>
+__device__ __forceinline__ void CandidateAt(uint32_t i, uint32_t n_c, const uint32_t* lkey, const uint64_t* lw,
+                                            const uint32_t* lstart, int n_slices, const SampleCandidates* cand,
+                                            uint32_t* key, uint64_t* w) {
+  if (n_c <= kCap) {
+    *key = lkey[i];
+    if (kWithW) *w = lw[i];
+  } else {
+    const int g = SliceOf(lstart, n_slices, i);
+    const uint32_t at_g = static_cast<uint32_t>(g) * kSlice + (i - lstart[g]);
+    *key = cand->key[at_g];
+    if (kWithW) *w = cand->w[at_g];
+  }
+}
+
+// top_k, levels 2 and 3: every workgroup picks level 1's digit from khist (the
+// same data in every workgroup, so the same digit) and stores its keys with that
+// digit; the last workgroup selects bits 19..8 and 7..0 among them in LDS,
+// stores the threshold key and clears khist for the next call.
+__global__ __launch_bounds__(kThreads) void SampleTopKCandKernel(Logits lg, int32_t top_k,
+                                                                 SampleScratch* __restrict__ s,
+                                                                 SampleCandidates* __restrict__ cand) {
+  __shared__ uint32_t hist[kBins];
+  __shared__ uint32_t lstart[kMaxSlices];
+  __shared__ uint32_t lkey[kTopKCandLds];
+  __shared__ uint64_t sh[kWaves];
+  __shared__ Pick pick;
+  __shared__ int last;
+  uint32_t key[kPerThread];
+  uint64_t none[kPerThread];
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j) {  // requested before the pick's histogram reads
+    const int64_t i = ElemIndex(j);
+    key[j] = i < lg.n ? OrderKey(LoadV(lg, i)) : 0u;
+    none[j] = 0;
+  }
+  const Pick p1 = PickDescending<kBins>(s->khist, static_cast<uint32_t>(top_k), sh, &pick);
+  auto match = [&](int j) { return ElemIndex(j) < lg.n && (key[j] >> LevelShift(1)) == p1.digit; };
+  StoreCandidates(key, none, match, false, s, cand, sh);
+  if (!ArriveLast(&s->arrive[kArriveTopK][0], &last)) return;
+
+  const int ns = static_cast<int>(gridDim.x);
+  const uint32_t n_c = GatherCandidates<false, kTopKCandLds>(s, cand, ns, lkey, nullptr, lstart, sh);
+  uint32_t prefix = p1.digit;
+  uint32_t rem = static_cast<uint32_t>(p1.carry);
+#pragma unroll
+  for (int level = 2; level <= 3; ++level) {
+    const int shift = LevelShift(level);
+    const uint32_t mask = (1u << LevelBits(level)) - 1u;
+    const int above = shift + LevelBits(level);
+    for (int b = threadIdx.x; b < kBins; b += kThreads) hist[b] = 0;
+    __syncthreads();
+    for (uint32_t c = threadIdx.x; c < n_c; c += kThreads) {
+      uint32_t k;
+      CandidateAt<false, kTopKCandLds>(c, n_c, lkey, nullptr, lstart, ns, cand, &k, nullptr);
+      if ((k >> above) == prefix) atomicAdd(&hist[(k >> shift) & mask], 1u);
+    }
+    __syncthreads();
+    const Pick p = level == 3 ? PickDescending<256>(hist, rem, sh, &pick) : PickDescending<kBins>(hist, rem, sh, &pick);
+    prefix = (prefix << LevelBits(level)) | p.digit;
+    rem = static_cast<uint32_t>(p.carry);
+  }
+  if (threadIdx.x == 0) s->kth_key = prefix;
+  for (int b = threadIdx.x; b < kBins; b += kThreads) s->khist[b] = 0;
 }
 
 // mx, inv and kth as every kernel after Sum sees them.
@@ -344,86 +594,15 @@ __device__ ProbCtx LoadProbCtx(const Logits& lg, int topk, const SampleScratch* 
   return c;
 }
 
-// ---------------------------------------------------------------- kernels
-
-// Per-slice max of the (scaled) logits; zeroes the radix histograms.
-__global__ __launch_bounds__(kThreads) void SamplePrepKernel(Logits lg, SampleScratch* __restrict__ s) {
-  __shared__ float shf[kWaves];
-  float m = -INFINITY;
-#pragma unroll
-  for (int j = 0; j < kPerThread; ++j) {
-    const int64_t i = ElemIndex(j);
-    if (i < lg.n) {
-      const float v = LoadV(lg, i);
-      if (v > m) m = v;
-    }
-  }
-  m = BlockMax(m, shf);
-  if (threadIdx.x == 0) s->max_part[blockIdx.x] = m;
-  uint32_t* kh = &s->khist[0][0];
-  uint64_t* ph = &s->phist[0][0];
-  for (int64_t k = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; k < 3 * kBins;
-       k += static_cast<int64_t>(gridDim.x) * kThreads) {
-    kh[k] = 0;
-    ph[k] = 0;
-  }
-}
-
-// Resolves top_k's level (level - 1) digit (from the histogram of the previous
-// kernel) and returns the key prefix after it; workgroup 0 records the state.
-__device__ KState ResolveTopK(int level, int32_t top_k, SampleScratch* s, uint64_t* sh, Pick* pick) {
-  const KState prev = level - 1 == 1 ? KState{0u, static_cast<uint32_t>(top_k)} : s->kstate[level - 2];
-  const int lv = level - 1;
-  const Pick p = PickLevel(lv, [&](auto nb) { return PickDescending<decltype(nb)::value>(s->khist[lv - 1], prev.rem, sh, pick); });
-  const KState st{(prev.prefix << LevelBits(lv)) | p.digit, static_cast<uint32_t>(p.carry)};
-  if (blockIdx.x == 0 && threadIdx.x == 0) s->kstate[lv] = st;
-  return st;
-}
-
-// top_k level histogram (count of keys per digit among keys matching the prefix).
-__global__ __launch_bounds__(kThreads) void SampleTopKKernel(Logits lg, int32_t top_k, int32_t level,
-                                                             SampleScratch* __restrict__ s) {
-  __shared__ uint32_t hist[kBins];
-  __shared__ uint64_t sh[kWaves];
-  __shared__ Pick pick;
-  uint32_t prefix = 0;
-  if (level > 1) prefix = ResolveTopK(level, top_k, s, sh, &pick).prefix;
-  for (int b = threadIdx.x; b < kBins; b += kThreads) hist[b] = 0;
-  __syncthreads();
-  const int shift = LevelShift(level);
-  const uint32_t mask = (1u << LevelBits(level)) - 1u;
-  const int above = shift + LevelBits(level);
-#pragma unroll
-  for (int j = 0; j < kPerThread; ++j) {
-    const int64_t i = ElemIndex(j);
-    if (i < lg.n) {
-      const uint32_t key = OrderKey(LoadV(lg, i));
-      if (level == 1 || (key >> above) == prefix) atomicAdd(&hist[(key >> shift) & mask], 1u);
-    }
-  }
-  __syncthreads();
-  for (int b = threadIdx.x; b < kBins; b += kThreads) {
-    if (hist[b] != 0) atomicAdd(&s->khist[level - 1][b], hist[b]);
-  }
-}
-
-// Per-slice sum of e = expf(v - mx) (resolving top_k's threshold first).
-__global__ __launch_bounds__(kThreads) void SampleSumKernel(Logits lg, int32_t topk, int32_t top_k,
-                                                            SampleScratch* __restrict__ s) {
+// Per-slice sum of e = expf(v - mx) (top_k's threshold applied).
+__global__ __launch_bounds__(kThreads) void SampleSumKernel(Logits lg, int32_t topk, SampleScratch* __restrict__ s) {
   __shared__ float shf[kWaves];
   __shared__ double shd[kWaves];
-  __shared__ uint64_t sh[kWaves];
-  __shared__ Pick pick;
   ProbCtx c;
   c.mx = MaxOfParts(s->max_part, NumSlices(lg.n), shf);
   c.inv = 1.0f;
   c.topk = topk;
-  c.kth = 0.0f;
-  if (topk) {
-    const KState st = ResolveTopK(4, top_k, s, sh, &pick);  // level 3's digit completes the key
-    c.kth = FromOrderKey(st.prefix);
-    if (blockIdx.x == 0 && threadIdx.x == 0) s->kth_key = st.prefix;
-  }
+  c.kth = topk ? FromOrderKey(s->kth_key) : 0.0f;
   double acc = 0.0;
 #pragma unroll
   for (int j = 0; j < kPerThread; ++j) {
@@ -434,101 +613,118 @@ __global__ __launch_bounds__(kThreads) void SampleSumKernel(Logits lg, int32_t t
   if (threadIdx.x == 0) s->sum_part[blockIdx.x] = acc;
 }
 
-// Resolves top_p's level (level - 1) digit; workgroup 0 records the state.
-__device__ PState ResolveTopP(int level, uint64_t thr, SampleScratch* s, uint64_t* sh, Pick* pick) {
-  const PState prev = level - 1 == 1 ? PState{0ull, 0ull, 0ull} : s->pstate[level - 2];
-  const int lv = level - 1;
-  PState st = prev;
-  if (!prev.none) {
-    const Pick p =
-        PickLevel(lv, [&](auto nb) { return PickAscending<decltype(nb)::value>(s->phist[lv - 1], prev.base, thr, sh, pick); });
-    if (p.found) {
-      st = PState{(prev.prefix << LevelBits(lv)) | p.digit, p.carry, 0ull};
-    } else {
-      st = PState{0ull, 0ull, 1ull};  // S never exceeds the threshold: no cut
-    }
-  }
-  if (blockIdx.x == 0 && threadIdx.x == 0) s->pstate[lv] = st;
-  return st;
-}
-
-// top_p level histogram: sum of Fix62(p) per digit among keys matching the prefix.
-__global__ __launch_bounds__(kThreads) void SampleTopPKernel(Logits lg, int32_t topk, uint64_t thr, int32_t level,
-                                                             SampleScratch* __restrict__ s) {
+// top_p level 1: sum of Fix62(p) per key digit (bits 31..20), added to phist.
+__global__ __launch_bounds__(kThreads) void SampleTopPKernel(Logits lg, int32_t topk, SampleScratch* __restrict__ s) {
   __shared__ uint64_t hist[kBins];
   __shared__ float shf[kWaves];
   __shared__ double shd[kWaves];
-  __shared__ uint64_t sh[kWaves];
-  __shared__ Pick pick;
   const ProbCtx c = LoadProbCtx(lg, topk, s, shf, shd);
-  uint64_t prefix = 0;
-  if (level > 1) {
-    const PState st = ResolveTopP(level, thr, s, sh, &pick);
-    if (st.none) return;  // uniform across the grid: every workgroup resolved the same state
-    prefix = st.prefix;
-  }
   for (int b = threadIdx.x; b < kBins; b += kThreads) hist[b] = 0;
   __syncthreads();
-  const int shift = LevelShift(level);
-  const uint32_t mask = (1u << LevelBits(level)) - 1u;
-  const int above = shift + LevelBits(level);
 #pragma unroll
   for (int j = 0; j < kPerThread; ++j) {
     const int64_t i = ElemIndex(j);
     if (i < lg.n) {
       const float p = ProbAt(lg, c, i);
-      const uint32_t key = OrderKey(p);
-      if (level == 1 || (key >> above) == prefix) {
-        const uint64_t w = Fix62(p);
-        if (w != 0) atomicAdd(reinterpret_cast<unsigned long long*>(&hist[(key >> shift) & mask]),
-                              static_cast<unsigned long long>(w));
-      }
+      const uint64_t w = Fix62(p);
+      if (w != 0) atomicAdd(reinterpret_cast<unsigned long long*>(&hist[OrderKey(p) >> LevelShift(1)]),
+                            static_cast<unsigned long long>(w));
     }
   }
   __syncthreads();
   for (int b = threadIdx.x; b < kBins; b += kThreads) {
     if (hist[b] != 0)
-      atomicAdd(reinterpret_cast<unsigned long long*>(&s->phist[level - 1][b]), static_cast<unsigned long long>(hist[b]));
+      atomicAdd(reinterpret_cast<unsigned long long*>(&s->phist[b]), static_cast<unsigned long long>(hist[b]));
   }
 }
 
-// Applies top_p's cut: per-slice argmax (from -inf) and double sum of what is left.
-__global__ __launch_bounds__(kThreads) void SampleCutKernel(Logits lg, int32_t topk, uint64_t thr,
-                                                            SampleScratch* __restrict__ s) {
+// top_p, levels 2 and 3 and the cut: every workgroup picks level 1's digit (the
+// smallest with S > thr) from phist and stores its (key, weight) pairs with
+// that digit; the last workgroup selects bits 19..8 and 7..0 among them in LDS,
+// which completes K* (the smallest key with S(K*) > thr), stores cut_key =
+// K* - 1 and the weight of the keys above the cut (the total less S below K*),
+// and clears phist for the next call. S never exceeding thr (no level-1 digit)
+// means no cut.
+__global__ __launch_bounds__(kThreads) void SampleTopPCandKernel(Logits lg, int32_t topk, uint64_t thr,
+                                                                 SampleScratch* __restrict__ s,
+                                                                 SampleCandidates* __restrict__ cand) {
+  __shared__ uint64_t hist[kBins];
+  __shared__ uint32_t lstart[kMaxSlices];
+  __shared__ uint32_t lkey[kTopPCandLds];
+  __shared__ uint64_t lw[kTopPCandLds];
   __shared__ float shf[kWaves];
   __shared__ double shd[kWaves];
   __shared__ uint64_t sh[kWaves];
-  __shared__ Best shb[kWaves];
   __shared__ Pick pick;
+  __shared__ int last;
+  float v[kPerThread];
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j) {  // requested before the partials and the histogram
+    const int64_t i = ElemIndex(j);
+    v[j] = i < lg.n ? lg.x[i] : 0.0f;
+  }
   const ProbCtx c = LoadProbCtx(lg, topk, s, shf, shd);
-  const PState st = ResolveTopP(4, thr, s, sh, &pick);  // level 3's digit completes the key K*
-  // cut = the largest key with S <= thr, i.e. K* - 1; no K* means no cut (NaN compares false)
-  const uint32_t cut_key = st.none ? 0xFFFFFFFFu : static_cast<uint32_t>(st.prefix) - 1u;
-  if (blockIdx.x == 0 && threadIdx.x == 0) s->cut_key = cut_key;
-  const float cut = FromOrderKey(cut_key);
-  Best b{-INFINITY, 0};
-  double acc = 0.0;
+  uint64_t total = 0;
+  const Pick p1 = PickAscending<kBins>(s->phist, 0ull, thr, sh, &pick, &total);
+  uint32_t key[kPerThread];
+  uint64_t w[kPerThread];
 #pragma unroll
   for (int j = 0; j < kPerThread; ++j) {
-    const int64_t i = ElemIndex(j);
-    if (i < lg.n) {
-      float p = ProbAt(lg, c, i);
-      if (p <= cut) p = 0.0f;
-      if (p > b.v) b = Best{p, static_cast<int32_t>(i)};
-      acc += static_cast<double>(p);
+    const float p = ElemIndex(j) < lg.n ? ProbOfRaw(lg, c, v[j]) : 0.0f;
+    key[j] = OrderKey(p);
+    w[j] = Fix62(p);
+  }
+  auto match = [&](int j) {
+    return p1.found && ElemIndex(j) < lg.n && w[j] != 0 && (key[j] >> LevelShift(1)) == p1.digit;
+  };
+  StoreCandidates(key, w, match, true, s, cand, sh);
+  if (!ArriveLast(&s->arrive[kArriveTopP][0], &last)) return;
+
+  uint32_t cut_key = 0xFFFFFFFFu;  // no cut
+  uint64_t kept = total;
+  if (p1.found) {
+    const int ns = static_cast<int>(gridDim.x);
+    const uint32_t n_c = GatherCandidates<true, kTopPCandLds>(s, cand, ns, lkey, lw, lstart, sh);
+    uint32_t prefix = p1.digit;
+    uint64_t base = p1.carry;
+    bool found = true;
+#pragma unroll
+    for (int level = 2; level <= 3; ++level) {
+      const int shift = LevelShift(level);
+      const uint32_t mask = (1u << LevelBits(level)) - 1u;
+      const int above = shift + LevelBits(level);
+      for (int b = threadIdx.x; b < kBins; b += kThreads) hist[b] = 0;
+      __syncthreads();
+      for (uint32_t k = threadIdx.x; k < n_c; k += kThreads) {
+        uint32_t ck;
+        uint64_t cw;
+        CandidateAt<true, kTopPCandLds>(k, n_c, lkey, lw, lstart, ns, cand, &ck, &cw);
+        if ((ck >> above) == prefix)
+          atomicAdd(reinterpret_cast<unsigned long long*>(&hist[(ck >> shift) & mask]),
+                    static_cast<unsigned long long>(cw));
+      }
+      __syncthreads();
+      const Pick p = level == 3 ? PickAscending<256>(hist, base, thr, sh, &pick)
+                                : PickAscending<kBins>(hist, base, thr, sh, &pick);
+      found = found && p.found;
+      prefix = (prefix << LevelBits(level)) | p.digit;
+      base = p.carry;
+    }
+    if (found) {  // always, given level 1's digit: its candidates carry S past thr
+      cut_key = prefix - 1u;
+      kept = total - base;
     }
   }
-  b = BlockBest(b, shb);
-  acc = BlockSumD(acc, shd);
   if (threadIdx.x == 0) {
-    s->best_val[blockIdx.x] = b.v;
-    s->best_idx[blockIdx.x] = b.i;
-    s->sum2_part[blockIdx.x] = acc;
+    s->cut_key = cut_key;
+    s->kept_w = kept;
   }
+  for (int b = threadIdx.x; b < kBins; b += kThreads) s->phist[b] = 0;
 }
 
 // Per-slice inverse-transform partials of probs: Fix52 sum and the double sum
 // (NaN when a value is outside [0, 2), which sends the transform to the serial loop).
+template <bool kDev>
 __device__ void WriteFixPartials(const float (&p)[kPerThread], const bool (&in)[kPerThread], SampleScratch* s,
                                  double* shd, uint64_t* sh) {
   uint64_t f = 0;
@@ -546,83 +742,32 @@ __device__ void WriteFixPartials(const float (&p)[kPerThread], const bool (&in)[
   (void)BlockExclScan(f, sh, &ftot);
   t = BlockSumD(ok ? t : NAN, shd);
   if (threadIdx.x == 0) {
-    s->fix_part[blockIdx.x] = ftot;
-    s->tot_part[blockIdx.x] = t;
+    St<kDev>(&s->fix_part[blockIdx.x], ftot);
+    St<kDev>(&s->tot_part[blockIdx.x], t);
   }
 }
 
-// Final probabilities: p = e * inv; with top_p the cut, the keep-one rule and
-// the second normalisation. Also the inverse-transform partials.
-__global__ __launch_bounds__(kThreads) void SampleNormKernel(Logits lg, int32_t topk, int32_t topp,
-                                                             float* __restrict__ probs, SampleScratch* __restrict__ s) {
-  __shared__ float shf[kWaves];
-  __shared__ double shd[kWaves];
-  __shared__ uint64_t sh[kWaves];
-  __shared__ Best shb[kWaves];
-  const ProbCtx c = LoadProbCtx(lg, topk, s, shf, shd);
-  float cut = 0.0f, inv2 = 1.0f;
-  bool forced = false, rescale = false;
-  int32_t best = 0;
-  if (topp) {
-    const int ns = NumSlices(lg.n);
-    cut = FromOrderKey(s->cut_key);
-    const Best b = BestOfParts(s->best_val, s->best_idx, ns, shb);
-    best = b.i;
-    forced = b.v == 0.0f;  // nothing survived the cut: the argmax is kept with 1
-    const double sum2 = SumOfParts(s->sum2_part, ns, shd) + (forced ? 1.0 : 0.0);
-    rescale = sum2 > 0.0;
-    if (rescale) inv2 = static_cast<float>(1.0 / sum2);
-  }
-  float p[kPerThread];
-  bool in[kPerThread];
-#pragma unroll
-  for (int j = 0; j < kPerThread; ++j) {
-    const int64_t i = ElemIndex(j);
-    in[j] = i < lg.n;
-    p[j] = 0.0f;
-    if (in[j]) {
-      float v = ProbAt(lg, c, i);
-      if (topp) {
-        if (v <= cut) v = 0.0f;
-        if (forced && i == best) v = 1.0f;
-        if (rescale) v *= inv2;
-      }
-      p[j] = v;
-      probs[i] = v;
-    }
-  }
-  WriteFixPartials(p, in, s, shd, sh);
-}
+// Where the inverse transform takes u: the device counter when counter_dev is
+// set, else u_val.
+struct Draw {
+  float u_val;
+  uint64_t seed;
+  const uint64_t* counter_dev;
+  int32_t* out_idx;
+};
 
-// Inverse-transform partials of caller-provided probabilities.
-__global__ __launch_bounds__(kThreads) void SampleFixKernel(const float* __restrict__ probs, int64_t n,
-                                                            SampleScratch* __restrict__ s) {
-  __shared__ double shd[kWaves];
-  __shared__ uint64_t sh[kWaves];
-  float p[kPerThread];
-  bool in[kPerThread];
-#pragma unroll
-  for (int j = 0; j < kPerThread; ++j) {
-    const int64_t i = ElemIndex(j);
-    in[j] = i < n;
-    p[j] = in[j] ? probs[i] : 0.0f;
-  }
-  WriteFixPartials(p, in, s, shd, sh);
-}
-
-// The inverse transform (one workgroup). u comes from the device counter when
-// counter_dev is set, else from u_val.
-__global__ __launch_bounds__(kThreads) void SampleInverseKernel(const float* __restrict__ probs, int64_t n, float u_val,
-                                                                uint64_t seed, const uint64_t* __restrict__ counter_dev,
-                                                                int32_t* __restrict__ out_idx,
-                                                                const SampleScratch* __restrict__ s) {
+// The inverse transform over probs[0, n) by one workgroup, from the slices'
+// Fix52 / double partials (in the last workgroup of the launch that wrote them,
+// after ArriveLast's acquire fence, or in a later launch).
+__device__ void InverseTransform(const float* __restrict__ probs, int64_t n, const Draw& d,
+                                 const SampleScratch* __restrict__ s) {
   __shared__ double shd[kWaves];
   __shared__ uint64_t sh[kWaves];
   __shared__ Best shb[kWaves];
   __shared__ float tile[kSlice];
   __shared__ int64_t hit;  // crossing index / slice, -1 none
   __shared__ uint64_t hit_lo, hit_hi;
-  const float u = counter_dev != nullptr ? CounterUniformOf(seed, *counter_dev) : u_val;
+  const float u = d.counter_dev != nullptr ? CounterUniformOf(d.seed, *d.counter_dev) : d.u_val;
   const int ns = static_cast<int>((n + kSlice - 1) / kSlice);
 
   // 1. slice totals: thread t owns slices [t * kPartsPerThread, ...)
@@ -743,13 +888,98 @@ __global__ __launch_bounds__(kThreads) void SampleInverseKernel(const float* __r
     b = BlockBest(b, shb);
     result = b.i;
   }
-  if (threadIdx.x == 0) *out_idx = static_cast<int32_t>(result);
+  if (threadIdx.x == 0) *d.out_idx = static_cast<int32_t>(result);
 }
 
-// Per-slice argmax: values above `init` only, ties to the smaller index.
-__global__ __launch_bounds__(kThreads) void ArgMaxPartKernel(const float* __restrict__ x, int64_t n, float init,
-                                                             SampleScratch* __restrict__ s) {
+// Final probabilities: p = e * inv; with top_p the cut, the keep-one rule and
+// the second normalisation (by the kept weight on the 2^-62 grid). Also the
+// inverse-transform partials; with kSample the last workgroup then draws the
+// token (probs and partials handed over device-coherent).
+template <bool kSample>
+__global__ __launch_bounds__(kThreads) void SampleNormKernel(Logits lg, int32_t topk, int32_t topp,
+                                                             float* __restrict__ probs, SampleScratch* __restrict__ s,
+                                                             Draw draw) {
+  __shared__ float shf[kWaves];
+  __shared__ double shd[kWaves];
+  __shared__ uint64_t sh[kWaves];
   __shared__ Best shb[kWaves];
+  __shared__ int last;
+  const ProbCtx c = LoadProbCtx(lg, topk, s, shf, shd);
+  float cut = 0.0f, inv2 = 1.0f;
+  bool forced = false, rescale = false;
+  int32_t best = 0;
+  if (topp) {
+    const int ns = NumSlices(lg.n);
+    cut = FromOrderKey(s->cut_key);  // NaN when there is no cut: nothing compares <= it
+    const Best b = BestOfParts(s->best_val, s->best_idx, ns, shb);  // the first maximum of the scaled logits
+    best = b.i;
+    // p is non-decreasing in the logit, so nothing survives the cut exactly when
+    // the largest p does not: then the argmax is kept with 1 (no argmax: every
+    // logit NaN)
+    forced = best >= 0 && best < lg.n && ProbAt(lg, c, best) <= cut;
+    const double sum2 = forced ? 1.0 : static_cast<double>(s->kept_w) * 0x1p-62;
+    rescale = sum2 > 0.0;
+    if (rescale) inv2 = static_cast<float>(1.0 / sum2);
+  }
+  float p[kPerThread];
+  bool in[kPerThread];
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j) {
+    const int64_t i = ElemIndex(j);
+    in[j] = i < lg.n;
+    p[j] = 0.0f;
+    if (in[j]) {
+      float v = ProbAt(lg, c, i);
+      if (topp) {
+        if (v <= cut) v = 0.0f;
+        if (forced && i == best) v = 1.0f;
+        if (rescale) v *= inv2;
+      }
+      p[j] = v;
+      St<kSample>(probs + i, v);
+    }
+  }
+  WriteFixPartials<kSample>(p, in, s, shd, sh);
+  if constexpr (kSample) {
+    if (ArriveLast(&s->arrive[kArriveFinal][0], &last)) InverseTransform(probs, lg.n, draw, s);
+  }
+}
+
+// The inverse transform as a launch of its own (one workgroup), after a Norm
+// launch without the draw.
+__global__ __launch_bounds__(kThreads) void SampleInverseKernel(const float* __restrict__ probs, int64_t n,
+                                                                const SampleScratch* __restrict__ s, Draw draw) {
+  InverseTransform(probs, n, draw, s);
+}
+
+// Inverse-transform partials of caller-provided probabilities; the last
+// workgroup then draws the token.
+__global__ __launch_bounds__(kThreads) void SampleFixKernel(const float* __restrict__ probs, int64_t n,
+                                                            SampleScratch* __restrict__ s, Draw draw) {
+  __shared__ double shd[kWaves];
+  __shared__ uint64_t sh[kWaves];
+  __shared__ int last;
+  float p[kPerThread];
+  bool in[kPerThread];
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j) {
+    const int64_t i = ElemIndex(j);
+    in[j] = i < n;
+    p[j] = in[j] ? probs[i] : 0.0f;
+  }
+  WriteFixPartials<true>(p, in, s, shd, sh);
+  // probs came from the caller (ordered by the launch); only the partials cross workgroups
+  if (ArriveLast(&s->arrive[kArriveFinal][0], &last)) InverseTransform(probs, n, draw, s);
+}
+
+// Per-slice argmax: values above `init` only, ties to the smaller index. With
+// out_idx the last workgroup reduces the partials into it (GpuArgMax);
+// otherwise a later launch reads them.
+__global__ __launch_bounds__(kThreads) void ArgMaxPartKernel(const float* __restrict__ x, int64_t n, float init,
+                                                             SampleScratch* __restrict__ s,
+                                                             int32_t* __restrict__ out_idx) {
+  __shared__ Best shb[kWaves];
+  __shared__ int last;
   Best b{init, 0};
 #pragma unroll
   for (int j = 0; j < kPerThread; ++j) {
@@ -760,18 +990,20 @@ __global__ __launch_bounds__(kThreads) void ArgMaxPartKernel(const float* __rest
     }
   }
   b = BlockBest(b, shb);
-  if (threadIdx.x == 0) {
-    s->best_val[blockIdx.x] = b.v;
-    s->best_idx[blockIdx.x] = b.i;
+  if (out_idx == nullptr) {
+    if (threadIdx.x == 0) {
+      s->best_val[blockIdx.x] = b.v;
+      s->best_idx[blockIdx.x] = b.i;
+    }
+    return;
   }
-}
-
-// GpuArgMax's result from the slice partials (one workgroup).
-__global__ __launch_bounds__(kThreads) void ArgMaxFinalKernel(int64_t n, int32_t* __restrict__ out_idx,
-                                                              const SampleScratch* __restrict__ s) {
-  __shared__ Best shb[kWaves];
-  const Best b = BestOfParts(s->best_val, s->best_idx, static_cast<int>((n + kSlice - 1) / kSlice), shb);
-  if (threadIdx.x == 0) *out_idx = b.i;
+  if (threadIdx.x == 0) {
+    St<true>(&s->best_val[blockIdx.x], b.v);
+    St<true>(&s->best_idx[blockIdx.x], b.i);
+  }
+  if (!ArriveLast(&s->arrive[kArriveArgMax][0], &last)) return;
+  const Best r = BestOfParts(s->best_val, s->best_idx, static_cast<int>(gridDim.x), shb);
+  if (threadIdx.x == 0) *out_idx = r.i;
 }
 
 // Greedy FilterToProbs: one-hot at the argmax.
@@ -791,21 +1023,29 @@ __global__ __launch_bounds__(kThreads) void OneHotKernel(int64_t n, float* __res
 // Library-owned, allocated once, never freed (a destructor running after the
 // HIP runtime has shut down can hang). Grid-sized state lives here, so sampling
 // allocates nothing after the first call or GpuSamplerWarmup.
+struct SamplerBuffers {
+  SampleScratch* s = nullptr;
+  SampleCandidates* cand = nullptr;
+};
 std::mutex g_scratch_mu;
-SampleScratch* g_scratch = nullptr;
+SamplerBuffers g_buffers;
 
-SampleScratch* Scratch() {
+SamplerBuffers Buffers() {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (g_scratch == nullptr) {
+  if (g_buffers.s == nullptr) {
     RPG_CHECK(!StreamIsCapturing(),
               "the sampler's scratch block is allocated on first use, which cannot happen during graph capture; "
               "call GpuSamplerWarmup() before capturing");
     void* p = nullptr;
+    void* c = nullptr;
     RPG_HIP_CHECK(hipMalloc(&p, sizeof(SampleScratch)));
-    RPG_HIP_CHECK(hipMemset(p, 0, sizeof(SampleScratch)));  // outside capture (checked above)
-    g_scratch = static_cast<SampleScratch*>(p);
+    RPG_HIP_CHECK(hipMemset(p, 0, sizeof(SampleScratch)));  // outside capture (checked above): counters, histograms
+    RPG_HIP_CHECK(hipMalloc(&c, sizeof(SampleCandidates)));
+    RPG_HIP_CHECK(hipDeviceSynchronize());
+    g_buffers.s = static_cast<SampleScratch*>(p);
+    g_buffers.cand = static_cast<SampleCandidates*>(c);
   }
-  return g_scratch;
+  return g_buffers;
 }
 
 void CheckVocab(int64_t n) {
@@ -816,31 +1056,37 @@ void CheckVocab(int64_t n) {
 
 unsigned Slices(int64_t n) { return static_cast<unsigned>((n + kSlice - 1) / kSlice); }
 
-// FilterToProbs launches (T > 0 or greedy); returns nothing, writes probs.
-void LaunchFilter(const float* logits, int64_t n, const SampleOptions& opt, float* probs, SampleScratch* s) {
+// The token drawn by the last workgroup of the normalising launch rather than
+// by a launch of its own.
+constexpr bool kDrawInNorm = true;
+
+// FilterToProbs launches for T > 0, then (draw.out_idx set) the token: Prep
+// [-> TopKCand] -> Sum [-> TopP -> TopPCand] -> Norm, the last workgroup of Norm
+// drawing the token.
+void LaunchSample(const float* logits, int64_t n, const SampleOptions& opt, float* probs, const SamplerBuffers& b,
+                  const Draw& draw) {
   const dim3 grid(Slices(n)), block(kThreads);
-  if (!(opt.temperature > 0.0f)) {
-    Launch("ArgMaxPartKernel", ArgMaxPartKernel, grid, block, logits, n, -INFINITY, s);
-    Launch("OneHotKernel", OneHotKernel, grid, block, n, probs, s);
-    return;
-  }
   Logits lg{logits, n, 1.0f / opt.temperature, opt.temperature != 1.0f ? 1 : 0};
   const int32_t topk = (opt.top_k > 1 && opt.top_k < n) ? 1 : 0;
   const int32_t topp = (opt.top_p > 0.0f && opt.top_p < 1.0f) ? 1 : 0;
   // S(t) <= 1 - top_p, on the 2^-62 grid of the weights
   const uint64_t thr = topp ? static_cast<uint64_t>(floor((1.0 - static_cast<double>(opt.top_p)) * 0x1p62)) : 0ull;
-  Launch("SamplePrepKernel", SamplePrepKernel, grid, block, lg, s);
-  if (topk) {
-    for (int32_t level = 1; level <= 3; ++level)
-      Launch("SampleTopKKernel", SampleTopKKernel, grid, block, lg, opt.top_k, level, s);
-  }
-  Launch("SampleSumKernel", SampleSumKernel, grid, block, lg, topk, opt.top_k, s);
+  Launch("SamplePrepKernel", SamplePrepKernel, grid, block, lg, topk, b.s);
+  if (topk) Launch("SampleTopKCandKernel", SampleTopKCandKernel, grid, block, lg, opt.top_k, b.s, b.cand);
+  Launch("SampleSumKernel", SampleSumKernel, grid, block, lg, topk, b.s);
   if (topp) {
-    for (int32_t level = 1; level <= 3; ++level)
-      Launch("SampleTopPKernel", SampleTopPKernel, grid, block, lg, topk, thr, level, s);
-    Launch("SampleCutKernel", SampleCutKernel, grid, block, lg, topk, thr, s);
+    Launch("SampleTopPKernel", SampleTopPKernel, grid, block, lg, topk, b.s);
+    Launch("SampleTopPCandKernel", SampleTopPCandKernel, grid, block, lg, topk, thr, b.s, b.cand);
   }
-  Launch("SampleNormKernel", SampleNormKernel, grid, block, lg, topk, topp, probs, s);
+  if (draw.out_idx != nullptr && kDrawInNorm) {
+    Launch("SampleNormKernel", SampleNormKernel<true>, grid, block, lg, topk, topp, probs, b.s, draw);
+  } else {
+    Launch("SampleNormKernel", SampleNormKernel<false>, grid, block, lg, topk, topp, probs, b.s, draw);
+    if (draw.out_idx != nullptr) {
+      Launch("SampleInverseKernel", SampleInverseKernel, dim3(1), block, static_cast<const float*>(probs), n, b.s,
+             draw);
+    }
+  }
 }
 
 void CheckBuffers(const void* a, const void* b) {
@@ -855,20 +1101,28 @@ uint64_t DevSplitMix64(uint64_t x) { return SplitMix64Of(x); }
 uint64_t DevCounterRng(uint64_t seed, uint64_t counter) { return CounterRngOf(seed, counter); }
 float DevCounterUniform(uint64_t seed, uint64_t counter) { return CounterUniformOf(seed, counter); }
 
-void GpuSamplerWarmup() { (void)Scratch(); }
+void GpuSamplerWarmup() { (void)Buffers(); }
 
 void GpuArgMax(const float* x_dev, int64_t n, int32_t* out_idx_dev) {
   CheckBuffers(x_dev, out_idx_dev);
   CheckVocab(n);
-  SampleScratch* s = Scratch();
-  Launch("ArgMaxPartKernel", ArgMaxPartKernel, dim3(Slices(n)), dim3(kThreads), x_dev, n, -FLT_MAX, s);
-  Launch("ArgMaxFinalKernel", ArgMaxFinalKernel, dim3(1), dim3(kThreads), n, out_idx_dev, s);
+  const SamplerBuffers b = Buffers();
+  Launch("ArgMaxPartKernel", ArgMaxPartKernel, dim3(Slices(n)), dim3(kThreads), x_dev, n, -FLT_MAX, b.s,
+         out_idx_dev);
 }
 
 void GpuFilterToProbs(const float* logits_dev, int64_t n, const SampleOptions& opt, float* probs_dev) {
   CheckBuffers(logits_dev, probs_dev);
   CheckVocab(n);
-  LaunchFilter(logits_dev, n, opt, probs_dev, Scratch());
+  const SamplerBuffers b = Buffers();
+  if (!(opt.temperature > 0.0f)) {
+    const dim3 grid(Slices(n)), block(kThreads);
+    Launch("ArgMaxPartKernel", ArgMaxPartKernel, grid, block, logits_dev, n, -INFINITY, b.s,
+           static_cast<int32_t*>(nullptr));
+    Launch("OneHotKernel", OneHotKernel, grid, block, n, probs_dev, b.s);
+    return;
+  }
+  LaunchSample(logits_dev, n, opt, probs_dev, b, Draw{0.0f, 0, nullptr, nullptr});
 }
 
 void GpuInverseSample(const float* probs_dev, int64_t n, float u, int32_t* out_idx_dev) {
@@ -878,10 +1132,9 @@ void GpuInverseSample(const float* probs_dev, int64_t n, float u, int32_t* out_i
   RPG_CHECK(!StreamIsCapturing(),
             "GpuInverseSample takes u from the host and is therefore not capturable; use GpuSampleTokenDev inside a "
             "graph");
-  SampleScratch* s = Scratch();
-  Launch("SampleFixKernel", SampleFixKernel, dim3(Slices(n)), dim3(kThreads), probs_dev, n, s);
-  Launch("SampleInverseKernel", SampleInverseKernel, dim3(1), dim3(kThreads), probs_dev, n, u, uint64_t{0},
-         static_cast<const uint64_t*>(nullptr), out_idx_dev, s);
+  const SamplerBuffers b = Buffers();
+  Launch("SampleFixKernel", SampleFixKernel, dim3(Slices(n)), dim3(kThreads), probs_dev, n, b.s,
+         Draw{u, 0, nullptr, out_idx_dev});
 }
 
 void GpuSampleToken(const float* logits_dev, int64_t n, const SampleOptions& opt, uint64_t seed, uint64_t counter,
@@ -896,10 +1149,7 @@ void GpuSampleToken(const float* logits_dev, int64_t n, const SampleOptions& opt
   RPG_CHECK(!StreamIsCapturing(),
             "GpuSampleToken takes the counter from the host and is therefore not capturable; use GpuSampleTokenDev "
             "inside a graph");
-  SampleScratch* s = Scratch();
-  LaunchFilter(logits_dev, n, opt, probs_dev, s);
-  Launch("SampleInverseKernel", SampleInverseKernel, dim3(1), dim3(kThreads), static_cast<const float*>(probs_dev), n,
-         CounterUniformOf(seed, counter), uint64_t{0}, static_cast<const uint64_t*>(nullptr), out_idx_dev, s);
+  LaunchSample(logits_dev, n, opt, probs_dev, Buffers(), Draw{CounterUniformOf(seed, counter), 0, nullptr, out_idx_dev});
 }
 
 void GpuSampleTokenDev(const float* logits_dev, int64_t n, const SampleOptions& opt, uint64_t seed,
@@ -912,10 +1162,7 @@ void GpuSampleTokenDev(const float* logits_dev, int64_t n, const SampleOptions& 
   CheckBuffers(logits_dev, out_idx_dev);
   RPG_CHECK(probs_dev != nullptr, "sampler: a probability buffer is null");
   CheckVocab(n);
-  SampleScratch* s = Scratch();
-  LaunchFilter(logits_dev, n, opt, probs_dev, s);
-  Launch("SampleInverseKernel", SampleInverseKernel, dim3(1), dim3(kThreads), static_cast<const float*>(probs_dev), n,
-         0.0f, seed, counter_dev, out_idx_dev, s);
+  LaunchSample(logits_dev, n, opt, probs_dev, Buffers(), Draw{0.0f, seed, counter_dev, out_idx_dev});
 }
 
 }  // namespace rpg

@@ -15,7 +15,9 @@
 //   * softmax: e = expf(v - max), summed in double, p = e * float(1/sum);
 //   * top_p (0 < p < 1): with S(t) = sum of p_i over bit-pattern keys <= t, the
 //     cut is the largest key with S <= 1 - top_p; every p_i <= cut becomes 0;
-//     if nothing is left the argmax gets 1; then p *= float(1/sum) again;
+//     if nothing is left the argmax gets 1; then p *= float(1/sum) again, the
+//     sum of the kept p taken on the same 2^-62 grid (within n * 2^-62 of the
+//     double sum);
 //   * inverse transform: the first index whose running double sum of p exceeds
 //     u; if none does, the first maximum of p;
 //   * u = CounterUniform(seed, counter) = (SplitMix64 of seed + gamma*counter)

@@ -107,6 +107,40 @@ def test_filter_matches_oracle(gpu, ora, cfg, n):
     assert np.all(err <= PROB_RTOL * np.abs(want)), float(np.max(err / np.maximum(np.abs(want), 1e-38)))
 
 
+def _tied_block_logits(n, block, seed):
+    """`block` values exactly 1.0 among n (the rest uniform in [-8, 0.5)): the
+    tied block holds ~90% of the softmax mass and one level-1 key bin."""
+    rng = np.random.default_rng(seed)
+    v = rng.uniform(-8.0, 0.5, n).astype(np.float32)
+    v[rng.choice(n, block, replace=False)] = np.float32(1.0)
+    return v
+
+
+@pytest.mark.parametrize("top_k,top_p", [(0, 0.5), (60000, 0.5), (0, 0.97)])
+def test_sample_many_candidates(gpu, ora, top_k, top_p):
+    """Radix selects whose level-1 digit holds tens of thousands of values (a
+    tied block of 60000): the candidates overflow the last workgroup's LDS copy
+    and every level reads them from their slices' regions. Kept set exact,
+    probabilities to 2^-20, tokens as the oracle's."""
+    import torch
+
+    n = 151936
+    case(f"many candidates: top_k {top_k}, top_p {top_p}")
+    logits = _tied_block_logits(n, 60000, 31)
+    logits_dev = dev(logits)
+    got = gpu_filter(gpu, logits_dev, n, 1.0, top_k, top_p)
+    want, margin = ora.filter_to_probs(logits, 1.0, top_k, top_p)
+    assert margin > 1e-9
+    assert np.array_equal(got > 0, want > 0), "kept sets differ"
+    err = np.abs(got.astype(np.float64) - want)
+    assert np.all(err <= PROB_RTOL * np.abs(want))
+    probs = torch.empty(n, dtype=torch.float32, device="cuda")
+    for c in range(4):
+        out = idx_buf()
+        gpu.GpuSampleToken(logits_dev, n, gpu.SampleOptions(1.0, top_k, top_p), 7, c, probs, out)
+        assert int(host(out)[0]) == ora.sample_token(logits, 1.0, top_k, top_p, 7, c)
+
+
 @pytest.mark.parametrize("cfg", [c for c in SAMPLE_CASES if c[0] > 0], ids=[c[5] for c in SAMPLE_CASES if c[0] > 0])
 def test_inverse_sample_exact_on_device_probs(gpu, ora, cfg):
     """The transform is a pure function of (probs, u): on the device's own
