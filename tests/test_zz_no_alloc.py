@@ -108,45 +108,46 @@ def _group_partials_floats(units, group, positions):
 
 
 def test_noalloc_attention_group4_boundary(gpu):
-    """GQA group 4 past 3072 positions (chunk kernel + merge launch): 45 x 44 =
-    1980 (token, kv head) pairs fit the 2^21-float scratch and match the allocating
-    entry bit for bit; 39 x 51 = 1989 pairs are rejected unlaunched. Below 3072
-    positions (one launch) the same 1989 pairs need no partials at all."""
+    """GQA group 4 past 3072 positions (chunk kernel + merge launch): 5 x 397 =
+    1985 (token, kv head) pairs fit the 2^21-float scratch and match the
+    allocating entry bit for bit; 6 x 331 = 1986 pairs are rejected unlaunched.
+    Below 3072 positions (one launch) the same 1986 pairs need no partials at all."""
     import torch
 
     lib = gpu.load_library()
-    rng = np.random.default_rng(78)
     max_seq, pos0 = 3200, 3100
     # (seq, n_kv_heads)
-    fits, over = (45, 44), (39, 51)
-    assert _group_partials_floats(fits[0] * fits[1], 4, pos0 + fits[0]) == 1980 * 1056 <= 1 << 21
-    assert _group_partials_floats(over[0] * over[1], 4, pos0 + over[0]) == 1989 * 1056 > 1 << 21
+    fits, over = (5, 397), (6, 331)
+    assert _group_partials_floats(fits[0] * fits[1], 4, pos0 + fits[0]) == 1985 * 1056 <= 1 << 21
+    assert _group_partials_floats(over[0] * over[1], 4, pos0 + over[0]) == 1986 * 1056 > 1 << 21
     assert _group_partials_floats(over[0] * over[1], 4, 1000 + over[0]) == 0
+
+    def inputs(seq, nh, nkv, seed):
+        gen = torch.Generator(device="cuda").manual_seed(seed)
+        q = torch.randn((seq, nh, 128), generator=gen, device="cuda")
+        kc = torch.randn((nkv, max_seq, 128), generator=gen, device="cuda").half().view(torch.int16)
+        vc = torch.randn((nkv, max_seq, 128), generator=gen, device="cuda").half().view(torch.int16)
+        return q, kc, vc
+
+    def both_equal(seq, nh, nkv, p0, q, kc, vc):
+        ref = torch.full((seq, nh, 128), float("nan"), dtype=torch.float32, device="cuda")
+        got = torch.full_like(ref, float("nan"))
+        assert _run(lib, lib.rpg_op_attention_from_cache, nh, nkv, p0, seq, q, kc, vc, max_seq, ref) == 0
+        assert _run(lib, lib.rpg_op_attention_from_cache_noalloc, nh, nkv, p0, seq, q, kc, vc, max_seq,
+                    got) == 0, lib.rpg_ops_last_error()
+        torch.cuda.synchronize()
+        assert bool(torch.all(torch.isfinite(ref)))
+        assert torch.equal(ref.view(torch.int32), got.view(torch.int32))
 
     seq, nkv = fits
     nh = 4 * nkv
-    _case(f"noalloc group-4 boundary: seq {seq}, {nh}/{nkv} heads, 1980 pairs (fits)")
-    q, kc, vc = _inputs(rng, nh, nkv, max_seq, seq)
-    qd = torch.from_numpy(q).cuda()
-    kd = torch.from_numpy(kc.view(np.int16)).cuda()
-    vd = torch.from_numpy(vc.view(np.int16)).cuda()
-    ref = torch.full((seq, nh, 128), float("nan"), dtype=torch.float32, device="cuda")
-    got = torch.full_like(ref, float("nan"))
-    assert _run(lib, lib.rpg_op_attention_from_cache, nh, nkv, pos0, seq, qd, kd, vd, max_seq, ref) == 0
-    assert _run(lib, lib.rpg_op_attention_from_cache_noalloc, nh, nkv, pos0, seq, qd, kd, vd, max_seq,
-                got) == 0, lib.rpg_ops_last_error()
-    torch.cuda.synchronize()
-    a = ref.cpu().numpy()
-    b = got.cpu().numpy()
-    assert np.all(np.isfinite(a))
-    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    _case(f"noalloc group-4 boundary: seq {seq}, {nh}/{nkv} heads, 1985 pairs at {pos0} (fits)")
+    both_equal(seq, nh, nkv, pos0, *inputs(seq, nh, nkv, 78))
 
     seq, nkv = over
     nh = 4 * nkv
-    _case(f"noalloc group-4 boundary: seq {seq}, {nh}/{nkv} heads, 1989 pairs (rejected)")
-    q = torch.zeros((seq, nh, 128), dtype=torch.float32, device="cuda")
-    kc = torch.zeros((nkv, max_seq, 128), dtype=torch.int16, device="cuda")
-    vc = torch.zeros_like(kc)
+    _case(f"noalloc group-4 boundary: seq {seq}, {nh}/{nkv} heads, 1986 pairs at {pos0} (rejected)")
+    q, kc, vc = inputs(seq, nh, nkv, 79)
     out = torch.full((seq, nh, 128), 7.0, dtype=torch.float32, device="cuda")
     rc = _run(lib, lib.rpg_op_attention_from_cache_noalloc, nh, nkv, pos0, seq, q, kc, vc, max_seq, out)
     assert rc < 0
@@ -154,18 +155,6 @@ def test_noalloc_attention_group4_boundary(gpu):
     torch.cuda.synchronize()
     assert bool(torch.all(out == 7.0)), "a rejected call must not launch"
 
-    # the same pairs at 1039 positions: one launch, no partials; the call goes through
-    pos0 = 1000
-    _case(f"noalloc group-4: seq {seq}, {nh}/{nkv} heads, 1989 pairs at {pos0} (one launch, accepted)")
-    gen = torch.Generator(device="cuda").manual_seed(79)
-    q = torch.randn((seq, nh, 128), generator=gen, device="cuda")
-    kc = torch.randn((nkv, max_seq, 128), generator=gen, device="cuda").half().view(torch.int16)
-    vc = torch.randn((nkv, max_seq, 128), generator=gen, device="cuda").half().view(torch.int16)
-    ref = torch.full((seq, nh, 128), float("nan"), dtype=torch.float32, device="cuda")
-    got = torch.full_like(ref, float("nan"))
-    assert _run(lib, lib.rpg_op_attention_from_cache, nh, nkv, pos0, seq, q, kc, vc, max_seq, ref) == 0
-    assert _run(lib, lib.rpg_op_attention_from_cache_noalloc, nh, nkv, pos0, seq, q, kc, vc, max_seq,
-                got) == 0, lib.rpg_ops_last_error()
-    torch.cuda.synchronize()
-    assert bool(torch.all(torch.isfinite(ref)))
-    assert torch.equal(ref.view(torch.int32), got.view(torch.int32))
+    # the same pairs at 1006 positions: one launch, no partials; the call goes through
+    _case(f"noalloc group-4: seq {seq}, {nh}/{nkv} heads, 1986 pairs at 1000 (one launch, accepted)")
+    both_equal(seq, nh, nkv, 1000, q, kc, vc)
