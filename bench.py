@@ -325,9 +325,28 @@ def measure_prefill_4b(torch, ops, tab, steps=5, warmup=2):
     """Prefill n = 4096 at Qwen3-4B shape, 36 layers (the 4096-slot caches are filled):
     the chain's step time, then each op's 36 launches back to back (median of 5
     batches) and, secondary, each op's average under dispatch-attached events."""
-    n, shape = 4096, QWEN3_4B
+    return measure_prefill_shape(torch, ops, tab, 4096, QWEN3_4B, 4, steps, warmup)
+
+
+# One GPU's share of Qwen3-1.7B under tensor parallelism over 8 GPUs: the hidden
+# size replicated (add + RMSNorm unchanged), 2 q heads and 1 kv head (with its
+# cache slice), 768 of the 6144 intermediate columns.
+QWEN3_1_7B_TP8 = dict(hidden=H, n_heads=HQ // 8, n_kv_heads=HKV // 8, inter=INTER // 8, layers=LAYERS)
+
+
+def measure_shard_tp8(torch, ops, tab, steps=5, warmup=2):
+    """The n = 2811 chain at one GPU's TP=8 shard shape (QWEN3_1_7B_TP8), measured
+    like the 4B section. The sharded ops are small launches (10-26 MB)."""
+    out = measure_prefill_shape(torch, ops, tab, N_PREFILL, QWEN3_1_7B_TP8, 8, steps, warmup)
+    out["shape"] = QWEN3_1_7B_TP8
+    return out
+
+
+def measure_prefill_shape(torch, ops, tab, n, shape, seed, steps=5, warmup=2):
+    """The chain at (n, shape): step time, each op's launches back to back (median
+    of 5 batches) and each op's average under dispatch-attached events."""
     gen = torch.Generator(device="cuda")
-    gen.manual_seed(4)
+    gen.manual_seed(seed)
     layers = [Layer(torch, n, gen, shape) for _ in range(shape["layers"])]
     for _ in range(warmup):
         for L in layers:
@@ -1054,6 +1073,8 @@ SECTIONS = {
     "sampler": lambda torch, ops: measure_sampler(torch, ops),
     "gather": lambda torch, ops: {"q4k": measure_gather(torch, ops, ops.GGML_Q4_K, 144),
                                   "q6k": measure_gather(torch, ops, ops.GGML_Q6_K, 210)},
+    "shard_tp8_n2811": lambda torch, ops: measure_shard_tp8(
+        torch, ops, torch.from_numpy(ops.build_rope_table(D, THETA, MAX_SEQ)).cuda()),
     "prefill_4b_n4096": lambda torch, ops: measure_prefill_4b(
         torch, ops, torch.from_numpy(ops.build_rope_table(D, THETA, MAX_SEQ)).cuda()),
 }
@@ -1139,6 +1160,8 @@ def main():
         extras["decode_n1"] = measure_decode(torch, ops, tab, max(20, args.steps))
         log("prefill n=4096 at the 4B shape, 36 layers")
         extras["prefill_4b_n4096"] = measure_prefill_4b(torch, ops, tab)
+        log("prefill n=2811 at one GPU's TP=8 shard of the 1.7B shape")
+        extras["shard_tp8_n2811"] = measure_shard_tp8(torch, ops, tab)
         log("decode matmuls (GpuMatMulQuant, n = 1)")
         extras["matmul_decode_n1"] = measure_matmul_decode(torch, ops)
         log("prefill matmuls (GpuMatMulQuant, n = 2811)")

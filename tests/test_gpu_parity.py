@@ -111,6 +111,39 @@ def test_embedding_gather_full_table(gpu, ora, t):
     assert np.array_equal(bits(host(x)), bits(want))
 
 
+@pytest.mark.parametrize("t", [12, 14])
+def test_embedding_gather_vocab_shards(gpu, ora, t):
+    """The vocabulary-parallel form of the gather over 8 GPUs: shard s holds rows
+    [s R, (s + 1) R) of token_embd and looks up ids - s R, so ids outside its rows
+    give zero rows. Each shard's rows for its own ids equal the full gather's bit
+    for bit, every other row is +0.0, and the sum over shards (the all-reduce)
+    equals the full gather."""
+    import torch
+
+    rows, cols, seq, shards = 151936, 2048, 2811, 8
+    shard_rows = rows // shards
+    case(f"gather vocab shards type={t} rows={rows} shards={shards}")
+    rng = np.random.default_rng(260 + t)
+    table = synth.quant_table(rng, t, rows, cols)
+    row_bytes = table.size // rows
+    toks = rng.integers(0, rows, seq, dtype=np.int64).astype(np.int32)
+    toks[:4] = [0, rows - 1, shard_rows - 1, shard_rows]
+    full = torch.empty((seq, cols), dtype=torch.float32, device="cuda")
+    gpu.GpuEmbeddingLookup(gpu.GpuTensor(dev(table), t, rows, cols), dev(toks), seq, full)
+    want = host(full)
+    total = np.zeros((seq, cols), np.float32)
+    for sh in range(shards):
+        part = table.reshape(rows, row_bytes)[sh * shard_rows:(sh + 1) * shard_rows].reshape(-1)
+        x = torch.full((seq, cols), np.nan, dtype=torch.float32, device="cuda")
+        gpu.GpuEmbeddingLookup(gpu.GpuTensor(dev(part), t, shard_rows, cols), dev(toks - sh * shard_rows), seq, x)
+        got = host(x)
+        mine = (toks >= sh * shard_rows) & (toks < (sh + 1) * shard_rows)
+        assert np.array_equal(bits(got[mine]), bits(want[mine])), sh
+        assert np.all(bits(got[~mine]) == 0), sh
+        total += got
+    assert np.array_equal(total, want)  # -0.0 values come back as +0.0 from the sum, as from the all-reduce
+
+
 @pytest.mark.parametrize("t", [0, 12, 14])
 @pytest.mark.parametrize("cols", [2560, 8448])
 def test_embedding_gather_edges(gpu, ora, t, cols):
@@ -323,6 +356,9 @@ QK_CASES = [
     # the launcher switches to buffer stores from 64 tokens on: both sides of that line
     ("1.7B n=63 (global stores)", 16, 8, 63, 17),
     ("1.7B n=64 (buffer stores)", 16, 8, 64, 4032),
+    # one GPU's share under tensor parallelism over 8 GPUs (one kv head each)
+    ("1.7B TP=8 shard n=2811", 2, 1, 2811, 0),
+    ("4B TP=8 shard n=4096", 4, 1, 4096, 0),
 ]
 
 
@@ -439,6 +475,8 @@ def test_qk_norm_rope_kv_unaligned_cache_base(gpu, ora, cache_off):
 
 @pytest.mark.parametrize("n,off", [(21 * 6144, 0), (2811 * 6144, 0), (6144, 0), (1, 0), (1001, 0), (1003, 1),
                                    (4096 * 9728, 0),
+                                   # TP=8 shards of the intermediate width (1.7B: 768 columns, 4B: 1216)
+                                   (2811 * 768, 0), (4096 * 1216, 0),
                                    # write-through stores from 131072 elements on; the last block partial
                                    (131071, 0), (131072, 0), (131072 + 2050, 0), (262147, 1)])
 def test_silu_mul(gpu, ora, n, off):
