@@ -149,18 +149,16 @@ RPG_OPS_API int32_t rpg_op_qk_norm_rope_kv_attention(const float* q, const float
 /* rpg_op_attention_from_cache for callers that cannot allocate device memory
  * (code under HIP graph capture, serving loops or harnesses that forbid
  * hipMalloc): same arguments, same kernels, bit-identical results, but the
- * partials of a split-key decode live in a fixed 8 MiB device array of the
- * library (one per GPU, held until the process ends), and the one-launch split
- * decode's arrival counters in a fixed array beside it, so no call ever
- * allocates. Limit: a call whose split needs more than 2^21 floats of partials
- * fails with an error and launches nothing. Up to 3072 positions a split decode
- * keeps 132 floats per (token, query head, workgroup of 4 chunks), at most
- * ~0.54 M floats, so every such call fits. Past 3072 positions it keeps 132
- * floats per (token, query head, chunk) (seq * n_heads * chunks * 132); the
- * split aims at ~2048 waves, so every call with a GQA group of 1 or 2, and with
- * a group of 4 up to 1985 (token, kv head) pairs, fits: from 1025 to 2047 pairs
- * a group-4 call takes two chunks, 1056 floats per pair (decode batches of up to
- * 62 tokens with 32 kv heads fit; 63 tokens with 32 kv heads do not).
+ * partials of a split-key decode live in a fixed 2 MiB device array of the
+ * library (one per GPU, held until the process ends), and the split decode's
+ * arrival counters in a fixed array beside it, so no call ever allocates.
+ * Limit: a call whose split needs more than 2^19 floats of partials fails with
+ * an error and launches nothing. A split decode keeps 132 floats per (token,
+ * query head, workgroup of 4 key chunks), none when one workgroup takes every
+ * chunk; the split aims at ~2048 waves, so the only calls over the limit have a
+ * GQA group of 4, 497 to 511 (token, kv head) pairs and a split of 5 to 8 chunks
+ * (1056 floats per pair; 496 pairs fit). Prefill-sized calls keep fewer key
+ * chunks when the array is too small for their partials.
  * Calls that overlap on one GPU (different streams) share the arrays and race.
  * No counterpart in the reference: it exists for callers that cannot allocate. */
 RPG_OPS_API int32_t rpg_op_attention_from_cache_noalloc(const float* q, int32_t n_heads, int32_t n_kv_heads,

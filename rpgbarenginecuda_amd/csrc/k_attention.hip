@@ -355,16 +355,19 @@ __global__ __launch_bounds__(kBlockThreads) void AttnMergeRowsKernel(const float
 // rounded to fp16. The wave of the chunk that holds pos stores the new K / V
 // rows into the cache and uses them for that key straight from LDS (the store
 // need not be visible to its own loads); the other chunks never read key pos.
-constexpr int kMaxFusedGroups = 32;
+// Waves (chunks) per workgroup of the one-launch decode, and so at most
+// kMaxGroupChunks / kFusedWaves workgroups per (token, kv head) pair.
+constexpr int kFusedWaves = 4;  // 8 measured slower: 10.1 against 8.9 us at 512 positions
+constexpr int kMaxFusedGroups = kMaxGroupChunks / kFusedWaves;
 // uint32 slots between two (token, kv head) pairs' arrival counters: one counter
 // per 256 bytes. Packed counters (8 pairs in one 32-byte line) serialized the
 // pairs' atomics on one line: 13.8 against 11.7 us at 4096 positions.
-constexpr int kCounterStride = 64;  // workgroups per pair in the one-launch decode: kMaxGroupChunks / kWaves
+constexpr int kCounterStride = 64;
 
 // The merge of the fused grouped decode (AttnDecodeGroupKernel<G, kPrep, true>),
 // reached by every wave of a workgroup with at least two live chunks per pair.
 // Partials are rows of kPartFloats: o[128], m, l.
-template <int G>
+template <int G, int kW>
 __device__ __forceinline__ void FusedMerge(float (*wpart)[G][kPartFloats], int* last_flag, const float (&m)[G],
                                            const float (&l)[G], const float (&o)[G][8], int lane, int wave, int r,
                                            int rho, int64_t t, int32_t kh, int32_t n_heads, int32_t n_kv_heads,
@@ -389,10 +392,10 @@ __device__ __forceinline__ void FusedMerge(float (*wpart)[G][kPartFloats], int* 
   if (hh < G) {
     float mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) mx = fmaxf(mx, wpart[w][hh][kD]);
+    for (int w = 0; w < kW; ++w) mx = fmaxf(mx, wpart[w][hh][kD]);
     float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
+    for (int w = 0; w < kW; ++w) {
       const float mw = wpart[w][hh][kD];
       const float f = mw == -INFINITY ? 0.0f : expf(mw - mx);
       L = __builtin_fmaf(wpart[w][hh][kD + 1], f, L);
@@ -445,7 +448,7 @@ __device__ __forceinline__ void FusedMerge(float (*wpart)[G][kPartFloats], int* 
     const float f = ml.x == -INFINITY ? 0.0f : expf(ml.x - mx);
     const float L = WaveSumF(ml.y * f);
     // every group's rows requested at once (one memory round trip), then summed in group order
-    static_assert(kMaxGroupChunks / kWaves <= kMaxFusedGroups, "a pair has at most kMaxFusedGroups workgroups");
+    static_assert(kMaxGroupChunks / kW <= kMaxFusedGroups, "a pair has at most kMaxFusedGroups workgroups");
     float2 v[kMaxFusedGroups];
 #pragma unroll
     for (int g = 0; g < kMaxFusedGroups; ++g) {
@@ -479,7 +482,7 @@ struct DecodePrep {
   uint16_t* v_store;
 };
 
-// kFused: one launch also merges. A workgroup takes kWaves consecutive chunks of
+// kFused: one launch also merges. A workgroup takes kFusedWaves consecutive chunks of
 // one (token, kv head); its waves' (m, l, o) meet in LDS and the workgroup stores
 // one partial per query head; the workgroup whose vector atomic on the pair's
 // counter (cnt[(t * n_kv_heads + kh) * kCounterStride]) arrives last merges the
@@ -490,30 +493,31 @@ struct DecodePrep {
 // atomic; the merging workgroup reads them with device-coherent loads. No wave
 // waits on another workgroup: the first workgroups to finish just leave.
 template <int G, bool kPrep = false, bool kFused = false>
-__global__ __launch_bounds__(kBlockThreads) void AttnDecodeGroupKernel(
+__global__ __launch_bounds__(kFused ? 64 * kFusedWaves : kBlockThreads) void AttnDecodeGroupKernel(
     const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t max_seq,
     int32_t n_heads, int32_t n_kv_heads, float scale, int64_t pos0_val, const int64_t* __restrict__ pos0_dev,
     int64_t seq, int32_t n_chunks, int64_t chunk_len, float* __restrict__ out, float* __restrict__ part,
     DecodePrep prep, uint32_t* __restrict__ cnt) {
   static_assert(!kPrep || G + 2 <= 8, "q heads, k and v: one 8-lane group each");
-  static_assert(!kFused || G <= kWaves, "the fused merge gives each query head of the group one wave");
+  constexpr int kW = kFused ? kFusedWaves : kWaves;  // waves per workgroup
+  static_assert(!kFused || G <= kW, "the fused merge gives each query head of the group one wave");
   struct PrepLds {
     float q[G][kD];
     uint16_t k[kD];
     uint16_t v[kD];
   };
-  __shared__ __attribute__((aligned(16))) PrepLds prep_lds[kPrep ? kWaves : 1];
-  __shared__ __attribute__((aligned(16))) float wpart[kFused ? kWaves : 1][kFused ? G : 1][kPartFloats];
+  __shared__ __attribute__((aligned(16))) PrepLds prep_lds[kPrep ? kW : 1];
+  __shared__ __attribute__((aligned(16))) float wpart[kFused ? kW : 1][kFused ? G : 1][kPartFloats];
   __shared__ int last_flag;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int32_t n_groups = kFused ? (n_chunks + kWaves - 1) / kWaves : 1;
+  const int32_t n_groups = kFused ? (n_chunks + kW - 1) / kW : 1;
   int64_t tk;
   int32_t c;
   if constexpr (kFused) {
     tk = static_cast<int64_t>(blockIdx.x) / n_groups;
     if (tk >= seq * n_kv_heads) return;  // uniform over the workgroup
-    c = (static_cast<int32_t>(blockIdx.x - tk * n_groups)) * kWaves + wave;
+    c = (static_cast<int32_t>(blockIdx.x - tk * n_groups)) * kW + wave;
   } else {
     const int64_t unit = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
     if (unit >= seq * n_kv_heads * n_chunks) return;  // no barriers below
@@ -524,8 +528,8 @@ __global__ __launch_bounds__(kBlockThreads) void AttnDecodeGroupKernel(
   const int32_t kh = static_cast<int32_t>(tk - t * n_kv_heads);
   const int64_t pos = ReadPos0(pos0_val, pos0_dev) + t;
   const int32_t live = LiveChunks(pos, chunk_len, n_chunks);
-  const int32_t live_groups = kFused ? (live + kWaves - 1) / kWaves : 0;
-  if (kFused && c / kWaves >= live_groups) return;  // the whole workgroup: no visible key (uniform)
+  const int32_t live_groups = kFused ? (live + kW - 1) / kW : 0;
+  if (kFused && c / kW >= live_groups) return;  // the whole workgroup: no visible key (uniform)
   // kFused: a wave past the live chunks keeps m = -inf, l = 0, o = 0 and joins the barriers
   const bool dead = c >= live;
   if (!kFused && dead) return;  // no key of this chunk is visible at this position
@@ -725,8 +729,8 @@ __global__ __launch_bounds__(kBlockThreads) void AttnDecodeGroupKernel(
     }
   }
   if constexpr (kFused) {
-    if (live > 1) return FusedMerge<G>(wpart, &last_flag, m, l, o, lane, wave, r, rho, t, kh, n_heads, n_kv_heads,
-                                        n_groups, live_groups, c / kWaves, out, part, cnt);
+    if (live > 1) return FusedMerge<G, kW>(wpart, &last_flag, m, l, o, lane, wave, r, rho, t, kh, n_heads,
+                                            n_kv_heads, n_groups, live_groups, c / kW, out, part, cnt);
     // one live chunk: its wave writes the output (the other waves are dead)
     if (dead) return;
   }
@@ -1097,7 +1101,7 @@ float* EnsurePartials(size_t floats) {
 // its own address; host code must use the address hipGetSymbolAddress returns
 // for the current device (AttnScratchForDevice), never the array's name, which
 // on the host is only a registration handle.
-constexpr size_t kNoAllocScratchFloats = size_t(1) << 21;  // 8 MiB
+constexpr size_t kNoAllocScratchFloats = size_t(1) << 19;  // 2 MiB
 static __device__ __align__(256) float scratch[kNoAllocScratchFloats];
 
 constexpr int kMaxScratchDevices = 64;
@@ -1231,15 +1235,9 @@ void PlanGroupChunks(int64_t units, int64_t positions, int32_t* n_chunks, int64_
 // kMaxGroupChunks chunks): what a captured decode graph may replay.
 size_t WarmupFloats(int64_t /*positions*/) { return static_cast<size_t>(64) * kMaxGroupChunks * kPartFloats; }
 
-// Split grouped decode in one launch (merge by the last workgroup of each pair)
-// up to this position budget, the chunk kernel plus AttnMergeKernel above it.
-// Measured on MI355X, Qwen3-1.7B decode (8 kv heads), kernel time per call: one
-// launch 9.0 / 9.7 / 11.7 us at positions 512 / 2048 / 4096, two launches 9.6 /
-// 9.9 / 11.0 us. Past ~3000 positions a pair has over 24 workgroups, and the
-// serialized atomics on its counter and the last workgroup's longer merge cost
-// more than the second launch.
-constexpr int64_t kFusedMaxPositions = 3072;
-
+// A split grouped decode is one launch (AttnDecodeGroupKernel<G, kPrep, true>,
+// merged by the last workgroup of each pair), whatever the position budget: a
+// captured decode graph plans for the whole cache and replays at every position.
 template <int G>
 void LaunchDecodeGroup(const ModelMeta& c, const Pos0Arg& p0, const float* q_dev, int64_t seq,
                        const uint16_t* k_layer, const uint16_t* v_layer, int64_t max_seq, float scale,
@@ -1249,30 +1247,30 @@ void LaunchDecodeGroup(const ModelMeta& c, const Pos0Arg& p0, const float* q_dev
   int64_t chunk_len;
   PlanGroupChunks(seq * c.n_kv_heads, positions, &n_chunks, &chunk_len);
   const int64_t pairs = seq * c.n_heads;
-  if (n_chunks > 1 && positions <= kFusedMaxPositions) {
-    // one launch: workgroups of kWaves chunks, merged by the pair's last workgroup
+  if (n_chunks > 1) {
+    // one launch: workgroups of kFusedWaves chunks, merged by the pair's last workgroup
     const int64_t kv_pairs = seq * c.n_kv_heads;
     RPG_CHECK(kv_pairs <= kFusedCounterPairs, "a split decode over %lld (token, kv head) pairs exceeds the %lld "
               "arrival counters", static_cast<long long>(kv_pairs), static_cast<long long>(kFusedCounterPairs));
-    const int32_t n_groups = (n_chunks + kWaves - 1) / kWaves;
+    const int32_t n_groups = (n_chunks + kFusedWaves - 1) / kFusedWaves;
     // one workgroup per pair holds every chunk: it merges in LDS and needs no partials
     float* part = n_groups > 1 ? sink.Get(static_cast<size_t>(pairs) * n_groups * kPartFloats) : nullptr;
     uint32_t* cnt = sink.Counters();
     const dim3 grid(static_cast<unsigned>(kv_pairs * n_groups));
     if (prep != nullptr) {
-      Launch("AttnDecodePrepFusedKernel", AttnDecodeGroupKernel<G, true, true>, grid, dim3(kBlockThreads), q_dev,
+      Launch("AttnDecodePrepFusedKernel", AttnDecodeGroupKernel<G, true, true>, grid, dim3(64 * kFusedWaves), q_dev,
              k_layer, v_layer, max_seq, c.n_heads, c.n_kv_heads, scale, p0.value, p0.dev, seq, n_chunks, chunk_len,
              out_dev, part, *prep, cnt);
     } else {
-      Launch("AttnDecodeFusedKernel", AttnDecodeGroupKernel<G, false, true>, grid, dim3(kBlockThreads), q_dev,
+      Launch("AttnDecodeFusedKernel", AttnDecodeGroupKernel<G, false, true>, grid, dim3(64 * kFusedWaves), q_dev,
              k_layer, v_layer, max_seq, c.n_heads, c.n_kv_heads, scale, p0.value, p0.dev, seq, n_chunks, chunk_len,
              out_dev, part, DecodePrep{}, cnt);
     }
     return;
   }
-  float* part = nullptr;
-  if (n_chunks > 1) part = sink.Get(static_cast<size_t>(pairs) * n_chunks * kPartFloats);
-  const int64_t units = seq * c.n_kv_heads * n_chunks;
+  // one chunk per (token, kv head): each wave writes its heads' outputs, no partials
+  const int64_t units = seq * c.n_kv_heads;
+  float* const part = nullptr;
   if (prep != nullptr) {
     Launch("AttnDecodePrepKernel", AttnDecodeGroupKernel<G, true>, dim3(GridFor(units, kWaves)),
            dim3(kBlockThreads), q_dev, k_layer, v_layer, max_seq, c.n_heads, c.n_kv_heads, scale, p0.value, p0.dev,
@@ -1281,10 +1279,6 @@ void LaunchDecodeGroup(const ModelMeta& c, const Pos0Arg& p0, const float* q_dev
     Launch("AttnDecodeGroupKernel", AttnDecodeGroupKernel<G>, dim3(GridFor(units, kWaves)), dim3(kBlockThreads),
            q_dev, k_layer, v_layer, max_seq, c.n_heads, c.n_kv_heads, scale, p0.value, p0.dev, seq, n_chunks,
            chunk_len, out_dev, part, DecodePrep{}, static_cast<uint32_t*>(nullptr));
-  }
-  if (n_chunks > 1) {
-    Launch("AttnMergeKernel", AttnMergeKernel, dim3(static_cast<unsigned>(pairs)), dim3(kBlockThreads), part, pairs,
-           n_chunks, c.n_heads, chunk_len, p0.value, p0.dev, out_dev);
   }
 }
 

@@ -41,11 +41,10 @@ def test_noalloc_attention_matches_allocating_entry(gpu):
     rng = np.random.default_rng(77)
     # (name, n_heads, n_kv_heads, max_seq, pos0, seq): the first call splits the
     # keys into the most chunks, the second is smaller; both use the scratch.
-    # Up to 3072 positions a split decode is one launch whose last workgroup per
-    # (token, kv head) merges; past that, the chunk kernel and a merge launch.
-    calls = [("4B shape, decode at 4095, 2 tokens (two launches)", 32, 8, 4096, 4094, 2),
-             ("1.7B shape, decode at 3000 (one launch, 24 workgroups per pair)", 16, 8, 3072, 3000, 1),
-             ("1.7B shape, decode at 700 (one launch)", 16, 8, 4096, 700, 1)]
+    # A split decode is one launch whose last workgroup per (token, kv head) merges.
+    calls = [("4B shape, decode at 4095, 2 tokens (32 workgroups per pair)", 32, 8, 4096, 4094, 2),
+             ("1.7B shape, decode at 3000 (24 workgroups per pair)", 16, 8, 3072, 3000, 1),
+             ("1.7B shape, decode at 700", 16, 8, 4096, 700, 1)]
     for name, nh, nkv, max_seq, pos0, seq in calls:
         _case(f"noalloc vs allocating: {name}")
         q, kc, vc = _inputs(rng, nh, nkv, max_seq, seq)
@@ -69,10 +68,10 @@ def test_noalloc_attention_rejects_oversized_split(gpu):
 
     lib = gpu.load_library()
     _case("noalloc rejects a split beyond its fixed scratch")
-    # GQA group 4 with 62 x 33 = 2046 (token, kv head) pairs past 3072 positions
-    # (chunk kernel + merge launch): the split takes 2 chunks, 62 x 132 heads x 2
-    # chunks x 132 floats = 2160576 > 2^21.
-    nh, nkv, max_seq, pos0, seq = 132, 33, 3200, 3100, 62
+    # GQA group 4 with 7 x 71 = 497 (token, kv head) pairs at 1007 positions: the
+    # split takes 5 chunks, 2 workgroups per pair, 497 x 4 heads x 2 x 132 floats
+    # = 524832 > 2^19.
+    nh, nkv, max_seq, pos0, seq = 284, 71, 1024, 1000, 7
     q = torch.zeros((seq, nh, 128), dtype=torch.float32, device="cuda")
     kc = torch.zeros((nkv, max_seq, 128), dtype=torch.int16, device="cuda")
     vc = torch.zeros_like(kc)
@@ -90,37 +89,33 @@ def test_noalloc_attention_rejects_oversized_split(gpu):
 
 def _group_partials_floats(units, group, positions):
     """Partials floats of a grouped decode call: chunks of a multiple of 32 keys,
-    enough for ~2048 waves over `units` (token, kv head) pairs; no split at >= 2048
-    units or <= 128 positions. Up to 3072 positions (one launch) 132 floats per
-    (token, query head, workgroup of 4 chunks), none when one workgroup takes every
-    chunk; past that 132 floats per (token, query head, chunk)."""
+    enough for ~2048 waves over `units` (token, kv head) pairs, no split at >= 2048
+    units or <= 128 positions; one launch whose workgroups take 4 chunks each and
+    keep 132 floats per (token, query head, workgroup), none when one workgroup
+    takes every chunk."""
     if units >= 2048 or positions <= 128:
         return 0
     want = min((2048 + units - 1) // units, 128)
     length = ((positions + want - 1) // want + 31) // 32 * 32
     chunks = (positions + length - 1) // length
-    if chunks <= 1:
-        return 0
-    if positions <= 3072:
-        groups = (chunks + 3) // 4
-        return units * group * groups * 132 if groups > 1 else 0
-    return units * group * chunks * 132
+    groups = (chunks + 3) // 4
+    return units * group * groups * 132 if groups > 1 else 0
 
 
 def test_noalloc_attention_group4_boundary(gpu):
-    """GQA group 4 past 3072 positions (chunk kernel + merge launch): 5 x 397 =
-    1985 (token, kv head) pairs fit the 2^21-float scratch and match the
-    allocating entry bit for bit; 6 x 331 = 1986 pairs are rejected unlaunched.
-    Below 3072 positions (one launch) the same 1986 pairs need no partials at all."""
+    """GQA group 4 split 5 ways (2 workgroups per pair): 16 x 31 = 496 (token, kv
+    head) pairs fit the 2^19-float scratch and match the allocating entry bit for
+    bit; 7 x 71 = 497 pairs are rejected unlaunched; the same 497 pairs at 107
+    positions (no split) need no partials and go through."""
     import torch
 
     lib = gpu.load_library()
-    max_seq, pos0 = 3200, 3100
+    max_seq, pos0 = 1024, 1000
     # (seq, n_kv_heads)
-    fits, over = (5, 397), (6, 331)
-    assert _group_partials_floats(fits[0] * fits[1], 4, pos0 + fits[0]) == 1985 * 1056 <= 1 << 21
-    assert _group_partials_floats(over[0] * over[1], 4, pos0 + over[0]) == 1986 * 1056 > 1 << 21
-    assert _group_partials_floats(over[0] * over[1], 4, 1000 + over[0]) == 0
+    fits, over = (16, 31), (7, 71)
+    assert _group_partials_floats(fits[0] * fits[1], 4, pos0 + fits[0]) == 496 * 1056 <= 1 << 19
+    assert _group_partials_floats(over[0] * over[1], 4, pos0 + over[0]) == 497 * 1056 > 1 << 19
+    assert _group_partials_floats(over[0] * over[1], 4, 100 + over[0]) == 0
 
     def inputs(seq, nh, nkv, seed):
         gen = torch.Generator(device="cuda").manual_seed(seed)
@@ -141,12 +136,12 @@ def test_noalloc_attention_group4_boundary(gpu):
 
     seq, nkv = fits
     nh = 4 * nkv
-    _case(f"noalloc group-4 boundary: seq {seq}, {nh}/{nkv} heads, 1985 pairs at {pos0} (fits)")
+    _case(f"noalloc group-4 boundary: seq {seq}, {nh}/{nkv} heads, 496 pairs at {pos0} (fits)")
     both_equal(seq, nh, nkv, pos0, *inputs(seq, nh, nkv, 78))
 
     seq, nkv = over
     nh = 4 * nkv
-    _case(f"noalloc group-4 boundary: seq {seq}, {nh}/{nkv} heads, 1986 pairs at {pos0} (rejected)")
+    _case(f"noalloc group-4 boundary: seq {seq}, {nh}/{nkv} heads, 497 pairs at {pos0} (rejected)")
     q, kc, vc = inputs(seq, nh, nkv, 79)
     out = torch.full((seq, nh, 128), 7.0, dtype=torch.float32, device="cuda")
     rc = _run(lib, lib.rpg_op_attention_from_cache_noalloc, nh, nkv, pos0, seq, q, kc, vc, max_seq, out)
@@ -155,6 +150,5 @@ def test_noalloc_attention_group4_boundary(gpu):
     torch.cuda.synchronize()
     assert bool(torch.all(out == 7.0)), "a rejected call must not launch"
 
-    # the same pairs at 1006 positions: one launch, no partials; the call goes through
-    _case(f"noalloc group-4: seq {seq}, {nh}/{nkv} heads, 1986 pairs at 1000 (one launch, accepted)")
-    both_equal(seq, nh, nkv, 1000, q, kc, vc)
+    _case(f"noalloc group-4: seq {seq}, {nh}/{nkv} heads, 497 pairs at 100 (no split, accepted)")
+    both_equal(seq, nh, nkv, 100, q, kc, vc)
