@@ -724,206 +724,6 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_
   }
 }
 
-// ---------------------------------------------------------------- one token on the matrix cores (Q6_K)
-//
-// For tall Q6_K matrices (the 151936-row output projection) the per-weight work of
-// MatVecQuantKernel (unpack, convert, fused multiply-add: ~5.5 VALU instructions
-// per weight, VALU busy 67% of the kernel) keeps the loads waiting. Here each
-// row's products run on the matrix cores while the loads keep the coalesced
-// row-wise pattern of MatVecQuantKernel: the row's 2048 (or nb * 256) weights
-// are taken as a 16 x 128 nb / 8 matrix A, segment m = columns 128 m' .. of the row
-// (m' = m + 16 i for rows wider than 8 blocks), and the activations likewise as
-// B^T (16 segments of x), so v_mfma_f32_16x16x32_f16 forms all 16 x 16 segment
-// products and the row's dot product is the sum of the diagonal. The other 240
-// products are discarded: the matrix cores have ~50x the throughput this needs.
-//
-// Numerics: A = sc * (q - 32), integers of magnitude <= 1024, exact in fp16, built
-// as (1024 + q) sc - 1056 sc in one fused step. x is scaled by 2^k (max |x| into
-// [2^13, 2^14)) and split into two fp16 terms x 2^k = hi + lo (~2^-22 |x|), both
-// multiplied into the same accumulator. Every product is exact in fp32; each
-// segment's sum is scaled by its block's d, the 16 diagonal terms are summed over
-// the wave and the total is scaled by 2^-k. The result is within the fp32
-// summation bound of the other kernels.
-//
-// Lane l: segment m = l % 16 (block m / 2, half hs = m % 2 of it) and column group
-// g = l / 16. MFMA step s (0..3) gives the lane elements 32 s + 8 g + [0, 8) of
-// its segment, i.e. quarter q = s, l = 8 g + i of the half: the nibble q >> 1 of
-// ql[64 hs + 32 (q & 1) + 8 g + i], bits 2q of qh[32 hs + 8 g + i], scale
-// sc[8 hs + 2 q + g / 2]. Per row a lane loads three 8-byte runs, the 8 scales of
-// its half and d (one instruction per field covers the whole row); its share of
-// x (the B operand, 32 floats as 64 halves) stays in registers for the kernel.
-// Measured on the 1.7B output projection: 57.5-59 us against 60.4-62.5 us for
-// MatVecQuantKernel; still VALU-bound (~4.2 VALU instructions per weight, VALU
-// busy 56%): building the exact fp16 operands costs about what the multiplies
-// did. Staging the rows through LDS with whole 16-byte loads gave the same time.
-typedef _Float16 MvF16x8 __attribute__((ext_vector_type(8)));
-typedef _Float16 MvH2 __attribute__((ext_vector_type(2)));
-typedef float MvF32x4 __attribute__((ext_vector_type(4)));
-
-constexpr int kMvRows = 2;                  // rows per wave step (loaded together, next step in flight)
-constexpr int64_t kMvMaxWaves = 256 * 16;   // grid cap: 16 waves per CU on 256 CUs
-constexpr uint32_t kMvMagic = 0x64646464u;  // byte 0x64 above a quant byte q: fp16 bits of 1024 + q
-
-// fp16 pairs (1024 + b0, 1024 + b1) and (1024 + b2, 1024 + b3) of a word's bytes.
-__device__ __forceinline__ MvH2 MvMagicLo(uint32_t w) {
-  return __builtin_bit_cast(MvH2, __builtin_amdgcn_perm(kMvMagic, w, 0x04010400u));
-}
-__device__ __forceinline__ MvH2 MvMagicHi(uint32_t w) {
-  return __builtin_bit_cast(MvH2, __builtin_amdgcn_perm(kMvMagic, w, 0x04030402u));
-}
-
-struct MvQ6Raw {
-  uint2 ql0, ql1, qh;  // ql[64 hs + 8 g], ql[64 hs + 32 + 8 g], qh[32 hs + 8 g]: 8 bytes each
-  uint2 sc;            // sc[8 hs .. 8 hs + 7]
-  uint32_t d;          // f16 bits
-};
-
-// The lane's bytes of one block half. Q6_K blocks are 2-byte aligned (210 bytes);
-// each 8-byte field comes from the three aligned dwords around it, byte-aligned
-// (unaligned loads would be split per lane by the address unit). The windows start
-// at most 2 bytes before the block, in an aligned dword (hence a page) shared with
-// its first bytes, and end at or before its byte 209.
-__device__ __forceinline__ MvQ6Raw MvLoadQ6(const uint8_t* blk, int hs, int g) {
-  const uint32_t sh = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(blk) & 3u);
-  const uint8_t* ab = blk - sh;
-  MvQ6Raw r;
-  r.ql0 = Window8(*reinterpret_cast<const uint3*>(ab + 64 * hs + 8 * g), sh);
-  r.ql1 = Window8(*reinterpret_cast<const uint3*>(ab + 64 * hs + 32 + 8 * g), sh);
-  r.qh = Window8(*reinterpret_cast<const uint3*>(ab + 128 + 32 * hs + 8 * g), sh);
-  r.sc = Window8(*reinterpret_cast<const uint3*>(ab + 192 + 8 * hs), sh);
-  r.d = *reinterpret_cast<const uint16_t*>(blk + 208);
-  return r;
-}
-
-// A operand of step q: sc * (q6 - 32) for the lane's 8 elements, exact.
-__device__ __forceinline__ MvF16x8 MvQ6Operand(const MvQ6Raw& r, int q, int g) {
-  const uint2 qlw = (q & 1) ? r.ql1 : r.ql0;
-  const int ns = (q >> 1) * 4;
-  // bits 2q..2q+1 of each qh byte moved to bits 4..5
-  const uint32_t h0 = 2 * q <= 4 ? r.qh.x << (4 - 2 * q) : r.qh.x >> (2 * q - 4);
-  const uint32_t h1 = 2 * q <= 4 ? r.qh.y << (4 - 2 * q) : r.qh.y >> (2 * q - 4);
-  const uint32_t q0 = ((qlw.x >> ns) & 0x0F0F0F0Fu) | (h0 & 0x30303030u);
-  const uint32_t q1 = ((qlw.y >> ns) & 0x0F0F0F0Fu) | (h1 & 0x30303030u);
-  // scale byte 2 q + g / 2 of the half's eight
-  const uint32_t sw = q < 2 ? r.sc.x : r.sc.y;
-  const int8_t sc8 = static_cast<int8_t>((sw >> (16 * (q & 1) + 8 * (g >> 1))) & 0xFFu);
-  const _Float16 sc = static_cast<_Float16>(static_cast<float>(sc8));
-  const _Float16 off = static_cast<_Float16>(-1056.0f) * sc;  // exact: 33 * 32 * sc
-  const MvH2 s2 = {sc, sc};
-  const MvH2 o2 = {off, off};
-  const MvH2 a = __builtin_elementwise_fma(MvMagicLo(q0), s2, o2);
-  const MvH2 b = __builtin_elementwise_fma(MvMagicHi(q0), s2, o2);
-  const MvH2 c = __builtin_elementwise_fma(MvMagicLo(q1), s2, o2);
-  const MvH2 e = __builtin_elementwise_fma(MvMagicHi(q1), s2, o2);
-  MvF16x8 v;
-  v[0] = a[0]; v[1] = a[1]; v[2] = b[0]; v[3] = b[1];
-  v[4] = c[0]; v[5] = c[1]; v[6] = e[0]; v[7] = e[1];
-  return v;
-}
-
-// kSeg: segments of 128 columns per lane row slot (1 for rows of <= 8 blocks,
-// 2 for <= 16, ...): segment m + 16 j for j < kSeg.
-template <int kSeg>
-__global__ __launch_bounds__(256) void MatVecMfmaQ6KKernel(const uint8_t* __restrict__ w, int64_t rows,
-                                                           int64_t row_bytes, int32_t nb,
-                                                           const float* __restrict__ x, float* __restrict__ out) {
-  // Kernel arguments fetched in one batch at entry (see MatVecQuantKernel).
-  asm volatile("" ::"s"(w), "s"(rows), "s"(row_bytes), "s"(nb), "s"(x), "s"(out));
-  const int lane = threadIdx.x & 63;
-  const int m = lane & 15;
-  const int g = lane >> 4;
-  const int hs = m & 1;
-  // 1. the lane's activations: segment m + 16 j, elements 32 s + 8 g + [0, 8)
-  float xv[kSeg][4][8];
-  float mx = 0.0f;
-#pragma unroll
-  for (int j = 0; j < kSeg; ++j) {
-    const int seg = m + 16 * j;
-    const bool live = seg < 2 * nb;
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const float* p = x + 128 * (live ? seg : 0) + 32 * st + 8 * g;  // a dead segment reads segment 0, zeroed
-      float4 a = *reinterpret_cast<const float4*>(p);
-      float4 b = *reinterpret_cast<const float4*>(p + 4);
-      if (!live) a = b = make_float4(0.f, 0.f, 0.f, 0.f);
-      xv[j][st][0] = a.x; xv[j][st][1] = a.y; xv[j][st][2] = a.z; xv[j][st][3] = a.w;
-      xv[j][st][4] = b.x; xv[j][st][5] = b.y; xv[j][st][6] = b.z; xv[j][st][7] = b.w;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) mx = fmaxf(mx, fabsf(xv[j][st][i]));
-    }
-  }
-  mx = WaveMaxF(mx);
-  int ex = 0;
-  if (mx > 0.0f && mx <= FLT_MAX) (void)frexpf(mx, &ex);  // mx in [2^(ex-1), 2^ex)
-  const int k = 14 - ex;  // 14 when x is all zero or not finite (the products then carry the inf / NaN)
-  MvF16x8 bhi[kSeg][4], blo[kSeg][4];
-#pragma unroll
-  for (int j = 0; j < kSeg; ++j) {
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float v = ldexpf(xv[j][st][i], k);
-        const _Float16 h = static_cast<_Float16>(v);
-        bhi[j][st][i] = h;
-        blo[j][st][i] = static_cast<_Float16>(v - static_cast<float>(h));
-      }
-    }
-  }
-
-  // 2. rows wave, wave + W, ... (W = all waves of the grid), kMvRows per step
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * 4 * kMvRows;
-  int64_t r0 = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * 4 + (threadIdx.x >> 6)))) *
-               kMvRows;
-  // the lane's diagonal element: row 4 g + r of the result tile is segment m when m == 4 g + r
-  const bool diag = (m >> 2) == g;
-  const int dr = m & 3;
-  auto load = [&](int64_t base, MvQ6Raw (&raw)[kMvRows][kSeg]) {
-#pragma unroll
-    for (int rr = 0; rr < kMvRows; ++rr) {
-      const int64_t row = base + rr < rows ? base + rr : rows - 1;  // clamped: loads stay in bounds
-#pragma unroll
-      for (int j = 0; j < kSeg; ++j) {
-        const int seg = m + 16 * j;
-        const int blk = seg < 2 * nb ? seg >> 1 : nb - 1;
-        raw[rr][j] = MvLoadQ6(w + row * row_bytes + static_cast<int64_t>(blk) * kQ6KBlockBytes, hs, g);
-      }
-    }
-  };
-  MvQ6Raw cur[kMvRows][kSeg];
-  load(r0 < rows ? r0 : 0, cur);
-  for (; r0 < rows; r0 += stride) {
-    MvQ6Raw nxt[kMvRows][kSeg];
-    load(r0 + stride < rows ? r0 + stride : r0, nxt);
-    float part[kMvRows];
-#pragma unroll
-    for (int rr = 0; rr < kMvRows; ++rr) {
-      float sum = 0.0f;
-#pragma unroll
-      for (int j = 0; j < kSeg; ++j) {
-        MvF32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int st = 0; st < 4; ++st) {
-          const MvF16x8 a = MvQ6Operand(cur[rr][j], st, g);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bhi[j][st], acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, blo[j][st], acc, 0, 0, 0);
-        }
-        const float dv = dr == 0 ? acc[0] : dr == 1 ? acc[1] : dr == 2 ? acc[2] : acc[3];
-        const bool live = m + 16 * j < 2 * nb;
-        sum = __builtin_fmaf(diag && live ? dv : 0.0f, HalfBitsToFloat(cur[rr][j].d), sum);
-      }
-      part[rr] = sum;
-    }
-    const float total = ReduceRows<kMvRows>(part, lane);
-    const int rr = ReducedRow<kMvRows>(lane);
-    if ((lane & 15) == 0 && lane < 16 * kMvRows && r0 + rr < rows) out[r0 + rr] = ldexpf(total, -k);
-#pragma unroll
-    for (int rr2 = 0; rr2 < kMvRows; ++rr2)
-#pragma unroll
-      for (int j = 0; j < kSeg; ++j) cur[rr2][j] = nxt[rr2][j];
-  }
-}
-
 // Wide rows (9 to 64 blocks; e.g. ffn_down, 4B projections): the WS waves of a
 // workgroup share RI rows, wave q taking the block groups q, q + WS, ... (a
 // group is 8 consecutive blocks, one per lane group), so a matrix with few rows
@@ -1090,20 +890,6 @@ void LaunchSplit(const char* name, const uint8_t* w, int64_t rows, int64_t row_b
   Launch(name, MatVecSplitKernel<kType, WS, NXW, RI>, dim3(grid), dim3(64 * WS), w, rows, row_bytes, nb, x, out);
 }
 
-// Q6_K one-token matvec on the matrix cores for matrices of at least this many
-// rows (the output projection), rows of at most 16 blocks.
-constexpr int64_t kMvMinRows = 16384;
-
-void LaunchMatVecMfmaQ6K(const uint8_t* w, int64_t rows, int64_t row_bytes, int32_t nb, const float* x, float* out) {
-  const int64_t need = (rows + 4 * kMvRows - 1) / (4 * kMvRows);
-  const unsigned grid = static_cast<unsigned>(need < kMvMaxWaves / 4 ? need : kMvMaxWaves / 4);
-  if (nb <= 8) {
-    Launch("MatVecMfmaQ6KKernel", MatVecMfmaQ6KKernel<1>, dim3(grid), dim3(256), w, rows, row_bytes, nb, x, out);
-  } else {
-    Launch("MatVecMfmaQ6KKernel", MatVecMfmaQ6KKernel<2>, dim3(grid), dim3(256), w, rows, row_bytes, nb, x, out);
-  }
-}
-
 // Rows per wave: enough waves to cover the chip first (a wave per row below
 // 8192 rows), then 2 or 4 rows so each lane's activations serve several rows.
 template <uint32_t kType>
@@ -1111,9 +897,6 @@ void LaunchByShape(const char* name, const uint8_t* w, int64_t rows, int64_t row
                    int64_t cols, int64_t n_tokens, float* out) {
   const char* dname = kType == kGgmlQ4_K ? "MatVecQ4KKernel" : "MatVecQ6KKernel";
   const char* sname = kType == kGgmlQ4_K ? "MatVecSplitQ4KKernel" : "MatVecSplitQ6KKernel";
-  if (kType == kGgmlQ6_K && n_tokens == 1 && rows >= kMvMinRows && nb <= 16) {
-    return LaunchMatVecMfmaQ6K(w, rows, row_bytes, nb, x, out);
-  }
   if (n_tokens == 1 && nb <= kGroups) {
     if (kType == kGgmlQ4_K && rows >= 32768) return LaunchDecode<kType, 4>(dname, w, rows, row_bytes, nb, x, out);
     return LaunchDecode<kType, 2>(dname, w, rows, row_bytes, nb, x, out);

@@ -39,7 +39,7 @@ def main() -> None:
         raise SystemExit("oracle/_ref/libref_quant.so missing: run `make -C oracle ref` where /root/reference exists")
     rng = np.random.default_rng(SEED)
     q4 = np.concatenate([synth.q4k_blocks(rng, 48), synth.special_q4k_blocks()])
-    q6 = np.concatenate([synth.q6k_blocks(rng, 48), synth.special_q6k_blocks()])
+    q6 = np.concatenate([synth.q6k_blocks(rng, 48, bench_scales=True), synth.special_q6k_blocks()])
     q4_out = pyoracle.ref_dequantize_row(12, q4.reshape(-1), q4.shape[0] * 256)
     q6_out = pyoracle.ref_dequantize_row(14, q6.reshape(-1), q6.shape[0] * 256)
 

@@ -4,8 +4,12 @@ All generators take a numpy Generator so a test's seed fixes its inputs.
 Q4_K / Q6_K tables follow the benchmark's description of the synthetic token_embd:
   Q4_K: d, dmin = fp16_rne(|N(0, 0.01)|); the 12 packed scale bytes uniform
         (every unpacked 6-bit scale/min uniform over 0..63); qs uniform bytes.
-  Q6_K: d = fp16_rne(|N(0, 0.01)|); scales int8 uniform over -32..31; ql / qh
-        uniform bytes (6-bit quants uniform).
+  Q6_K: d = fp16_rne(|N(0, 0.01)|); ql / qh uniform bytes (6-bit quants uniform);
+        scales int8 over the format's whole range by default: uniform over
+        -128..127 with one scale of each block set to -128, which is what the
+        llama.cpp quantiser writes (the block's largest-magnitude scale maps to
+        -128). bench_scales=True gives the benchmark's table instead, scales
+        uniform over -32..31, where every sc * (q - 32) fits in 11 bits.
 """
 from __future__ import annotations
 
@@ -34,10 +38,15 @@ def q4k_blocks(rng: np.random.Generator, n_blocks: int) -> np.ndarray:
     return b
 
 
-def q6k_blocks(rng: np.random.Generator, n_blocks: int) -> np.ndarray:
+def q6k_blocks(rng: np.random.Generator, n_blocks: int, bench_scales: bool = False) -> np.ndarray:
     """n_blocks raw Q6_K super-blocks, shape [n_blocks, 210] uint8."""
     b = rng.integers(0, 256, size=(n_blocks, Q6K_BYTES), dtype=np.uint8)
-    b[:, 192:208] = rng.integers(-32, 32, size=(n_blocks, 16)).astype(np.int8).view(np.uint8)
+    if bench_scales:
+        sc = rng.integers(-32, 32, size=(n_blocks, 16)).astype(np.int8)
+    else:
+        sc = rng.integers(-128, 128, size=(n_blocks, 16)).astype(np.int8)
+        sc[np.arange(n_blocks), rng.integers(0, 16, size=n_blocks)] = -128
+    b[:, 192:208] = sc.view(np.uint8)
     d = f16_bits(np.abs(rng.normal(0.0, 0.01, n_blocks)))
     b[:, 208:210] = d.view(np.uint8).reshape(n_blocks, 2)
     return b
@@ -70,10 +79,13 @@ def model_q4k_blocks(rng: np.random.Generator, n_blocks: int, d: float = 0.002) 
     return b
 
 
-def model_q6k_blocks(rng: np.random.Generator, n_blocks: int, d: float = 1e-4) -> np.ndarray:
-    """Q6_K blocks with trained-weight-like values: d sc (q - 32), zero mean."""
+def model_q6k_blocks(rng: np.random.Generator, n_blocks: int, d: float = 2.5e-5) -> np.ndarray:
+    """Q6_K blocks with trained-weight-like values: d sc (q - 32), zero mean, the
+    scales over the whole int8 range with one -128 per block (as quantised)."""
     b = rng.integers(0, 256, size=(n_blocks, Q6K_BYTES), dtype=np.uint8)
-    b[:, 192:208] = rng.integers(-32, 32, size=(n_blocks, 16)).astype(np.int8).view(np.uint8)
+    sc = rng.integers(-128, 128, size=(n_blocks, 16)).astype(np.int8)
+    sc[np.arange(n_blocks), rng.integers(0, 16, size=n_blocks)] = -128
+    b[:, 192:208] = sc.view(np.uint8)
     dd = f16_bits(np.full(n_blocks, d) * rng.uniform(0.5, 1.5, n_blocks))
     b[:, 208:210] = dd.view(np.uint8).reshape(n_blocks, 2)
     return b
@@ -91,13 +103,14 @@ def model_table(rng: np.random.Generator, ggml_type: int, rows: int, cols: int) 
     raise ValueError(ggml_type)
 
 
-def quant_table(rng: np.random.Generator, ggml_type: int, rows: int, cols: int) -> np.ndarray:
+def quant_table(rng: np.random.Generator, ggml_type: int, rows: int, cols: int,
+                bench_scales: bool = False) -> np.ndarray:
     """A [rows, cols] table as raw bytes, shape [rows * row_bytes] uint8."""
     nb = cols // 256
     if ggml_type == 12:
         return q4k_blocks(rng, rows * nb).reshape(-1)
     if ggml_type == 14:
-        return q6k_blocks(rng, rows * nb).reshape(-1)
+        return q6k_blocks(rng, rows * nb, bench_scales).reshape(-1)
     if ggml_type == 0:
         return rng.normal(0.0, 1.0, rows * cols).astype(np.float32).view(np.uint8)
     raise ValueError(ggml_type)

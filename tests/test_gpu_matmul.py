@@ -85,9 +85,9 @@ SHAPES = [
     (12, 300, 16384, 1),     # 64 blocks per row: the widest LDS-staged decode
     (14, 100, 20480, 1),     # 80 blocks per row: the tiled kernel
     (12, 40000, 2048, 1),    # 4 rows per wave
-    (14, 40001, 2048, 1),    # Q6_K on the matrix cores, ragged last tile of 16 rows
-    (14, 16384, 2048, 1),    # ... the smallest such matrix, whole tiles
-    (14, 16393, 2560, 1),    # ... 10 blocks per row (4B width), ragged tile
+    (14, 40001, 2048, 1),    # tall Q6_K (output-projection width), odd row count
+    (14, 16384, 2048, 1),
+    (14, 16393, 2560, 1),    # ... 10 blocks per row (4B width)
     (12, 2048, 2048, 2),
     (14, 2048, 2048, 3),
     (12, 1000, 2048, 4),
@@ -129,14 +129,17 @@ def test_matmul_quant_vs_f64(gpu, ora, t, rows, cols, n):
     check(host(out), exact, absdot, cols, factored_magnitude(ora, t, w, rows, cols, x))
 
 
-def test_matmul_quant_lm_head_shape(gpu, ora):
-    """The 1.7B output projection: [151936, 2048] Q6_K at n = 1."""
+@pytest.mark.parametrize("bench_scales", [False, True], ids=["int8 scales", "bench scales"])
+def test_matmul_quant_lm_head_shape(gpu, ora, bench_scales):
+    """The 1.7B output projection: [151936, 2048] Q6_K at n = 1, with the scales
+    a quantised model carries (the whole int8 range, -128 in every block) and
+    with the benchmark's table (scales in -32..31)."""
     import torch
 
     t, rows, cols = 14, 151936, 2048
-    case(f"matmul lm_head rows={rows}")
+    case(f"matmul lm_head rows={rows} bench_scales={bench_scales}")
     rng = np.random.default_rng(790)
-    w = synth.quant_table(rng, t, rows, cols)
+    w = synth.quant_table(rng, t, rows, cols, bench_scales=bench_scales)
     x = rng.normal(0, 1, (1, cols)).astype(np.float32)
     out = torch.empty((1, rows), dtype=torch.float32, device="cuda")
     wd = dev(w)
@@ -151,14 +154,14 @@ def test_matmul_quant_lm_head_shape(gpu, ora):
 
 
 @pytest.mark.parametrize("scale", [0.0, 1e-30, 1e30, "outlier"])
-def test_matmul_q6k_matrix_core_decode_activation_range(gpu, ora, scale):
-    """The matrix-core Q6_K decode splits x 2^k into two fp16 terms with 2^k chosen
-    from max |x|: all-zero rows, tiny and huge activations and one outlier 2^20
-    times the rest all stay within the summation bound."""
+def test_matmul_q6k_decode_activation_range(gpu, ora, scale):
+    """Tall Q6_K one-token matvec (the output projection's kernel): all-zero rows,
+    tiny and huge activations and one outlier 2^20 times the rest all stay within
+    the summation bound, with scales over the whole int8 range."""
     import torch
 
     t, rows, cols = 14, 16400, 2048
-    case(f"matmul Q6_K matrix-core decode, activations x {scale}")
+    case(f"matmul Q6_K tall decode, activations x {scale}")
     rng = np.random.default_rng(791)
     w = synth.quant_table(rng, t, rows, cols)
     x = rng.normal(0, 1, (1, cols)).astype(np.float32)
@@ -167,15 +170,36 @@ def test_matmul_q6k_matrix_core_decode_activation_range(gpu, ora, scale):
     else:
         x = (x * np.float32(scale)).astype(np.float32)
     out = torch.full((1, rows), np.nan, dtype=torch.float32, device="cuda")
-    gpu.profile_start(4)
     gpu.GpuMatMulQuant(gpu.GpuTensor(dev(w), t, rows, cols), dev(x), 1, out)
-    gpu.profile_stop()
-    assert "MatVecMfmaQ6KKernel" in gpu.profile_report()
     exact, absdot = ora.matmul_quant_f64(t, w, rows, cols, x)
     got = host(out)
     if scale == 0.0:
         assert np.all(got == 0.0)
     check(got, exact, absdot, cols)
+
+
+def test_matmul_q6k_extreme_scales(gpu, ora):
+    """Q6_K blocks at the ends of the format: scales -128 and 127 with quants 0
+    and 63, so |sc (q - 32)| reaches 4096 (12 significant bits, more than fp16
+    holds) in every decode and prefill kernel; the results must stay within the
+    summation bound, and -128 * -32 * d exact."""
+    import torch
+
+    cols = 2048
+    for rows, n in ((16400, 1), (1024, 1), (300, 5), (2048, 64)):
+        case(f"matmul Q6_K extreme scales [{rows} x {cols}] x {n}")
+        rng = np.random.default_rng(792 + n)
+        w = synth.quant_table(rng, 14, rows, cols).reshape(-1, 210)
+        w[:, 0:128] = np.where(rng.random((w.shape[0], 128)) < 0.5, 0x00, 0xFF)  # q low nibbles 0 / 15
+        w[:, 128:192] = np.where(rng.random((w.shape[0], 64)) < 0.5, 0x00, 0xFF)  # high bits 0 / 3 -> q 0 / 63
+        sc = np.where(rng.random((w.shape[0], 16)) < 0.5, -128, 127).astype(np.int8)
+        w[:, 192:208] = sc.view(np.uint8)
+        w = w.reshape(-1)
+        x = rng.normal(0, 1, (n, cols)).astype(np.float32)
+        out = torch.full((n, rows), np.nan, dtype=torch.float32, device="cuda")
+        gpu.GpuMatMulQuant(gpu.GpuTensor(dev(w), 14, rows, cols), dev(x), n, out)
+        exact, absdot = ora.matmul_quant_f64(14, w, rows, cols, x)
+        check(host(out), exact, absdot, cols)
 
 
 @pytest.mark.parametrize("t,w_off,x_off", [(12, 4, 0), (14, 1, 0), (14, 2, 0), (12, 0, 1), (0, 0, 0), (0, 4, 3)])

@@ -9,9 +9,10 @@ against the generic per-element kernel on the same weights and inputs.
 The kernels sum in different orders (that is where their speed comes from), so
 bit equality is asked on inputs where every order gives the exact sum: fp16
 scales that are powers of two (Q4_K d = dmin = 2^-4, Q6_K d = 2^-6, Q6_K scales
-in [-32, 31]) and activations in {-1, 0, 1}. Every product is then a multiple of
-the scale below 2^11 of it, every partial sum an exact multiple of it below 2^24
-of it -- including the matrix cores' fp16-split operands, which are exact
+over the whole int8 range, one -128 per block) and activations in {-1, 0, 1}.
+Every product is then a multiple of the scale below 2^12 of it, and every partial
+sum an exact multiple of it below 2^24 of it (checked per row: sum |w| stays
+below that) -- including the matrix cores' fp16-split operands, which are exact
 integers here -- so any misplaced block, scale, nibble or column shows as a bit
 difference, and both must equal the oracle's exact float64 result. On general
 inputs (random scales and activations) the generic kernel is held to the same
@@ -40,7 +41,9 @@ def exact_table(rng, qtype, rows, cols):
         raw[:, 0:2] = np.frombuffer(np.float16(2.0 ** -4).tobytes(), np.uint8)  # d
         raw[:, 2:4] = np.frombuffer(np.float16(2.0 ** -4).tobytes(), np.uint8)  # dmin
     else:
-        raw[:, 192:208] = rng.integers(-32, 32, size=(blocks, 16)).astype(np.int8).view(np.uint8)  # scales
+        sc = rng.integers(-128, 128, size=(blocks, 16)).astype(np.int8)  # scales, the whole int8 range
+        sc[np.arange(blocks), rng.integers(0, 16, size=blocks)] = -128
+        raw[:, 192:208] = sc.view(np.uint8)
         raw[:, 208:210] = np.frombuffer(np.float16(2.0 ** -6).tobytes(), np.uint8)  # d
     return raw.reshape(-1)
 
@@ -52,8 +55,8 @@ CASES = [
     ("decode Q4_K, 4 rows per wave", Q4_K, 32768, 2048, 1, "MatVecQ4KKernel"),
     ("decode Q6_K", Q6_K, 1024, 2048, 1, "MatVecQ6KKernel"),
     ("decode Q6_K, split columns", Q6_K, 2048, 6144, 1, "MatVecSplitQ6KKernel"),
-    ("decode Q6_K on the matrix cores, ragged tile", Q6_K, 16400, 2048, 1, "MatVecMfmaQ6KKernel"),
-    ("decode Q6_K on the matrix cores, 10 blocks per row", Q6_K, 16384, 2560, 1, "MatVecMfmaQ6KKernel"),
+    ("decode Q6_K, tall matrix", Q6_K, 16400, 2048, 1, "MatVecQ6KKernel"),
+    ("decode Q6_K, tall, 10 blocks per row", Q6_K, 16384, 2560, 1, "MatVecSplitQ6KKernel"),
     ("decode Q4_K, split columns", Q4_K, 1024, 4096, 1, "MatVecSplitQ4KKernel"),
     ("small batch Q4_K", Q4_K, 2048, 2048, 8, "MatMulQ4KKernel"),
     ("small batch Q6_K", Q6_K, 1024, 2048, 5, "MatMulQ6KKernel"),
@@ -69,6 +72,10 @@ CASES = [
      "MatMulMfmaQ6KPlanes"),
     ("decoded weight planes Q4_K, 10 blocks per row (4B shape)", Q4_K, 1024, 2560, 520, "MatMulMfmaQ4KPlanes"),
 ]
+
+
+def _dequant(ora, qtype, raw, rows, cols):
+    return ora.dequantize_row(qtype, raw, rows * cols).reshape(rows, cols).astype(np.float64)
 
 
 def _run(gpu, qtype, w, rows, cols, x, n_tokens, force_generic):
@@ -94,6 +101,9 @@ def test_specialised_equals_generic_bit_for_bit(gpu, ora, name, qtype, rows, col
     _case(f"generic vs specialised: {name} [{rows} x {cols}] x {n_tokens} tokens")
     rng = np.random.default_rng(rows * 7 + cols + n_tokens)
     raw = exact_table(rng, qtype, rows, cols)
+    unit = 2.0 ** -6 if qtype == Q6_K else 2.0 ** -4  # every weight is an integer multiple of d
+    wabs = np.abs(_dequant(ora, qtype, raw, rows, cols)).sum(axis=1, dtype=np.float64)
+    assert np.all(wabs / unit < 2.0 ** 24), "premise: every partial sum exact in fp32"
     x = rng.integers(-1, 2, size=(n_tokens, cols)).astype(np.float32)
     w = torch.from_numpy(raw).cuda()
     xd = torch.from_numpy(x).cuda()
