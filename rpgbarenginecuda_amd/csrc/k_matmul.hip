@@ -323,6 +323,81 @@ __global__ __launch_bounds__(kMmBlock) void MatMulQuantKernel(const uint8_t* __r
   }
 }
 
+// A lane's field offsets inside a row (bytes from the row's first byte), for rows
+// that start at a multiple of 4 bytes (Q4_K rows always do; Q6_K rows when the
+// matrix base and the row size are multiples of 4). They do not change from row
+// to row, so each load is the row's wave-uniform address plus a 32-bit lane offset
+// and an immediate: no per-row address arithmetic on the vector unit.
+struct LaneOffs {
+  uint32_t a;   // Q4_K: the block header; Q6_K: the aligned dword before ql run 0 (run 1 at +32)
+  uint32_t b;   // Q4_K: the lane's 16 qs bytes; Q6_K: the aligned dword before the qh run
+  uint32_t c;   // Q6_K: the first scale dword (the second at +4)
+  uint32_t c3;  // Q6_K: the third scale dword (+4 again when the block is 4-aligned)
+  uint32_t d;   // Q6_K: d
+  uint32_t sh;  // Q6_K: the block's byte offset inside its aligned dword (0 or 2)
+};
+
+template <uint32_t kType>
+__device__ __forceinline__ LaneOffs MakeLaneOffs(uint32_t blk_off, int s) {
+  LaneOffs o;
+  if (kType == kGgmlQ4_K) {
+    o.a = blk_off;
+    o.b = blk_off + 16 + 32 * (s >> 1) + 16 * (s & 1);
+    o.c = o.c3 = o.d = o.sh = 0;
+  } else {
+    const uint32_t h = static_cast<uint32_t>(s >> 2);
+    const uint32_t lq = 8u * static_cast<uint32_t>(s & 3);
+    o.sh = blk_off & 3u;
+    const uint32_t ab = blk_off - o.sh;
+    o.a = ab + 64 * h + lq;
+    o.b = ab + 128 + 32 * h + lq;
+    o.c = ab + 192 + 8 * h;
+    o.c3 = o.c + 4 + 2 * o.sh;
+    o.d = blk_off + 208;
+  }
+  return o;
+}
+
+// LoadLaneBytes for rows that start at a multiple of 4 bytes, through a buffer
+// resource on the matrix (wave-uniform), the row's byte offset in a scalar
+// register and the lane's row-invariant offsets: same bytes, same windows.
+typedef unsigned int LbU32x3 __attribute__((ext_vector_type(3)));
+typedef unsigned int LbU32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int LbU32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t MatrixResource(const uint8_t* base) {
+  // 0x00020000: raw (untyped) buffer, 32-bit data format; no record limit (the
+  // row offsets stay below 2^31, and every field read lies inside its block's
+  // aligned dwords).
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(base), static_cast<short>(0), -1, 0x00020000);
+}
+
+template <uint32_t kType>
+__device__ __forceinline__ LaneBytes LoadLaneBytesBuf(__amdgpu_buffer_rsrc_t rs, uint32_t row_off, const LaneOffs& o) {
+  LaneBytes r;
+  if (kType == kGgmlQ4_K) {
+    const LbU32x4 a = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(o.a), static_cast<int>(row_off), 0);
+    const LbU32x4 b = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(o.b), static_cast<int>(row_off), 0);
+    r.a = make_uint4(a.x, a.y, a.z, a.w);
+    r.b = make_uint4(b.x, b.y, b.z, b.w);
+    r.d6 = 0;
+  } else {
+    const LbU32x3 f0 = __builtin_amdgcn_raw_buffer_load_b96(rs, static_cast<int>(o.a), static_cast<int>(row_off), 0);
+    const LbU32x3 f1 = __builtin_amdgcn_raw_buffer_load_b96(rs, static_cast<int>(o.a + 32), static_cast<int>(row_off), 0);
+    const LbU32x3 fh = __builtin_amdgcn_raw_buffer_load_b96(rs, static_cast<int>(o.b), static_cast<int>(row_off), 0);
+    const LbU32x2 s01 = __builtin_amdgcn_raw_buffer_load_b64(rs, static_cast<int>(o.c), static_cast<int>(row_off), 0);
+    const uint32_t s2 = __builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(o.c3), static_cast<int>(row_off), 0);
+    const uint16_t d = __builtin_amdgcn_raw_buffer_load_b16(rs, static_cast<int>(o.d), static_cast<int>(row_off), 0);
+    const uint2 ql0 = Window8(make_uint3(f0.x, f0.y, f0.z), o.sh);
+    const uint2 ql1 = Window8(make_uint3(f1.x, f1.y, f1.z), o.sh);
+    const uint2 qh = Window8(make_uint3(fh.x, fh.y, fh.z), o.sh);
+    const uint2 sc = Window8(make_uint3(s01.x, s01.y, s2), o.sh);
+    r.a = make_uint4(ql0.x, ql0.y, ql1.x, ql1.y);
+    r.b = make_uint4(qh.x, qh.y, sc.x, sc.y);
+    r.d6 = d;
+  }
+  return r;
+}
+
 // ---------------------------------------------------------------- decode (one token)
 //
 // One token, rows of at most 16 super-blocks (cols <= 4096: every Qwen3-1.7B /
@@ -434,27 +509,31 @@ __device__ __forceinline__ float BlockDot(const LaneBytes& r, int s, const float
     acc = __builtin_fmaf(d9 * static_cast<float>(sc1), shi, acc);
     return __builtin_fmaf(-(dmin * static_cast<float>(m1)), sx[1], acc);
   } else {
+    // Bytes 4(q6 - 32) = (q6 << 2) ^ 0x80 as signed int8, q6 = nib | h << 4, built
+    // in place: bits 2-5 the low nibble (ql shifted by 2 either way), bits 6-7 the
+    // 2-bit high part h (qh shifted so that field q lands there), the ^ 0x80
+    // applied to all of qh once (it flips the top bit of every 2-bit field). The
+    // group factor d * sc / 4 = (d / 4) * sc is exact either way.
     const int is = (s & 3) >> 1;
-    const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.d6)));
+    const float d4 = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.d6))) * 0.25f;
     const uint32_t ql[2][2] = {{r.a.x, r.a.y}, {r.a.z, r.a.w}};
-    const uint32_t qh[2] = {r.b.x, r.b.y};
-    const uint32_t scw[2] = {r.b.z, r.b.w};
+    const uint32_t qhx[2] = {r.b.x ^ 0xAAAAAAAAu, r.b.y ^ 0xAAAAAAAAu};
+    // scale is + 2 q of the half's eight: byte 2 (q & 1) of scs[q >> 1]
+    const uint32_t scs[2] = {r.b.z >> (8 * is), r.b.w >> (8 * is)};
     float acc = 0.0f;
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const int si = is + 2 * q;
-      const int8_t sc = static_cast<int8_t>(ByteOf(scw[si >> 2], si & 3));
+      const float dsc = d4 * SByteF(scs[q >> 1], 2 * (q & 1));
       float part = 0.0f;
 #pragma unroll
       for (int k = 0; k < 2; ++k) {
-        const uint32_t nib = (q < 2 ? ql[q & 1][k] : ql[q & 1][k] >> 4) & 0x0F0F0F0Fu;
-        const uint32_t hi2 = (2 * q >= 4 ? qh[k] >> (2 * q - 4) : qh[k] << (4 - 2 * q)) & 0x30303030u;
-        // bytes 4(q6 - 32) as signed int8: (q6 << 2) ^ 0x80 with q6 = nib | hi2 < 64
-        const uint32_t b = Opaque(((nib | hi2) << 2) ^ 0x80808080u);
+        const uint32_t lo = q < 2 ? ql[q & 1][k] << 2 : ql[q & 1][k] >> 2;
+        const uint32_t hi = qhx[k] << (6 - 2 * q);
+        const uint32_t b = Opaque((lo & 0x3C3C3C3Cu) | (hi & 0xC0C0C0C0u));
 #pragma unroll
         for (int j = 0; j < 4; ++j) part = __builtin_fmaf(SByteF(b, j), xv[8 * q + 4 * k + j], part);
       }
-      acc = __builtin_fmaf((d * static_cast<float>(sc)) * 0.25f, part, acc);
+      acc = __builtin_fmaf(dsc, part, acc);
     }
     return acc;
   }
@@ -495,9 +574,23 @@ struct NormPrologue {
   float eps;
 };
 
+// The first three segment ends clamped to 32 bits (the launcher keeps every row
+// index below 2^31), so the per-row segment lookup compares in scalar registers:
+// the scalar unit has no ordered 64-bit compare, and 64-bit ones run on the
+// vector unit.
+struct SegEnds32 {
+  int32_t e[3];
+};
+__device__ __forceinline__ SegEnds32 Ends32(const MatSegs& sg) {
+  SegEnds32 r;
+#pragma unroll
+  for (int i = 0; i < 3; ++i) r.e[i] = static_cast<int32_t>(sg.end[i] < INT32_MAX ? sg.end[i] : INT32_MAX);
+  return r;
+}
 // Segment of global row r (uniform over the wave, so scalar).
-__device__ __forceinline__ int SegOf(const MatSegs& sg, int64_t r) {
-  return (r >= sg.end[0]) + (r >= sg.end[1]) + (r >= sg.end[2]);
+__device__ __forceinline__ int SegOf(const SegEnds32& se, int64_t r) {
+  const int32_t r32 = static_cast<int32_t>(r);
+  return (r32 >= se.e[0]) + (r32 >= se.e[1]) + (r32 >= se.e[2]);
 }
 
 // a[i] through selects over constant indices. Indexing the kernel-argument
@@ -533,7 +626,11 @@ __device__ __forceinline__ int64_t SegFirst(const MatSegs& sg, int i) {
 // (v * scale) * w), before the dot products; the sum of squares is taken in
 // another order than GpuAddRmsNorm's, so the scale can differ from it in the
 // last bit of the double sum.
-template <uint32_t kType, int NX, int RI, bool kPaired = false, uint32_t kTypeB = kType, bool kNorm = false>
+// kAl4: every row of every segment starts at a multiple of 4 bytes and lies below
+// 2^31 bytes from its segment's base (checked by the launcher), so the weight
+// loads take the buffer form of LoadLaneBytesBuf.
+template <uint32_t kType, int NX, int RI, bool kPaired = false, uint32_t kTypeB = kType, bool kNorm = false,
+          bool kAl4 = false>
 __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_t rows, int64_t row_bytes, int32_t nb,
                                                               const float* __restrict__ x, NormPrologue nrm) {
   static_assert(!kNorm || NX == 1, "the norm prologue needs the whole row in one wave");
@@ -551,10 +648,13 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_
   asm volatile("" ::"s"(sg.w[0]), "s"(sg.w[1]), "s"(sg.w[2]), "s"(sg.w[3]), "s"(sg.end[0]), "s"(sg.end[1]),
                "s"(sg.end[2]), "s"(rows), "s"(row_bytes), "s"(nb), "s"(x));
 
+  const SegEnds32 se = Ends32(sg);
   // Row bookkeeping is uniform over the wave: keep it in scalar registers.
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * kWavesPerBlock * RI;
-  int64_t r0 = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(
-                   static_cast<int>(blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6)))) * RI;
+  // (32-bit: the launcher keeps rows + stride below 2^31, and the scalar unit
+  // compares 32-bit values only.)
+  const int32_t nrows = static_cast<int32_t>(rows);
+  const int32_t stride = static_cast<int32_t>(gridDim.x) * kWavesPerBlock * RI;
+  int32_t r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6))) * RI;
   // No early exit for waves past the last row: a branch here would keep the
   // compiler from fetching the remaining kernel arguments in the first batch. Such
   // waves load the last row's bytes (the load below clamps the row) and skip the
@@ -566,6 +666,8 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_
   float xvb[kMixed ? NX : 1][32];  // the same activations in kTypeB's lane order
   float sxb[kMixed ? NX : 1][2];
   int64_t lane_off_b[kMixed ? NX : 1];
+  LaneOffs offs[NX];
+  LaneOffs offs_b[kMixed ? NX : 1];
   if (kNorm) {
     // The workgroup forms h once: each thread takes 4-float slices of the row,
     // the sum of squares meets in LDS (waves added in a fixed order), and h is
@@ -621,7 +723,7 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_
       }
       RunSums(xvb[0], sxb[0]);
     }
-    if (r0 >= rows) return;  // after the workgroup's barriers
+    if (r0 >= nrows) return;  // after the workgroup's barriers
   }
 #pragma unroll
   for (int it = 0; it < (kNorm ? 0 : NX); ++it) {
@@ -646,53 +748,78 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_
     }
   }
 
+#pragma unroll
+  for (int it = 0; it < NX; ++it) {
+    offs[it] = MakeLaneOffs<kType>(static_cast<uint32_t>(lane_off[it]), s);
+    if (kMixed) offs_b[it] = MakeLaneOffs<kTypeB>(static_cast<uint32_t>(lane_off_b[it]), s);
+  }
+
   // Rows past the end are clamped to the last row (loads stay in bounds; results are dropped).
-  auto load = [&](int64_t base_row, LaneBytes (&lb)[RI][NX]) {
+  auto load = [&](int32_t base_row, LaneBytes (&lb)[RI][NX]) {
     if (kPaired) {
-      const int64_t p = (base_row < rows ? base_row : rows - 2) >> 1;
+      const int64_t p = (base_row < nrows ? base_row : nrows - 2) >> 1;
 #pragma unroll
       for (int r = 0; r < RI; ++r) {
-        const uint8_t* rp = sg.w[r] + p * row_bytes;
+        if (kAl4) {
+          const __amdgpu_buffer_rsrc_t rs = MatrixResource(sg.w[r]);
+          const uint32_t ro = static_cast<uint32_t>(p * row_bytes);
 #pragma unroll
-        for (int it = 0; it < NX; ++it) lb[r][it] = LoadLaneBytes<kType>(rp + lane_off[it], s);
+          for (int it = 0; it < NX; ++it) lb[r][it] = LoadLaneBytesBuf<kType>(rs, ro, offs[it]);
+        } else {
+          const uint8_t* rp = sg.w[r] + p * row_bytes;
+#pragma unroll
+          for (int it = 0; it < NX; ++it) lb[r][it] = LoadLaneBytes<kType>(rp + lane_off[it], s);
+        }
       }
       return;
     }
     // base_row is clamped before the segment lookup: past the last row the lookup
     // would name an unused (null) segment, and the row offset from its first row
     // would be negative.
-    const int64_t br = base_row < rows ? base_row : rows - 1;
-    const int sgi = SegOf(sg, br);
+    const int32_t br = base_row < nrows ? base_row : nrows - 1;
+    const int sgi = SegOf(se, br);
     const uint8_t* wseg = PickSeg(sg.w, sgi);
     const int64_t first = SegFirst(sg, sgi);
     if (kMixed && ((sg.b_mask >> sgi) & 1u)) {
 #pragma unroll
       for (int r = 0; r < RI; ++r) {
-        const int64_t row = br + r < rows ? br + r : rows - 1;
-        const uint8_t* rp = wseg + (row - first) * sg.row_bytes_b;
+        const int64_t row = br + r < nrows ? br + r : nrows - 1;
+        if (kAl4) {
+          const uint32_t ro = static_cast<uint32_t>((row - first) * sg.row_bytes_b);
 #pragma unroll
-        for (int it = 0; it < NX; ++it) lb[r][it] = LoadLaneBytes<kTypeB>(rp + lane_off_b[it], s);
+          for (int it = 0; it < NX; ++it) lb[r][it] = LoadLaneBytesBuf<kTypeB>(MatrixResource(wseg), ro, offs_b[it]);
+        } else {
+          const uint8_t* rp = wseg + (row - first) * sg.row_bytes_b;
+#pragma unroll
+          for (int it = 0; it < NX; ++it) lb[r][it] = LoadLaneBytes<kTypeB>(rp + lane_off_b[it], s);
+        }
       }
       return;
     }
 #pragma unroll
     for (int r = 0; r < RI; ++r) {
-      const int64_t row = br + r < rows ? br + r : rows - 1;
-      const uint8_t* rp = wseg + (row - first) * row_bytes;
+      const int64_t row = br + r < nrows ? br + r : nrows - 1;
+      if (kAl4) {
+        const uint32_t ro = static_cast<uint32_t>((row - first) * row_bytes);
 #pragma unroll
-      for (int it = 0; it < NX; ++it) lb[r][it] = LoadLaneBytes<kType>(rp + lane_off[it], s);
+        for (int it = 0; it < NX; ++it) lb[r][it] = LoadLaneBytesBuf<kType>(MatrixResource(wseg), ro, offs[it]);
+      } else {
+        const uint8_t* rp = wseg + (row - first) * row_bytes;
+#pragma unroll
+        for (int it = 0; it < NX; ++it) lb[r][it] = LoadLaneBytes<kType>(rp + lane_off[it], s);
+      }
     }
   };
 
   LaneBytes cur[RI][NX];
   load(r0, cur);
-  for (; r0 < rows; r0 += stride) {
+  for (; r0 < nrows; r0 += stride) {
     LaneBytes nxt[RI][NX];
-    load(r0 + stride < rows ? r0 + stride : r0, nxt);
+    load(r0 + stride < nrows ? r0 + stride : r0, nxt);
     float acc[RI];
 #pragma unroll
     for (int r = 0; r < RI; ++r) acc[r] = 0.0f;
-    const bool row_b = kMixed && ((sg.b_mask >> SegOf(sg, r0)) & 1u);
+    const bool row_b = kMixed && ((sg.b_mask >> SegOf(se, r0)) & 1u);
 #pragma unroll
     for (int it = 0; it < NX; ++it) {
       if (c + kGroups * it < nb) {
@@ -713,9 +840,9 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_
       if (lane == 0) sg.out[0][r0 >> 1] = dev::SiluMul(g, u);
     } else {
       const int rr = ReducedRow<RI>(lane);
-      const int sgi = SegOf(sg, r0);
+      const int sgi = SegOf(se, r0);
       const int64_t first = SegFirst(sg, sgi);
-      if ((lane & 15) == 0 && lane < 16 * RI && r0 + rr < rows) PickSeg(sg.out, sgi)[r0 - first + rr] = total;
+      if ((lane & 15) == 0 && lane < 16 * RI && r0 + rr < nrows) PickSeg(sg.out, sgi)[r0 - first + rr] = total;
     }
 #pragma unroll
     for (int r = 0; r < RI; ++r)
@@ -730,7 +857,7 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_
 // still fills the chip. Each wave keeps the activations of its NXW groups in
 // registers and reduces its partial sums; the WS partials of a row meet in LDS
 // and wave 0 adds them in wave order, so results are deterministic.
-template <uint32_t kType, int WS, int NXW, int RI>
+template <uint32_t kType, int WS, int NXW, int RI, bool kAl4 = false>
 __global__ __launch_bounds__(64 * WS) void MatVecSplitKernel(const uint8_t* __restrict__ w, int64_t rows,
                                                              int64_t row_bytes, int32_t nb,
                                                              const float* __restrict__ x, float* __restrict__ out) {
@@ -763,13 +890,23 @@ __global__ __launch_bounds__(64 * WS) void MatVecSplitKernel(const uint8_t* __re
     RunSums(xv[it], sx[it]);
   }
 
+  LaneOffs offs[NXW];
+#pragma unroll
+  for (int it = 0; it < NXW; ++it) offs[it] = MakeLaneOffs<kType>(static_cast<uint32_t>(lane_off[it]), s);
+
   auto load = [&](int64_t base_row, LaneBytes (&lb)[RI][NXW]) {
 #pragma unroll
     for (int r = 0; r < RI; ++r) {
       const int64_t row = base_row + r < rows ? base_row + r : rows - 1;
-      const uint8_t* rp = w + row * row_bytes;
+      if (kAl4) {
+        const uint32_t ro = static_cast<uint32_t>(row * row_bytes);
 #pragma unroll
-      for (int it = 0; it < NXW; ++it) lb[r][it] = LoadLaneBytes<kType>(rp + lane_off[it], s);
+        for (int it = 0; it < NXW; ++it) lb[r][it] = LoadLaneBytesBuf<kType>(MatrixResource(w), ro, offs[it]);
+      } else {
+        const uint8_t* rp = w + row * row_bytes;
+#pragma unroll
+        for (int it = 0; it < NXW; ++it) lb[r][it] = LoadLaneBytes<kType>(rp + lane_off[it], s);
+      }
     }
   };
 
@@ -845,6 +982,25 @@ void LaunchQuant(const char* name, const uint8_t* w, int64_t rows, int64_t row_b
 // or more), at most kDecodeGrid workgroups (16 waves per CU).
 constexpr int64_t kDecodeGrid = 1024;
 
+// Whether every row of the launch starts at a multiple of 4 bytes and below 2^31
+// bytes from its segment's base (the buffer-load form of the decode kernels).
+bool RowsAligned4(const MatSegs& sg, int32_t n_seg, int64_t row_bytes, bool paired) {
+  const int64_t lim = int64_t(1) << 31;
+  if (paired) {
+    const int64_t pairs = sg.end[0] / 2;
+    return (row_bytes & 3) == 0 && (reinterpret_cast<uintptr_t>(sg.w[0]) & 3) == 0 &&
+           (reinterpret_cast<uintptr_t>(sg.w[1]) & 3) == 0 && pairs * row_bytes < lim;
+  }
+  for (int32_t i = 0; i < n_seg; ++i) {
+    const int64_t rb = ((sg.b_mask >> i) & 1u) ? sg.row_bytes_b : row_bytes;
+    const int64_t first = i == 0 ? 0 : sg.end[i - 1];
+    if ((rb & 3) != 0 || (reinterpret_cast<uintptr_t>(sg.w[i]) & 3) != 0 || (sg.end[i] - first) * rb >= lim) {
+      return false;
+    }
+  }
+  return true;
+}
+
 // nrm != nullptr: the launch forms the norm itself (x is then the residual
 // stream); nrm->x_out is cleared afterwards, so a group of launches writes the
 // updated residual once.
@@ -852,8 +1008,22 @@ template <uint32_t kType, int RI, bool kPaired = false, uint32_t kTypeB = kType>
 void LaunchDecodeSegs(const char* name, const MatSegs& sg, int32_t n_seg, int64_t row_bytes, int32_t nb,
                       const float* x, NormPrologue* nrm = nullptr) {
   const int64_t rows = sg.end[n_seg - 1];
+  RPG_CHECK(rows < (int64_t(1) << 31) - kDecodeGrid * kWavesPerBlock * RI, "too many rows for one decode launch: %lld",
+            static_cast<long long>(rows));
   const int64_t need = (rows + kWavesPerBlock * RI - 1) / (kWavesPerBlock * RI);
   const unsigned grid = static_cast<unsigned>(need < kDecodeGrid ? need : kDecodeGrid);
+  constexpr bool kHasQ6 = kType == kGgmlQ6_K || kTypeB == kGgmlQ6_K;
+  if (kHasQ6 && RowsAligned4(sg, n_seg, row_bytes, kPaired)) {
+    if (nrm != nullptr) {
+      Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB, true, kHasQ6>, dim3(grid), dim3(kMmBlock), sg,
+             rows, row_bytes, nb, x, *nrm);
+      nrm->x_out = nullptr;
+      return;
+    }
+    Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB, false, kHasQ6>, dim3(grid), dim3(kMmBlock), sg, rows,
+           row_bytes, nb, x, NormPrologue{});
+    return;
+  }
   if (nrm != nullptr) {
     Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB, true>, dim3(grid), dim3(kMmBlock), sg, rows,
            row_bytes, nb, x, *nrm);
@@ -887,6 +1057,11 @@ void LaunchSplit(const char* name, const uint8_t* w, int64_t rows, int64_t row_b
   const int64_t max_grid = NXW == 1 ? 4096 : 1024;
   const int64_t need = (rows + RI - 1) / RI;
   const unsigned grid = static_cast<unsigned>(need < max_grid ? need : max_grid);
+  if (kType == kGgmlQ6_K && RowsAligned4(OneSeg(w, rows, out), 1, row_bytes, false)) {
+    Launch(name, MatVecSplitKernel<kType, WS, NXW, RI, kType == kGgmlQ6_K>, dim3(grid), dim3(64 * WS), w, rows,
+           row_bytes, nb, x, out);
+    return;
+  }
   Launch(name, MatVecSplitKernel<kType, WS, NXW, RI>, dim3(grid), dim3(64 * WS), w, rows, row_bytes, nb, x, out);
 }
 
