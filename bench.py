@@ -624,7 +624,7 @@ def measure_matmul_decode(torch, ops, reps=20, span=768 << 20):
             "grouped": grouped,
             "token_matmul_us_grouped": round(LAYERS * grouped["layer_us"] + res[OUTPUT_MATRIX[0]]["us"], 1),
             "note": "n = 1, Qwen3-1.7B Q4_K_M layout; token_matmul_us = 28 layers + output projection, "
-                    "matmuls only; _grouped = with q/k and gate/up fused per layer (GpuMatMulQuantGroup); "
+                    "matmuls only; _grouped = with q/k/v and gate/up fused per layer (GpuMatMulQuantGroup); "
                     "us: dispatch-attached events (a ~4 us floor under any kernel); us_back_to_back: 100 "
                     "launches captured in one HIP graph, replays timed with stream events (the per-launch "
                     "cost in a graph-replayed decode loop), beside launch_floor_us_back_to_back for a "
@@ -632,11 +632,15 @@ def measure_matmul_decode(torch, ops, reps=20, span=768 << 20):
 
 
 def measure_matmul_decode_grouped(torch, ops, reps, span):
-    """One 1.7B layer's decode matmuls as GpuMatMulQuantGroup launches: [q, k] (Q4_K),
-    [v] (Q6_K), [o], [gate, up], [down]; copies rotated past the Infinity Cache."""
+    """One 1.7B layer's decode matmuls as GpuMatMulQuantGroup launches: [q, k, v] (Q4_K,
+    Q4_K, Q6_K in one launch), [o], [gate, up], [down]; copies rotated past the Infinity
+    Cache. `forward` times the same matrices in the launches the decode step issues: the
+    attention and FFN norms formed inside the q / k / v and gate / up launches
+    (GpuNormMatMulQuantGroup, GpuNormMatMulQuantSwiGLU, the latter writing silu(gate) * up),
+    then o and down."""
     mats = {name: (t, rows, cols) for name, t, rows, cols in DECODE_MATRICES}
-    groups = [["attn_q", "attn_k"], ["attn_v"], ["attn_output"], ["ffn_gate", "ffn_up"], ["ffn_down"]]
-    res, layer_us, layer_b2b = {}, 0.0, 0.0
+    groups = [["attn_q", "attn_k", "attn_v"], ["attn_output"], ["ffn_gate", "ffn_up"], ["ffn_down"]]
+    res, layer_us, layer_b2b, forward = {}, 0.0, 0.0, {}
     for grp in groups:
         specs = [mats[n] for n in grp]
         sizes = [rows * (cols // 256) * (144 if t == 12 else 210) for t, rows, cols in specs]
@@ -676,9 +680,29 @@ def measure_matmul_decode_grouped(torch, ops, reps, span):
                               "us_back_to_back": round(b2b, 2), "GBps_back_to_back": round(nbytes / b2b / 1e3, 1)}
         layer_us += us
         layer_b2b += b2b
+        if grp[0] in ("attn_q", "ffn_gate"):
+            # the same group with the norm formed inside the launch, as the decode step runs it
+            d = torch.randn((1, cols), device="cuda", generator=gen)
+            nw = torch.randn((1, cols), device="cuda", generator=gen)
+            x_out = torch.empty_like(x)
+            if grp[0] == "attn_q":
+                def launch(i):
+                    assert ops.GpuNormMatMulQuantGroup(x, d, nw, 1e-6, x_out, sets[i % copies], outs)
+            else:
+                def launch(i):
+                    st = sets[i % copies]
+                    assert ops.GpuNormMatMulQuantSwiGLU(x, d, nw, 1e-6, x_out, st[0], st[1], outs[0], outs[1])
+            forward[grp[0]] = round(back_to_back_us(torch, ops, launch), 2)
+        else:
+            forward[grp[0]] = round(b2b, 2)
         del sets, x, outs
         torch.cuda.empty_cache()
-    return {"groups": res, "layer_us": round(layer_us, 2), "layer_us_back_to_back": round(layer_b2b, 2)}
+    return {"groups": res, "layer_us": round(layer_us, 2), "layer_us_back_to_back": round(layer_b2b, 2),
+            "forward_back_to_back": {"norm+attn_q+attn_k+attn_v": forward["attn_q"],
+                                     "attn_output": forward["attn_output"],
+                                     "norm+ffn_gate+ffn_up+swiglu": forward["ffn_gate"],
+                                     "ffn_down": forward["ffn_down"],
+                                     "layer_us": round(sum(forward.values()), 2)}}
 
 
 def measure_matmul_prefill(torch, ops, n=N_PREFILL, reps=3):
@@ -778,10 +802,13 @@ def measure_attention(torch, ops, reps=20):
         rep = ops.profile_report()
         us = sum(k["total_us"] for k in rep.values()) / reps
         nbytes = 2 * nkv * (pos0 + 1) * d * 2 + 2 * 4 * nh * d
+        b2b = back_to_back_us(torch, ops, lambda i: ops.GpuAttentionFromCache(
+            nh, nkv, d, pos0, q1, 1, kc[i % copies], vc[i % copies], max_seq, o1))
         out["decode"][f"pos{pos0}"] = {"us": round(us, 2), "GBps": round(nbytes / us / 1e3, 1),
                                        "pct_peak": round(nbytes / us / 1e3 / PEAK_GBPS * 100, 1),
                                        "kernels": {n: round(k["avg_us"], 2) for n, k in rep.items()},
-                                       "bytes": nbytes}
+                                       "bytes": nbytes, "us_back_to_back": round(b2b, 2),
+                                       "GBps_back_to_back": round(nbytes / b2b / 1e3, 1)}
     n = N_PREFILL
     qp = torch.randn((n, nh, d), generator=gen, device="cuda")
     op = torch.empty_like(qp)
@@ -805,13 +832,24 @@ def measure_attention(torch, ops, reps=20):
 def measure_sampler(torch, ops, reps=50):
     """Device argmax and sampling over Qwen3's vocabulary (151936 logits, the
     reference's synthetic logits seed 5): kernel microseconds per call (sum of
-    the launches, dispatch-attached events) and the stream's wall time per call.
-    Latency-bound: a few MB of traffic per call."""
+    the launches, dispatch-attached events), the stream's wall time per call, and
+    us_back_to_back: the call (its device-counter form, as a graph-replayed decode
+    loop runs it) captured 100 times in one HIP graph, per call. Latency-bound: a
+    few MB of traffic per call."""
     n = VOCAB
     x = torch.rand(n, generator=torch.Generator(device="cuda").manual_seed(5), device="cuda") * 16 - 8
     probs = torch.empty(n, device="cuda")
     idx = torch.empty(1, dtype=torch.int32, device="cuda")
     ops.GpuSamplerWarmup()
+    counter = torch.zeros(1, dtype=torch.int64, device="cuda")
+    graph_forms = {
+        "argmax": lambda i: ops.GpuArgMax(x, n, idx),
+        "sample_T0.7_topp0.95": lambda i: ops.GpuSampleTokenDev(x, n, ops.SampleOptions(0.7, 0, 0.95), 1, counter,
+                                                                probs, idx),
+        "sample_T0.7_topk20_topp0.95": lambda i: ops.GpuSampleTokenDev(x, n, ops.SampleOptions(0.7, 20, 0.95), 1,
+                                                                       counter, probs, idx),
+        "sample_T1": lambda i: ops.GpuSampleTokenDev(x, n, ops.SampleOptions(1.0, 0, 1.0), 1, counter, probs, idx),
+    }
     cases = {
         "argmax": lambda: ops.GpuArgMax(x, n, idx),
         "sample_T0.7_topp0.95": lambda: ops.GpuSampleToken(x, n, ops.SampleOptions(0.7, 0, 0.95), 1, 3, probs, idx),
@@ -838,6 +876,7 @@ def measure_sampler(torch, ops, reps=50):
         e1.record()
         torch.cuda.synchronize()
         res[name] = {"kernel_us": round(kus, 2), "wall_us": round(e0.elapsed_time(e1) * 1e3 / reps, 2),
+                     "us_back_to_back": round(back_to_back_us(torch, ops, graph_forms[name]), 2),
                      "launches": int(sum(k["count"] for k in rep.values()) // reps),
                      "kernels": {k_: round(v["avg_us"], 2) for k_, v in rep.items()}}
     return {"vocab": n, **res}
