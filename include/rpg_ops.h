@@ -150,8 +150,9 @@ RPG_OPS_API int32_t rpg_op_qk_norm_rope_kv_attention(const float* q, const float
  * (code under HIP graph capture, serving loops or harnesses that forbid
  * hipMalloc): same arguments, same kernels, bit-identical results, but the
  * partials of a split-key decode live in a fixed 2 MiB device array of the
- * library (one per GPU, held until the process ends), and the split decode's
- * arrival counters in a fixed array beside it, so no call ever allocates.
+ * library (one per GPU, held until the process ends), and the arrival counters
+ * of the split decode and of the prefill's in-launch chunk merge in fixed arrays
+ * beside it, so no call ever allocates.
  * Limit: a call whose split needs more than 2^19 floats of partials fails with
  * an error and launches nothing. A split decode keeps 132 floats per (token,
  * query head, workgroup of 4 key chunks), none when one workgroup takes every

@@ -190,6 +190,15 @@ __device__ __forceinline__ uint2 LoadBufU2(__amdgpu_buffer_rsrc_t rs, uint32_t b
   return make_uint2(v.x, v.y);
 }
 constexpr int kLoadDevicePolicy = 16;  // sc1
+template <int kPolicy>
+__device__ __forceinline__ float4 LoadBuf4(__amdgpu_buffer_rsrc_t rs, uint32_t byte_off) {
+  const U32x4 v = __builtin_amdgcn_raw_buffer_load_b128(rs, static_cast<int>(byte_off), 0, kPolicy);
+  return make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+}
+template <int kPolicy>
+__device__ __forceinline__ float LoadBuf1(__amdgpu_buffer_rsrc_t rs, uint32_t byte_off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, static_cast<int>(byte_off), 0, kPolicy));
+}
 
 __device__ __forceinline__ void StoreDeviceThrough4(__amdgpu_buffer_rsrc_t rs, uint32_t byte_off, float4 v) {
   StoreBuf4<kStoreDeviceThroughPolicy>(rs, byte_off, v);

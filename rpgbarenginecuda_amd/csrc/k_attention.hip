@@ -787,6 +787,10 @@ constexpr int kFaKeys = 64;       // keys per LDS block
 constexpr float kFaLazyLog2 = 8;  // the running max moves when a block's max exceeds it by more (log2 units)
 constexpr int kFaOrderMax = 1024; // (token tile, key chunk) pairs an ordered launch can list
 constexpr int kFaKStride = 136;   // halves per K row in LDS (128 + 8: conflict-free 16-byte reads)
+constexpr int kFaCounterStride = 16;       // uint32 slots between two (tile, head) arrival counters (64 bytes)
+constexpr int64_t kFaCounterSlots = 8192;  // (tile, head) counters per half (allocating / no-allocation)
+constexpr int kFaFusedMaxChunks = 4;       // key chunks the fused merge takes (more: a separate merge launch)
+constexpr int64_t kFaPartBlock = kFaTokens * (kD + 2);  // fused-merge partial floats per (tile, head, chunk)
 constexpr int kFaVStride = 160;   // halves per V row in LDS (128 + 32: conflict-free transposing reads)
 
 // ds_read_b64_tr_b16: in each 16-lane group, lane j receives element j % 4 of
@@ -832,7 +836,7 @@ __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
     const float* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc, int64_t max_seq,
     int32_t n_heads, int32_t group, float scale, int64_t pos0_val, const int64_t* __restrict__ pos0_dev, int64_t seq,
     int32_t n_chunks, int64_t chunk_len, int32_t tiles, float* __restrict__ out, float* __restrict__ part,
-    FaOrder order) {
+    FaOrder order, uint32_t* __restrict__ cnt) {
   __shared__ __attribute__((aligned(16))) _Float16 ks[kFaKeys * kFaKStride];
   __shared__ __attribute__((aligned(16))) _Float16 vs[kFaKeys * kFaVStride];
   const int lane = threadIdx.x & 63;
@@ -1026,39 +1030,157 @@ __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
   }
 
   // ---- out[tq][h][dim]: register r of tile dt is dim 32 dt + (r % 4) + 8 (r / 4) + 4 hf
-  if (!qvalid) return;
-  const int32_t live = LiveChunks(qpos, chunk_len, n_chunks);
   // A chunk past the query's live chunks saw none of its keys and writes
   // nothing: in particular, for a query whose keys all lie in chunk 0, only
   // chunk 0 writes its output (another chunk would overwrite it with zeros).
-  if (chunk >= live) return;
-  if (live > 1) {  // a partial of this chunk
-    float* pp = part + ((tq * n_heads + h) * n_chunks + chunk) * kPartFloats;
+  const int32_t live = qvalid ? LiveChunks(qpos, chunk_len, n_chunks) : 0;
+  if (chunk < live && live == 1) {
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    float* orow = out + (tq * n_heads + h) * kD;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 v = make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
+                                     o[dt][4 * g + 3] * inv);
+        *reinterpret_cast<float4*>(orow + 32 * dt + 8 * g + 4 * hf) = v;
+      }
+    }
+  }
+  if (cnt == nullptr) {
+    // partials for AttnMergeRowsKernel: rows [token][head][chunk] of kPartFloats
+    if (chunk < live && live > 1) {
+      float* pp = part + ((tq * n_heads + h) * n_chunks + chunk) * kPartFloats;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const float4 v = make_float4(o[dt][4 * g], o[dt][4 * g + 1], o[dt][4 * g + 2], o[dt][4 * g + 3]);
+          *reinterpret_cast<float4*>(pp + 32 * dt + 8 * g + 4 * hf) = v;
+        }
+      }
+      if (hf == 0) {
+        pp[kD] = m;
+        pp[kD + 1] = l;
+      }
+    }
+    return;
+  }
+  // ---- fused merge: partials in blocks of kFaPartBlock floats per (tile, head,
+  // chunk), laid out [float4 q4 = 8 dt + 2 g + hf][token of the tile] and then
+  // (m, l) per token, so each store instruction writes 32 consecutive tokens'
+  // 16 bytes: whole 128-byte lines, as the device-scope write-through stores need
+  // (partial lines make them several times slower). Offsets stay below 2^31 (the
+  // launcher caps the partials at kFaMaxPartialFloats).
+  const __amdgpu_buffer_rsrc_t prs = dev::OutResource(part, static_cast<uint32_t>(kFaMaxPartialFloats * 4));
+  const int tloc = 32 * wv + col;
+  auto block_of = [&](int32_t c) -> uint32_t {
+    return static_cast<uint32_t>(((static_cast<int64_t>(tile) * n_heads + h) * n_chunks + c) * kFaPartBlock) * 4u;
+  };
+  if (chunk < live && live > 1) {
+    const uint32_t blk = block_of(chunk);
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const float4 v = make_float4(o[dt][4 * g], o[dt][4 * g + 1], o[dt][4 * g + 2], o[dt][4 * g + 3]);
-        *reinterpret_cast<float4*>(pp + 32 * dt + 8 * g + 4 * hf) = v;
+        dev::StoreBuf4<dev::kStoreDeviceThroughPolicy>(prs, blk + 16u * ((8 * dt + 2 * g + hf) * kFaTokens + tloc), v);
       }
     }
     if (hf == 0) {
-      pp[kD] = m;
-      pp[kD + 1] = l;
-    }
-    return;
-  }
-  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-  float* orow = out + (tq * n_heads + h) * kD;
-#pragma unroll
-  for (int dt = 0; dt < 4; ++dt) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const float4 v = make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
-                                   o[dt][4 * g + 3] * inv);
-      *reinterpret_cast<float4*>(orow + 32 * dt + 8 * g + 4 * hf) = v;
+      dev::StoreBufU2<dev::kStoreDeviceThroughPolicy>(prs, blk + 4u * (kFaTokens * kD) + 8u * tloc,
+                                                      make_uint2(__float_as_uint(m), __float_as_uint(l)));
     }
   }
+  const int32_t tile_live = LiveChunks(last_key, chunk_len, n_chunks);  // the workgroups of this (tile, head)
+  if (tile_live == 1) return;  // uniform: no partials in this tile
+  // Wait for this thread's partial stores to be acknowledged (device-scope
+  // write-through: visible to every XCD), then count the workgroup in. The
+  // clobber keeps the compiler from moving memory accesses across the wait.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __shared__ int last_flag;
+  __syncthreads();
+  uint32_t* counter = cnt + (static_cast<int64_t>(tile) * n_heads + h) * kFaCounterStride;
+  if (threadIdx.x == 0) {
+    const uint32_t before = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_flag = before == static_cast<uint32_t>(tile_live - 1);
+  }
+  __syncthreads();
+  if (!last_flag) return;  // uniform
+  // The last workgroup of the (tile, head) merges: each lane its own query's
+  // chunks, AttnMergeRowsKernel's arithmetic (chunk maxima, then the weights and
+  // normaliser summed in chunk order), with this workgroup's own chunk from its
+  // registers (the very values it stored) and the others' partials through
+  // device-coherent (sc1) loads issued after the barrier that follows the atomic,
+  // one chunk's 64 values at a time.
+  if (qvalid && live > 1) {
+    float mc[kFaFusedMaxChunks], lc[kFaFusedMaxChunks];
+#pragma unroll
+    for (int c = 0; c < kFaFusedMaxChunks; ++c) {
+      mc[c] = -INFINITY;
+      lc[c] = 0.0f;
+      if (c < live && c != chunk) {
+        const uint2 u = dev::LoadBufU2<dev::kLoadDevicePolicy>(prs, block_of(c) + 4u * (kFaTokens * kD) + 8u * tloc);
+        mc[c] = __uint_as_float(u.x);
+        lc[c] = __uint_as_float(u.y);
+      } else if (c == chunk) {
+        mc[c] = m;
+        lc[c] = l;
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < kFaFusedMaxChunks; ++c) {
+      if (c < live) mx = fmaxf(mx, mc[c]);
+    }
+    float L = 0.0f;
+    F32x16 acc[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) acc[dt] = F32x16{};
+#pragma unroll
+    for (int c = 0; c < kFaFusedMaxChunks; ++c) {
+      if (c < live) {
+        const float f = mc[c] == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(mc[c] - mx);
+        L = __builtin_fmaf(lc[c], f, L);
+        if (c == chunk) {
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[dt][r] = __builtin_fmaf(o[dt][r], f, acc[dt][r]);
+        } else {
+          const uint32_t blk = block_of(c);
+          float4 v[4][4];
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+              v[dt][g] = dev::LoadBuf4<dev::kLoadDevicePolicy>(prs, blk + 16u * ((8 * dt + 2 * g + hf) * kFaTokens + tloc));
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+              acc[dt][4 * g] = __builtin_fmaf(v[dt][g].x, f, acc[dt][4 * g]);
+              acc[dt][4 * g + 1] = __builtin_fmaf(v[dt][g].y, f, acc[dt][4 * g + 1]);
+              acc[dt][4 * g + 2] = __builtin_fmaf(v[dt][g].z, f, acc[dt][4 * g + 2]);
+              acc[dt][4 * g + 3] = __builtin_fmaf(v[dt][g].w, f, acc[dt][4 * g + 3]);
+            }
+        }
+      }
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    float* orow = out + (tq * n_heads + h) * kD;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 v = make_float4(acc[dt][4 * g] * inv, acc[dt][4 * g + 1] * inv, acc[dt][4 * g + 2] * inv,
+                                     acc[dt][4 * g + 3] * inv);
+        *reinterpret_cast<float4*>(orow + 32 * dt + 8 * g + 4 * hf) = v;
+      }
+    }
+  }
+  // every workgroup of the (tile, head) has counted in: ready for the next call
+  if (threadIdx.x == 0) __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------- partials buffer
@@ -1167,6 +1289,34 @@ uint32_t* CountersForCurrentDevice() {
   return t.ptr[dev];
 }
 
+// Arrival counters of the prefill's fused chunk merge, one per (token tile,
+// head), used the same way (zero between launches); first half for the allocating
+// entry points, second for the no-allocation one. A launch with more (tile, head)
+// pairs than a half holds merges in a separate launch.
+static __device__ __align__(256) uint32_t fa_counters[2 * kFaCounterSlots * kFaCounterStride];
+
+CounterTable& FaCounterTableInstance() {
+  static CounterTable* t = new CounterTable();
+  return *t;
+}
+
+// Device address of `fa_counters` on the current device, looked up once per device.
+uint32_t* FaCountersForCurrentDevice() {
+  int dev = -1;
+  RPG_HIP_CHECK(hipGetDevice(&dev));
+  RPG_CHECK(dev >= 0 && dev < kMaxScratchDevices, "device %d is beyond the %d devices the counter table tracks", dev,
+            kMaxScratchDevices);
+  CounterTable& t = FaCounterTableInstance();
+  std::lock_guard<std::mutex> lock(t.mu);
+  if (t.ptr[dev] == nullptr) {
+    void* p = nullptr;
+    RPG_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(fa_counters)));
+    RPG_CHECK(p != nullptr, "hipGetSymbolAddress returned no address for the prefill counters on device %d", dev);
+    t.ptr[dev] = static_cast<uint32_t*>(p);
+  }
+  return t.ptr[dev];
+}
+
 // Where a split-key launch keeps its chunk partials: the library's grow-only
 // buffer (fixed == nullptr) or a fixed region that must already be big enough.
 // The one-launch decode also takes its arrival counters from here.
@@ -1176,6 +1326,9 @@ struct PartialsSink {
 
   uint32_t* Counters() const {
     return CountersForCurrentDevice() + (fixed == nullptr ? 0 : kFusedCounterPairs * kCounterStride);
+  }
+  uint32_t* PrefillCounters() const {
+    return FaCountersForCurrentDevice() + (fixed == nullptr ? 0 : kFaCounterSlots * kFaCounterStride);
   }
 
   float* Get(size_t floats) const {
@@ -1324,13 +1477,18 @@ void AttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev, in
     int64_t fa_chunks = (max_blocks + per - 1) / per;
     const int64_t room = static_cast<int64_t>(
         sink.Capacity() < static_cast<size_t>(kFaMaxPartialFloats) ? sink.Capacity() : kFaMaxPartialFloats);
-    const int64_t cap = room / (seq * c.n_heads * kPartFloats);
+    const int64_t per_chunk = std::max(seq * c.n_heads * kPartFloats, tiles * c.n_heads * kFaPartBlock);
+    const int64_t cap = room / per_chunk;
     if (fa_chunks > cap) fa_chunks = cap;
     if (fa_chunks > kMaxChunks) fa_chunks = kMaxChunks;
     if (fa_chunks < 1) fa_chunks = 1;
     const int64_t fa_len = (max_blocks + fa_chunks - 1) / fa_chunks * kFaKeys;
     fa_chunks = (positions + fa_len - 1) / fa_len;
-    float* part = fa_chunks > 1 ? sink.Get(static_cast<size_t>(pairs) * fa_chunks * kPartFloats) : nullptr;
+    // the fused merge's blocks cover whole tiles: tiles * 128 * 130 floats per (head, chunk), against
+    // seq * 132 for the separate merge's rows
+    const int64_t fused_floats = tiles * c.n_heads * fa_chunks * kFaPartBlock;
+    const int64_t rows_floats = pairs * fa_chunks * kPartFloats;
+    float* part = fa_chunks > 1 ? sink.Get(static_cast<size_t>(std::max(fused_floats, rows_floats))) : nullptr;
     const int64_t n_pairs = tiles * fa_chunks;
     RPG_CHECK(n_pairs * c.n_heads < (int64_t{1} << 31), "prefill attention grid too large");
     // (tile, chunk) pairs sorted by their key blocks over the position budget,
@@ -1353,11 +1511,16 @@ void AttentionFromCache(const ModelMeta& c, int64_t pos0, const float* q_dev, in
       for (int64_t i = 0; i < n_pairs; ++i) order.e[i] = static_cast<uint16_t>(by_size[i].second);
       order.n = static_cast<int32_t>(n_pairs);
     }
+    // the last workgroup of each (tile, head) merges the tile's partials, unless the
+    // counters cannot cover every (tile, head)
+    uint32_t* cnt = fa_chunks > 1 && fa_chunks <= kFaFusedMaxChunks && tiles * c.n_heads <= kFaCounterSlots
+                        ? sink.PrefillCounters()
+                        : nullptr;
     Launch("AttnPrefillMfmaKernel", AttnPrefillMfmaKernel, dim3(static_cast<unsigned>(n_pairs * c.n_heads)),
            dim3(kBlockThreads), q_dev, k_layer, v_layer, max_seq, c.n_heads, c.n_heads / c.n_kv_heads, scale,
            p0.value, p0.dev, seq, static_cast<int32_t>(fa_chunks), fa_len, static_cast<int32_t>(tiles), out_dev,
-           part, order);
-    if (fa_chunks > 1) {
+           part, order, cnt);
+    if (fa_chunks > 1 && cnt == nullptr) {
       Launch("AttnMergeRowsKernel", AttnMergeRowsKernel, dim3(GridFor(pairs * (kD / 4), kBlockThreads)),
              dim3(kBlockThreads), static_cast<const float*>(part), pairs, static_cast<int32_t>(fa_chunks), c.n_heads,
              fa_len, p0.value, p0.dev, out_dev);
@@ -1409,6 +1572,7 @@ void GpuAttentionFromCacheNoAlloc(const ModelMeta& c, int64_t pos0, const float*
 void GpuAttentionNoAllocInit() {
   (void)ScratchForCurrentDevice();
   (void)CountersForCurrentDevice();
+  (void)FaCountersForCurrentDevice();
 }
 
 size_t GpuAttentionNoAllocScratchBytes() { return kNoAllocScratchFloats * sizeof(float); }
@@ -1475,6 +1639,7 @@ void GpuAttentionWarmupShmem(int64_t sh_positions) {
   RPG_CHECK(sh_positions > 0, "attention warmup: the position budget has to be at least 1 (got %lld)", static_cast<long long>(sh_positions));
   EnsurePartials(WarmupFloats(sh_positions));
   (void)CountersForCurrentDevice();
+  (void)FaCountersForCurrentDevice();
 }
 
 }  // namespace rpg

@@ -74,6 +74,10 @@ CASES = [
     ("prefill n=129 (tile edge)", 8, 2, 512, 5, 129),
     ("1.7B prefill n=1024", 16, 8, 1024, 0, 1024),
     ("4B prefill n=300 after 1000", 32, 8, 4096, 1000, 300),
+    # key chunks of the matrix-core prefill: up to 4 merged by the last workgroup of each
+    # (token tile, head), more by a separate merge launch
+    ("1.7B prefill n=128 after 1920 (4 key chunks, merged in the launch)", 16, 8, 4096, 1920, 128),
+    ("1.7B prefill n=300 after 3000 (7 key chunks, merge launch)", 16, 8, 4096, 3000, 300),
 ]
 
 

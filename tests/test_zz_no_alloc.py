@@ -44,7 +44,8 @@ def test_noalloc_attention_matches_allocating_entry(gpu):
     # A split decode is one launch whose last workgroup per (token, kv head) merges.
     calls = [("4B shape, decode at 4095, 2 tokens (32 workgroups per pair)", 32, 8, 4096, 4094, 2),
              ("1.7B shape, decode at 3000 (24 workgroups per pair)", 16, 8, 3072, 3000, 1),
-             ("1.7B shape, decode at 700", 16, 8, 4096, 700, 1)]
+             ("1.7B shape, decode at 700", 16, 8, 4096, 700, 1),
+             ("prefill of 100 tokens at 1900, 4 key chunks merged in the launch", 4, 2, 2048, 1900, 100)]
     for name, nh, nkv, max_seq, pos0, seq in calls:
         _case(f"noalloc vs allocating: {name}")
         q, kc, vc = _inputs(rng, nh, nkv, max_seq, seq)
