@@ -264,11 +264,6 @@ __device__ float MaxOfParts(const float* parts, int n_slices, float* sh) {
   for (int g = threadIdx.x; g < n_slices; g += kThreads) m = fmaxf(m, parts[g]);
   return BlockMax(m, sh);
 }
-__device__ double SumOfParts(const double* parts, int n_slices, double* sh) {
-  double s = 0.0;
-  for (int g = threadIdx.x; g < n_slices; g += kThreads) s += parts[g];
-  return BlockSumD(s, sh);
-}
 __device__ Best BestOfParts(const float* vals, const int32_t* idx, int n_slices, Best* sh) {
   Best b{-INFINITY, 0x7FFFFFFF};
   for (int g = threadIdx.x; g < n_slices; g += kThreads) b = Better(b, Best{vals[g], idx[g]});
@@ -392,25 +387,40 @@ __device__ __forceinline__ int64_t ElemIndex(int j) {
 // ---------------------------------------------------------------- kernels
 
 // Per-slice max and first argmax of the (scaled) logits; with top_k also the
-// level-1 count histogram of their keys (bits 31..20), added to khist.
+// level-1 count histogram of their keys (bits 31..20), added to khist; without
+// top_k also the slice's sum of expf(v - m) against its own maximum m (the
+// softmax normaliser then combines the slices, LoadProbCtx, and needs no launch
+// of its own).
 __global__ __launch_bounds__(kThreads) void SamplePrepKernel(Logits lg, int32_t topk, SampleScratch* __restrict__ s) {
   __shared__ uint32_t hist[kBins];
   __shared__ Best shb[kWaves];
+  __shared__ double shd[kWaves];
   if (topk) {
     for (int b = threadIdx.x; b < kBins; b += kThreads) hist[b] = 0;
     __syncthreads();
   }
   Best b{-INFINITY, 0x7FFFFFFF};
+  float v[kPerThread];
 #pragma unroll
   for (int j = 0; j < kPerThread; ++j) {
     const int64_t i = ElemIndex(j);
+    v[j] = -INFINITY;
     if (i < lg.n) {
-      const float v = LoadV(lg, i);
-      if (v > b.v || (v == b.v && b.i == 0x7FFFFFFF)) b = Best{v, static_cast<int32_t>(i)};
-      if (topk) atomicAdd(&hist[OrderKey(v) >> LevelShift(1)], 1u);
+      v[j] = LoadV(lg, i);
+      if (v[j] > b.v || (v[j] == b.v && b.i == 0x7FFFFFFF)) b = Best{v[j], static_cast<int32_t>(i)};
+      if (topk) atomicAdd(&hist[OrderKey(v[j]) >> LevelShift(1)], 1u);
     }
   }
   b = BlockBest(b, shb);
+  if (!topk) {
+    double acc = 0.0;
+#pragma unroll
+    for (int j = 0; j < kPerThread; ++j) {
+      if (v[j] != -INFINITY) acc += static_cast<double>(expf(v[j] - b.v));
+    }
+    acc = BlockSumD(acc, shd);
+    if (threadIdx.x == 0) s->sum_part[blockIdx.x] = acc;
+  }
   if (threadIdx.x == 0) {
     s->max_part[blockIdx.x] = b.v;
     s->best_val[blockIdx.x] = b.v;
@@ -586,9 +596,34 @@ __global__ __launch_bounds__(kThreads) void SampleTopKCandKernel(Logits lg, int3
 // mx, inv and kth as every kernel after Sum sees them.
 __device__ ProbCtx LoadProbCtx(const Logits& lg, int topk, const SampleScratch* s, float* shf, double* shd) {
   const int ns = NumSlices(lg.n);
+  // both partials of a thread's slices requested at once (one memory round trip),
+  // then the maximum and the normaliser: with top_k the slices' sums, otherwise
+  // sum_g sum_part[g] exp(m_g - mx) over the slices' own maxima m_g (a slice of
+  // -inf maxima adds its own sum, 0 or NaN); each term then differs from a direct
+  // sum of expf(v - mx) by float rounding of the exponentials only (~1e-7)
+  float mp[kPartsPerThread];
+  double sp[kPartsPerThread];
+#pragma unroll
+  for (int k = 0; k < kPartsPerThread; ++k) {
+    const int g = threadIdx.x + k * kThreads;
+    mp[k] = g < ns ? s->max_part[g] : -INFINITY;
+    sp[k] = g < ns ? s->sum_part[g] : 0.0;
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int k = 0; k < kPartsPerThread; ++k) m = fmaxf(m, mp[k]);
   ProbCtx c;
-  c.mx = MaxOfParts(s->max_part, ns, shf);
-  c.inv = static_cast<float>(1.0 / SumOfParts(s->sum_part, ns, shd));
+  c.mx = BlockMax(m, shf);
+  // without top_k the slices' sums were taken against their own maxima (SamplePrepKernel)
+  double t = 0.0;
+#pragma unroll
+  for (int k = 0; k < kPartsPerThread; ++k) {
+    if (threadIdx.x + k * kThreads < ns) {
+      t += (topk || mp[k] == -INFINITY) ? sp[k]
+                                         : sp[k] * exp(static_cast<double>(mp[k]) - static_cast<double>(c.mx));
+    }
+  }
+  c.inv = static_cast<float>(1.0 / BlockSumD(t, shd));
   c.topk = topk;
   c.kth = topk ? FromOrderKey(s->kth_key) : 0.0f;
   return c;
@@ -618,14 +653,20 @@ __global__ __launch_bounds__(kThreads) void SampleTopPKernel(Logits lg, int32_t 
   __shared__ uint64_t hist[kBins];
   __shared__ float shf[kWaves];
   __shared__ double shd[kWaves];
-  const ProbCtx c = LoadProbCtx(lg, topk, s, shf, shd);
+  float raw[kPerThread];
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j) {  // requested before the partials
+    const int64_t i = ElemIndex(j);
+    raw[j] = i < lg.n ? lg.x[i] : 0.0f;
+  }
   for (int b = threadIdx.x; b < kBins; b += kThreads) hist[b] = 0;
+  const ProbCtx c = LoadProbCtx(lg, topk, s, shf, shd);
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < kPerThread; ++j) {
     const int64_t i = ElemIndex(j);
     if (i < lg.n) {
-      const float p = ProbAt(lg, c, i);
+      const float p = ProbOfRaw(lg, c, raw[j]);
       const uint64_t w = Fix62(p);
       if (w != 0) atomicAdd(reinterpret_cast<unsigned long long*>(&hist[OrderKey(p) >> LevelShift(1)]),
                             static_cast<unsigned long long>(w));
@@ -904,6 +945,12 @@ __global__ __launch_bounds__(kThreads) void SampleNormKernel(Logits lg, int32_t 
   __shared__ uint64_t sh[kWaves];
   __shared__ Best shb[kWaves];
   __shared__ int last;
+  float raw[kPerThread];
+#pragma unroll
+  for (int j = 0; j < kPerThread; ++j) {  // requested before the partials
+    const int64_t i = ElemIndex(j);
+    raw[j] = i < lg.n ? lg.x[i] : 0.0f;
+  }
   const ProbCtx c = LoadProbCtx(lg, topk, s, shf, shd);
   float cut = 0.0f, inv2 = 1.0f;
   bool forced = false, rescale = false;
@@ -929,7 +976,7 @@ __global__ __launch_bounds__(kThreads) void SampleNormKernel(Logits lg, int32_t 
     in[j] = i < lg.n;
     p[j] = 0.0f;
     if (in[j]) {
-      float v = ProbAt(lg, c, i);
+      float v = ProbOfRaw(lg, c, raw[j]);
       if (topp) {
         if (v <= cut) v = 0.0f;
         if (forced && i == best) v = 1.0f;
@@ -1073,7 +1120,7 @@ void LaunchSample(const float* logits, int64_t n, const SampleOptions& opt, floa
   const uint64_t thr = topp ? static_cast<uint64_t>(floor((1.0 - static_cast<double>(opt.top_p)) * 0x1p62)) : 0ull;
   Launch("SamplePrepKernel", SamplePrepKernel, grid, block, lg, topk, b.s);
   if (topk) Launch("SampleTopKCandKernel", SampleTopKCandKernel, grid, block, lg, opt.top_k, b.s, b.cand);
-  Launch("SampleSumKernel", SampleSumKernel, grid, block, lg, topk, b.s);
+  if (topk) Launch("SampleSumKernel", SampleSumKernel, grid, block, lg, topk, b.s);  // else formed by Prep
   if (topp) {
     Launch("SampleTopPKernel", SampleTopPKernel, grid, block, lg, topk, b.s);
     Launch("SampleTopPCandKernel", SampleTopPCandKernel, grid, block, lg, topk, thr, b.s, b.cand);
