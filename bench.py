@@ -802,6 +802,9 @@ def measure_attention(torch, ops, reps=20):
         rep = ops.profile_report()
         us = sum(k["total_us"] for k in rep.values()) / reps
         nbytes = 2 * nkv * (pos0 + 1) * d * 2 + 2 * 4 * nh * d
+        # a captured launch reads its position from the staging scalar on every replay
+        ops.stage_pos0(pos0)
+        torch.cuda.synchronize()
         b2b = back_to_back_us(torch, ops, lambda i: ops.GpuAttentionFromCache(
             nh, nkv, d, pos0, q1, 1, kc[i % copies], vc[i % copies], max_seq, o1))
         out["decode"][f"pos{pos0}"] = {"us": round(us, 2), "GBps": round(nbytes / us / 1e3, 1),
