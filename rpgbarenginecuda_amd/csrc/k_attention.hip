@@ -66,6 +66,14 @@ __device__ __forceinline__ int32_t LiveChunks(int64_t pos, int64_t chunk_len, in
   const int64_t live = pos / chunk_len + 1;
   return live < n_chunks ? static_cast<int32_t>(live) : n_chunks;
 }
+// The same count through a 32-bit division when pos and chunk_len fit (every
+// real position): the 64-bit division is a long vector-unit sequence in front
+// of the first K / V load.
+__device__ __forceinline__ int32_t LiveChunks32(int64_t pos, int64_t chunk_len, int32_t n_chunks) {
+  if (pos < 0 || pos > INT32_MAX || chunk_len > INT32_MAX) return LiveChunks(pos, chunk_len, n_chunks);
+  const uint32_t live = static_cast<uint32_t>(pos) / static_cast<uint32_t>(chunk_len) + 1u;
+  return live < static_cast<uint32_t>(n_chunks) ? static_cast<int32_t>(live) : n_chunks;
+}
 
 // Wave reductions: DPP inside each 16-lane row (lane pairs xor 1, xor 2, then
 // mirrored halves and rows, which pair every lane with a partner of the other
@@ -80,17 +88,43 @@ __device__ __forceinline__ float DppMov(float v, int ctrl_sel) {
   }
   return __int_as_float(m);
 }
+// Across the four rows (every lane of each row holding its row's value): row 1
+// takes row 0's value and row 3 row 2's (row_bcast:15, rows 1 and 3 written),
+// then rows 2 and 3 take row 1's (row_bcast:31), so lane 63 ends with
+// op(op(r3, r2), op(r1, r0)), which it hands to the whole wave as a scalar. With
+// a commutative op that is the value the xor-16 / xor-32 exchange forms, and it
+// takes two DPP moves instead of two LDS permutes. Every lane must be active.
+template <typename Op>
+__device__ __forceinline__ float AcrossRows(float v, float identity, Op op) {
+  const int id = __float_as_int(identity);
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(v), 0x142, 0xA, 0xF, false)));
+  v = op(v, __int_as_float(__builtin_amdgcn_update_dpp(id, __float_as_int(v), 0x143, 0xC, 0xF, false)));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
 __device__ __forceinline__ float WaveMax(float v) {
 #pragma unroll
   for (int k = 0; k < 4; ++k) v = fmaxf(v, DppMov(v, k));
-  v = fmaxf(v, __shfl_xor(v, 16, 64));
-  return fmaxf(v, __shfl_xor(v, 32, 64));
+  return AcrossRows(v, -INFINITY, [](float a, float b) { return fmaxf(a, b); });
 }
 __device__ __forceinline__ float WaveSumF(float v) {
 #pragma unroll
   for (int k = 0; k < 4; ++k) v += DppMov(v, k);
-  v += __shfl_xor(v, 16, 64);
-  return v + __shfl_xor(v, 32, 64);
+  return AcrossRows(v, 0.0f, [](float a, float b) { return a + b; });
+}
+// Lane 2 i of the caller's 16-lane row, broadcast to the whole row (row_newbcast).
+__device__ __forceinline__ float RowLane2i(float v, int i) {
+  int m;
+  switch (i) {
+    case 0: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150, 0xF, 0xF, false); break;
+    case 1: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x152, 0xF, 0xF, false); break;
+    case 2: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x154, 0xF, 0xF, false); break;
+    case 3: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x156, 0xF, 0xF, false); break;
+    case 4: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x158, 0xF, 0xF, false); break;
+    case 5: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x15A, 0xF, 0xF, false); break;
+    case 6: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x15C, 0xF, 0xF, false); break;
+    default: m = __builtin_amdgcn_mov_dpp(__float_as_int(v), 0x15E, 0xF, 0xF, false); break;
+  }
+  return __int_as_float(m);
 }
 
 __device__ __forceinline__ float HalfToF(uint32_t bits) {
@@ -368,22 +402,22 @@ constexpr int kCounterStride = 64;
 // reached by every wave of a workgroup with at least two live chunks per pair.
 // Partials are rows of kPartFloats: o[128], m, l.
 template <int G, int kW>
-__device__ __forceinline__ void FusedMerge(float (*wpart)[G][kPartFloats], int* last_flag, const float (&m)[G],
+__device__ __forceinline__ void FusedMerge(float (*wpart)[4][G][kPartFloats], int* last_flag, const float (&m)[G],
                                            const float (&l)[G], const float (&o)[G][8], int lane, int wave, int r,
                                            int rho, int64_t t, int32_t kh, int32_t n_heads, int32_t n_kv_heads,
                                            int32_t n_groups, int32_t live_groups, int32_t grp,
                                            float* __restrict__ out, float* __restrict__ part,
                                            uint32_t* __restrict__ cnt) {
-  // 1. the workgroup's chunks, in chunk order: wave w's (m, l, o) to LDS, then wave hh < G merges head hh
-  if (r == 0) {
+  // 1. the workgroup's chunks, in chunk order: wave w's (m, l) and its four
+  // rows' partial o (each row r summed over keys 4 i + r; the rows' sum is taken
+  // here instead of by cross-row exchanges) to LDS, then wave hh < G merges head hh
 #pragma unroll
-    for (int hh = 0; hh < G; ++hh) {
-      *reinterpret_cast<float4*>(&wpart[wave][hh][8 * rho]) = make_float4(o[hh][0], o[hh][1], o[hh][2], o[hh][3]);
-      *reinterpret_cast<float4*>(&wpart[wave][hh][8 * rho + 4]) = make_float4(o[hh][4], o[hh][5], o[hh][6], o[hh][7]);
-      if (rho == 0) {
-        wpart[wave][hh][kD] = m[hh];
-        wpart[wave][hh][kD + 1] = l[hh];
-      }
+  for (int hh = 0; hh < G; ++hh) {
+    *reinterpret_cast<float4*>(&wpart[wave][r][hh][8 * rho]) = make_float4(o[hh][0], o[hh][1], o[hh][2], o[hh][3]);
+    *reinterpret_cast<float4*>(&wpart[wave][r][hh][8 * rho + 4]) = make_float4(o[hh][4], o[hh][5], o[hh][6], o[hh][7]);
+    if (lane == 0) {
+      wpart[wave][0][hh][kD] = m[hh];
+      wpart[wave][0][hh][kD + 1] = l[hh];
     }
   }
   __syncthreads();
@@ -392,16 +426,18 @@ __device__ __forceinline__ void FusedMerge(float (*wpart)[G][kPartFloats], int* 
   if (hh < G) {
     float mx = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < kW; ++w) mx = fmaxf(mx, wpart[w][hh][kD]);
+    for (int w = 0; w < kW; ++w) mx = fmaxf(mx, wpart[w][0][hh][kD]);
     float L = 0.0f, o0 = 0.0f, o1 = 0.0f;
 #pragma unroll
     for (int w = 0; w < kW; ++w) {
-      const float mw = wpart[w][hh][kD];
+      const float mw = wpart[w][0][hh][kD];
       const float f = mw == -INFINITY ? 0.0f : expf(mw - mx);
-      L = __builtin_fmaf(wpart[w][hh][kD + 1], f, L);
-      const float2 v = *reinterpret_cast<const float2*>(&wpart[w][hh][2 * lane]);
-      o0 = __builtin_fmaf(v.x, f, o0);
-      o1 = __builtin_fmaf(v.y, f, o1);
+      L = __builtin_fmaf(wpart[w][0][hh][kD + 1], f, L);
+      float2 v[4];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) v[rr] = *reinterpret_cast<const float2*>(&wpart[w][rr][hh][2 * lane]);
+      o0 = __builtin_fmaf((v[0].x + v[1].x) + (v[2].x + v[3].x), f, o0);
+      o1 = __builtin_fmaf((v[0].y + v[1].y) + (v[2].y + v[3].y), f, o1);
     }
     if (live_groups == 1) {  // one workgroup holds every live chunk: the output directly
       const float inv = L > 0.0f ? 1.0f / L : 0.0f;
@@ -507,27 +543,39 @@ __global__ __launch_bounds__(kFused ? 64 * kFusedWaves : kBlockThreads) void Att
     uint16_t v[kD];
   };
   __shared__ __attribute__((aligned(16))) PrepLds prep_lds[kPrep ? kW : 1];
-  __shared__ __attribute__((aligned(16))) float wpart[kFused ? kW : 1][kFused ? G : 1][kPartFloats];
+  __shared__ __attribute__((aligned(16))) float wpart[kFused ? kW : 1][kFused ? 4 : 1][kFused ? G : 1][kPartFloats];
   __shared__ int last_flag;
+  // Every kernel argument the first K / V loads depend on, fetched in one batch:
+  // the empty asm takes them as scalar inputs (it emits nothing), so their loads
+  // are issued together at entry instead of next to each use, where each waited
+  // for the one before (five serial scalar round trips ahead of the first load).
+  asm volatile("" ::"s"(kc), "s"(vc), "s"(max_seq), "s"(n_kv_heads), "s"(pos0_val), "s"(pos0_dev), "s"(seq),
+               "s"(n_chunks), "s"(chunk_len), "s"(q), "s"(n_heads));
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // in a scalar register: the chunk, its key range and the merge's buffer
+  // descriptors derive from it, and a vector wave index would put each buffer
+  // access of the merge in a loop over the distinct descriptors
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   const int32_t n_groups = kFused ? (n_chunks + kW - 1) / kW : 1;
   int64_t tk;
   int32_t c;
   if constexpr (kFused) {
-    tk = static_cast<int64_t>(blockIdx.x) / n_groups;
+    // 32-bit: the grid is below 2^32 workgroups and n_groups positive
+    const uint32_t tk32 = blockIdx.x / static_cast<uint32_t>(n_groups);
+    tk = tk32;
     if (tk >= seq * n_kv_heads) return;  // uniform over the workgroup
-    c = (static_cast<int32_t>(blockIdx.x - tk * n_groups)) * kW + wave;
+    c = static_cast<int32_t>(blockIdx.x - tk32 * static_cast<uint32_t>(n_groups)) * kW + wave;
   } else {
     const int64_t unit = static_cast<int64_t>(blockIdx.x) * kWaves + wave;
     if (unit >= seq * n_kv_heads * n_chunks) return;  // no barriers below
     tk = unit / n_chunks;
     c = static_cast<int32_t>(unit - tk * n_chunks);
   }
-  const int64_t t = tk / n_kv_heads;
+  // tk < 2^32 in both forms (the unfused grid is also below 2^32 / kWaves workgroups)
+  const int64_t t = static_cast<uint32_t>(tk) / static_cast<uint32_t>(n_kv_heads);
   const int32_t kh = static_cast<int32_t>(tk - t * n_kv_heads);
   const int64_t pos = ReadPos0(pos0_val, pos0_dev) + t;
-  const int32_t live = LiveChunks(pos, chunk_len, n_chunks);
+  const int32_t live = LiveChunks32(pos, chunk_len, n_chunks);
   const int32_t live_groups = kFused ? (live + kW - 1) / kW : 0;
   if (kFused && c / kW >= live_groups) return;  // the whole workgroup: no visible key (uniform)
   // kFused: a wave past the live chunks keeps m = -inf, l = 0, o = 0 and joins the barriers
@@ -541,20 +589,28 @@ __global__ __launch_bounds__(kFused ? 64 * kFusedWaves : kBlockThreads) void Att
   const int rho = lane & 15;
   const int r = lane >> 4;
   const bool writer = kPrep && c == live - 1;  // the chunk that holds key pos
-  const uint16_t* kb = kc + static_cast<int64_t>(kh) * max_seq * kD + 8 * rho;
-  const uint16_t* vb = vc + static_cast<int64_t>(kh) * max_seq * kD + 8 * rho;
-  // A slab of 32 keys; rows past hi are clamped to hi - 1 (always a valid
-  // address; their probability is 0). With kPipe the next slab's rows are
-  // loaded while this one is scored (G <= 2: the second set of 16 registers per
-  // row fits), and the first slab is requested before anything else.
+  // A slab of 32 keys through buffer resources on the chunk's rows [lo, hi) of
+  // K and V: a row at or past hi reads as zeros (the resource's bound), so no row
+  // index is clamped; such keys get probability 0. The lane's offset inside a
+  // slab (row 4 i + r, bytes 16 rho..) is fixed, the slab's first row a scalar
+  // offset. With kPipe the next slab's rows are loaded while this one is scored
+  // (G <= 2: the second set of 16 registers per row fits), and the first slab is
+  // requested before anything else.
+  const int64_t head_row0 = static_cast<int64_t>(kh) * max_seq + lo;
+  const uint32_t chunk_bytes = static_cast<uint32_t>(hi - lo) * (kD * 2);
+  const __amdgpu_buffer_rsrc_t krs = dev::OutResource(const_cast<uint16_t*>(kc + head_row0 * kD), chunk_bytes);
+  const __amdgpu_buffer_rsrc_t vrs = dev::OutResource(const_cast<uint16_t*>(vc + head_row0 * kD), chunk_bytes);
+  const uint32_t lane_off = static_cast<uint32_t>(r) * (kD * 2) + 16u * static_cast<uint32_t>(rho);
   constexpr bool kPipe = G <= 2;
   auto load_slab = [&](int64_t base, uint4 (&kw)[8], uint4 (&vw)[8]) {
+    const int so = __builtin_amdgcn_readfirstlane(static_cast<int>(static_cast<uint32_t>(base - lo) * (kD * 2)));
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      int64_t key = base + 4 * i + r;
-      key = key < hi ? key : hi - 1;
-      kw[i] = *reinterpret_cast<const uint4*>(kb + key * kD);
-      vw[i] = *reinterpret_cast<const uint4*>(vb + key * kD);
+      const int vo = static_cast<int>(lane_off + static_cast<uint32_t>(i) * (4 * kD * 2));
+      const dev::U32x4 a = __builtin_amdgcn_raw_buffer_load_b128(krs, vo, so, 0);
+      const dev::U32x4 b = __builtin_amdgcn_raw_buffer_load_b128(vrs, vo, so, 0);
+      kw[i] = make_uint4(a.x, a.y, a.z, a.w);
+      vw[i] = make_uint4(b.x, b.y, b.z, b.w);
     }
   };
   uint4 kw[8], vw[8];
@@ -624,22 +680,14 @@ __global__ __launch_bounds__(kFused ? 64 * kFusedWaves : kBlockThreads) void Att
     for (int j = 0; j < 8; ++j) o[hh][j] = 0.0f;
   }
 
-  for (int64_t base = lo; base < hi; base += 32) {
-    uint4 kn[8], vn[8];
-    if (kPipe) {
-      if (base + 32 < hi) load_slab(base + 32, kn, vn);  // uniform: the chunk's last slab prefetches nothing
-      __builtin_amdgcn_sched_barrier(0);  // keep the next slab's loads ahead of this slab's scores
-    } else {
-      load_slab(base, kw, vw);
-    }
+  // One slab: scores, online softmax, P.V. first: the chunk's first slab, where
+  // m is -inf and o is zero, so o needs no rescale (l * corr is 0 there too).
+  auto slab = [&](uint4 (&kw)[8], const uint4 (&vw)[8], int64_t base, bool first) {
     if (writer) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        int64_t key = base + 4 * i + r;
-        key = key < hi ? key : hi - 1;
-        if (key == pos) {  // the row this launch stores: from LDS, not the cache
+        if (base + 4 * i + r == pos) {  // the row this launch stores: from LDS, not the cache
           kw[i] = knew;
-          vw[i] = vnew;
         }
       }
     }
@@ -662,28 +710,34 @@ __global__ __launch_bounds__(kFused ? 64 * kFusedWaves : kBlockThreads) void Att
         a1 = __builtin_fmaf(qv[hh][7], HalfToF(wd[3] >> 16), a1);
         sp[i] = a0 + a1;
       }
-      // transposing butterfly over the 16-lane row
+      // Transposing butterfly over the 16-lane row, in DPP moves. The partners
+      // are rho ^ 15 (row mirror), rho ^ 7 (half-row mirror), rho ^ 2, rho ^ 1:
+      // each differs from rho in the bit that step splits on (3, 2, 1, 0), so
+      // the lane with that bit set keeps the upper half of the values and its
+      // partner the lower half, and the lane sets a value has gathered stay
+      // cosets of {0, 15}, {0, 7, 8, 15}, ... in rho's bits: disjoint, all 16
+      // lanes at the end. Lane rho ends with key 4 (rho >> 1) + r.
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const bool up = rho & 8;
         const float mine = up ? sp[j + 4] : sp[j];
         const float other = up ? sp[j] : sp[j + 4];
-        sp[j] = mine + __shfl_xor(other, 8, 16);
+        sp[j] = mine + DppMov(other, 3);
       }
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
         const bool up = rho & 4;
         const float mine = up ? sp[j + 2] : sp[j];
         const float other = up ? sp[j] : sp[j + 2];
-        sp[j] = mine + __shfl_xor(other, 4, 16);
+        sp[j] = mine + DppMov(other, 2);
       }
       {
         const bool up = rho & 2;
         const float mine = up ? sp[1] : sp[0];
         const float other = up ? sp[0] : sp[1];
-        sp[0] = mine + __shfl_xor(other, 2, 16);
+        sp[0] = mine + DppMov(other, 1);
       }
-      sp[0] += __shfl_xor(sp[0], 1, 16);
+      sp[0] += DppMov(sp[0], 0);
       const float sc = valid ? sp[0] * scale : -INFINITY;
       const float bm = WaveMax(sc);
       const float mn = fmaxf(m[hh], bm);
@@ -691,34 +745,54 @@ __global__ __launch_bounds__(kFused ? 64 * kFusedWaves : kBlockThreads) void Att
       p[hh] = valid ? expf(sc - mn) : 0.0f;
       l[hh] = l[hh] * corr + WaveSumF((rho & 1) ? 0.0f : p[hh]);  // each key once
       m[hh] = mn;
+      if (!first) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[hh][j] *= corr;
+        for (int j = 0; j < 8; ++j) o[hh][j] *= corr;
+      }
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const uint32_t wd[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
-      float vf[8];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        vf[2 * k] = HalfToF(wd[k] & 0xFFFFu);
-        vf[2 * k + 1] = HalfToF(wd[k] >> 16);
+      uint32_t wd[4] = {vw[i].x, vw[i].y, vw[i].z, vw[i].w};
+      if (writer && base + 4 * i + r == pos) {
+        wd[0] = vnew.x; wd[1] = vnew.y; wd[2] = vnew.z; wd[3] = vnew.w;
       }
 #pragma unroll
       for (int hh = 0; hh < G; ++hh) {
-        const float pi = __shfl(p[hh], 16 * r + 2 * i, 64);  // probability of key base + 4 i + r
+        const float pi = RowLane2i(p[hh], i);  // probability of key base + 4 i + r (lane 2 i of row r)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) o[hh][j] = __builtin_fmaf(pi, vf[j], o[hh][j]);
+        for (int k = 0; k < 4; ++k) {
+          o[hh][2 * k] = __builtin_fmaf(pi, HalfToF(wd[k] & 0xFFFFu), o[hh][2 * k]);
+          o[hh][2 * k + 1] = __builtin_fmaf(pi, HalfToF(wd[k] >> 16), o[hh][2 * k + 1]);
+        }
       }
     }
-    if (kPipe) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        kw[i] = kn[i];
-        vw[i] = vn[i];
-      }
+  };
+  if (kPipe) {
+    // ping-pong between the two register sets, so no loaded row is copied
+    uint4 kn[8], vn[8];
+    for (int64_t base = lo; base < hi; base += 64) {
+      const bool more = base + 32 < hi;  // uniform
+      if (more) load_slab(base + 32, kn, vn);
+      __builtin_amdgcn_sched_barrier(0);  // keep the next slab's loads ahead of this slab's scores
+      slab(kw, vw, base, base == lo);
+      if (!more) break;
+      if (base + 64 < hi) load_slab(base + 64, kw, vw);
+      __builtin_amdgcn_sched_barrier(0);
+      slab(kn, vn, base + 32, false);
+    }
+  } else {
+    for (int64_t base = lo; base < hi; base += 32) {
+      load_slab(base, kw, vw);
+      slab(kw, vw, base, base == lo);
     }
   }
 
+  if constexpr (kFused) {
+    if (live > 1) return FusedMerge<G, kW>(wpart, &last_flag, m, l, o, lane, wave, r, rho, t, kh, n_heads,
+                                            n_kv_heads, n_groups, live_groups, c / kW, out, part, cnt);
+    // one live chunk: its wave writes the output (the other waves are dead)
+    if (dead) return;
+  }
   // the four rows' partial outputs
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
@@ -727,12 +801,6 @@ __global__ __launch_bounds__(kFused ? 64 * kFusedWaves : kBlockThreads) void Att
       o[hh][j] += __shfl_xor(o[hh][j], 16, 64);
       o[hh][j] += __shfl_xor(o[hh][j], 32, 64);
     }
-  }
-  if constexpr (kFused) {
-    if (live > 1) return FusedMerge<G, kW>(wpart, &last_flag, m, l, o, lane, wave, r, rho, t, kh, n_heads,
-                                            n_kv_heads, n_groups, live_groups, c / kW, out, part, cnt);
-    // one live chunk: its wave writes the output (the other waves are dead)
-    if (dead) return;
   }
   if (r != 0) return;
 #pragma unroll
@@ -1398,6 +1466,10 @@ void LaunchDecodeGroup(const ModelMeta& c, const Pos0Arg& p0, const float* q_dev
                        const PartialsSink& sink = PartialsSink{}) {
   int32_t n_chunks;
   int64_t chunk_len;
+  // the kernel forms (token, kv head) indices and chunk offsets in 32 bits
+  RPG_CHECK(seq * c.n_kv_heads < (int64_t{1} << 32) && max_seq <= INT32_MAX / (2 * kD),
+            "decode attention over %lld (token, kv head) pairs and %lld cache rows exceeds the kernel's 32-bit "
+            "indexing", static_cast<long long>(seq * c.n_kv_heads), static_cast<long long>(max_seq));
   PlanGroupChunks(seq * c.n_kv_heads, positions, &n_chunks, &chunk_len);
   const int64_t pairs = seq * c.n_heads;
   if (n_chunks > 1) {
