@@ -484,12 +484,21 @@ __device__ __forceinline__ float SByteF(uint32_t w, int k) {
 template <uint32_t kType>
 __device__ __forceinline__ float BlockDot(const LaneBytes& r, int s, const float (&xv)[32], const float (&sx)[2]) {
   if (kType == kGgmlQ4_K) {
-    const int g = s >> 1;
     const float d = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.a.x & 0xFFFFu)));
     const float dmin = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(r.a.x >> 16)));
-    uint32_t sc0, m0, sc1, m1;
-    ScaleMinK4(2 * g, r.a.y, r.a.z, r.a.w, &sc0, &m0);
-    ScaleMinK4(2 * g + 1, r.a.y, r.a.z, r.a.w, &sc1, &m1);
+    // Lane s of the block's 8 lanes decodes sub-block s's scale and min and forms
+    // its two factors; lane s needs sub-blocks 2 (s >> 1) and 2 (s >> 1) + 1,
+    // which lanes s & ~1 and s | 1 of its quad hold (DPP quad_perm [0,0,2,2] and
+    // [1,1,3,3]). Same factors, same bits, as decoding both here. The 8 lanes of
+    // a block take the same branches, so their quads are whole.
+    uint32_t scs, ms;
+    ScaleMinK4(s, r.a.y, r.a.z, r.a.w, &scs, &ms);
+    const float fa = (d * kNibbleScale) * static_cast<float>(scs);
+    const float fb = -(dmin * static_cast<float>(ms));
+    const float a0 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(fa), 0xA0, 0xF, 0xF, false));
+    const float b0 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(fb), 0xA0, 0xF, 0xF, false));
+    const float a1 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(fa), 0xF5, 0xF, 0xF, false));
+    const float b1 = __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(fb), 0xF5, 0xF, 0xF, false));
     const uint32_t qw[4] = {r.b.x, r.b.y, r.b.z, r.b.w};
     float slo = 0.0f, shi = 0.0f;  // 2^-9 sum(q x) of the two runs
 #pragma unroll
@@ -503,11 +512,10 @@ __device__ __forceinline__ float BlockDot(const LaneBytes& r, int s, const float
         shi = __builtin_fmaf(hi[j], xv[16 + 4 * k + j], shi);
       }
     }
-    const float d9 = d * kNibbleScale;
-    float acc = (d9 * static_cast<float>(sc0)) * slo;
-    acc = __builtin_fmaf(-(dmin * static_cast<float>(m0)), sx[0], acc);
-    acc = __builtin_fmaf(d9 * static_cast<float>(sc1), shi, acc);
-    return __builtin_fmaf(-(dmin * static_cast<float>(m1)), sx[1], acc);
+    float acc = a0 * slo;
+    acc = __builtin_fmaf(b0, sx[0], acc);
+    acc = __builtin_fmaf(a1, shi, acc);
+    return __builtin_fmaf(b1, sx[1], acc);
   } else {
     // Bytes 4(q6 - 32) = (q6 << 2) ^ 0x80 as signed int8, q6 = nib | h << 4, built
     // in place: bits 2-5 the low nibble (ql shifted by 2 either way), bits 6-7 the
@@ -811,15 +819,12 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_
     }
   };
 
-  LaneBytes cur[RI][NX];
-  load(r0, cur);
-  for (; r0 < nrows; r0 += stride) {
-    LaneBytes nxt[RI][NX];
-    load(r0 + stride < nrows ? r0 + stride : r0, nxt);
+  // One row step on bytes already loaded.
+  auto step = [&](const LaneBytes (&cur)[RI][NX], int32_t rs) {
     float acc[RI];
 #pragma unroll
     for (int r = 0; r < RI; ++r) acc[r] = 0.0f;
-    const bool row_b = kMixed && ((sg.b_mask >> SegOf(se, r0)) & 1u);
+    const bool row_b = kMixed && ((sg.b_mask >> SegOf(se, rs)) & 1u);
 #pragma unroll
     for (int it = 0; it < NX; ++it) {
       if (c + kGroups * it < nb) {
@@ -834,20 +839,45 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_
     }
     const float total = ReduceRows<RI>(acc, lane);
     if (kPaired) {
-      // lanes 0 and 16 hold the gate and up totals of pair r0 / 2
+      // lanes 0 and 16 hold the gate and up totals of pair rs / 2
       const float g = __shfl(total, 0, 64);
       const float u = __shfl(total, 16, 64);
-      if (lane == 0) sg.out[0][r0 >> 1] = dev::SiluMul(g, u);
+      if (lane == 0) sg.out[0][rs >> 1] = dev::SiluMul(g, u);
     } else {
       const int rr = ReducedRow<RI>(lane);
-      const int sgi = SegOf(se, r0);
+      const int sgi = SegOf(se, rs);
       const int64_t first = SegFirst(sg, sgi);
-      if ((lane & 15) == 0 && lane < 16 * RI && r0 + rr < nrows) PickSeg(sg.out, sgi)[r0 - first + rr] = total;
+      if ((lane & 15) == 0 && lane < 16 * RI && rs + rr < nrows) PickSeg(sg.out, sgi)[rs - first + rr] = total;
     }
+  };
+  if constexpr (kMixed) {
+    // Two register sets used in turn, so no loaded byte is copied: with both
+    // types' decode paths in the loop, the copy of the next step's bytes cost
+    // more than the second set (q / k / v of a Q4_K_M layer: 5.5 -> 4.9 us; the
+    // single-type kernels measured slower this way).
+    LaneBytes ba[RI][NX], bb[RI][NX];
+    load(r0, ba);
+    while (r0 < nrows) {
+      const int32_t r1 = r0 + stride;
+      if (r1 < nrows) load(r1, bb);
+      step(ba, r0);
+      if (r1 >= nrows) break;
+      r0 = r1 + stride;
+      if (r0 < nrows) load(r0, ba);
+      step(bb, r1);
+    }
+  } else {
+    LaneBytes cur[RI][NX];
+    load(r0, cur);
+    for (; r0 < nrows; r0 += stride) {
+      LaneBytes nxt[RI][NX];
+      load(r0 + stride < nrows ? r0 + stride : r0, nxt);
+      step(cur, r0);
 #pragma unroll
-    for (int r = 0; r < RI; ++r)
+      for (int r = 0; r < RI; ++r)
 #pragma unroll
-      for (int it = 0; it < NX; ++it) cur[r][it] = nxt[r][it];
+        for (int it = 0; it < NX; ++it) cur[r][it] = nxt[r][it];
+    }
   }
 }
 
@@ -1012,15 +1042,14 @@ void LaunchDecodeSegs(const char* name, const MatSegs& sg, int32_t n_seg, int64_
             static_cast<long long>(rows));
   const int64_t need = (rows + kWavesPerBlock * RI - 1) / (kWavesPerBlock * RI);
   const unsigned grid = static_cast<unsigned>(need < kDecodeGrid ? need : kDecodeGrid);
-  constexpr bool kHasQ6 = kType == kGgmlQ6_K || kTypeB == kGgmlQ6_K;
-  if (kHasQ6 && RowsAligned4(sg, n_seg, row_bytes, kPaired)) {
+  if (RowsAligned4(sg, n_seg, row_bytes, kPaired)) {
     if (nrm != nullptr) {
-      Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB, true, kHasQ6>, dim3(grid), dim3(kMmBlock), sg,
+      Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB, true, true>, dim3(grid), dim3(kMmBlock), sg,
              rows, row_bytes, nb, x, *nrm);
       nrm->x_out = nullptr;
       return;
     }
-    Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB, false, kHasQ6>, dim3(grid), dim3(kMmBlock), sg, rows,
+    Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB, false, true>, dim3(grid), dim3(kMmBlock), sg, rows,
            row_bytes, nb, x, NormPrologue{});
     return;
   }
@@ -1057,9 +1086,9 @@ void LaunchSplit(const char* name, const uint8_t* w, int64_t rows, int64_t row_b
   const int64_t max_grid = NXW == 1 ? 4096 : 1024;
   const int64_t need = (rows + RI - 1) / RI;
   const unsigned grid = static_cast<unsigned>(need < max_grid ? need : max_grid);
-  if (kType == kGgmlQ6_K && RowsAligned4(OneSeg(w, rows, out), 1, row_bytes, false)) {
-    Launch(name, MatVecSplitKernel<kType, WS, NXW, RI, kType == kGgmlQ6_K>, dim3(grid), dim3(64 * WS), w, rows,
-           row_bytes, nb, x, out);
+  if (RowsAligned4(OneSeg(w, rows, out), 1, row_bytes, false)) {
+    Launch(name, MatVecSplitKernel<kType, WS, NXW, RI, true>, dim3(grid), dim3(64 * WS), w, rows, row_bytes, nb, x,
+           out);
     return;
   }
   Launch(name, MatVecSplitKernel<kType, WS, NXW, RI>, dim3(grid), dim3(64 * WS), w, rows, row_bytes, nb, x, out);
