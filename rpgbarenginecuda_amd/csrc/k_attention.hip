@@ -871,6 +871,32 @@ __device__ __forceinline__ F16x4 VTr(const _Float16* lds_ptr) {
   return __builtin_bit_cast(F16x4, v);
 }
 
+// x as two fp16 terms, *h = fp16(x) and *l = fp16(x - h) (the difference is
+// exact in fp32). Each remainder is one mixed-precision FMA, h * -1 + x with h
+// read as fp16 and the exact result rounded straight to fp16 into one half of
+// the packed pair: the same bits as converting h back, subtracting and
+// converting, in one instruction instead of three. (Written out because the
+// compiler folds a multiply by -1 into a subtraction and then needs the
+// conversions.)
+__device__ __forceinline__ uint32_t RemainderPair(uint32_t hpair, float x0, float x1) {
+  uint32_t d;
+  asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]\n\t"
+      "v_fma_mixhi_f16 %0, %1, -1.0, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+      : "=&v"(d)
+      : "v"(hpair), "v"(x0), "v"(x1));
+  return d;
+}
+__device__ __forceinline__ void SplitPair(const float (&x)[8], F16x8* h, F16x8* l) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) (*h)[j] = static_cast<_Float16>(x[j]);
+  typedef unsigned int U32x4v __attribute__((ext_vector_type(4)));
+  const U32x4v hw = __builtin_bit_cast(U32x4v, *h);
+  U32x4v lw;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) lw[k] = RemainderPair(hw[k], x[2 * k], x[2 * k + 1]);
+  *l = __builtin_bit_cast(F16x8, lw);
+}
+
 __device__ __forceinline__ F16x8 SplitTerm(float (&x)[8]) {
   // x <- x - fp16(x), returning fp16(x) (round to nearest even; the difference is exact in fp32)
   F16x8 h;
@@ -1077,8 +1103,8 @@ __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
       float pr[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) pr[j] = st[mt][rb + j];
-      const F16x8 ph = SplitTerm(pr);
-      const F16x8 pl = SplitTerm(pr);
+      F16x8 ph, pl;
+      SplitPair(pr, &ph, &pl);
       const int koff = 32 * mt + 16 * (ks2 & 1) + 4 * hf;  // keys koff + 0..3 and koff + 8..11
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
