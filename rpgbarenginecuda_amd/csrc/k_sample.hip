@@ -168,11 +168,64 @@ __device__ __forceinline__ Best BlockBest(Best x, Best* sh) {
   return r;
 }
 
+// Wave-level steps through DPP moves (VALU, a few cycles) instead of LDS
+// permutes (a round trip through the LDS unit each, in dependent chains):
+// a 64-bit value moved as two 32-bit halves; lanes the pattern gives no source
+// (or rows outside row_mask) keep `old`.
+template <int kCtrl, int kRowMask = 0xF>
+__device__ __forceinline__ uint64_t DppU64(uint64_t v, uint64_t old) {
+  const int lo = __builtin_amdgcn_update_dpp(static_cast<int>(static_cast<uint32_t>(old)),
+                                             static_cast<int>(static_cast<uint32_t>(v)), kCtrl, kRowMask, 0xF, false);
+  const int hi = __builtin_amdgcn_update_dpp(static_cast<int>(static_cast<uint32_t>(old >> 32)),
+                                             static_cast<int>(static_cast<uint32_t>(v >> 32)), kCtrl, kRowMask, 0xF,
+                                             false);
+  return (static_cast<uint64_t>(static_cast<uint32_t>(hi)) << 32) | static_cast<uint32_t>(lo);
+}
+template <int kCtrl, int kRowMask = 0xF>
+__device__ __forceinline__ float DppF(float v, float old) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(__float_as_int(old), __float_as_int(v), kCtrl, kRowMask, 0xF, false));
+}
+template <int kCtrl, int kRowMask = 0xF>
+__device__ __forceinline__ double DppDbl(double v, double old) {
+  return __builtin_bit_cast(double, DppU64<kCtrl, kRowMask>(__builtin_bit_cast(uint64_t, v),
+                                                             __builtin_bit_cast(uint64_t, old)));
+}
+// Row steps (quad_perm [1,0,3,2], [2,3,0,1], half-row mirror, row mirror) leave
+// every lane of a 16-lane row with the row's op-total; rows 1 and 3 then take
+// rows 0 and 2 (row_bcast:15) and rows 2 and 3 take row 1 (row_bcast:31), so
+// lane 63 ends with the wave's total. Every lane must be active.
+__device__ __forceinline__ float WaveMaxTo63(float v) {
+  v = fmaxf(v, DppF<0xB1>(v, v));
+  v = fmaxf(v, DppF<0x4E>(v, v));
+  v = fmaxf(v, DppF<0x141>(v, v));
+  v = fmaxf(v, DppF<0x140>(v, v));
+  v = fmaxf(v, DppF<0x142, 0xA>(v, -INFINITY));
+  return fmaxf(v, DppF<0x143, 0xC>(v, -INFINITY));
+}
+__device__ __forceinline__ double WaveSumTo63(double v) {
+  v += DppDbl<0xB1>(v, 0.0);
+  v += DppDbl<0x4E>(v, 0.0);
+  v += DppDbl<0x141>(v, 0.0);
+  v += DppDbl<0x140>(v, 0.0);
+  v += DppDbl<0x142, 0xA>(v, 0.0);
+  return v + DppDbl<0x143, 0xC>(v, 0.0);
+}
+// Inclusive prefix sum over the wave: row_shr 1, 2, 4, 8 inside each row, then
+// the rows' totals as above.
+__device__ __forceinline__ uint64_t WaveInclScanU64(uint64_t v) {
+  v += DppU64<0x111>(v, 0);
+  v += DppU64<0x112>(v, 0);
+  v += DppU64<0x114>(v, 0);
+  v += DppU64<0x118>(v, 0);
+  v += DppU64<0x142, 0xA>(v, 0);
+  return v + DppU64<0x143, 0xC>(v, 0);
+}
+
 // Maximum of non-NaN values (callers never pass NaN: they only keep v > m).
 __device__ __forceinline__ float BlockMax(float v, float* sh) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  v = WaveMaxTo63(v);
+  if ((threadIdx.x & 63) == 63) sh[threadIdx.x >> 6] = v;
   __syncthreads();
   float r = sh[0];
 #pragma unroll
@@ -181,12 +234,11 @@ __device__ __forceinline__ float BlockMax(float v, float* sh) {
   return r;
 }
 
-// Sum in a fixed tree: the butterfly gives every lane the same value
-// (each pair adds the same two operands), then the wave totals left to right.
+// Sum in a fixed tree (the same in every workgroup and run): the wave's DPP
+// tree, then the wave totals left to right.
 __device__ __forceinline__ double BlockSumD(double v, double* sh) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  if ((threadIdx.x & 63) == 0) sh[threadIdx.x >> 6] = v;
+  v = WaveSumTo63(v);
+  if ((threadIdx.x & 63) == 63) sh[threadIdx.x >> 6] = v;
   __syncthreads();
   double r = sh[0];
 #pragma unroll
@@ -199,12 +251,7 @@ __device__ __forceinline__ double BlockSumD(double v, double* sh) {
 __device__ __forceinline__ uint64_t BlockExclScan(uint64_t v, uint64_t* sh, uint64_t* total) {
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
-  uint64_t incl = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const uint64_t o = __shfl_up(incl, off, 64);
-    if (lane >= off) incl += o;
-  }
+  const uint64_t incl = WaveInclScanU64(v);
   if (lane == 63) sh[w] = incl;
   __syncthreads();
   uint64_t before = 0, tot = 0;
