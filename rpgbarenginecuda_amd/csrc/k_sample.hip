@@ -361,16 +361,12 @@ __device__ Pick PickDescending(const uint32_t* hist, uint32_t rem, uint64_t* sh,
 // top_p: the smallest digit d with base + sum(digit <= d) > thr; carry = base + sum(digit < d).
 // *total_out (optional) gets the histogram's total.
 template <int kNumBins>
-__device__ Pick PickAscending(const uint64_t* hist, uint64_t base, uint64_t thr, uint64_t* sh, Pick* pick,
-                              uint64_t* total_out = nullptr) {
+__device__ Pick PickAscendingOf(const uint64_t (&h)[kNumBins / kThreads], uint64_t base, uint64_t thr, uint64_t* sh,
+                                Pick* pick, uint64_t* total_out = nullptr) {
   constexpr int kPer = kNumBins / kThreads;
-  uint64_t h[kPer];
   uint64_t s = 0;
 #pragma unroll
-  for (int b = 0; b < kPer; ++b) {
-    h[b] = hist[threadIdx.x * kPer + b];
-    s += h[b];
-  }
+  for (int b = 0; b < kPer; ++b) s += h[b];
   uint64_t total;
   const uint64_t below = BlockExclScan(s, sh, &total);
   if (total_out != nullptr) *total_out = total;
@@ -390,6 +386,14 @@ __device__ Pick PickAscending(const uint64_t* hist, uint64_t base, uint64_t thr,
   const Pick r = *pick;
   __syncthreads();
   return r;
+}
+template <int kNumBins>
+__device__ Pick PickAscending(const uint64_t* hist, uint64_t base, uint64_t thr, uint64_t* sh, Pick* pick,
+                              uint64_t* total_out = nullptr) {
+  uint64_t h[kNumBins / kThreads];
+#pragma unroll
+  for (int b = 0; b < kNumBins / kThreads; ++b) h[b] = hist[threadIdx.x * (kNumBins / kThreads) + b];
+  return PickAscendingOf<kNumBins>(h, base, thr, sh, pick, total_out);
 }
 
 
@@ -626,10 +630,17 @@ __global__ __launch_bounds__(kThreads) void SampleTopKCandKernel(Logits lg, int3
     const int above = shift + LevelBits(level);
     for (int b = threadIdx.x; b < kBins; b += kThreads) hist[b] = 0;
     __syncthreads();
-    for (uint32_t c = threadIdx.x; c < n_c; c += kThreads) {
-      uint32_t k;
-      CandidateAt<false, kTopKCandLds>(c, n_c, lkey, nullptr, lstart, ns, cand, &k, nullptr);
-      if ((k >> above) == prefix) atomicAdd(&hist[(k >> shift) & mask], 1u);
+    if (n_c <= kTopKCandLds) {  // uniform: the LDS copy, read through an LDS address
+      for (uint32_t c = threadIdx.x; c < n_c; c += kThreads) {
+        const uint32_t k = lkey[c];
+        if ((k >> above) == prefix) atomicAdd(&hist[(k >> shift) & mask], 1u);
+      }
+    } else {
+      for (uint32_t c = threadIdx.x; c < n_c; c += kThreads) {
+        uint32_t k;
+        CandidateAt<false, kTopKCandLds>(c, n_c, lkey, nullptr, lstart, ns, cand, &k, nullptr);
+        if ((k >> above) == prefix) atomicAdd(&hist[(k >> shift) & mask], 1u);
+      }
     }
     __syncthreads();
     const Pick p = level == 3 ? PickDescending<256>(hist, rem, sh, &pick) : PickDescending<kBins>(hist, rem, sh, &pick);
@@ -751,9 +762,14 @@ __global__ __launch_bounds__(kThreads) void SampleTopPCandKernel(Logits lg, int3
     const int64_t i = ElemIndex(j);
     v[j] = i < lg.n ? lg.x[i] : 0.0f;
   }
+  // the thread's level-1 bins, requested with the logits (before the barriers of
+  // the partials' reductions, which would otherwise hold these loads back)
+  uint64_t h1[kBins / kThreads];
+#pragma unroll
+  for (int b = 0; b < kBins / kThreads; ++b) h1[b] = s->phist[threadIdx.x * (kBins / kThreads) + b];
   const ProbCtx c = LoadProbCtx(lg, topk, s, shf, shd);
   uint64_t total = 0;
-  const Pick p1 = PickAscending<kBins>(s->phist, 0ull, thr, sh, &pick, &total);
+  const Pick p1 = PickAscendingOf<kBins>(h1, 0ull, thr, sh, &pick, &total);
   uint32_t key[kPerThread];
   uint64_t w[kPerThread];
 #pragma unroll
@@ -783,13 +799,22 @@ __global__ __launch_bounds__(kThreads) void SampleTopPCandKernel(Logits lg, int3
       const int above = shift + LevelBits(level);
       for (int b = threadIdx.x; b < kBins; b += kThreads) hist[b] = 0;
       __syncthreads();
-      for (uint32_t k = threadIdx.x; k < n_c; k += kThreads) {
-        uint32_t ck;
-        uint64_t cw;
-        CandidateAt<true, kTopPCandLds>(k, n_c, lkey, lw, lstart, ns, cand, &ck, &cw);
-        if ((ck >> above) == prefix)
-          atomicAdd(reinterpret_cast<unsigned long long*>(&hist[(ck >> shift) & mask]),
-                    static_cast<unsigned long long>(cw));
+      if (n_c <= kTopPCandLds) {  // uniform: the LDS copy, read through LDS addresses
+        for (uint32_t k = threadIdx.x; k < n_c; k += kThreads) {
+          const uint32_t ck = lkey[k];
+          if ((ck >> above) == prefix)
+            atomicAdd(reinterpret_cast<unsigned long long*>(&hist[(ck >> shift) & mask]),
+                      static_cast<unsigned long long>(lw[k]));
+        }
+      } else {
+        for (uint32_t k = threadIdx.x; k < n_c; k += kThreads) {
+          uint32_t ck;
+          uint64_t cw;
+          CandidateAt<true, kTopPCandLds>(k, n_c, lkey, lw, lstart, ns, cand, &ck, &cw);
+          if ((ck >> above) == prefix)
+            atomicAdd(reinterpret_cast<unsigned long long*>(&hist[(ck >> shift) & mask]),
+                      static_cast<unsigned long long>(cw));
+        }
       }
       __syncthreads();
       const Pick p = level == 3 ? PickAscending<256>(hist, base, thr, sh, &pick)
@@ -843,6 +868,18 @@ struct Draw {
   const uint64_t* counter_dev;
   int32_t* out_idx;
 };
+
+// The draw with u resolved at kernel entry: the device counter is constant for
+// the launch, so every workgroup reads it with its first loads and the last
+// workgroup's inverse transform does not wait one more memory round trip for it.
+__device__ __forceinline__ Draw ResolvedDraw(Draw d) {
+  if (d.counter_dev != nullptr) {
+    d.u_val = CounterUniformOf(d.seed, *d.counter_dev);
+    d.counter_dev = nullptr;
+    asm volatile("" ::"v"(d.u_val));  // formed here, not next to its use in the last workgroup
+  }
+  return d;
+}
 
 // The inverse transform over probs[0, n) by one workgroup, from the slices'
 // Fix52 / double partials (in the last workgroup of the launch that wrote them,
@@ -986,32 +1023,50 @@ __device__ void InverseTransform(const float* __restrict__ probs, int64_t n, con
 template <bool kSample>
 __global__ __launch_bounds__(kThreads) void SampleNormKernel(Logits lg, int32_t topk, int32_t topp,
                                                              float* __restrict__ probs, SampleScratch* __restrict__ s,
-                                                             Draw draw) {
+                                                             Draw draw0) {
   __shared__ float shf[kWaves];
   __shared__ double shd[kWaves];
   __shared__ uint64_t sh[kWaves];
   __shared__ Best shb[kWaves];
   __shared__ int last;
+  const Draw draw = kSample ? ResolvedDraw(draw0) : draw0;
+  __shared__ float best_raw;
   float raw[kPerThread];
 #pragma unroll
   for (int j = 0; j < kPerThread; ++j) {  // requested before the partials
     const int64_t i = ElemIndex(j);
     raw[j] = i < lg.n ? lg.x[i] : 0.0f;
   }
+  // top_p's inputs requested with the logits, ahead of the partials' reductions
+  // (whose barriers would otherwise hold each load back to a round trip of its
+  // own): the cut, the kept weight, the slices' first maxima and the logit at
+  // each thread's slice maximum (the block's argmax is one of them)
+  const int ns = NumSlices(lg.n);
+  uint32_t cut_key = 0;
+  uint64_t kept_w = 0;
+  Best bt{-INFINITY, 0x7FFFFFFF};
+  float bt_raw = 0.0f;
+  if (topp) {
+    cut_key = s->cut_key;
+    kept_w = s->kept_w;
+    for (int g = threadIdx.x; g < ns; g += kThreads) bt = Better(bt, Best{s->best_val[g], s->best_idx[g]});
+    if (bt.i >= 0 && bt.i < lg.n) bt_raw = lg.x[bt.i];
+  }
   const ProbCtx c = LoadProbCtx(lg, topk, s, shf, shd);
   float cut = 0.0f, inv2 = 1.0f;
   bool forced = false, rescale = false;
   int32_t best = 0;
   if (topp) {
-    const int ns = NumSlices(lg.n);
-    cut = FromOrderKey(s->cut_key);  // NaN when there is no cut: nothing compares <= it
-    const Best b = BestOfParts(s->best_val, s->best_idx, ns, shb);  // the first maximum of the scaled logits
+    cut = FromOrderKey(cut_key);  // NaN when there is no cut: nothing compares <= it
+    const Best b = BlockBest(bt, shb);  // the first maximum of the scaled logits
     best = b.i;
+    if (bt.i == b.i && b.i >= 0 && b.i < lg.n) best_raw = bt_raw;  // threads holding that index agree
+    __syncthreads();
     // p is non-decreasing in the logit, so nothing survives the cut exactly when
     // the largest p does not: then the argmax is kept with 1 (no argmax: every
     // logit NaN)
-    forced = best >= 0 && best < lg.n && ProbAt(lg, c, best) <= cut;
-    const double sum2 = forced ? 1.0 : static_cast<double>(s->kept_w) * 0x1p-62;
+    forced = best >= 0 && best < lg.n && ProbOfRaw(lg, c, best_raw) <= cut;
+    const double sum2 = forced ? 1.0 : static_cast<double>(kept_w) * 0x1p-62;
     rescale = sum2 > 0.0;
     if (rescale) inv2 = static_cast<float>(1.0 / sum2);
   }
@@ -1049,10 +1104,11 @@ __global__ __launch_bounds__(kThreads) void SampleInverseKernel(const float* __r
 // Inverse-transform partials of caller-provided probabilities; the last
 // workgroup then draws the token.
 __global__ __launch_bounds__(kThreads) void SampleFixKernel(const float* __restrict__ probs, int64_t n,
-                                                            SampleScratch* __restrict__ s, Draw draw) {
+                                                            SampleScratch* __restrict__ s, Draw draw0) {
   __shared__ double shd[kWaves];
   __shared__ uint64_t sh[kWaves];
   __shared__ int last;
+  const Draw draw = ResolvedDraw(draw0);
   float p[kPerThread];
   bool in[kPerThread];
 #pragma unroll
