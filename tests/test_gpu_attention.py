@@ -61,6 +61,10 @@ CASES = [
     ("1.7B decode at 0", 16, 8, 4096, 0, 1),
     ("1.7B decode at 4095 (full cache)", 16, 8, 4096, 4095, 1),
     ("4B decode at 1000", 32, 8, 4096, 1000, 1),
+    # several 32-key slabs per chunk: the rescale between slabs and the two alternating slab buffers
+    ("1.7B decode at 100 (one chunk, 4 slabs)", 16, 8, 4096, 100, 1),
+    ("4B decode at 90 (one chunk, 3 slabs, group 4)", 32, 8, 4096, 90, 1),
+    ("1.7B decode at 6000 of 8192 (64-key chunks, 2 slabs each, merged)", 16, 8, 8192, 6000, 1),
     ("1.7B prefill n=21", 16, 8, 4096, 0, 21),
     ("1.7B small batch continuation", 16, 8, 4096, 300, 3),
     ("1.7B prefill n=512 after 100", 16, 8, 1024, 100, 512),
