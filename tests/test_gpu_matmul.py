@@ -275,6 +275,9 @@ GROUPS = [
     ("mixed, one Q6_K of odd rows (not fused)", [(12, 256), (14, 7)], 256, 1),
     ("odd rows (not fused)", [(12, 1001), (12, 7)], 256, 1),
     ("Q4_K of 32768+ rows (own shape)", [(12, 20000), (12, 16000)], 256, 1),
+    # mixed types with several row steps per wave (the mixed kernel's two row buffers in turn)
+    ("mixed, ~3 row steps per wave, buffer loads", [(12, 12000), (14, 12000)], 512, 1),
+    ("mixed, ~3 row steps per wave, unaligned Q6_K rows", [(12, 20000), (14, 4000)], 256, 1),
     ("prefill (one call per matrix)", [(12, 256), (14, 128)], 512, 40),
     ("prefill, decoded planes", [(12, 2048), (12, 1024), (14, 1024)], 2048, 600),
     ("small batch", [(12, 256), (12, 256)], 512, 3),
@@ -366,6 +369,7 @@ NORM_GROUPS = [
     ("Q4_K of 32768+ rows (4 rows per wave)", [(12, 33000)], 256, True, True),
     ("runs, odd rows", [(14, 300), (12, 200), (12, 7), (14, 64), (14, 64)], 512, True, True),
     ("three blocks per row", [(12, 128), (14, 96)], 768, True, True),
+    ("mixed, ~3 row steps per wave", [(12, 12000), (14, 12000)], 512, True, True),
 ]
 
 
