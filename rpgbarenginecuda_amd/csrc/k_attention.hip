@@ -938,8 +938,15 @@ __global__ __launch_bounds__(256, 2) void AttnPrefillMfmaKernel(
   const int hf = lane >> 5;    // which half of the keys / dims this lane holds
   const int col = lane & 31;   // the lane's query within the wave
   const int32_t pair = static_cast<int32_t>(blockIdx.x) / n_heads;
-  const int h = static_cast<int>(blockIdx.x) - pair * n_heads;
-  const int kh = h / group;
+  // Slot i of the pair's n_heads workgroups takes kv head i % n_kv and query head
+  // (i % n_kv) group + i / n_kv of it: the heads sharing a kv head sit n_kv
+  // slots apart. Workgroups go to the XCDs in turn (id mod 8), so with 8 kv heads
+  // (every Qwen3 shape here) all heads of a kv head, in every tile, run on one
+  // XCD and read its K / V rows through one L2 instead of `group` of them.
+  const int slot = static_cast<int>(blockIdx.x) - pair * n_heads;
+  const int n_kv = n_heads / group;
+  const int kh = slot % n_kv;
+  const int h = kh * group + slot / n_kv;
   int32_t chunk, tile;
   if (order.n > 0) {
     const uint32_t entry = order.e[pair];
