@@ -50,6 +50,9 @@ constexpr int kMmBlock = 256;        // 4 waves per workgroup
 constexpr int kWavesPerBlock = kMmBlock / 64;
 constexpr int kGroupLanes = 8;       // lanes sharing one super-block
 constexpr int kGroups = 64 / kGroupLanes;
+// Waves per workgroup of the one-token decode kernel (MatVecQuantKernel).
+constexpr int kDecWaves = 4;
+constexpr int kDecBlock = 64 * kDecWaves;
 
 bool Aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 
@@ -639,7 +642,7 @@ __device__ __forceinline__ int64_t SegFirst(const MatSegs& sg, int i) {
 // loads take the buffer form of LoadLaneBytesBuf.
 template <uint32_t kType, int NX, int RI, bool kPaired = false, uint32_t kTypeB = kType, bool kNorm = false,
           bool kAl4 = false>
-__global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_t rows, int64_t row_bytes, int32_t nb,
+__global__ __launch_bounds__(kDecBlock) void MatVecQuantKernel(MatSegs sg, int64_t rows, int64_t row_bytes, int32_t nb,
                                                               const float* __restrict__ x, NormPrologue nrm) {
   static_assert(!kNorm || NX == 1, "the norm prologue needs the whole row in one wave");
   constexpr int64_t kBB = BlockBytesOf<kType>::value;
@@ -661,8 +664,8 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_
   // (32-bit: the launcher keeps rows + stride below 2^31, and the scalar unit
   // compares 32-bit values only.)
   const int32_t nrows = static_cast<int32_t>(rows);
-  const int32_t stride = static_cast<int32_t>(gridDim.x) * kWavesPerBlock * RI;
-  int32_t r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6))) * RI;
+  const int32_t stride = static_cast<int32_t>(gridDim.x) * kDecWaves * RI;
+  int32_t r0 = __builtin_amdgcn_readfirstlane(static_cast<int>(blockIdx.x * kDecWaves + (threadIdx.x >> 6))) * RI;
   // No early exit for waves past the last row: a branch here would keep the
   // compiler from fetching the remaining kernel arguments in the first batch. Such
   // waves load the last row's bytes (the load below clamps the row) and skip the
@@ -681,13 +684,14 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_
     // the sum of squares meets in LDS (waves added in a fixed order), and h is
     // staged in LDS, from where each wave reads its lanes' elements.
     __shared__ float hs[kGroups * kQK_K];
-    __shared__ double part[kWavesPerBlock];
-    const int n = nb * kQK_K;  // <= kGroups * kQK_K = 4 * kMmBlock * 2
+    __shared__ double part[kDecWaves];
+    static_assert(kGroups * kQK_K <= 8 * kDecBlock, "two float4 per thread cover the row");
+    const int n = nb * kQK_K;  // <= kGroups * kQK_K
     float4 v[2], wv[2];
     double ss = 0.0;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int i = 4 * static_cast<int>(threadIdx.x) + 4 * kMmBlock * j;
+      const int i = 4 * static_cast<int>(threadIdx.x) + 4 * kDecBlock * j;
       if (i < n) {
         v[j] = dev::Load4(x + i);
         if (nrm.d != nullptr) {
@@ -704,11 +708,11 @@ __global__ __launch_bounds__(kMmBlock) void MatVecQuantKernel(MatSegs sg, int64_
     __syncthreads();
     double total = part[0];
 #pragma unroll
-    for (int q = 1; q < kWavesPerBlock; ++q) total += part[q];
+    for (int q = 1; q < kDecWaves; ++q) total += part[q];
     const float scale = dev::RmsScale(total, n, nrm.eps);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-      const int i = 4 * static_cast<int>(threadIdx.x) + 4 * kMmBlock * j;
+      const int i = 4 * static_cast<int>(threadIdx.x) + 4 * kDecBlock * j;
       if (i < n) dev::Store4(hs + i, dev::ScaleMul(v[j], scale, wv[j]));
     }
     __syncthreads();
@@ -1009,8 +1013,8 @@ void LaunchQuant(const char* name, const uint8_t* w, int64_t rows, int64_t row_b
 }
 
 // Decode: persistent waves, 2 rows per step (4 for Q4_K matrices of 32768 rows
-// or more), at most kDecodeGrid workgroups (16 waves per CU).
-constexpr int64_t kDecodeGrid = 1024;
+// or more), at most kDecodeWaves waves (16 per CU).
+constexpr int64_t kDecodeWaves = 4096;
 
 // Whether every row of the launch starts at a multiple of 4 bytes and below 2^31
 // bytes from its segment's base (the buffer-load form of the decode kernels).
@@ -1038,28 +1042,29 @@ template <uint32_t kType, int RI, bool kPaired = false, uint32_t kTypeB = kType>
 void LaunchDecodeSegs(const char* name, const MatSegs& sg, int32_t n_seg, int64_t row_bytes, int32_t nb,
                       const float* x, NormPrologue* nrm = nullptr) {
   const int64_t rows = sg.end[n_seg - 1];
-  RPG_CHECK(rows < (int64_t(1) << 31) - kDecodeGrid * kWavesPerBlock * RI, "too many rows for one decode launch: %lld",
+  RPG_CHECK(rows < (int64_t(1) << 31) - kDecodeWaves * RI, "too many rows for one decode launch: %lld",
             static_cast<long long>(rows));
-  const int64_t need = (rows + kWavesPerBlock * RI - 1) / (kWavesPerBlock * RI);
-  const unsigned grid = static_cast<unsigned>(need < kDecodeGrid ? need : kDecodeGrid);
+  const int64_t need = (rows + kDecWaves * RI - 1) / (kDecWaves * RI);
+  const int64_t cap = kDecodeWaves / kDecWaves;
+  const unsigned grid = static_cast<unsigned>(need < cap ? need : cap);
   if (RowsAligned4(sg, n_seg, row_bytes, kPaired)) {
     if (nrm != nullptr) {
-      Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB, true, true>, dim3(grid), dim3(kMmBlock), sg,
+      Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB, true, true>, dim3(grid), dim3(kDecBlock), sg,
              rows, row_bytes, nb, x, *nrm);
       nrm->x_out = nullptr;
       return;
     }
-    Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB, false, true>, dim3(grid), dim3(kMmBlock), sg, rows,
+    Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB, false, true>, dim3(grid), dim3(kDecBlock), sg, rows,
            row_bytes, nb, x, NormPrologue{});
     return;
   }
   if (nrm != nullptr) {
-    Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB, true>, dim3(grid), dim3(kMmBlock), sg, rows,
+    Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB, true>, dim3(grid), dim3(kDecBlock), sg, rows,
            row_bytes, nb, x, *nrm);
     nrm->x_out = nullptr;
     return;
   }
-  Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB>, dim3(grid), dim3(kMmBlock), sg, rows, row_bytes, nb,
+  Launch(name, MatVecQuantKernel<kType, 1, RI, kPaired, kTypeB>, dim3(grid), dim3(kDecBlock), sg, rows, row_bytes, nb,
          x, NormPrologue{});
 }
 
